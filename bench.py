@@ -1,0 +1,292 @@
+"""Benchmark of the sparse-FFN decode hot path on one MI355X.
+
+Default workload (one step = one decode token through one layer):
+  Falcon-7B-shaped ReLU FFN layer, d_model=4544, d_ff=18176, Q4_0 weights in
+  the bundled layout, rank-128 fp32 predictor, threshold giving ~5% (909)
+  active neurons; each step runs predictor -> selection -> gathered up/down
+  FFN on the device (llg_hipd_ffn_predict_sparse), with a fresh x per token.
+  Steps rotate over LAYERS distinct HBM copies of the layer so that the
+  gathered rows are not served from the 256 MB MALL.
+
+Output: one JSON line (see the contract in the repository's docs), with a
+`roofline` object for the sparse FFN kernels (algorithmic gathered bytes /
+their average event-timed duration on the library's stream) and a
+`cpu_baseline` object (the oracle's restatement of the reference CPU path,
+timed on a bounded sample on this host).
+
+Other workloads (--workload dense-q4_0 | dense-q8_0 | dense-f16 | window |
+moe-decode | moe-prefill) measure the remaining hot-path configurations.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "llama.go_amd"))
+
+HBM_PEAK_GBS = 8000.0
+H, FF, RANK, N_ACTIVE = 4544, 18176, 128, 909
+Q4_ROW = H // 32 * 18                # 2556 B per GGUF Q4_0 row
+BUNDLE_ALG = 2 * Q4_ROW              # 5112 B per neuron (unpadded)
+PRED_BYTES = (RANK * H + FF * RANK) * 4
+
+
+def log(msg: str):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def vp(t) -> C.c_void_p:
+    return C.c_void_p(t.data_ptr())
+
+
+class Timer:
+    """HIP events recorded on the library's own stream."""
+
+    def __init__(self, torch, stream_ptr: int):
+        self.torch = torch
+        self.stream = torch.cuda.ExternalStream(stream_ptr)
+
+    def event(self):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record(self.stream)
+        return e
+
+
+def threshold_for(logits: np.ndarray, n: int) -> float:
+    s = np.sort(logits.astype(np.float32))[::-1]
+    return float(np.float32((np.float64(s[n - 1]) + np.float64(s[n])) / 2))
+
+
+def bench_sparse(args, torch, llg, dev):
+    gg = llg.gguf
+    L = args.layers
+    log(f"sparse: generating layer on GPU (d={H}, ff={FF}, Q4_0), {L} HBM copies")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x11A3A000)
+    up = gg.quantize(torch.randn((FF, H), generator=g, device="cuda") * 0.02, gg.Q4_0)
+    dn = gg.quantize(torch.randn((FF, H), generator=g, device="cuda") * 0.02, gg.Q4_0)
+    wup = (torch.randn((RANK, H), generator=g, device="cuda") * 0.05).contiguous()
+    wout = (torch.randn((FF, RANK), generator=g, device="cuda") * 0.05).contiguous()
+    n_x = 64
+    X = torch.randn((n_x, H), generator=g, device="cuda").contiguous()
+    # threshold: midpoint of the 909th/910th largest logit for the first token
+    hid = torch.relu(wup.double() @ X[0].double())
+    lg = (wout.double() @ hid).float().cpu().numpy()
+    thr = threshold_for(lg, N_ACTIVE)
+    torch.cuda.synchronize()  # the library's stream does not wait on torch's
+    bundles, wups, wouts = [], [], []
+    for _ in range(L):
+        bundles.append(dev.upload_bundle(up, dn, gg.Q4_0, H, FF))
+        wups.append(dev.upload_matrix(wup, gg.F32, RANK, H))
+        wouts.append(dev.upload_matrix(wout, gg.F32, FF, RANK))
+    out = torch.empty((n_x, H), device="cuda")
+    act = torch.empty((L, FF), dtype=torch.int32, device="cuda")
+    nact = torch.zeros((L, 1), dtype=torch.int32, device="cuda")
+    lib = dev.lib
+
+    def step(i):
+        l = i % L
+        x = X[i % n_x]
+        rc = lib.llg_hipd_ffn_predict_sparse(dev.h, wups[l].id, wouts[l].id, 0, bundles[l].id,
+                                             vp(x), vp(x), thr, gg.ACT_RELU, vp(out[i % n_x]),
+                                             vp(act[l]), vp(nact[l]))
+        if rc:
+            dev.check(rc, "ffn_predict_sparse")
+
+    def ffn_only(i):
+        l = i % L
+        rc = lib.llg_hipd_ffn_sparse(dev.h, bundles[l].id, vp(X[i % n_x]), vp(act[l]),
+                                     vp(nact[l]), gg.ACT_RELU, vp(out[i % n_x]))
+        if rc:
+            dev.check(rc, "ffn_sparse")
+
+    def pred_only(i):
+        l = i % L
+        x = X[i % n_x]
+        rc = lib.llg_hipd_predict(dev.h, wups[l].id, wouts[l].id, 0, vp(x), thr, vp(act[l]),
+                                  vp(nact[l]), None)
+        if rc:
+            dev.check(rc, "predict")
+
+    tm = Timer(torch, dev.stream)
+    for i in range(args.warmup):
+        step(i)
+    dev.sync()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    e0 = tm.event()
+    for i in range(args.steps):
+        step(i)
+    e1 = tm.event()
+    dev.sync()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = e0.elapsed_time(e1) / args.steps
+    mean_active = float(nact.float().mean().item())
+
+    # kernel-level timing: the gathered FFN pair and the predictor, separately
+    def time_region(fn, n):
+        a = tm.event()
+        for i in range(n):
+            fn(i)
+        b = tm.event()
+        dev.sync()
+        return a.elapsed_time(b) / n
+
+    ffn_ms = time_region(ffn_only, args.steps)
+    pred_ms = time_region(pred_only, args.steps)
+    for h_ in bundles + wups + wouts:
+        h_.release()
+
+    alg_bytes = N_ACTIVE * BUNDLE_ALG
+    ffn_gbs = alg_bytes / (ffn_ms * 1e-3) / 1e9
+    res = {
+        "metric": "sparse-FFN decode tokens/s on 1 MI355X + achieved HBM GB/s vs 8 TB/s peak",
+        "value": 1000.0 / ms_step,
+        "unit": "tokens/s",
+        "ms_per_step": ms_step,
+        "dtype": "f32",
+        "config": {"workload": "falcon7b-ffn-layer-q4_0-5pct-sparse-decode", "d_model": H,
+                   "d_ff": FF, "predictor_rank": RANK, "weights": "Q4_0 bundled",
+                   "target_active": N_ACTIVE, "mean_active": mean_active, "batch": 1,
+                   "layer_copies_rotated": L, "step": "predict+select+gathered up/down FFN"},
+        "roofline": {"bound": "hbm", "kernel": "k_sparse_up + k_sparse_down",
+                     "achieved": ffn_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": ffn_gbs / HBM_PEAK_GBS, "traffic": None,
+                     "alg_bytes_per_launch": alg_bytes, "avg_launch_us": ffn_ms * 1e3},
+        "breakdown": {"ffn_sparse_us": ffn_ms * 1e3, "predict_us": pred_ms * 1e3,
+                      "predict_gbs": PRED_BYTES / (pred_ms * 1e-3) / 1e9,
+                      "step_alg_bytes": alg_bytes + PRED_BYTES,
+                      "step_gbs": (alg_bytes + PRED_BYTES) / (ms_step * 1e-3) / 1e9,
+                      "wall_s": wall},
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline_sparse(args, up.cpu().numpy(), dn.cpu().numpy(),
+                                                  wup.cpu().numpy(), wout.cpu().numpy(),
+                                                  X.cpu().numpy(), thr)
+    return res
+
+
+def cpu_baseline_sparse(args, up, dn, wup, wout, X, thr):
+    """The oracle's restatement of ffnFlash path 2 (predictor.go:51-83 +
+    ffn_flash.go:254-299), single-threaded, on a bounded sample of tokens."""
+    from oracle import refcpu as R
+
+    log("cpu baseline: oracle predict + ffnSparseLoad, 1 thread")
+    n, t0 = 0, time.perf_counter()
+    while True:
+        x = X[n % X.shape[0]]
+        active, _ = R.predict(wup, wout, None, x, thr)
+        R.ffn_sparse_load(up, dn, R.Q4_0, H, FF, x, active)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= args.cpu_seconds or n >= args.cpu_max_tokens:
+            break
+    return {"value": n / el, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{n} decode tokens of the same layer (predict + sparse FFN), "
+                      f"{el:.1f} s, weights in host memory (no SSD I/O)"}
+
+
+def bench_dense(args, torch, llg, dev, t):
+    gg = llg.gguf
+    L = args.layers
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x11A3A001)
+    up = gg.quantize(torch.randn((FF, H), generator=g, device="cuda") * 0.02, t)
+    down = gg.quantize(torch.randn((H, FF), generator=g, device="cuda") * 0.02, t)
+    torch.cuda.synchronize()
+    ups = [dev.upload_matrix(up, t, FF, H) for _ in range(L)]
+    downs = [dev.upload_matrix(down, t, H, FF) for _ in range(L)]
+    X = torch.randn((64, H), generator=g, device="cuda")
+    out = torch.empty((64, H), device="cuda")
+    torch.cuda.synchronize()
+    tm = Timer(torch, dev.stream)
+
+    def step(i):
+        rc = dev.lib.llg_hipd_ffn_dense(dev.h, ups[i % L].id, downs[i % L].id, vp(X[i % 64]),
+                                        gg.ACT_RELU, vp(out[i % 64]))
+        if rc:
+            dev.check(rc, "ffn_dense")
+
+    for i in range(args.warmup):
+        step(i)
+    dev.sync()
+    e0 = tm.event()
+    for i in range(args.steps):
+        step(i)
+    e1 = tm.event()
+    dev.sync()
+    ms = e0.elapsed_time(e1) / args.steps
+    alg = 2 * FF * gg.byte_size(t, H)
+    gbs = alg / (ms * 1e-3) / 1e9
+    for h_ in ups + downs:
+        h_.release()
+    return {"metric": "dense-FFN decode tokens/s + achieved HBM GB/s", "value": 1000.0 / ms,
+            "unit": "tokens/s", "ms_per_step": ms, "dtype": "f32",
+            "config": {"workload": f"falcon7b-ffn-layer-{gg.TYPE_NAMES[t].lower()}-dense-decode",
+                       "d_model": H, "d_ff": FF, "layer_copies_rotated": L},
+            "roofline": {"bound": "hbm", "kernel": "k_matvec_q (up) + k_matvec_q (down)",
+                         "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                         "alg_bytes_per_launch": alg, "avg_launch_us": ms * 1e3}}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--workload", default="sparse",
+                    choices=["sparse", "dense-q4_0", "dense-q8_0", "dense-f16"])
+    ap.add_argument("--layers", type=int, default=0,
+                    help="distinct HBM copies rotated per step (0 = enough to defeat the MALL)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-max-tokens", type=int, default=2000)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the sparse-FFN path runs on a single MI355X; see DESIGN.md for sharding)",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.layers <= 0:
+        args.layers = 128 if args.workload == "sparse" else 6
+
+    import torch
+    import llg
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = llg.Device()
+    gg = llg.gguf
+    if args.workload == "sparse":
+        res = bench_sparse(args, torch, llg, dev)
+    else:
+        t = {"dense-q4_0": gg.Q4_0, "dense-q8_0": gg.Q8_0, "dense-f16": gg.F16}[args.workload]
+        res = bench_dense(args, torch, llg, dev, t)
+    res.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                "data": "synthetic (seeded N(0,0.02) weights, N(0,1) inputs)"})
+    res.setdefault("cpu_baseline", None)
+    order = ["metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
+             "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config", "roofline",
+             "cpu_baseline"]
+    line = {k: res[k] for k in order if k in res}
+    line.update({k: v for k, v in res.items() if k not in line})
+    dev.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,195 @@
+/*
+ * llg_hip.h -- C ABI of the MI355X (gfx950) sparse-FFN library.
+ *
+ * Drop-in replacement for the reference's native bridge
+ * metal/metal_bridge.h:1-20 (AndersHsueh/llama.go), extended with the
+ * sparse-FFN hot path that the reference runs on the CPU:
+ *   predictor + selection   inference/predictor.go:51-83
+ *   gathered sparse FFN     inference/ffn_flash.go:254-299
+ *   dense dequant FFN       inference/forward.go:318-353, tensor/ops.go:39-60
+ *   sliding window          inference/window.go:71-180
+ *   MoE router + experts    inference/moe_forward.go:32-150
+ *   GGUF dequant            tensor/dtype.go:12-82, 249-293, 417-443
+ *
+ * Conventions (kept from metal_bridge.h):
+ *   - an opaque device handle; llg_hip_init returns NULL when no GPU is usable;
+ *   - every entry point returns int: 0 = OK, <0 = argument error (LLG_E_*),
+ *     >0 = a hipError_t from the runtime;  llg_hip_last_error() describes it;
+ *   - llg_hip_* entry points take caller-owned HOST buffers and are synchronous
+ *     (they return after the device work has completed, like the Metal
+ *     bridge's commit + waitUntilCompleted);
+ *   - llg_hipd_* entry points take DEVICE pointers for activations/outputs,
+ *     enqueue on the handle's stream and return without waiting; call
+ *     llg_hip_sync() (or order work on llg_hip_stream()) before reading results;
+ *   - weights are uploaded once into library-owned device objects identified
+ *     by int64 handles (cgo forbids C from keeping Go pointers after a call);
+ *   - a handle is not thread-safe: callers serialise calls per handle.
+ *
+ * Element types are GGUF ggml_type codes (gguf/types.go:40-61): F32=0, F16=1,
+ * Q4_0=2, Q8_0=8.  Activations are model.ActivationType (model/model.go:97-103):
+ * ReLU=0, GELU=1, SiLU=2.
+ */
+#ifndef LLG_HIP_H
+#define LLG_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *LlgHipDevice;
+
+enum {
+    LLG_TYPE_F32 = 0,
+    LLG_TYPE_F16 = 1,
+    LLG_TYPE_Q4_0 = 2,
+    LLG_TYPE_Q8_0 = 8,
+};
+
+enum { LLG_ACT_RELU = 0, LLG_ACT_GELU = 1, LLG_ACT_SILU = 2 };
+
+enum {
+    LLG_OK = 0,
+    LLG_E_ARG = -1,     /* null pointer, non-positive or mismatched size */
+    LLG_E_TYPE = -2,    /* ggml type not supported (dtype.go:266) */
+    LLG_E_ALIGN = -3,   /* element count not a multiple of the block size (types.go:98-100) */
+    LLG_E_RANGE = -4,   /* neuron / row index out of range (storage.go:292-294) */
+    LLG_E_HANDLE = -5,  /* unknown or wrong-kind object handle */
+    LLG_E_NOMEM = -6,   /* device or pinned allocation failed */
+    LLG_E_HPARAM = -7,  /* invalid MoE hparams (moe_forward.go:38-40) */
+    LLG_E_NODEV = -8,   /* null device handle */
+};
+
+/* ---- device lifecycle: metal_bridge.h:7-10 ------------------------------ */
+int llg_hip_available(void);                  /* llama_metal_available */
+LlgHipDevice llg_hip_init(void);              /* llama_metal_init: NULL if unavailable */
+void llg_hip_free(LlgHipDevice dev);          /* llama_metal_free */
+const char *llg_hip_last_error(LlgHipDevice dev);
+/* The hipStream_t (as void*) that llg_hipd_* calls enqueue on. */
+void *llg_hip_stream(LlgHipDevice dev);
+int llg_hip_sync(LlgHipDevice dev);
+
+/* ---- Metal-parity entry points: metal_bridge.h:12-20 -------------------- */
+/* y[rows] = W[rows*cols] @ x[cols], fp32 (llama_metal_matvec, used by
+ * inference/forward.go:395-405). */
+int llg_hip_matvec(LlgHipDevice dev, const float *w, int rows, int cols, const float *x,
+                   float *y);
+/* out[n] = x[n] / sqrt(sum(x^2)/n + eps) * weight[n] (llama_metal_rmsnorm,
+ * used by inference/forward.go:409-418). */
+int llg_hip_rmsnorm(LlgHipDevice dev, const float *x, const float *weight, float *out, int n,
+                    float eps);
+
+/* ---- weight residency (replaces flash/storage.go reads: weights live in HBM) */
+/* A row-major matrix of `rows` rows x `cols` elements, given as GGUF tensor
+ * bytes (rows * ByteSize(cols), gguf/types.go:90-102).  Row r is addressed as
+ * in flash/storage.go:296 (offset = r * ByteSize(cols)).  *mat gets a handle. */
+int llg_hip_upload_matrix(LlgHipDevice dev, const void *gguf_raw, int ggml_type, int rows,
+                          int cols, int64_t *mat);
+/* Same, from a device pointer to the GGUF bytes (copied; source not retained). */
+int llg_hipd_upload_matrix(LlgHipDevice dev, const void *d_gguf_raw, int ggml_type, int rows,
+                           int cols, int64_t *mat);
+/* Row-column bundle (flash/bundle.go:37-111): neuron i stores ffn_up row i
+ * (up_raw, ff rows of ByteSize(h)) contiguous with ffn_down row i (down_t_raw,
+ * the [ff x h] layout the sparse path reads, ffn_flash.go:267).  Bytes stay
+ * quantized; one contiguous span per neuron. */
+int llg_hip_upload_bundle(LlgHipDevice dev, const void *up_raw, const void *down_t_raw,
+                          int ggml_type, int h, int ff, int64_t *bundle);
+int llg_hipd_upload_bundle(LlgHipDevice dev, const void *d_up_raw, const void *d_down_t_raw,
+                           int ggml_type, int h, int ff, int64_t *bundle);
+int llg_hip_release(LlgHipDevice dev, int64_t handle);
+/* Per-neuron byte stride of a bundle and per-row stride of a matrix in HBM. */
+int llg_hip_object_info(LlgHipDevice dev, int64_t handle, int *ggml_type, int *rows,
+                        int *cols, int64_t *row_stride);
+
+/* ---- dequant: tensor/dtype.go:12-82 (bit-exact with float16ToFloat32 :417-443) */
+/* Rows [row0, row0+nrows) of a matrix (or, for a bundle, neuron rows with the
+ * up row first then the down row: 2*h floats per neuron) to fp32. */
+int llg_hip_dequant(LlgHipDevice dev, int64_t handle, int row0, int nrows, float *out);
+
+/* ---- predictor: inference/predictor.go:51-83 ---------------------------- */
+/* wup: F32 matrix [rank x h]; wout: F32 matrix [ff x rank]; bias: F32 [1 x ff]
+ * matrix or 0.  a: the predictor input [h] (the layer's attention output).
+ * active (capacity ff) receives {i : logit_i > threshold} ascending;
+ * logits (optional, [ff]) receives the logits. */
+int llg_hip_predict(LlgHipDevice dev, int64_t wup, int64_t wout, int64_t bias, const float *a,
+                    float threshold, int32_t *active, int *n_active, float *logits);
+/* Selection alone on given logits (predictor.go:76-82): the bit-exact hook. */
+int llg_hip_select(LlgHipDevice dev, const float *logits, int ff, float threshold,
+                   int32_t *active, int *n_active);
+
+/* ---- sparse FFN: inference/ffn_flash.go:254-299 ------------------------- */
+/* out[h] = sum_{j in active} act(up_j . x) * down_j, skipping zero activations;
+ * n_active == 0 gives zeros.  Indices must be in [0, ff). */
+int llg_hip_ffn_sparse(LlgHipDevice dev, int64_t bundle, const float *x, const int32_t *active,
+                       int n_active, int act, float *out);
+/* Path 2 of ffnFlash (ffn_flash.go:225-231): predict on `a`, then sparse FFN
+ * on `x`, without a host round trip.  active/n_active optional outputs. */
+int llg_hip_ffn_predict_sparse(LlgHipDevice dev, int64_t wup, int64_t wout, int64_t bias,
+                               int64_t bundle, const float *a, const float *x, float threshold,
+                               int act, float *out, int32_t *active, int *n_active);
+
+/* ---- dense path: inference/forward.go:318-353, tensor/ops.go:39-60 ------- */
+/* y[rows] = dequant(W) @ x for any supported matrix type. */
+int llg_hip_matvec_q(LlgHipDevice dev, int64_t mat, const float *x, float *y);
+/* out = down @ act(up @ x); up [ff x h], down [h x ff] (standard GGUF layout). */
+int llg_hip_ffn_dense(LlgHipDevice dev, int64_t up, int64_t down, const float *x, int act,
+                      float *out);
+
+/* ---- sliding window: inference/window.go -------------------------------- */
+/* NewNeuronCache (window.go:48-63) over a bundle, window size k >= 1. */
+int llg_hip_window_create(LlgHipDevice dev, int64_t bundle, int k, int64_t *win);
+/* Update (window.go:71-117): evict neurons only the expiring slot needed,
+ * gather-copy the active neurons not resident, record the set.  n_loaded
+ * receives |toLoad|, n_resident NumCached() (window.go:183); both optional. */
+int llg_hip_window_update(LlgHipDevice dev, int64_t win, const int32_t *active, int n_active,
+                          int *n_loaded, int *n_resident);
+/* FFNForward (window.go:143-180) over the resident rows. */
+int llg_hip_window_ffn(LlgHipDevice dev, int64_t win, const float *x, const int32_t *active,
+                       int n_active, int act, float *out);
+/* Resident flags: resident[n] = 1 if neuron n is resident (capacity ff). */
+int llg_hip_window_resident(LlgHipDevice dev, int64_t win, uint8_t *resident, int *n_resident);
+
+/* ---- MoE: inference/moe_forward.go:32-150 ------------------------------- */
+/* router: F32 matrix [n_exp x hidden]; gate_exps/up_exps: matrices of
+ * n_exp*eff rows x hidden (GGUF dims [hidden, eff, n_exp]); down_exps:
+ * n_exp*hidden rows x eff (dims [eff, hidden, n_exp]).  x: [n_tok x hidden];
+ * out: [n_tok x hidden].  ids/weights (optional, [n_tok x k]) receive the
+ * chosen experts in accumulation order (descending probability, ties to the
+ * lower index) and p/wsum.  n_tok == 1 is the decode path; n_tok > 1 groups
+ * tokens per expert and runs the grouped MFMA GEMM. */
+int llg_hip_moe_ffn(LlgHipDevice dev, int64_t router, int64_t gate_exps, int64_t up_exps,
+                    int64_t down_exps, int n_exp, int k, const float *x, int n_tok, float *out,
+                    int32_t *ids, float *weights);
+/* Router stage on given logits [n_tok x n_exp] (softmax, top-k, renorm). */
+int llg_hip_moe_route(LlgHipDevice dev, const float *logits, int n_tok, int n_exp, int k,
+                      int32_t *ids, float *weights);
+
+/* ---- device-pointer (async) variants for HBM-resident callers ----------- */
+int llg_hipd_predict(LlgHipDevice dev, int64_t wup, int64_t wout, int64_t bias,
+                     const float *d_a, float threshold, int32_t *d_active,
+                     int32_t *d_n_active, float *d_logits);
+/* n_active is read on the device from d_n_active; indices are not range-checked
+ * on this path (they come from llg_hipd_predict or a checked caller). */
+int llg_hipd_ffn_sparse(LlgHipDevice dev, int64_t bundle, const float *d_x,
+                        const int32_t *d_active, const int32_t *d_n_active, int act,
+                        float *d_out);
+int llg_hipd_ffn_predict_sparse(LlgHipDevice dev, int64_t wup, int64_t wout, int64_t bias,
+                                int64_t bundle, const float *d_a, const float *d_x,
+                                float threshold, int act, float *d_out, int32_t *d_active,
+                                int32_t *d_n_active);
+int llg_hipd_matvec_q(LlgHipDevice dev, int64_t mat, const float *d_x, float *d_y);
+int llg_hipd_ffn_dense(LlgHipDevice dev, int64_t up, int64_t down, const float *d_x, int act,
+                       float *d_out);
+int llg_hipd_window_step(LlgHipDevice dev, int64_t win, const float *d_x,
+                         const int32_t *d_active, const int32_t *d_n_active, int act,
+                         float *d_out);
+int llg_hipd_moe_ffn(LlgHipDevice dev, int64_t router, int64_t gate_exps, int64_t up_exps,
+                     int64_t down_exps, int n_exp, int k, const float *d_x, int n_tok,
+                     float *d_out, int32_t *d_ids, float *d_weights);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LLG_HIP_H */

@@ -1,0 +1,339 @@
+// llg_common.hpp -- shared host/device definitions for the gfx950 sparse-FFN library.
+//
+// HBM row layout ("row format").  A GGUF row of `cols` elements
+// (gguf/types.go:90-102: ByteSize = cols/32 * 18 for Q4_0, * 34 for Q8_0) is
+// stored per row as struct-of-arrays so that every lane can issue 16-byte
+// aligned loads:
+//   Q4_0: [ qs: nb x 16 B ][ d: nb x 2 B (f16) ][ pad to 128 B ]
+//   Q8_0: [ qs: nb x 32 B ][ d: nb x 2 B (f16) ][ pad to 128 B ]
+//   F16 : [ cols x 2 B ][ pad ]      F32: [ cols x 4 B ][ pad ]
+// where nb = cols / 32.  The bytes of each block are the GGUF bytes
+// unchanged; only the scale and the quants of one row are split apart.  For
+// Q4_0 the reference decodes element 2i from the low nibble and element 2i+1
+// from the high nibble of byte i (tensor/dtype.go:73-79), so nibble p of the
+// little-endian 32-bit word w of a block is element 8w + p.
+//
+// A bundle (flash/bundle.go:22-24) stores, per neuron, the up row followed by
+// the down row, each in the row format above: one contiguous span of
+// 2 * stride bytes per neuron.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "../../include/llg_hip.h"
+
+#define LLG_ROW_ALIGN 128
+
+struct RowFmt {
+    int type;        // ggml type code
+    int cols;        // elements per row
+    int nb;          // 32-element blocks per row (cols / 32, rounded up for F16/F32)
+    int d_off;       // byte offset of the f16 scales inside a row (Q4_0 / Q8_0)
+    long long stride;  // bytes per row in HBM
+};
+
+static inline long long llg_align(long long v, long long a) { return (v + a - 1) / a * a; }
+
+// Returns 0 and fills *f, or an LLG_E_* code (types.go:93-100 semantics).
+static inline int llg_row_fmt(int type, int cols, RowFmt *f) {
+    if (cols <= 0) return LLG_E_ARG;
+    f->type = type;
+    f->cols = cols;
+    switch (type) {
+    case LLG_TYPE_Q4_0:
+        if (cols % 32) return LLG_E_ALIGN;
+        f->nb = cols / 32;
+        f->d_off = f->nb * 16;
+        f->stride = llg_align((long long)f->nb * 18, LLG_ROW_ALIGN);
+        return 0;
+    case LLG_TYPE_Q8_0:
+        if (cols % 32) return LLG_E_ALIGN;
+        f->nb = cols / 32;
+        f->d_off = f->nb * 32;
+        f->stride = llg_align((long long)f->nb * 34, LLG_ROW_ALIGN);
+        return 0;
+    case LLG_TYPE_F16:
+        f->nb = (cols + 31) / 32;
+        f->d_off = 0;
+        f->stride = llg_align((long long)cols * 2, LLG_ROW_ALIGN);
+        return 0;
+    case LLG_TYPE_F32:
+        f->nb = (cols + 31) / 32;
+        f->d_off = 0;
+        f->stride = llg_align((long long)cols * 4, LLG_ROW_ALIGN);
+        return 0;
+    default:
+        return LLG_E_TYPE;
+    }
+}
+
+// GGUF bytes per row: gguf/types.go:90-102.
+static inline long long llg_gguf_row_bytes(int type, int cols) {
+    switch (type) {
+    case LLG_TYPE_Q4_0: return (long long)(cols / 32) * 18;
+    case LLG_TYPE_Q8_0: return (long long)(cols / 32) * 34;
+    case LLG_TYPE_F16: return (long long)cols * 2;
+    case LLG_TYPE_F32: return (long long)cols * 4;
+    default: return -1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+
+// f16 -> f32 with the reference's semantics (tensor/dtype.go:417-443):
+// subnormals normalised, +-Inf kept, every NaN becomes sign|0x7FC00000.
+__device__ __forceinline__ float llg_f16_ref(uint32_t h) {
+    uint32_t sign = (h >> 15) << 31;
+    uint32_t e = (h >> 10) & 0x1F;
+    uint32_t m = h & 0x3FF;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            // normalise: shift the leading one into bit 10
+            int lz = __clz(m) - 21;  // m < 0x400, so clz(m) >= 22; lz = shifts needed
+            m = (m << lz) & 0x3FF;
+            bits = sign | ((uint32_t)(113 - lz) << 23) | (m << 13);
+        }
+    } else if (e == 31) {
+        bits = sign | (m ? 0x7FC00000u : 0x7F800000u);
+    } else {
+        bits = sign | ((e + 112) << 23) | (m << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+// Hardware f16 -> f32 (identical to llg_f16_ref for every non-NaN input).
+__device__ __forceinline__ float llg_f16(uint32_t h) {
+    return __half2float(__ushort_as_half((unsigned short)h));
+}
+
+__device__ __forceinline__ float llg_wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Activations, with the reference's rounding: ops.go:168-189.
+__device__ __forceinline__ float llg_act(int act, float v) {
+    if (act == LLG_ACT_SILU) {
+        return v / (1.0f + (float)exp(-(double)v));
+    } else if (act == LLG_ACT_GELU) {
+        const float c = 0.7978845608028654f;
+        const float k = 0.044715f;
+        float inner = c * (v + k * v * v * v);
+        return 0.5f * v * (1.0f + (float)tanh((double)inner));
+    }
+    return v < 0.0f ? 0.0f : v;  // NaN and -0.0 pass through, as ops.go:170
+}
+
+// One 32-element block b of a row: dot with x[32] (x given as 8 float4).
+template <int T>
+__device__ __forceinline__ float llg_block_dot(const uint8_t *__restrict__ row, const RowFmt &f,
+                                               int b, const float4 *__restrict__ x4);
+
+template <>
+__device__ __forceinline__ float llg_block_dot<LLG_TYPE_Q4_0>(const uint8_t *__restrict__ row,
+                                                               const RowFmt &f, int b,
+                                                               const float4 *__restrict__ x4) {
+    const uint4 q = *reinterpret_cast<const uint4 *>(row + (size_t)b * 16);
+    const float d = llg_f16(*reinterpret_cast<const unsigned short *>(row + f.d_off + b * 2));
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 xa = x4[2 * i], xb = x4[2 * i + 1];
+        const uint32_t v = w[i];
+        s += (float)((int)((v >> 0) & 15) - 8) * xa.x;
+        s += (float)((int)((v >> 4) & 15) - 8) * xa.y;
+        s += (float)((int)((v >> 8) & 15) - 8) * xa.z;
+        s += (float)((int)((v >> 12) & 15) - 8) * xa.w;
+        s += (float)((int)((v >> 16) & 15) - 8) * xb.x;
+        s += (float)((int)((v >> 20) & 15) - 8) * xb.y;
+        s += (float)((int)((v >> 24) & 15) - 8) * xb.z;
+        s += (float)((int)((v >> 28) & 15) - 8) * xb.w;
+    }
+    return s * d;
+}
+
+template <>
+__device__ __forceinline__ float llg_block_dot<LLG_TYPE_Q8_0>(const uint8_t *__restrict__ row,
+                                                               const RowFmt &f, int b,
+                                                               const float4 *__restrict__ x4) {
+    const uint4 qa = *reinterpret_cast<const uint4 *>(row + (size_t)b * 32);
+    const uint4 qb = *reinterpret_cast<const uint4 *>(row + (size_t)b * 32 + 16);
+    const float d = llg_f16(*reinterpret_cast<const unsigned short *>(row + f.d_off + b * 2));
+    const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 xv = x4[i];
+        const uint32_t v = w[i];
+        s += (float)(int8_t)(v & 0xFF) * xv.x;
+        s += (float)(int8_t)((v >> 8) & 0xFF) * xv.y;
+        s += (float)(int8_t)((v >> 16) & 0xFF) * xv.z;
+        s += (float)(int8_t)(v >> 24) * xv.w;
+    }
+    return s * d;
+}
+
+template <>
+__device__ __forceinline__ float llg_block_dot<LLG_TYPE_F16>(const uint8_t *__restrict__ row,
+                                                              const RowFmt &f, int b,
+                                                              const float4 *__restrict__ x4) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(row + (size_t)b * 64);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint4 q = p[i];
+        const float4 xa = x4[2 * i], xb = x4[2 * i + 1];
+        s += llg_f16(q.x & 0xFFFF) * xa.x;
+        s += llg_f16(q.x >> 16) * xa.y;
+        s += llg_f16(q.y & 0xFFFF) * xa.z;
+        s += llg_f16(q.y >> 16) * xa.w;
+        s += llg_f16(q.z & 0xFFFF) * xb.x;
+        s += llg_f16(q.z >> 16) * xb.y;
+        s += llg_f16(q.w & 0xFFFF) * xb.z;
+        s += llg_f16(q.w >> 16) * xb.w;
+    }
+    return s;
+}
+
+template <>
+__device__ __forceinline__ float llg_block_dot<LLG_TYPE_F32>(const uint8_t *__restrict__ row,
+                                                              const RowFmt &f, int b,
+                                                              const float4 *__restrict__ x4) {
+    const float4 *p = reinterpret_cast<const float4 *>(row + (size_t)b * 128);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 w = p[i];
+        const float4 xv = x4[i];
+        s += w.x * xv.x;
+        s += w.y * xv.y;
+        s += w.z * xv.z;
+        s += w.w * xv.w;
+    }
+    return s;
+}
+
+// acc[0..31] += u * dequant(block b of row).
+template <int T>
+__device__ __forceinline__ void llg_block_axpy(const uint8_t *__restrict__ row, const RowFmt &f,
+                                               int b, float u, float *acc);
+
+template <>
+__device__ __forceinline__ void llg_block_axpy<LLG_TYPE_Q4_0>(const uint8_t *__restrict__ row,
+                                                               const RowFmt &f, int b, float u,
+                                                               float *acc) {
+    const uint4 q = *reinterpret_cast<const uint4 *>(row + (size_t)b * 16);
+    const float s = u * llg_f16(*reinterpret_cast<const unsigned short *>(row + f.d_off + b * 2));
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int p = 0; p < 8; p++)
+            acc[8 * i + p] += s * (float)((int)((w[i] >> (4 * p)) & 15) - 8);
+}
+
+template <>
+__device__ __forceinline__ void llg_block_axpy<LLG_TYPE_Q8_0>(const uint8_t *__restrict__ row,
+                                                               const RowFmt &f, int b, float u,
+                                                               float *acc) {
+    const uint4 qa = *reinterpret_cast<const uint4 *>(row + (size_t)b * 32);
+    const uint4 qb = *reinterpret_cast<const uint4 *>(row + (size_t)b * 32 + 16);
+    const float s = u * llg_f16(*reinterpret_cast<const unsigned short *>(row + f.d_off + b * 2));
+    const uint32_t w[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int p = 0; p < 4; p++) acc[4 * i + p] += s * (float)(int8_t)((w[i] >> (8 * p)) & 0xFF);
+}
+
+template <>
+__device__ __forceinline__ void llg_block_axpy<LLG_TYPE_F16>(const uint8_t *__restrict__ row,
+                                                              const RowFmt &f, int b, float u,
+                                                              float *acc) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(row + (size_t)b * 64);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint4 q = p[i];
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            acc[8 * i + 2 * k] += u * llg_f16(w[k] & 0xFFFF);
+            acc[8 * i + 2 * k + 1] += u * llg_f16(w[k] >> 16);
+        }
+    }
+}
+
+template <>
+__device__ __forceinline__ void llg_block_axpy<LLG_TYPE_F32>(const uint8_t *__restrict__ row,
+                                                              const RowFmt &f, int b, float u,
+                                                              float *acc) {
+    const float4 *p = reinterpret_cast<const float4 *>(row + (size_t)b * 128);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 w = p[i];
+        acc[4 * i + 0] += u * w.x;
+        acc[4 * i + 1] += u * w.y;
+        acc[4 * i + 2] += u * w.z;
+        acc[4 * i + 3] += u * w.w;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side runtime objects (defined in llg_runtime.hip)
+// ---------------------------------------------------------------------------
+#ifdef __cplusplus
+#include <string>
+
+enum LlgKind { LLG_KIND_MATRIX = 1, LLG_KIND_BUNDLE = 2, LLG_KIND_WINDOW = 3 };
+
+struct LlgObject {
+    int kind;
+    int id_self;
+    uint8_t *d;          // device bytes
+    size_t bytes;
+    RowFmt fmt;          // row format (matrix rows, or each half of a bundle)
+    int rows;            // matrix rows, or bundle neurons (ff)
+    long long stride;    // matrix: bytes per row; bundle: bytes per neuron (2 * fmt.stride)
+    void *ext;           // kind-specific state (window)
+};
+
+struct LlgDevice;
+
+// Runtime services used by every translation unit.
+LlgDevice *llg_dev(LlgHipDevice h);
+hipStream_t llg_dev_stream(LlgDevice *d);
+int llg_set_error(LlgDevice *d, int code, const char *fmt, ...);
+int llg_hip_error(LlgDevice *d, hipError_t e, const char *what);
+LlgObject *llg_get(LlgDevice *d, int64_t h, int kind);
+int64_t llg_register(LlgDevice *d, LlgObject *o);
+// Device workspace of at least `bytes`, valid until the next llg_ws call that
+// grows it (growth synchronises the device before freeing the old buffer).
+void *llg_ws(LlgDevice *d, size_t bytes, int *rc);
+// Copy host -> device workspace slot / device -> host, on the stream.
+int llg_h2d(LlgDevice *d, void *dst, const void *src, size_t bytes);
+int llg_d2h(LlgDevice *d, void *dst, const void *src, size_t bytes);
+int llg_sync_dev(LlgDevice *d);
+int llg_device_id(LlgDevice *d);
+int llg_cu_count(LlgDevice *d);
+
+#define LLG_LAUNCH_CHECK(dev, what)                                     \
+    do {                                                                \
+        hipError_t _e = hipGetLastError();                              \
+        if (_e != hipSuccess) return llg_hip_error((dev), _e, (what)); \
+    } while (0)
+
+#define LLG_HIP_TRY(dev, expr)                                          \
+    do {                                                                \
+        hipError_t _e = (expr);                                         \
+        if (_e != hipSuccess) return llg_hip_error((dev), _e, #expr);   \
+    } while (0)
+#endif

@@ -1,0 +1,434 @@
+"""Host-side binding of libllg_hip.so, the gfx950 sparse-FFN library.
+
+This module mirrors the reference's Go API for the hot path so that callers
+and tests read like the reference's own code:
+
+  reference (AndersHsueh/llama.go)              here
+  metal.Available / NewDevice / Device.Close    available(), Device(), Device.close()
+    (metal/metal.go:46-70)
+  Device.MatMulVec / Device.RMSNorm             Device.mat_mul_vec / Device.rms_norm
+    (metal/metal.go:72-113)
+  Predictor{WUp,WOut,Bias,Threshold}.Predict    Predictor(...).predict(attn_out)
+    (inference/predictor.go:21-83)
+  FlashContext.ffnSparseLoad                    ffn_sparse_load(dev, bundle, x, active, act)
+    (inference/ffn_flash.go:254-299)
+  Context.ffn dense ReLU/GELU                   ffn_dense(dev, up, down, x, act)
+    (inference/forward.go:318-367)
+  NeuronCache.Update / FFNForward / NumCached   NeuronCache(dev, bundle, k).update / ...
+    (inference/window.go:48-183)
+  moeFFN                                        moe_ffn(dev, router, gate, up, down, ...)
+    (inference/moe_forward.go:32-79)
+
+Go's `error` returns become LlgError exceptions carrying the library's return
+code and message.  Every compute call runs on the GPU through the C ABI in
+include/llg_hip.h; there is no CPU fallback: without the built library or a
+GPU these calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+from . import gguf  # noqa: F401  (re-exported helpers)
+from .gguf import ACT_GELU, ACT_RELU, ACT_SILU, F16, F32, Q4_0, Q8_0  # noqa: F401
+
+LIB_PATH = Path(__file__).resolve().parent / "libllg_hip.so"
+
+# Return codes (include/llg_hip.h)
+LLG_OK = 0
+LLG_E_ARG = -1
+LLG_E_TYPE = -2
+LLG_E_ALIGN = -3
+LLG_E_RANGE = -4
+LLG_E_HANDLE = -5
+LLG_E_NOMEM = -6
+LLG_E_HPARAM = -7
+LLG_E_NODEV = -8
+
+_i32p = C.POINTER(C.c_int32)
+_f32p = C.POINTER(C.c_float)
+_i64p = C.POINTER(C.c_int64)
+_ip = C.POINTER(C.c_int)
+_vp = C.c_void_p
+_i64 = C.c_int64
+
+# name -> (restype, argtypes); the full C ABI of include/llg_hip.h
+_SIGS = {
+    "llg_hip_available": (C.c_int, []),
+    "llg_hip_init": (_vp, []),
+    "llg_hip_free": (None, [_vp]),
+    "llg_hip_last_error": (C.c_char_p, [_vp]),
+    "llg_hip_stream": (_vp, [_vp]),
+    "llg_hip_sync": (C.c_int, [_vp]),
+    "llg_hip_matvec": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp]),
+    "llg_hip_rmsnorm": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_float]),
+    "llg_hip_upload_matrix": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _i64p]),
+    "llg_hipd_upload_matrix": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _i64p]),
+    "llg_hip_upload_bundle": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, _i64p]),
+    "llg_hipd_upload_bundle": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, _i64p]),
+    "llg_hip_release": (C.c_int, [_vp, _i64]),
+    "llg_hip_object_info": (C.c_int, [_vp, _i64, _ip, _ip, _ip, _i64p]),
+    "llg_hip_dequant": (C.c_int, [_vp, _i64, C.c_int, C.c_int, _vp]),
+    "llg_hip_predict": (C.c_int, [_vp, _i64, _i64, _i64, _vp, C.c_float, _vp, _ip, _vp]),
+    "llg_hip_select": (C.c_int, [_vp, _vp, C.c_int, C.c_float, _vp, _ip]),
+    "llg_hip_ffn_sparse": (C.c_int, [_vp, _i64, _vp, _vp, C.c_int, C.c_int, _vp]),
+    "llg_hip_ffn_predict_sparse": (
+        C.c_int, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, C.c_float, C.c_int, _vp, _vp, _ip]),
+    "llg_hip_matvec_q": (C.c_int, [_vp, _i64, _vp, _vp]),
+    "llg_hip_ffn_dense": (C.c_int, [_vp, _i64, _i64, _vp, C.c_int, _vp]),
+    "llg_hip_window_create": (C.c_int, [_vp, _i64, C.c_int, _i64p]),
+    "llg_hip_window_update": (C.c_int, [_vp, _i64, _vp, C.c_int, _ip, _ip]),
+    "llg_hip_window_ffn": (C.c_int, [_vp, _i64, _vp, _vp, C.c_int, C.c_int, _vp]),
+    "llg_hip_window_resident": (C.c_int, [_vp, _i64, _vp, _ip]),
+    "llg_hip_moe_ffn": (
+        C.c_int, [_vp, _i64, _i64, _i64, _i64, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp, _vp]),
+    "llg_hip_moe_route": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
+    "llg_hipd_predict": (C.c_int, [_vp, _i64, _i64, _i64, _vp, C.c_float, _vp, _vp, _vp]),
+    "llg_hipd_ffn_sparse": (C.c_int, [_vp, _i64, _vp, _vp, _vp, C.c_int, _vp]),
+    "llg_hipd_ffn_predict_sparse": (
+        C.c_int, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, C.c_float, C.c_int, _vp, _vp, _vp]),
+    "llg_hipd_matvec_q": (C.c_int, [_vp, _i64, _vp, _vp]),
+    "llg_hipd_ffn_dense": (C.c_int, [_vp, _i64, _i64, _vp, C.c_int, _vp]),
+    "llg_hipd_window_step": (C.c_int, [_vp, _i64, _vp, _vp, _vp, C.c_int, _vp]),
+    "llg_hipd_moe_ffn": (
+        C.c_int, [_vp, _i64, _i64, _i64, _i64, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp, _vp]),
+}
+
+_lib = None
+
+
+class LlgError(RuntimeError):
+    """A nonzero return code from the library (the Go side's `error`)."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{msg} (rc={code})")
+        self.code = code
+
+
+def load_library(path: str | Path | None = None) -> C.CDLL:
+    """Load libllg_hip.so and bind every entry point; raises if it is not built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise FileNotFoundError(
+            f"{p} is not built; run __graft_entry__.build() (hipcc --offload-arch=gfx950)")
+    lib = C.CDLL(str(p))
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def available() -> bool:
+    """metal.Available (metal/metal.go:46-49)."""
+    return bool(load_library().llg_hip_available())
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class Device:
+    """metal.Device (metal/metal.go:40-113) for gfx950: an opaque context with
+    its own HIP stream.  All llg_hip_* calls are synchronous."""
+
+    def __init__(self):
+        self.lib = load_library()
+        h = self.lib.llg_hip_init()
+        if not h:
+            raise LlgError(LLG_E_NODEV, "llg: no usable HIP device")
+        self.h = C.c_void_p(h)
+
+    # -- lifecycle --------------------------------------------------------
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.llg_hip_free(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def check(self, rc: int, what: str = ""):
+        if rc != 0:
+            msg = self.lib.llg_hip_last_error(self.h)
+            raise LlgError(rc, f"{what}: {msg.decode() if msg else ''}")
+
+    @property
+    def stream(self) -> int:
+        return int(self.lib.llg_hip_stream(self.h) or 0)
+
+    def sync(self):
+        self.check(self.lib.llg_hip_sync(self.h), "sync")
+
+    # -- Metal-parity calls -------------------------------------------------
+    def mat_mul_vec(self, w, rows: int, cols: int, x) -> np.ndarray:
+        """Device.MatMulVec (metal/metal.go:72-92)."""
+        w, x = _f32(w).ravel(), _f32(x).ravel()
+        if w.size != rows * cols:
+            raise LlgError(LLG_E_ARG, f"MatMulVec: w length {w.size} != rows*cols {rows * cols}")
+        if x.size != cols:
+            raise LlgError(LLG_E_ARG, f"MatMulVec: x length {x.size} != cols {cols}")
+        y = np.empty(rows, np.float32)
+        self.check(self.lib.llg_hip_matvec(self.h, _ptr(w), rows, cols, _ptr(x), _ptr(y)),
+                   "MatMulVec")
+        return y
+
+    def rms_norm(self, x, weight, eps: float) -> np.ndarray:
+        """Device.RMSNorm (metal/metal.go:94-113)."""
+        x, weight = _f32(x).ravel(), _f32(weight).ravel()
+        if weight.size != x.size:
+            raise LlgError(LLG_E_ARG, "RMSNorm: weight length != x length")
+        out = np.empty_like(x)
+        self.check(self.lib.llg_hip_rmsnorm(self.h, _ptr(x), _ptr(weight), _ptr(out), x.size,
+                                            eps), "RMSNorm")
+        return out
+
+    # -- residency ---------------------------------------------------------------
+    def upload_matrix(self, raw, ggml_type: int, rows: int, cols: int) -> "Handle":
+        """GGUF bytes of a [rows x cols] tensor (host numpy/torch-CPU or a CUDA tensor)."""
+        out = C.c_int64()
+        if _is_device_tensor(raw):
+            rc = self.lib.llg_hipd_upload_matrix(self.h, C.c_void_p(raw.data_ptr()), ggml_type,
+                                                 rows, cols, C.byref(out))
+        else:
+            a = _host_bytes(raw)
+            rc = self.lib.llg_hip_upload_matrix(self.h, _ptr(a), ggml_type, rows, cols,
+                                                C.byref(out))
+        self.check(rc, "upload_matrix")
+        return Handle(self, out.value, "matrix")
+
+    def upload_f32(self, m) -> "Handle":
+        m = _f32(m)
+        if m.ndim == 1:
+            m = m.reshape(1, -1)
+        return self.upload_matrix(m, F32, m.shape[0], m.shape[1])
+
+    def upload_bundle(self, up_raw, down_t_raw, ggml_type: int, h: int, ff: int) -> "Handle":
+        """flash.CreateBundle (flash/bundle.go:37-111) into HBM, bytes kept quantized."""
+        out = C.c_int64()
+        if _is_device_tensor(up_raw):
+            rc = self.lib.llg_hipd_upload_bundle(self.h, C.c_void_p(up_raw.data_ptr()),
+                                                 C.c_void_p(down_t_raw.data_ptr()), ggml_type, h,
+                                                 ff, C.byref(out))
+        else:
+            a, b = _host_bytes(up_raw), _host_bytes(down_t_raw)
+            rc = self.lib.llg_hip_upload_bundle(self.h, _ptr(a), _ptr(b), ggml_type, h, ff,
+                                                C.byref(out))
+        self.check(rc, "upload_bundle")
+        return Handle(self, out.value, "bundle")
+
+    def dequant(self, handle: "Handle", row0: int, nrows: int) -> np.ndarray:
+        info = handle.info()
+        per = info["cols"] * (2 if handle.is_bundle else 1)
+        out = np.empty(nrows * per, np.float32)
+        self.check(self.lib.llg_hip_dequant(self.h, handle.id, row0, nrows, _ptr(out)), "dequant")
+        return out.reshape(nrows, per)
+
+    def select(self, logits, threshold: float) -> np.ndarray:
+        """predictor.go:76-82 on given logits (the bit-exact selection hook)."""
+        lg = _f32(logits).ravel()
+        act = np.empty(max(lg.size, 1), np.int32)
+        n = C.c_int()
+        self.check(self.lib.llg_hip_select(self.h, _ptr(lg), lg.size, threshold, _ptr(act),
+                                           C.byref(n)), "select")
+        return act[: n.value].copy()
+
+    def matvec_q(self, mat: "Handle", x) -> np.ndarray:
+        info = mat.info()
+        x = _f32(x).ravel()
+        y = np.empty(info["rows"], np.float32)
+        self.check(self.lib.llg_hip_matvec_q(self.h, mat.id, _ptr(x), _ptr(y)), "matvec_q")
+        return y
+
+    def moe_route(self, logits, k: int):
+        lg = _f32(logits)
+        if lg.ndim == 1:
+            lg = lg.reshape(1, -1)
+        n_tok, n_exp = lg.shape
+        ids = np.empty((n_tok, k), np.int32)
+        w = np.empty((n_tok, k), np.float32)
+        self.check(self.lib.llg_hip_moe_route(self.h, _ptr(lg), n_tok, n_exp, k, _ptr(ids),
+                                              _ptr(w)), "moe_route")
+        return ids, w
+
+
+def _is_device_tensor(a) -> bool:
+    return hasattr(a, "is_cuda") and bool(getattr(a, "is_cuda"))
+
+
+def _host_bytes(a) -> np.ndarray:
+    if hasattr(a, "numpy"):
+        a = a.contiguous().numpy()
+    return np.ascontiguousarray(a).view(np.uint8).ravel()
+
+
+class Handle:
+    """A library-owned device object (matrix, bundle or window)."""
+
+    def __init__(self, dev: Device, hid: int, kind: str):
+        self.dev = dev
+        self.id = hid
+        self.kind = kind
+
+    def info(self) -> dict:
+        t, r, c, s = C.c_int(), C.c_int(), C.c_int(), C.c_int64()
+        self.dev.check(self.dev.lib.llg_hip_object_info(self.dev.h, self.id, C.byref(t),
+                                                        C.byref(r), C.byref(c), C.byref(s)),
+                       "object_info")
+        return {"type": t.value, "rows": r.value, "cols": c.value, "stride": s.value}
+
+    @property
+    def is_bundle(self) -> bool:
+        return self.kind == "bundle"
+
+    def release(self):
+        if self.id:
+            self.dev.check(self.dev.lib.llg_hip_release(self.dev.h, self.id), "release")
+            self.id = 0
+
+
+class Predictor:
+    """inference.Predictor (predictor.go:21-34): WUp [rank x h], WOut [ff x rank],
+    optional Bias [ff], Threshold."""
+
+    def __init__(self, dev: Device, w_up, w_out, bias=None, threshold: float = 0.0):
+        w_up, w_out = _f32(w_up), _f32(w_out)
+        self.dev = dev
+        self.h, self.rank, self.ff = w_up.shape[1], w_up.shape[0], w_out.shape[0]
+        self.w_up = dev.upload_f32(w_up)
+        self.w_out = dev.upload_f32(w_out)
+        self.bias = dev.upload_f32(_f32(bias).reshape(1, -1)) if bias is not None else None
+        self.threshold = float(threshold)
+
+    @property
+    def bias_id(self) -> int:
+        return self.bias.id if self.bias is not None else 0
+
+    def predict(self, attn_out, return_logits: bool = False):
+        """Predict (predictor.go:51-83): ascending indices with logit > Threshold."""
+        a = _f32(attn_out).ravel()
+        act = np.empty(self.ff, np.int32)
+        n = C.c_int()
+        logits = np.empty(self.ff, np.float32) if return_logits else None
+        self.dev.check(self.dev.lib.llg_hip_predict(
+            self.dev.h, self.w_up.id, self.w_out.id, self.bias_id, _ptr(a), self.threshold,
+            _ptr(act), C.byref(n), _ptr(logits) if logits is not None else None), "Predict")
+        idx = act[: n.value].copy()
+        return (idx, logits) if return_logits else idx
+
+
+def ffn_sparse_load(dev: Device, bundle: Handle, x, active, act: int = ACT_RELU) -> np.ndarray:
+    """ffnSparseLoad (ffn_flash.go:254-299) over an HBM bundle."""
+    x = _f32(x).ravel()
+    a = _i32(active).ravel()
+    out = np.empty_like(x)
+    dev.check(dev.lib.llg_hip_ffn_sparse(dev.h, bundle.id, _ptr(x), _ptr(a) if a.size else None,
+                                         a.size, act, _ptr(out)), "ffnSparseLoad")
+    return out
+
+
+def ffn_predict_sparse(dev: Device, pred: Predictor, bundle: Handle, attn_out, x,
+                       act: int = ACT_RELU):
+    """ffnFlash path 2 (ffn_flash.go:225-231): Predict then ffnSparseLoad, on the device."""
+    a, x = _f32(attn_out).ravel(), _f32(x).ravel()
+    out = np.empty_like(x)
+    idx = np.empty(pred.ff, np.int32)
+    n = C.c_int()
+    dev.check(dev.lib.llg_hip_ffn_predict_sparse(
+        dev.h, pred.w_up.id, pred.w_out.id, pred.bias_id, bundle.id, _ptr(a), _ptr(x),
+        pred.threshold, act, _ptr(out), _ptr(idx), C.byref(n)), "ffnFlash")
+    return out, idx[: n.value].copy()
+
+
+def ffn_dense(dev: Device, up: Handle, down: Handle, x, act: int = ACT_RELU) -> np.ndarray:
+    """Context.ffn ReLU/GELU path (forward.go:342-367): down @ act(up @ x)."""
+    x = _f32(x).ravel()
+    out = np.empty_like(x)
+    dev.check(dev.lib.llg_hip_ffn_dense(dev.h, up.id, down.id, _ptr(x), act, _ptr(out)), "ffn")
+    return out
+
+
+class NeuronCache:
+    """inference.NeuronCache (window.go:21-245) with its rows resident in HBM."""
+
+    def __init__(self, dev: Device, bundle: Handle, window_size: int):
+        self.dev = dev
+        self.bundle = bundle
+        self.window_size = window_size
+        out = C.c_int64()
+        dev.check(dev.lib.llg_hip_window_create(dev.h, bundle.id, window_size, C.byref(out)),
+                  "NewNeuronCache")
+        self.win = Handle(dev, out.value, "window")
+        self.last_loaded = 0
+        self._num = 0
+
+    def update(self, active_neurons) -> int:
+        """Update (window.go:71-117); returns the number of rows loaded."""
+        a = _i32(active_neurons).ravel()
+        nl, nr = C.c_int(), C.c_int()
+        self.dev.check(self.dev.lib.llg_hip_window_update(
+            self.dev.h, self.win.id, _ptr(a) if a.size else None, a.size, C.byref(nl),
+            C.byref(nr)), "NeuronCache.Update")
+        self.last_loaded, self._num = nl.value, nr.value
+        return nl.value
+
+    def ffn_forward(self, x, active_neurons, act: int = ACT_RELU) -> np.ndarray:
+        """FFNForward (window.go:143-180)."""
+        x = _f32(x).ravel()
+        a = _i32(active_neurons).ravel()
+        out = np.empty_like(x)
+        self.dev.check(self.dev.lib.llg_hip_window_ffn(
+            self.dev.h, self.win.id, _ptr(x), _ptr(a) if a.size else None, a.size, act,
+            _ptr(out)), "NeuronCache.FFNForward")
+        return out
+
+    def num_cached(self) -> int:
+        """NumCached (window.go:183)."""
+        return self._num
+
+    def resident(self) -> np.ndarray:
+        ff = self.bundle.info()["rows"]
+        flags = np.empty(ff, np.uint8)
+        n = C.c_int()
+        self.dev.check(self.dev.lib.llg_hip_window_resident(self.dev.h, self.win.id,
+                                                            _ptr(flags), C.byref(n)), "resident")
+        self._num = n.value
+        return np.flatnonzero(flags).astype(np.int32)
+
+
+def moe_ffn(dev: Device, router: Handle, gate: Handle, up: Handle, down: Handle, n_exp: int,
+            k: int, x):
+    """moeFFN (moe_forward.go:32-79) for one or more tokens x [n_tok x hidden].
+
+    Returns (out [n_tok x hidden], expert ids [n_tok x k], weights [n_tok x k])."""
+    x = _f32(x)
+    squeeze = x.ndim == 1
+    if squeeze:
+        x = x.reshape(1, -1)
+    n_tok = x.shape[0]
+    out = np.empty_like(x)
+    ids = np.empty((n_tok, k), np.int32)
+    w = np.empty((n_tok, k), np.float32)
+    dev.check(dev.lib.llg_hip_moe_ffn(dev.h, router.id, gate.id, up.id, down.id, n_exp, k,
+                                      _ptr(x), n_tok, _ptr(out), _ptr(ids), _ptr(w)), "moeFFN")
+    if squeeze:
+        return out[0], ids[0], w[0]
+    return out, ids, w

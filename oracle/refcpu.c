@@ -1,0 +1,543 @@
+/*
+ * refcpu.c -- CPU oracle for llama.go's sparse-FFN path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file restates the reference's Go CPU code
+ * (AndersHsueh/llama.go) in C so that the HIP path can be checked against it
+ * on the same inputs.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg load it, and only as the checker or the timed CPU
+ * baseline; the product library never links or calls it.
+ *
+ * Build: see oracle/Makefile (gcc -O2 -ffp-contract=off, no fast-math), so
+ * that float arithmetic is IEEE single with no FMA contraction, like Go's
+ * gc compiler on amd64.
+ *
+ * Pinning: every function here is checked by tests/test_oracle.py against
+ * known-answer vectors, float64 brute force, closed forms or invariants
+ * (the header of that file lists which check pins which function).
+ */
+#include "refcpu.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- gguf/types.go:70-102 ------------------------------------------------ */
+static int type_info(int t, int *block, int *tsize) {
+    switch (t) {
+    case REFCPU_F32: *block = 1; *tsize = 4; return 0;   /* types.go:71 */
+    case REFCPU_F16: *block = 1; *tsize = 2; return 0;   /* types.go:72 */
+    case REFCPU_Q4_0: *block = 32; *tsize = 18; return 0; /* types.go:73 */
+    case REFCPU_Q8_0: *block = 32; *tsize = 34; return 0; /* types.go:77 */
+    default: return -1;
+    }
+}
+
+int64_t refcpu_byte_size(int t, int64_t n) {
+    int bs, ts;
+    if (type_info(t, &bs, &ts) != 0) return -1;          /* types.go:93-96 */
+    if (n % bs != 0) return -1;                          /* types.go:98-100 */
+    return (n / bs) * (int64_t)ts;                       /* types.go:101 */
+}
+
+/* ---- tensor/dtype.go:417-443 -------------------------------------------- */
+static float bits_f32(uint32_t u) {
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+float refcpu_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h >> 15) << 31;
+    uint32_t exp = (uint32_t)((h >> 10) & 0x1F);
+    uint32_t mant = (uint32_t)(h & 0x3FF);
+    switch (exp) {
+    case 0:
+        if (mant == 0) return bits_f32(sign);
+        /* subnormal: normalise (dtype.go:427-434) */
+        exp = 1;
+        while ((mant & 0x400) == 0) {
+            mant <<= 1;
+            exp--; /* uint32 wrap, exactly as Go's uint32 arithmetic */
+        }
+        mant &= ~(uint32_t)0x400;
+        return bits_f32(sign | ((exp + 127 - 15) << 23) | (mant << 13));
+    case 31:
+        if (mant == 0) return bits_f32(sign | 0x7F800000u); /* +-Inf */
+        return bits_f32(sign | 0x7FC00000u);                /* NaN, payload dropped */
+    default:
+        return bits_f32(sign | ((exp + 127 - 15) << 23) | (mant << 13));
+    }
+}
+
+static uint16_t le16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* ---- tensor/dtype.go:12-82, 249-268 ------------------------------------- */
+int64_t refcpu_dequantize(const uint8_t *raw, int64_t nbytes, int t, float *out) {
+    switch (t) {
+    case REFCPU_F32: { /* dtype.go:26-38 */
+        if (nbytes % 4) return -1;
+        int64_t n = nbytes / 4;
+        for (int64_t i = 0; i < n; i++) {
+            uint32_t u = (uint32_t)raw[4 * i] | ((uint32_t)raw[4 * i + 1] << 8) |
+                         ((uint32_t)raw[4 * i + 2] << 16) | ((uint32_t)raw[4 * i + 3] << 24);
+            out[i] = bits_f32(u);
+        }
+        return n;
+    }
+    case REFCPU_F16: { /* dtype.go:12-24 */
+        if (nbytes % 2) return -1;
+        int64_t n = nbytes / 2;
+        for (int64_t i = 0; i < n; i++) out[i] = refcpu_f16_to_f32(le16(raw + 2 * i));
+        return n;
+    }
+    case REFCPU_Q8_0: { /* dtype.go:41-58 */
+        if (nbytes % 34) return -1;
+        int64_t nb = nbytes / 34;
+        for (int64_t b = 0; b < nb; b++) {
+            const uint8_t *base = raw + b * 34;
+            float scale = refcpu_f16_to_f32(le16(base));
+            for (int i = 0; i < 32; i++) {
+                int8_t q = (int8_t)base[2 + i];
+                out[b * 32 + i] = (float)q * scale;
+            }
+        }
+        return nb * 32;
+    }
+    case REFCPU_Q4_0: { /* dtype.go:62-82 -- interleaved nibble order */
+        if (nbytes % 18) return -1;
+        int64_t nb = nbytes / 18;
+        for (int64_t b = 0; b < nb; b++) {
+            const uint8_t *base = raw + b * 18;
+            float scale = refcpu_f16_to_f32(le16(base));
+            for (int i = 0; i < 16; i++) {
+                uint8_t packed = base[2 + i];
+                int8_t lo = (int8_t)((uint8_t)(packed & 0x0F) - 8);
+                int8_t hi = (int8_t)((uint8_t)(packed >> 4) - 8);
+                out[b * 32 + i * 2] = (float)lo * scale;
+                out[b * 32 + i * 2 + 1] = (float)hi * scale;
+            }
+        }
+        return nb * 32;
+    }
+    default:
+        return -1; /* dtype.go:266 */
+    }
+}
+
+/* ---- tensor/ops.go ------------------------------------------------------ */
+void refcpu_matmulvec(const float *w, int out_dim, int in_dim, const float *x, float *y) {
+    for (int i = 0; i < out_dim; i++) { /* ops.go:51-58 */
+        float sum = 0.0f;
+        const float *row = w + (size_t)i * in_dim;
+        for (int j = 0; j < in_dim; j++) sum += row[j] * x[j];
+        y[i] = sum;
+    }
+}
+
+void refcpu_relu(float *x, int n) { /* ops.go:168-174: NaN and -0.0 pass through */
+    for (int i = 0; i < n; i++)
+        if (x[i] < 0) x[i] = 0;
+}
+
+void refcpu_silu(float *x, int n) { /* ops.go:177-181 */
+    for (int i = 0; i < n; i++) {
+        float v = x[i];
+        x[i] = v / (1.0f + (float)exp((double)(-v)));
+    }
+}
+
+void refcpu_gelu(float *x, int n) { /* ops.go:184-189, untyped consts become float32 */
+    const float c = (float)0.7978845608028654;
+    const float k = (float)0.044715;
+    for (int i = 0; i < n; i++) {
+        float v = x[i];
+        float inner = c * (v + k * v * v * v);
+        x[i] = 0.5f * v * (1.0f + (float)tanh((double)inner));
+    }
+}
+
+void refcpu_activation(int act, float *x, int n) { /* ffn_flash.go:303-312 */
+    if (act == REFCPU_ACT_SILU)
+        refcpu_silu(x, n);
+    else if (act == REFCPU_ACT_GELU)
+        refcpu_gelu(x, n);
+    else
+        refcpu_relu(x, n);
+}
+
+void refcpu_rmsnorm(const float *x, const float *w, float *out, int n, float eps) {
+    float sum_sq = 0.0f; /* ops.go:124-127 */
+    for (int i = 0; i < n; i++) sum_sq += x[i] * x[i];
+    float rms = (float)sqrt((double)(sum_sq / (float)n) + (double)eps);
+    float scale = 1.0f / rms;
+    for (int i = 0; i < n; i++) out[i] = x[i] * scale * w[i];
+}
+
+void refcpu_layernorm(const float *x, const float *w, const float *b, float *out, int n,
+                      float eps) {
+    float mean = 0.0f; /* ops.go:148-162 */
+    for (int i = 0; i < n; i++) mean += x[i];
+    mean /= (float)n;
+    float var = 0.0f;
+    for (int i = 0; i < n; i++) {
+        float d = x[i] - mean;
+        var += d * d;
+    }
+    var /= (float)n;
+    float sd = (float)sqrt((double)var + (double)eps);
+    for (int i = 0; i < n; i++) out[i] = (x[i] - mean) / sd * w[i] + b[i];
+}
+
+/* ---- inference/forward.go:463-479 --------------------------------------- */
+void refcpu_softmax_inplace(float *v, int n) {
+    float maxv = v[0];
+    for (int i = 0; i < n; i++)
+        if (v[i] > maxv) maxv = v[i];
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) {
+        float e = (float)exp((double)(v[i] - maxv));
+        v[i] = e;
+        sum += e;
+    }
+    for (int i = 0; i < n; i++) v[i] /= sum;
+}
+
+/* ---- inference/predictor.go --------------------------------------------- */
+int refcpu_select(const float *logits, int ff, float thr, int32_t *active) {
+    int n = 0; /* predictor.go:76-82 */
+    for (int i = 0; i < ff; i++)
+        if (logits[i] > thr) active[n++] = i;
+    return n;
+}
+
+int refcpu_predict(const float *wup, const float *wout, const float *bias, int h, int rank,
+                   int ff, const float *a, float thr, int32_t *active, float *logits_out) {
+    if (!wup || !wout) return -1; /* predictor.go:52-54 */
+    float *hidden = (float *)malloc(sizeof(float) * (size_t)rank);
+    float *logits = logits_out ? logits_out : (float *)malloc(sizeof(float) * (size_t)ff);
+    refcpu_matmulvec(wup, rank, h, a, hidden); /* :57 */
+    refcpu_relu(hidden, rank);                 /* :61 */
+    refcpu_matmulvec(wout, ff, rank, hidden, logits); /* :64 */
+    if (bias)                                  /* :69-73, tensor.Add ops.go:87-95 */
+        for (int i = 0; i < ff; i++) logits[i] += bias[i];
+    int n = refcpu_select(logits, ff, thr, active);
+    free(hidden);
+    if (!logits_out) free(logits);
+    return n;
+}
+
+/* ---- flash/storage.go:246-319 ------------------------------------------- */
+int refcpu_read_rows(const uint8_t *raw, int t, int in_dim, int out_dim, const int32_t *rows,
+                     int n_rows, float *out) {
+    int64_t rb = refcpu_byte_size(t, in_dim); /* :253 */
+    if (rb < 0) return -1;
+    for (int i = 0; i < n_rows; i++) {
+        int32_t r = rows[i];
+        if (r < 0 || r >= out_dim) return -2; /* :292-294 */
+        int64_t off = (int64_t)r * rb;        /* :296 */
+        if (refcpu_dequantize(raw + off, rb, t, out + (size_t)i * in_dim) < 0) return -1;
+    }
+    return 0;
+}
+
+/* ---- inference/ffn_flash.go:254-299 ------------------------------------- */
+int refcpu_ffn_sparse_load(const uint8_t *up_raw, const uint8_t *down_t_raw, int t, int h,
+                           int ff, const float *x, const int32_t *active, int n_active,
+                           int act, float *out) {
+    memset(out, 0, sizeof(float) * (size_t)h);
+    if (n_active == 0) return 0; /* :255-257 */
+    float *up_rows = (float *)malloc(sizeof(float) * (size_t)n_active * h);
+    float *down_rows = (float *)malloc(sizeof(float) * (size_t)n_active * h);
+    float *inter = (float *)malloc(sizeof(float) * (size_t)n_active);
+    int rc = refcpu_read_rows(up_raw, t, h, ff, active, n_active, up_rows); /* :262 */
+    if (rc == 0) rc = refcpu_read_rows(down_t_raw, t, h, ff, active, n_active, down_rows);
+    if (rc == 0) {
+        for (int j = 0; j < n_active; j++) { /* :273-281 */
+            const float *row = up_rows + (size_t)j * h;
+            float dot = 0.0f;
+            for (int d = 0; d < h; d++) dot += row[d] * x[d];
+            inter[j] = dot;
+        }
+        refcpu_activation(act, inter, n_active); /* :284-285 */
+        for (int j = 0; j < n_active; j++) {     /* :288-298 */
+            if (inter[j] == 0) continue;
+            const float *row = down_rows + (size_t)j * h;
+            float scale = inter[j];
+            for (int d = 0; d < h; d++) out[d] += scale * row[d];
+        }
+    }
+    free(up_rows);
+    free(down_rows);
+    free(inter);
+    return rc;
+}
+
+/* ---- inference/forward.go:318-353, 428-445 ------------------------------ */
+int refcpu_ffn_dense(const uint8_t *up_raw, const uint8_t *down_raw, int t, int h, int ff,
+                     const float *x, int act, float *out) {
+    int64_t nu = (int64_t)h * ff;
+    int64_t bu = refcpu_byte_size(t, nu);
+    if (bu < 0 || refcpu_byte_size(t, h) < 0 || refcpu_byte_size(t, ff) < 0) return -1;
+    float *up = (float *)malloc(sizeof(float) * (size_t)nu);   /* ReadTensor, storage.go:111-128 */
+    float *down = (float *)malloc(sizeof(float) * (size_t)nu);
+    float *hid = (float *)malloc(sizeof(float) * (size_t)ff);
+    refcpu_dequantize(up_raw, bu, t, up);
+    refcpu_dequantize(down_raw, bu, t, down);
+    refcpu_matmulvec(up, ff, h, x, hid);   /* forward.go:343: FFNUp shape [F, h] */
+    refcpu_activation(act, hid, ff);       /* forward.go:347 (ReLU) / 361 (GELU) */
+    refcpu_matmulvec(down, h, ff, hid, out); /* forward.go:348: FFNDown shape [h, F] */
+    free(up);
+    free(down);
+    free(hid);
+    return 0;
+}
+
+/* ---- inference/window.go ------------------------------------------------ */
+struct refcpu_neuron_cache {
+    float *matrix;       /* [max_neurons, 2*hidden] bundled up|down, window.go:23 */
+    int *pointers;       /* matrix row -> neuron, :25 */
+    int *in_cache;       /* neuron -> matrix row or -1 (the Go map), :27 */
+    int32_t **last_k;    /* ring of active sets, :30 */
+    int *last_k_len;
+    int *last_k_set;     /* non-nil flag for each ring slot */
+    int window_head;     /* :31 */
+    int num_used, max_neurons, hidden, window, ff;
+    const uint8_t *up_raw, *down_raw;
+    int type;
+};
+
+refcpu_neuron_cache *refcpu_nc_new(int max_neurons, int hidden, int window, int ff,
+                                   const uint8_t *up_raw, const uint8_t *down_raw, int t) {
+    refcpu_neuron_cache *c = (refcpu_neuron_cache *)calloc(1, sizeof(*c)); /* window.go:48-63 */
+    c->matrix = (float *)calloc((size_t)max_neurons * 2 * hidden, sizeof(float));
+    c->pointers = (int *)calloc((size_t)max_neurons, sizeof(int));
+    c->in_cache = (int *)malloc(sizeof(int) * (size_t)ff);
+    for (int i = 0; i < ff; i++) c->in_cache[i] = -1;
+    c->last_k = (int32_t **)calloc((size_t)window, sizeof(int32_t *));
+    c->last_k_len = (int *)calloc((size_t)window, sizeof(int));
+    c->last_k_set = (int *)calloc((size_t)window, sizeof(int));
+    c->max_neurons = max_neurons;
+    c->hidden = hidden;
+    c->window = window;
+    c->ff = ff;
+    c->up_raw = up_raw;
+    c->down_raw = down_raw;
+    c->type = t;
+    return c;
+}
+
+void refcpu_nc_free(refcpu_neuron_cache *c) {
+    if (!c) return;
+    for (int i = 0; i < c->window; i++) free(c->last_k[i]);
+    free(c->last_k);
+    free(c->last_k_len);
+    free(c->last_k_set);
+    free(c->matrix);
+    free(c->pointers);
+    free(c->in_cache);
+    free(c);
+}
+
+static void nc_evict(refcpu_neuron_cache *c, int n) { /* window.go:188-204 */
+    int row = c->in_cache[n];
+    if (row < 0) return;
+    int last = c->num_used - 1;
+    size_t w = (size_t)2 * c->hidden;
+    if (row != last) {
+        memcpy(c->matrix + (size_t)row * w, c->matrix + (size_t)last * w, w * sizeof(float));
+        c->pointers[row] = c->pointers[last];
+        c->in_cache[c->pointers[row]] = row;
+    }
+    c->in_cache[n] = -1;
+    c->num_used--;
+}
+
+static int nc_load_rows(refcpu_neuron_cache *c, const int32_t *neurons, int n) {
+    int h = c->hidden; /* window.go:207-245 */
+    float *up = (float *)malloc(sizeof(float) * (size_t)n * h);
+    float *down = (float *)malloc(sizeof(float) * (size_t)n * h);
+    int rc = refcpu_read_rows(c->up_raw, c->type, h, c->ff, neurons, n, up); /* :211 */
+    if (rc == 0) rc = refcpu_read_rows(c->down_raw, c->type, h, c->ff, neurons, n, down);
+    if (rc == 0) {
+        for (int j = 0; j < n; j++) {
+            if (c->num_used >= c->max_neurons) { /* grow by 10%: :222-232 */
+                int new_cap = c->max_neurons + c->max_neurons / 10 + 1;
+                c->matrix = (float *)realloc(c->matrix, sizeof(float) * (size_t)new_cap * 2 * h);
+                c->pointers = (int *)realloc(c->pointers, sizeof(int) * (size_t)new_cap);
+                c->max_neurons = new_cap;
+            }
+            int row = c->num_used;
+            c->pointers[row] = neurons[j];
+            c->in_cache[neurons[j]] = row;
+            float *dest = c->matrix + (size_t)row * 2 * h; /* :238-240 */
+            memcpy(dest, up + (size_t)j * h, sizeof(float) * (size_t)h);
+            memcpy(dest + h, down + (size_t)j * h, sizeof(float) * (size_t)h);
+            c->num_used++;
+        }
+    }
+    free(up);
+    free(down);
+    return rc;
+}
+
+int refcpu_nc_update(refcpu_neuron_cache *c, const int32_t *active, int n_active,
+                     int *n_loaded_out, int32_t *load_list_out) {
+    int head = c->window_head;
+    if (c->last_k_set[head]) { /* window.go:73-95 */
+        char *still = (char *)calloc((size_t)c->ff, 1);
+        for (int i = 0; i < c->window; i++) {
+            if (i == head || !c->last_k_set[i]) continue;
+            for (int j = 0; j < c->last_k_len[i]; j++) still[c->last_k[i][j]] = 1;
+        }
+        for (int j = 0; j < n_active; j++) still[active[j]] = 1;
+        for (int j = 0; j < c->last_k_len[head]; j++) {
+            int n = c->last_k[head][j];
+            if (!still[n]) nc_evict(c, n);
+        }
+        free(still);
+    }
+    int32_t *to_load = (int32_t *)malloc(sizeof(int32_t) * (size_t)(n_active ? n_active : 1));
+    int nl = 0; /* :98-103 */
+    for (int j = 0; j < n_active; j++)
+        if (c->in_cache[active[j]] < 0) to_load[nl++] = active[j];
+    int rc = 0;
+    if (nl > 0) rc = nc_load_rows(c, to_load, nl); /* :106-110 */
+    if (n_loaded_out) *n_loaded_out = nl;
+    if (load_list_out) memcpy(load_list_out, to_load, sizeof(int32_t) * (size_t)nl);
+    free(to_load);
+    if (rc != 0) return rc;
+    /* :113-114 record the active set (a private copy) and advance the head */
+    free(c->last_k[head]);
+    c->last_k[head] = (int32_t *)malloc(sizeof(int32_t) * (size_t)(n_active ? n_active : 1));
+    memcpy(c->last_k[head], active, sizeof(int32_t) * (size_t)n_active);
+    c->last_k_len[head] = n_active;
+    c->last_k_set[head] = 1;
+    c->window_head = (head + 1) % c->window;
+    return 0;
+}
+
+int refcpu_nc_ffn_forward(refcpu_neuron_cache *c, const float *x, const int32_t *active,
+                          int n_active, int act, float *out) {
+    int h = c->hidden; /* window.go:143-180 */
+    float *inter = (float *)calloc((size_t)(n_active ? n_active : 1), sizeof(float));
+    for (int j = 0; j < n_active; j++) {
+        int row = c->in_cache[active[j]];
+        if (row < 0) continue; /* :150-152 */
+        const float *up = c->matrix + (size_t)row * 2 * h;
+        float dot = 0.0f;
+        for (int d = 0; d < h; d++) dot += up[d] * x[d];
+        inter[j] = dot;
+    }
+    refcpu_activation(act, inter, n_active);
+    memset(out, 0, sizeof(float) * (size_t)h);
+    for (int j = 0; j < n_active; j++) {
+        if (inter[j] == 0) continue; /* :167-169 */
+        int row = c->in_cache[active[j]];
+        if (row < 0) continue;
+        const float *down = c->matrix + (size_t)row * 2 * h + h;
+        float scale = inter[j];
+        for (int d = 0; d < h; d++) out[d] += scale * down[d];
+    }
+    free(inter);
+    return 0;
+}
+
+int refcpu_nc_num_cached(const refcpu_neuron_cache *c) { return c->num_used; } /* :183 */
+
+int refcpu_nc_is_cached(const refcpu_neuron_cache *c, int n) {
+    return (n >= 0 && n < c->ff && c->in_cache[n] >= 0) ? 1 : 0;
+}
+
+/* ---- inference/moe_forward.go:32-150 ------------------------------------ */
+int refcpu_moe_route(const float *logits_in, int n_exp, int k, int32_t *ids_out, float *w_out) {
+    if (k <= 0 || n_exp <= 0 || k > n_exp) return -1;
+    float *p = (float *)malloc(sizeof(float) * (size_t)n_exp);
+    int *idx = (int *)malloc(sizeof(int) * (size_t)n_exp);
+    memcpy(p, logits_in, sizeof(float) * (size_t)n_exp);
+    refcpu_softmax_inplace(p, n_exp); /* :47 */
+    for (int i = 0; i < n_exp; i++) idx[i] = i;
+    /* :58 sort.Slice descending.  Go's pdqsort runs insertion sort for n <= 12,
+     * which keeps equal scores in index order; a stable insertion sort restates it. */
+    for (int i = 1; i < n_exp; i++) {
+        int cur = idx[i];
+        int j = i;
+        while (j > 0 && p[cur] > p[idx[j - 1]]) {
+            idx[j] = idx[j - 1];
+            j--;
+        }
+        idx[j] = cur;
+    }
+    float wsum = 0.0f; /* :62-68 */
+    for (int i = 0; i < k; i++) wsum += p[idx[i]];
+    if (wsum < 1e-9f) wsum = 1.0f;
+    for (int i = 0; i < k; i++) {
+        ids_out[i] = idx[i];
+        w_out[i] = p[idx[i]] / wsum; /* :73 e.score/wsum */
+    }
+    free(p);
+    free(idx);
+    return 0;
+}
+
+int refcpu_moe_ffn(const float *router, const uint8_t *gate_raw, const uint8_t *up_raw,
+                   const uint8_t *down_raw, int t, int hidden, int eff, int n_exp, int k,
+                   const float *x, float *out, int32_t *ids_out, float *w_out) {
+    if (k <= 0 || n_exp <= 0 || eff <= 0) return -1; /* :38-40 */
+    if (k > n_exp) return -1;
+    int64_t rb_h = refcpu_byte_size(t, hidden);
+    int64_t rb_f = refcpu_byte_size(t, eff);
+    if (rb_h < 0 || rb_f < 0) return -1;
+    float *logits = (float *)malloc(sizeof(float) * (size_t)n_exp);
+    refcpu_matmulvec(router, n_exp, hidden, x, logits); /* :43 */
+    int32_t *ids = (int32_t *)malloc(sizeof(int32_t) * (size_t)k);
+    float *ws = (float *)malloc(sizeof(float) * (size_t)k);
+    refcpu_moe_route(logits, n_exp, k, ids, ws);
+    float *gu = (float *)malloc(sizeof(float) * (size_t)eff * hidden); /* ExpertScratch */
+    float *dn = (float *)malloc(sizeof(float) * (size_t)hidden * eff);
+    float *gate = (float *)malloc(sizeof(float) * (size_t)eff);
+    float *up = (float *)malloc(sizeof(float) * (size_t)eff);
+    float *hv = (float *)malloc(sizeof(float) * (size_t)eff);
+    memset(out, 0, sizeof(float) * (size_t)hidden); /* :71 */
+    for (int s = 0; s < k; s++) {                   /* :72-77 */
+        int e = ids[s];
+        float w = ws[s];
+        /* :96 ReadContiguousRows(gate, e*eff, eff) -- storage.go:72-94 */
+        refcpu_dequantize(gate_raw + (int64_t)e * eff * rb_h, rb_h * eff, t, gu);
+        for (int j = 0; j < eff; j++) { /* :102-109 */
+            const float *row = gu + (size_t)j * hidden;
+            float dot = 0.0f;
+            for (int d = 0; d < hidden; d++) dot += row[d] * x[d];
+            gate[j] = dot;
+        }
+        refcpu_dequantize(up_raw + (int64_t)e * eff * rb_h, rb_h * eff, t, gu); /* :112 */
+        for (int j = 0; j < eff; j++) { /* :118-125 */
+            const float *row = gu + (size_t)j * hidden;
+            float dot = 0.0f;
+            for (int d = 0; d < hidden; d++) dot += row[d] * x[d];
+            up[j] = dot;
+        }
+        for (int j = 0; j < eff; j++) { /* :128-132 */
+            float g = gate[j];
+            float silu = g / (1.0f + (float)exp(-(double)g));
+            hv[j] = silu * up[j];
+        }
+        refcpu_dequantize(down_raw + (int64_t)e * hidden * rb_f, rb_f * hidden, t, dn); /* :135 */
+        for (int d = 0; d < hidden; d++) { /* :141-148 */
+            const float *row = dn + (size_t)d * eff;
+            float dot = 0.0f;
+            for (int j = 0; j < eff; j++) dot += row[j] * hv[j];
+            out[d] += w * dot;
+        }
+    }
+    if (ids_out) memcpy(ids_out, ids, sizeof(int32_t) * (size_t)k);
+    if (w_out) memcpy(w_out, ws, sizeof(float) * (size_t)k);
+    free(logits);
+    free(ids);
+    free(ws);
+    free(gu);
+    free(dn);
+    free(gate);
+    free(up);
+    free(hv);
+    return 0;
+}

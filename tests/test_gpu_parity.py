@@ -1,0 +1,347 @@
+"""GPU parity: the gfx950 library (through the C ABI) against the CPU oracle
+on the same seeded inputs.
+
+Bars (from the hot-path contract):
+  - dequantized values, active index sets and MoE expert ids: bit-exact;
+  - FFN outputs: max |gpu - oracle| <= 1e-3 * max |oracle| (fp32 accumulation);
+  - predictor logits: fp32 reordering only (max rel 1e-5 of max |logit|).
+Sizes are the configs' real shapes where the oracle finishes in seconds, and
+tiny/ragged shapes for the edge cases.
+"""
+import numpy as np
+import pytest
+import torch
+
+import llg
+import llg.gguf as gg
+from oracle import refcpu as R
+from tests.helpers import (make_sparse_layer, max_rel_err, normal, quant, threshold_for,
+                           window_sets)
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # FFN output tolerance relative to the output's max-abs
+
+
+def gpu_normal(shape, std, seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return torch.randn(shape, generator=g, device="cuda", dtype=torch.float32) * std
+
+
+def gpu_quant(shape, std, seed, t) -> np.ndarray:
+    """Big weights: drawn and quantized on the GPU, bytes returned to the host."""
+    return gg.quantize(gpu_normal(shape, std, seed), t).cpu().numpy()
+
+
+# ---------------------------------------------------------------- dequant
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16, gg.F32])
+def test_dequant_bit_exact(dev, rng, t):
+    rows, cols = 37, 4544
+    raw = quant(normal(rng, (rows, cols), 0.02), t)
+    if t in (gg.Q4_0, gg.Q8_0):
+        bs = 18 if t == gg.Q4_0 else 34
+        specials = [0x0001, 0x03FF, 0x7C00, 0xFC00, 0x7E01, 0xFE00, 0x8000, 0x0000, 0x7BFF]
+        for i, hb in enumerate(specials):  # f16 scale specials, incl. NaN payloads
+            raw[i, 0:2] = [hb & 0xFF, hb >> 8]
+            raw[i, bs:bs + 2] = [hb & 0xFF, hb >> 8]
+    elif t == gg.F16:
+        raw[0, :8] = np.array([0x0001, 0x7E01, 0xFC00, 0x8000], np.uint16).view(np.uint8)
+    m = dev.upload_matrix(raw, t, rows, cols)
+    got = dev.dequant(m, 0, rows)
+    ref = np.stack([R.dequantize(raw[r], t) for r in range(rows)])
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    part = dev.dequant(m, 5, 3)
+    assert np.array_equal(part.view(np.uint32), ref[5:8].view(np.uint32))
+    m.release()
+
+
+def test_dequant_bundle_rows(dev, rng):
+    h, ff = 256, 50
+    up, dn = make_sparse_layer(rng, h, ff, gg.Q4_0)
+    b = dev.upload_bundle(up, dn, gg.Q4_0, h, ff)
+    got = dev.dequant(b, 10, 4)
+    for i in range(4):
+        assert np.array_equal(got[i, :h], R.dequantize(up[10 + i], gg.Q4_0))
+        assert np.array_equal(got[i, h:], R.dequantize(dn[10 + i], gg.Q4_0))
+    b.release()
+
+
+# ---------------------------------------------------------------- selection
+@pytest.mark.parametrize("ff", [1, 63, 64, 65, 1000, 18176, 100003])
+def test_select_bit_exact(dev, rng, ff):
+    lg = normal(rng, ff, 1.0)
+    lg[rng.choice(ff, min(ff, 5), replace=False)] = 0.25  # ties exactly at the threshold
+    for thr in (0.25, 1.645, -10.0, 10.0):
+        assert np.array_equal(dev.select(lg, thr), R.select(lg, thr))
+
+
+# ---------------------------------------------------------------- predictor
+@pytest.mark.parametrize("h,rank,ff,bias", [(64, 16, 256, True), (4544, 128, 18176, False),
+                                            (4544, 128, 18176, True), (96, 20, 300, False)])
+def test_predict(dev, rng, h, rank, ff, bias):
+    wup, wout = normal(rng, (rank, h), 0.05), normal(rng, (ff, rank), 0.05)
+    b = normal(rng, ff, 0.01) if bias else None
+    a = normal(rng, h, 1.0)
+    _, ref_lg = R.predict(wup, wout, b, a, 0.0)
+    n_target = max(1, int(round(0.05 * ff)))
+    thr = threshold_for(ref_lg, n_target)
+    ref_act, _ = R.predict(wup, wout, b, a, thr)
+    assert ref_act.size == n_target
+    p = llg.Predictor(dev, wup, wout, b, thr)
+    act, lg = p.predict(a, return_logits=True)
+    assert np.max(np.abs(lg - ref_lg)) <= 1e-5 * np.max(np.abs(ref_lg))
+    assert np.array_equal(act, ref_act)
+    # selection on the oracle's own logits is bit-exact by construction of the hook
+    assert np.array_equal(dev.select(ref_lg, thr), ref_act)
+
+
+# ---------------------------------------------------------------- sparse FFN
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16, gg.F32])
+@pytest.mark.parametrize("h,ff,n", [(64, 64, 1), (128, 512, 40), (256, 333, 333)])
+def test_ffn_sparse_small(dev, rng, t, h, ff, n):
+    up, dn = make_sparse_layer(rng, h, ff, t)
+    x = normal(rng, h, 1.0)
+    active = np.sort(rng.choice(ff, n, replace=False)).astype(np.int32)
+    b = dev.upload_bundle(up, dn, t, h, ff)
+    for act in (gg.ACT_RELU, gg.ACT_SILU, gg.ACT_GELU):
+        got = llg.ffn_sparse_load(dev, b, x, active, act)
+        ref = R.ffn_sparse_load(up, dn, t, h, ff, x, active, act)
+        assert max_rel_err(got, ref) <= TOL, (t, h, ff, n, act)
+    b.release()
+
+
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16])
+def test_ffn_sparse_config0(dev, rng, t):
+    """Falcon-7B-shaped layer, d=4544, F=18176, 909 active neurons."""
+    h, ff = 4544, 18176
+    up = gpu_quant((ff, h), 0.02, 11, t)
+    dn = gpu_quant((ff, h), 0.02, 12, t)
+    x = normal(rng, h, 1.0)
+    active = np.sort(rng.choice(ff, 909, replace=False)).astype(np.int32)
+    b = dev.upload_bundle(up, dn, t, h, ff)
+    got = llg.ffn_sparse_load(dev, b, x, active)
+    ref = R.ffn_sparse_load(up, dn, t, h, ff, x, active)
+    assert max_rel_err(got, ref) <= TOL
+    # unsorted and repeated indices are accepted like the reference's []int
+    perm = active[::-1].copy()
+    assert max_rel_err(llg.ffn_sparse_load(dev, b, x, perm),
+                       R.ffn_sparse_load(up, dn, t, h, ff, x, perm)) <= TOL
+    b.release()
+
+
+def test_ffn_sparse_edge_cases(dev, rng):
+    h, ff = 64, 64
+    up, dn = make_sparse_layer(rng, h, ff, gg.Q4_0)
+    b = dev.upload_bundle(up, dn, gg.Q4_0, h, ff)
+    x = normal(rng, h, 1.0)
+    assert np.all(llg.ffn_sparse_load(dev, b, x, np.array([], np.int32)) == 0)
+    with pytest.raises(llg.LlgError) as e:
+        llg.ffn_sparse_load(dev, b, x, np.array([3, 64], np.int32))
+    assert e.value.code == llg.LLG_E_RANGE
+    with pytest.raises(llg.LlgError) as e:
+        llg.ffn_sparse_load(dev, b, x, np.array([-1], np.int32))
+    assert e.value.code == llg.LLG_E_RANGE
+    allact = np.arange(ff, dtype=np.int32)
+    assert max_rel_err(llg.ffn_sparse_load(dev, b, x, allact),
+                       R.ffn_sparse_load(up, dn, gg.Q4_0, h, ff, x, allact)) <= TOL
+    b.release()
+
+
+def test_ffn_predict_sparse_config0(dev, rng):
+    """Path 2 of ffnFlash: predictor + selection + gathered FFN in one call."""
+    h, ff, rank = 4544, 18176, 128
+    up = gpu_quant((ff, h), 0.02, 21, gg.Q4_0)
+    dn = gpu_quant((ff, h), 0.02, 22, gg.Q4_0)
+    wup, wout = normal(rng, (rank, h), 0.05), normal(rng, (ff, rank), 0.05)
+    x = normal(rng, h, 1.0)
+    _, lg = R.predict(wup, wout, None, x, 0.0)
+    thr = threshold_for(lg, 909)
+    ref_act, _ = R.predict(wup, wout, None, x, thr)
+    ref = R.ffn_sparse_load(up, dn, gg.Q4_0, h, ff, x, ref_act)
+    b = dev.upload_bundle(up, dn, gg.Q4_0, h, ff)
+    p = llg.Predictor(dev, wup, wout, None, thr)
+    out, act = llg.ffn_predict_sparse(dev, p, b, x, x)
+    assert np.array_equal(act, ref_act)
+    assert max_rel_err(out, ref) <= TOL
+    b.release()
+
+
+# ---------------------------------------------------------------- dense path
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16, gg.F32])
+def test_matvec_q_small(dev, rng, t):
+    rows, cols = 77, 320
+    w = quant(normal(rng, (rows, cols), 0.02), t)
+    x = normal(rng, cols, 1.0)
+    m = dev.upload_matrix(w, t, rows, cols)
+    ref = R.matmulvec(np.stack([R.dequantize(w[r], t) for r in range(rows)]), x)
+    assert max_rel_err(dev.matvec_q(m, x), ref) <= 1e-5
+    m.release()
+
+
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16])
+def test_ffn_dense_config1(dev, rng, t):
+    """Dense naive path (window=0): full up matvec, ReLU, full down matvec."""
+    h, ff = 4544, 18176
+    up = gpu_quant((ff, h), 0.02, 31, t)
+    down = gpu_quant((h, ff), 0.02, 32, t)
+    x = normal(rng, h, 1.0)
+    u = dev.upload_matrix(up, t, ff, h)
+    d = dev.upload_matrix(down, t, h, ff)
+    got = llg.ffn_dense(dev, u, d, x)
+    ref = R.ffn_dense(up, down, t, h, ff, x)
+    assert max_rel_err(got, ref) <= TOL
+    u.release()
+    d.release()
+
+
+def test_ffn_dense_shape_mismatch(dev, rng):
+    up = quant(normal(rng, (64, 32), 0.02), gg.Q4_0)
+    m = dev.upload_matrix(up, gg.Q4_0, 64, 32)
+    with pytest.raises(llg.LlgError) as e:
+        llg.ffn_dense(dev, m, m, normal(rng, 32, 1.0))
+    assert e.value.code == llg.LLG_E_ARG
+
+
+# ---------------------------------------------------------------- window
+@pytest.mark.parametrize("k", [1, 2, 5])
+def test_window_tiny_closed_forms(dev, rng, k):
+    h, ff = 64, 96
+    up, dn = make_sparse_layer(rng, h, ff, gg.Q4_0)
+    b = dev.upload_bundle(up, dn, gg.Q4_0, h, ff)
+    nc = llg.NeuronCache(dev, b, k)
+    ref = R.NeuronCache(max(256, ff * k // 5), h, k, ff, up, dn, gg.Q4_0)
+    sets = window_sets(rng, ff, 16, 24, 0.6)
+    sets.insert(5, np.array([], np.int32))  # an empty active set
+    for A in sets:
+        n_loaded = nc.update(A)
+        ref_loaded = ref.update(A)
+        assert n_loaded == ref_loaded.size
+        assert nc.num_cached() == ref.num_cached()
+        assert np.array_equal(nc.resident(), ref.resident())
+        x = normal(rng, h, 1.0)
+        got = nc.ffn_forward(x, A)
+        exp = ref.ffn_forward(x, A)
+        assert max_rel_err(got, exp) <= TOL
+    b.release()
+
+
+def test_window_config2(dev, rng):
+    """64 tokens, k=5, 909 active per token with 70% carried over."""
+    h, ff = 4544, 18176
+    up = gpu_quant((ff, h), 0.02, 41, gg.Q4_0)
+    dn = gpu_quant((ff, h), 0.02, 42, gg.Q4_0)
+    b = dev.upload_bundle(up, dn, gg.Q4_0, h, ff)
+    nc = llg.NeuronCache(dev, b, 5)
+    ref = R.NeuronCache(ff * 5 // 5, h, 5, ff, up, dn, gg.Q4_0)
+    sets = window_sets(rng, ff, 909, 64, 0.7)
+    for t, A in enumerate(sets):
+        assert nc.update(A) == ref.update(A).size
+        assert nc.num_cached() == ref.num_cached()
+        if t % 8 == 7:
+            x = normal(rng, h, 1.0)
+            assert max_rel_err(nc.ffn_forward(x, A), ref.ffn_forward(x, A)) <= TOL
+    assert np.array_equal(nc.resident(), ref.resident())
+    b.release()
+
+
+def test_window_rejects_duplicates(dev, rng):
+    up, dn = make_sparse_layer(rng, 32, 32, gg.Q4_0)
+    b = dev.upload_bundle(up, dn, gg.Q4_0, 32, 32)
+    nc = llg.NeuronCache(dev, b, 2)
+    with pytest.raises(llg.LlgError):
+        nc.update(np.array([1, 1], np.int32))
+    b.release()
+
+
+# ---------------------------------------------------------------- MoE
+def test_moe_route_bit_exact(dev, rng):
+    lg = normal(rng, (200, 8), 1.5)
+    lg[0] = 0.0                          # all tied
+    lg[1] = [0, 1, 1, 1, 0, 0, 0, 0]     # three-way tie for first
+    ids, w = dev.moe_route(lg, 2)
+    for t in range(lg.shape[0]):
+        rid, rw = R.moe_route(lg[t], 2)
+        assert np.array_equal(ids[t], rid)
+        assert np.array_equal(w[t].view(np.uint32), rw.view(np.uint32)), t
+
+
+def make_moe(rng, d, eff, E, t, seed=None):
+    router = normal(rng, (E, d), 0.02)
+    if seed is None:
+        gate = quant(normal(rng, (E * eff, d), 0.02), t)
+        up = quant(normal(rng, (E * eff, d), 0.02), t)
+        down = quant(normal(rng, (E * d, eff), 0.02), t)
+    else:
+        gate = gpu_quant((E * eff, d), 0.02, seed, t)
+        up = gpu_quant((E * eff, d), 0.02, seed + 1, t)
+        down = gpu_quant((E * d, eff), 0.02, seed + 2, t)
+    return router, gate, up, down
+
+
+def upload_moe(dev, router, gate, up, down, d, eff, E, t):
+    return (dev.upload_f32(router), dev.upload_matrix(gate, t, E * eff, d),
+            dev.upload_matrix(up, t, E * eff, d), dev.upload_matrix(down, t, E * d, eff))
+
+
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16])
+def test_moe_tiny(dev, rng, t):
+    d, eff, E, k = 64, 96, 4, 2
+    router, gate, up, down = make_moe(rng, d, eff, E, t)
+    router *= 10  # spread the router so softmax is not flat
+    hs = upload_moe(dev, router, gate, up, down, d, eff, E, t)
+    x = normal(rng, (16, d), 1.0)
+    out, ids, w = llg.moe_ffn(dev, *hs, E, k, x)
+    for i in range(16):
+        ro, rid, rw = R.moe_ffn(router, gate, up, down, t, d, eff, E, k, x[i])
+        assert np.array_equal(ids[i], rid)
+        assert max_rel_err(out[i], ro) <= TOL
+    for hnd in hs:
+        hnd.release()
+
+
+def test_moe_decode_config3(dev, rng):
+    """Mixtral-shaped layer: d=4096, 8 experts of 14336, top-2, Q4_0, one token."""
+    d, eff, E, k = 4096, 14336, 8, 2
+    router, gate, up, down = make_moe(rng, d, eff, E, gg.Q4_0, seed=51)
+    hs = upload_moe(dev, router, gate, up, down, d, eff, E, gg.Q4_0)
+    x = normal(rng, d, 1.0)
+    out, ids, w = llg.moe_ffn(dev, *hs, E, k, x)
+    ro, rid, rw = R.moe_ffn(router, gate, up, down, gg.Q4_0, d, eff, E, k, x)
+    assert np.array_equal(ids, rid)
+    assert max_rel_err(out, ro) <= TOL
+    for hnd in hs:
+        hnd.release()
+
+
+def test_moe_invalid_hparams(dev, rng):
+    d, eff, E = 64, 96, 4
+    router, gate, up, down = make_moe(rng, d, eff, E, gg.Q4_0)
+    hs = upload_moe(dev, router, gate, up, down, d, eff, E, gg.Q4_0)
+    with pytest.raises(llg.LlgError) as e:
+        llg.moe_ffn(dev, *hs, E, 0, normal(rng, d, 1.0))
+    assert e.value.code == llg.LLG_E_HPARAM
+
+
+# ---------------------------------------------------------------- Metal parity
+def test_metal_parity_matvec_rmsnorm(dev, rng):
+    for rows, cols in [(1, 1), (7, 33), (300, 4544)]:
+        w, x = normal(rng, (rows, cols), 0.1), normal(rng, cols, 1.0)
+        assert max_rel_err(dev.mat_mul_vec(w, rows, cols, x), R.matmulvec(w, x)) <= 1e-5
+    x, wt = normal(rng, 4544, 1.0), normal(rng, 4544, 1.0)
+    assert max_rel_err(dev.rms_norm(x, wt, 1e-5), R.rmsnorm(x, wt, 1e-5)) <= 1e-5
+    with pytest.raises(llg.LlgError):
+        dev.mat_mul_vec(w, rows, cols + 1, x)
+
+
+def test_bad_handles_and_types(dev, rng):
+    with pytest.raises(llg.LlgError) as e:
+        dev.upload_matrix(np.zeros(36, np.uint8), 12, 1, 64)  # Q4_K is out of scope
+    assert e.value.code == llg.LLG_E_TYPE
+    with pytest.raises(llg.LlgError) as e:
+        dev.upload_matrix(np.zeros(36, np.uint8), gg.Q4_0, 1, 48)
+    assert e.value.code == llg.LLG_E_ALIGN
+    fake = llg.Handle(dev, 999999, "bundle")
+    with pytest.raises(llg.LlgError) as e:
+        llg.ffn_sparse_load(dev, fake, np.zeros(64, np.float32), np.array([0], np.int32))
+    assert e.value.code == llg.LLG_E_HANDLE
