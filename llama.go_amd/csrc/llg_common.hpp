@@ -113,10 +113,31 @@ __device__ __forceinline__ float llg_f16(uint32_t h) {
     return __half2float(__ushort_as_half((unsigned short)h));
 }
 
-__device__ __forceinline__ float llg_wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// DPP lane moves (GFX9 encodings): quad_perm xor-1 = 0xB1, xor-2 = 0x4E;
+// row_ror:n = 0x120 + n rotates within each row of 16 lanes.
+template <int CTRL>
+__device__ __forceinline__ float llg_dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 4 lanes of each quad, in every lane of the quad.
+__device__ __forceinline__ float llg_quad_sum(float v) {
+    v += llg_dpp<0xB1>(v);
+    v += llg_dpp<0x4E>(v);
     return v;
+}
+
+// Sum over the wavefront, returned in every lane: quad and row sums through
+// DPP, then the four row sums read out with v_readlane.
+__device__ __forceinline__ float llg_wave_sum(float v) {
+    v = llg_quad_sum(v);
+    v += llg_dpp<0x124>(v);  // row_ror:4
+    v += llg_dpp<0x128>(v);  // row_ror:8
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
 // Activations, with the reference's rounding: ops.go:168-189.
@@ -284,6 +305,211 @@ __device__ __forceinline__ void llg_block_axpy<LLG_TYPE_F32>(const uint8_t *__re
         acc[4 * i + 1] += u * w.y;
         acc[4 * i + 2] += u * w.z;
         acc[4 * i + 3] += u * w.w;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Split load / compute forms of one 32-element block.  Kernels load the raw
+// bytes of all the blocks a lane owns first (BlockRaw), so their memory
+// requests are in flight together, and only then dequantize and use them.
+// ---------------------------------------------------------------------------
+template <int T>
+struct BlockRaw;
+template <>
+struct BlockRaw<LLG_TYPE_Q4_0> {
+    uint4 q;
+    unsigned short d;
+};
+template <>
+struct BlockRaw<LLG_TYPE_Q8_0> {
+    uint4 q0, q1;
+    unsigned short d;
+};
+template <>
+struct BlockRaw<LLG_TYPE_F16> {
+    uint4 q[4];
+};
+template <>
+struct BlockRaw<LLG_TYPE_F32> {
+    float4 q[8];
+};
+
+template <int T>
+__device__ __forceinline__ void llg_block_load(BlockRaw<T> &r, const uint8_t *__restrict__ row,
+                                               const RowFmt &f, int b);
+template <>
+__device__ __forceinline__ void llg_block_load<LLG_TYPE_Q4_0>(BlockRaw<LLG_TYPE_Q4_0> &r,
+                                                               const uint8_t *__restrict__ row,
+                                                               const RowFmt &f, int b) {
+    r.q = *reinterpret_cast<const uint4 *>(row + (size_t)b * 16);
+    r.d = *reinterpret_cast<const unsigned short *>(row + f.d_off + b * 2);
+}
+template <>
+__device__ __forceinline__ void llg_block_load<LLG_TYPE_Q8_0>(BlockRaw<LLG_TYPE_Q8_0> &r,
+                                                               const uint8_t *__restrict__ row,
+                                                               const RowFmt &f, int b) {
+    r.q0 = *reinterpret_cast<const uint4 *>(row + (size_t)b * 32);
+    r.q1 = *reinterpret_cast<const uint4 *>(row + (size_t)b * 32 + 16);
+    r.d = *reinterpret_cast<const unsigned short *>(row + f.d_off + b * 2);
+}
+template <>
+__device__ __forceinline__ void llg_block_load<LLG_TYPE_F16>(BlockRaw<LLG_TYPE_F16> &r,
+                                                              const uint8_t *__restrict__ row,
+                                                              const RowFmt &f, int b) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(row + (size_t)b * 64);
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.q[i] = p[i];
+}
+template <>
+__device__ __forceinline__ void llg_block_load<LLG_TYPE_F32>(BlockRaw<LLG_TYPE_F32> &r,
+                                                              const uint8_t *__restrict__ row,
+                                                              const RowFmt &f, int b) {
+    const float4 *p = reinterpret_cast<const float4 *>(row + (size_t)b * 128);
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.q[i] = p[i];
+}
+
+// dot(dequant(block), x[32]) from loaded bytes.
+template <int T>
+__device__ __forceinline__ float llg_raw_dot(const BlockRaw<T> &r, const float4 *x4);
+template <>
+__device__ __forceinline__ float llg_raw_dot<LLG_TYPE_Q4_0>(const BlockRaw<LLG_TYPE_Q4_0> &r,
+                                                             const float4 *x4) {
+    const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 xa = x4[2 * i], xb = x4[2 * i + 1];
+        const uint32_t v = w[i];
+        s += (float)((int)((v >> 0) & 15) - 8) * xa.x;
+        s += (float)((int)((v >> 4) & 15) - 8) * xa.y;
+        s += (float)((int)((v >> 8) & 15) - 8) * xa.z;
+        s += (float)((int)((v >> 12) & 15) - 8) * xa.w;
+        s += (float)((int)((v >> 16) & 15) - 8) * xb.x;
+        s += (float)((int)((v >> 20) & 15) - 8) * xb.y;
+        s += (float)((int)((v >> 24) & 15) - 8) * xb.z;
+        s += (float)((int)((v >> 28) & 15) - 8) * xb.w;
+    }
+    return s * llg_f16(r.d);
+}
+template <>
+__device__ __forceinline__ float llg_raw_dot<LLG_TYPE_Q8_0>(const BlockRaw<LLG_TYPE_Q8_0> &r,
+                                                             const float4 *x4) {
+    const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 xv = x4[i];
+        const uint32_t v = w[i];
+        s += (float)(int8_t)(v & 0xFF) * xv.x;
+        s += (float)(int8_t)((v >> 8) & 0xFF) * xv.y;
+        s += (float)(int8_t)((v >> 16) & 0xFF) * xv.z;
+        s += (float)(int8_t)(v >> 24) * xv.w;
+    }
+    return s * llg_f16(r.d);
+}
+template <>
+__device__ __forceinline__ float llg_raw_dot<LLG_TYPE_F16>(const BlockRaw<LLG_TYPE_F16> &r,
+                                                            const float4 *x4) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint4 q = r.q[i];
+        const float4 xa = x4[2 * i], xb = x4[2 * i + 1];
+        s += llg_f16(q.x & 0xFFFF) * xa.x;
+        s += llg_f16(q.x >> 16) * xa.y;
+        s += llg_f16(q.y & 0xFFFF) * xa.z;
+        s += llg_f16(q.y >> 16) * xa.w;
+        s += llg_f16(q.z & 0xFFFF) * xb.x;
+        s += llg_f16(q.z >> 16) * xb.y;
+        s += llg_f16(q.w & 0xFFFF) * xb.z;
+        s += llg_f16(q.w >> 16) * xb.w;
+    }
+    return s;
+}
+template <>
+__device__ __forceinline__ float llg_raw_dot<LLG_TYPE_F32>(const BlockRaw<LLG_TYPE_F32> &r,
+                                                            const float4 *x4) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 xv = x4[i];
+        s += r.q[i].x * xv.x;
+        s += r.q[i].y * xv.y;
+        s += r.q[i].z * xv.z;
+        s += r.q[i].w * xv.w;
+    }
+    return s;
+}
+
+// acc[0..31] += u * dequant(block) from loaded bytes.
+template <int T>
+__device__ __forceinline__ void llg_raw_axpy(const BlockRaw<T> &r, float u, float *acc);
+template <>
+__device__ __forceinline__ void llg_raw_axpy<LLG_TYPE_Q4_0>(const BlockRaw<LLG_TYPE_Q4_0> &r,
+                                                             float u, float *acc) {
+    const float s = u * llg_f16(r.d);
+    const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int p = 0; p < 8; p++)
+            acc[8 * i + p] += s * (float)((int)((w[i] >> (4 * p)) & 15) - 8);
+}
+template <>
+__device__ __forceinline__ void llg_raw_axpy<LLG_TYPE_Q8_0>(const BlockRaw<LLG_TYPE_Q8_0> &r,
+                                                             float u, float *acc) {
+    const float s = u * llg_f16(r.d);
+    const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int p = 0; p < 4; p++) acc[4 * i + p] += s * (float)(int8_t)((w[i] >> (8 * p)) & 0xFF);
+}
+template <>
+__device__ __forceinline__ void llg_raw_axpy<LLG_TYPE_F16>(const BlockRaw<LLG_TYPE_F16> &r,
+                                                            float u, float *acc) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t w[4] = {r.q[i].x, r.q[i].y, r.q[i].z, r.q[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            acc[8 * i + 2 * k] += u * llg_f16(w[k] & 0xFFFF);
+            acc[8 * i + 2 * k + 1] += u * llg_f16(w[k] >> 16);
+        }
+    }
+}
+template <>
+__device__ __forceinline__ void llg_raw_axpy<LLG_TYPE_F32>(const BlockRaw<LLG_TYPE_F32> &r,
+                                                            float u, float *acc) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        acc[4 * i + 0] += u * r.q[i].x;
+        acc[4 * i + 1] += u * r.q[i].y;
+        acc[4 * i + 2] += u * r.q[i].z;
+        acc[4 * i + 3] += u * r.q[i].w;
+    }
+}
+
+// Stage x[nb*32] into LDS with XS floats per 32-float block (XS = 36 keeps
+// the 16-byte reads of 16 consecutive lanes on 64 distinct banks).  Each
+// thread issues up to 8 of its float4 loads before storing any.
+template <int XS>
+__device__ __forceinline__ void llg_stage_x(float *xs, const float *__restrict__ x, int nb) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    const int n4 = nb * 8;
+    for (int i0 = threadIdx.x; i0 < n4; i0 += 8 * blockDim.x) {
+        float4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = i0 + k * blockDim.x;
+            v[k] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int i = i0 + k * blockDim.x;
+            if (i < n4) reinterpret_cast<float4 *>(xs + (i >> 3) * XS)[i & 7] = v[k];
+        }
     }
 }
 

@@ -1,220 +1,140 @@
-// llg_ffn.hip -- gathered sparse FFN over row-column bundles
-// (inference/ffn_flash.go:254-299, window.go:143-180) and the dense
-// dequant-matvec FFN (inference/forward.go:318-353, tensor/ops.go:39-60).
+// llg_ffn.hip -- dense dequant-matvec FFN (inference/forward.go:318-353,
+// tensor/ops.go:39-60) and the sparse-FFN entry points (kernels in
+// llg_sparse.hip).
 //
-// Sparse FFN, two passes over the active list:
-//   k_sparse_up   one wavefront per active neuron: u_j = act(up_j . x);
-//                 lane l reduces blocks l, l+64, ... of the up row (16-byte
-//                 nibble loads, f16 scale), then a wavefront sum.  Also
-//                 zeroes `out` for the next pass.
-//   k_sparse_down workgroup (slice s, group g): the 256 outputs of 8
-//                 consecutive blocks of the down rows, over neurons of
-//                 group g; u_j == 0 rows are skipped as at ffn_flash.go:290;
-//                 one fp32 atomic add per output per workgroup.  The
-//                 blockIdx -> (s, g) map keeps all slices of one neuron
-//                 group on one XCD so the group's scale lines are fetched
-//                 into that XCD's L2 once.
+// k_matvec_q: y[r] = act(sum_b block_dot(row r, b, x)).  A workgroup owns a
+// tile of MV_TILE rows and one column chunk of at most MV_CHUNK blocks; it
+// stages that chunk of x in LDS (36-float stride per 32-float block, so 16
+// lanes reading one block each hit distinct banks).  Each wavefront takes
+// MV_ROWS rows at a time and issues the loads of all its blocks of those rows
+// before using them; every x block read from LDS serves MV_ROWS rows.  With
+// one chunk the row sum is final and the activation is applied; with several
+// chunks each workgroup adds its partial with an fp32 atomic into a zeroed y.
 #include "llg_common.hpp"
 #include "llg_internal.hpp"
 
-#define UP_WAVES 4
-#define DN_SLICE_BLOCKS 8
-
-template <int T>
-__global__ __launch_bounds__(256) void k_sparse_up(
-    const uint8_t *__restrict__ base, long long bstride, RowFmt f,
-    const int32_t *__restrict__ slot_of, const float *__restrict__ x,
-    const int32_t *__restrict__ active, const int32_t *__restrict__ n_active_p, int act,
-    float *__restrict__ u, float *__restrict__ out) {
-    const int n_active = *n_active_p;
-    const int gtid = blockIdx.x * blockDim.x + threadIdx.x;
-    for (int i = gtid; i < f.cols; i += gridDim.x * blockDim.x) out[i] = 0.0f;
-    const int lane = threadIdx.x & 63;
-    const int nwaves = gridDim.x * UP_WAVES;
-    for (int j = blockIdx.x * UP_WAVES + (threadIdx.x >> 6); j < n_active; j += nwaves) {
-        const int n = active[j];
-        const long long slot = slot_of ? slot_of[n] : n;
-        if (slot < 0) {  // not resident: window.go:150-152 leaves the activation at 0
-            if (lane == 0) u[j] = 0.0f;
-            continue;
-        }
-        const uint8_t *row = base + slot * bstride;
-        float s = 0.0f;
-        for (int b = lane; b < f.nb; b += 64)
-            s += llg_block_dot<T>(row, f, b, reinterpret_cast<const float4 *>(x + b * 32));
-        s = llg_wave_sum(s);
-        if (lane == 0) u[j] = llg_act(act, s);
-    }
-}
-
-template <int T>
-__global__ __launch_bounds__(256) void k_sparse_down(
-    const uint8_t *__restrict__ base, long long bstride, RowFmt f,
-    const int32_t *__restrict__ slot_of, const int32_t *__restrict__ active,
-    const int32_t *__restrict__ n_active_p, const float *__restrict__ u, int n_slices,
-    int n_groups, float *__restrict__ out) {
-    __shared__ float red[4][DN_SLICE_BLOCKS * 32];
-    // XCD-aware tile map: workgroups are dispatched round-robin over 8 XCDs,
-    // so id % 8 selects the XCD; group g lives on XCD g % 8.
-    const int id = blockIdx.x;
-    const int xcd = id & 7;
-    const int k = id >> 3;
-    const int g = xcd + 8 * (k / n_slices);
-    const int s = k % n_slices;
-    const int n_active = *n_active_p;
-    const int chunk = (n_active + n_groups - 1) / n_groups;
-    const int j0 = g * chunk;
-    const int j1 = min(n_active, j0 + chunk);
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int bl = lane & 7;
-    const int sub = lane >> 3;
-    const int b = s * DN_SLICE_BLOCKS + bl;
-    float acc[32];
-#pragma unroll
-    for (int e = 0; e < 32; e++) acc[e] = 0.0f;
-    if (b < f.nb) {
-        for (int j = j0 + wave * 8 + sub; j < j1; j += 32) {
-            const float uj = u[j];
-            if (uj == 0.0f) continue;  // ffn_flash.go:290 / window.go:167
-            const int n = active[j];
-            const long long slot = slot_of ? slot_of[n] : n;
-            llg_block_axpy<T>(base + slot * bstride + f.stride, f, b, uj, acc);
-        }
-    }
-#pragma unroll
-    for (int e = 0; e < 32; e++) {
-        float v = acc[e];
-        v += __shfl_xor(v, 8, 64);
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        acc[e] = v;
-    }
-    if (sub == 0) {
-#pragma unroll
-        for (int e = 0; e < 32; e++) red[wave][bl * 32 + e] = acc[e];
-    }
-    __syncthreads();
-    const int t = threadIdx.x;
-    const int o = s * DN_SLICE_BLOCKS * 32 + t;
-    if (o < f.cols && j0 < j1) {
-        const float v = red[0][t] + red[1][t] + red[2][t] + red[3][t];
-        unsafeAtomicAdd(out + o, v);
-    }
-}
-
-size_t llg_sparse_ws_bytes(int max_active) {
-    return (size_t)llg_align((long long)(max_active > 0 ? max_active : 1) * 4, 256);
-}
-
-template <int T>
-static void sparse_launch(hipStream_t st, const uint8_t *base, long long bstride, const RowFmt &f,
-                          const int32_t *slot_of, const float *x, const int32_t *active,
-                          const int32_t *n_active, int max_active, int act, float *out,
-                          float *u) {
-    int up_grid = (max_active + UP_WAVES - 1) / UP_WAVES;
-    if (up_grid < 1) up_grid = 1;
-    if (up_grid > 1024) up_grid = 1024;
-    hipLaunchKernelGGL(k_sparse_up<T>, dim3(up_grid), dim3(256), 0, st, base, bstride, f,
-                       slot_of, x, active, n_active, act, u, out);
-    const int n_slices = (f.nb + DN_SLICE_BLOCKS - 1) / DN_SLICE_BLOCKS;
-    int n_groups = (max_active + 15) / 16;
-    n_groups = (n_groups + 7) / 8 * 8;
-    if (n_groups < 8) n_groups = 8;
-    if (n_groups > 64) n_groups = 64;
-    hipLaunchKernelGGL(k_sparse_down<T>, dim3(n_slices * n_groups), dim3(256), 0, st, base,
-                       bstride, f, slot_of, active, n_active, u, n_slices, n_groups, out);
-}
-
-int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, const RowFmt &f,
-                       const int32_t *slot_of, const float *d_x, const int32_t *d_active,
-                       const int32_t *d_n_active, int max_active, int act, float *d_out,
-                       uint8_t *ws) {
-    hipStream_t st = llg_dev_stream(d);
-    float *u = reinterpret_cast<float *>(ws);
-    switch (f.type) {
-    case LLG_TYPE_Q4_0:
-        sparse_launch<LLG_TYPE_Q4_0>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                     max_active, act, d_out, u);
-        break;
-    case LLG_TYPE_Q8_0:
-        sparse_launch<LLG_TYPE_Q8_0>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                     max_active, act, d_out, u);
-        break;
-    case LLG_TYPE_F16:
-        sparse_launch<LLG_TYPE_F16>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                    max_active, act, d_out, u);
-        break;
-    case LLG_TYPE_F32:
-        sparse_launch<LLG_TYPE_F32>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                    max_active, act, d_out, u);
-        break;
-    default:
-        return llg_set_error(d, LLG_E_TYPE, "sparse ffn: unsupported type %d", f.type);
-    }
-    LLG_LAUNCH_CHECK(d, "sparse ffn");
-    return 0;
-}
-
-// ---------------------------------------------------------------------------
-// Dense dequant-matvec: y[r] = act(sum_b block_dot(row r, b, x)).
-// Each wavefront owns MV_ROWS consecutive rows and reuses every x block it
-// loads for all of them.
-// ---------------------------------------------------------------------------
 #define MV_ROWS 2
+#define MV_TILE 32        // rows per workgroup (4 wavefronts x 4 passes x MV_ROWS)
+#define MV_CHUNK 160      // max blocks of x staged per workgroup
+#define MV_XS 36          // staged floats per 32-float block
+#define MV_BATCH 3        // blocks per lane whose loads are issued together
 
 template <int T>
 __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w, long long stride,
-                                                  RowFmt f, int rows, const float *__restrict__ x,
-                                                  int act, float *__restrict__ y) {
-    const int lane = threadIdx.x & 63;
-    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * MV_ROWS;
-    if (r0 >= rows) return;
-    float s[MV_ROWS];
-#pragma unroll
-    for (int i = 0; i < MV_ROWS; i++) s[i] = 0.0f;
-    for (int b = lane; b < f.nb; b += 64) {
-        float4 x4[8];
-        const float4 *xp = reinterpret_cast<const float4 *>(x + b * 32);
-#pragma unroll
-        for (int i = 0; i < 8; i++) x4[i] = xp[i];
-#pragma unroll
-        for (int i = 0; i < MV_ROWS; i++)
-            if (r0 + i < rows) s[i] += llg_block_dot<T>(w + (long long)(r0 + i) * stride, f, b, x4);
+                                                  RowFmt f, int rows, int chunk_blocks,
+                                                  const float *__restrict__ x, int act,
+                                                  float *__restrict__ y, float *__restrict__ zero,
+                                                  int zero_n) {
+    extern __shared__ float xs[];
+    const int n_chunks = (f.nb + chunk_blocks - 1) / chunk_blocks;
+    const int tile = blockIdx.x / n_chunks;
+    const int ch = blockIdx.x % n_chunks;
+    const int cb0 = ch * chunk_blocks;
+    const int cnb = min(chunk_blocks, f.nb - cb0);
+    if (zero) {
+        const int gtid = blockIdx.x * blockDim.x + threadIdx.x;
+        for (int i = gtid; i < zero_n; i += gridDim.x * blockDim.x) zero[i] = 0.0f;
     }
+    llg_stage_x<MV_XS>(xs, x + (size_t)cb0 * 32, cnb);
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r_end = min(rows, (tile + 1) * MV_TILE);
+    for (int r0 = tile * MV_TILE + wave * MV_ROWS; r0 < r_end; r0 += 4 * MV_ROWS) {
+        float s[MV_ROWS];
 #pragma unroll
-    for (int i = 0; i < MV_ROWS; i++) {
-        const float v = llg_wave_sum(s[i]);
-        if (lane == 0 && r0 + i < rows) y[r0 + i] = act >= 0 ? llg_act(act, v) : v;
+        for (int q = 0; q < MV_ROWS; q++) s[q] = 0.0f;
+        for (int bl0 = lane; bl0 < cnb; bl0 += 64 * MV_BATCH) {
+            // request the bytes of all MV_BATCH x MV_ROWS blocks, then use them
+            BlockRaw<T> r[MV_BATCH][MV_ROWS];
+#pragma unroll
+            for (int i = 0; i < MV_BATCH; i++)
+#pragma unroll
+                for (int q = 0; q < MV_ROWS; q++)
+                    if (bl0 + 64 * i < cnb && r0 + q < r_end)
+                        llg_block_load<T>(r[i][q], w + (long long)(r0 + q) * stride, f,
+                                          cb0 + bl0 + 64 * i);
+#pragma unroll
+            for (int i = 0; i < MV_BATCH; i++) {
+                const int bl = bl0 + 64 * i;
+                if (bl >= cnb) continue;
+                const float4 *xb = reinterpret_cast<const float4 *>(xs + bl * MV_XS);
+#pragma unroll
+                for (int q = 0; q < MV_ROWS; q++)
+                    if (r0 + q < r_end) s[q] += llg_raw_dot<T>(r[i][q], xb);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < MV_ROWS; q++) {
+            const float v = llg_wave_sum(s[q]);
+            if (lane == 0 && r0 + q < r_end) {
+                if (n_chunks == 1)
+                    y[r0 + q] = act >= 0 ? llg_act(act, v) : v;
+                else
+                    unsafeAtomicAdd(y + r0 + q, v);
+            }
+        }
     }
 }
 
-int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y) {
+static int mv_chunk_blocks(const RowFmt &f, int act) {
+    // An activation needs the whole row in one workgroup.
+    if (act >= 0 || f.nb <= MV_CHUNK) return f.nb;
+    const int n_chunks = (f.nb + MV_CHUNK - 1) / MV_CHUNK;
+    return (f.nb + n_chunks - 1) / n_chunks;
+}
+
+// zero/zero_n: a buffer the launch also clears (the next kernel's atomic target).
+static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y,
+                         float *zero, int zero_n) {
     hipStream_t st = llg_dev_stream(d);
     const RowFmt &f = w->fmt;
-    const int grid = (w->rows + 4 * MV_ROWS - 1) / (4 * MV_ROWS);
+    const int cb = mv_chunk_blocks(f, act);
+    const int n_chunks = (f.nb + cb - 1) / cb;
+    const size_t lds = (size_t)cb * MV_XS * 4;
+    if (lds > 160 * 1024)
+        return llg_set_error(d, LLG_E_ARG, "matvec: row of %d elements too long", f.cols);
+    if (n_chunks > 1 && zero != d_y) {
+        LLG_HIP_TRY(d, hipMemsetAsync(d_y, 0, (size_t)w->rows * 4, st));
+    }
+    const int grid = (w->rows + MV_TILE - 1) / MV_TILE * n_chunks;
     switch (f.type) {
     case LLG_TYPE_Q4_0:
-        hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_Q4_0>, dim3(grid), dim3(256), 0, st, w->d,
-                           w->stride, f, w->rows, d_x, act, d_y);
+        hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_Q4_0>, dim3(grid), dim3(256), lds, st, w->d,
+                           w->stride, f, w->rows, cb, d_x, act, d_y, zero, zero_n);
         break;
     case LLG_TYPE_Q8_0:
-        hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_Q8_0>, dim3(grid), dim3(256), 0, st, w->d,
-                           w->stride, f, w->rows, d_x, act, d_y);
+        hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_Q8_0>, dim3(grid), dim3(256), lds, st, w->d,
+                           w->stride, f, w->rows, cb, d_x, act, d_y, zero, zero_n);
         break;
     case LLG_TYPE_F16:
-        hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_F16>, dim3(grid), dim3(256), 0, st, w->d,
-                           w->stride, f, w->rows, d_x, act, d_y);
+        hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_F16>, dim3(grid), dim3(256), lds, st, w->d,
+                           w->stride, f, w->rows, cb, d_x, act, d_y, zero, zero_n);
         break;
     case LLG_TYPE_F32:
-        hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_F32>, dim3(grid), dim3(256), 0, st, w->d,
-                           w->stride, f, w->rows, d_x, act, d_y);
+        hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_F32>, dim3(grid), dim3(256), lds, st, w->d,
+                           w->stride, f, w->rows, cb, d_x, act, d_y, zero, zero_n);
         break;
     default:
         return llg_set_error(d, LLG_E_TYPE, "matvec: unsupported type %d", f.type);
     }
     LLG_LAUNCH_CHECK(d, "matvec_q");
     return 0;
+}
+
+int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y) {
+    return matvec_launch(d, w, d_x, act, d_y, nullptr, 0);
+}
+
+// Dense FFN: hid = act(up . x) (whole rows), then out = down . hid; the up
+// launch clears `out` when the down matvec accumulates over column chunks.
+static int dense_enqueue(LlgDevice *d, const LlgObject *up, const LlgObject *down,
+                         const float *d_x, int act, float *hid, float *d_out) {
+    const int down_chunks = (down->fmt.nb + mv_chunk_blocks(down->fmt, -1) - 1) /
+                            mv_chunk_blocks(down->fmt, -1);
+    int rc = matvec_launch(d, up, d_x, act, hid, down_chunks > 1 ? d_out : nullptr,
+                           down->rows);
+    if (rc) return rc;
+    return matvec_launch(d, down, hid, -1, d_out, d_out, 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -285,26 +205,29 @@ int llg_hip_ffn_sparse(LlgHipDevice h, int64_t hb, const float *x, const int32_t
     return llg_sync_dev(d);
 }
 
+static int check_fused(LlgDevice *d, int64_t hwup, int64_t hwout, int64_t hbias, int64_t hb,
+                       LlgObject **wup, LlgObject **wout, LlgObject **bias, LlgObject **b) {
+    int rc = llg_check_predictor(d, hwup, hwout, hbias, wup, wout, bias);
+    if (rc) return rc;
+    if ((rc = check_bundle(d, hb, b))) return rc;
+    if ((*wout)->rows != (*b)->rows || (*wup)->fmt.cols != (*b)->fmt.cols)
+        return llg_set_error(d, LLG_E_ARG, "predict_sparse: predictor/bundle shape mismatch");
+    return 0;
+}
+
 int llg_hipd_ffn_predict_sparse(LlgHipDevice h, int64_t hwup, int64_t hwout, int64_t hbias,
                                 int64_t hb, const float *d_a, const float *d_x, float thr,
                                 int act, float *d_out, int32_t *d_active, int32_t *d_n_active) {
     LlgDevice *d = llg_dev(h);
     if (!d) return LLG_E_NODEV;
     LlgObject *wup, *wout, *bias, *b;
-    int rc = llg_check_predictor(d, hwup, hwout, hbias, &wup, &wout, &bias);
+    int rc = check_fused(d, hwup, hwout, hbias, hb, &wup, &wout, &bias, &b);
     if (rc) return rc;
-    if ((rc = check_bundle(d, hb, &b))) return rc;
-    if (wout->rows != b->rows || wup->fmt.cols != b->fmt.cols)
-        return llg_set_error(d, LLG_E_ARG, "predict_sparse: predictor/bundle shape mismatch");
-    if (!d_a || !d_x || !d_out || !d_active || !d_n_active)
-        return llg_set_error(d, LLG_E_ARG, "predict_sparse: null pointer");
-    const long long o_sp = llg_align(llg_predict_ws_bytes(wup->rows, wout->rows), 256);
-    uint8_t *ws = (uint8_t *)llg_ws(d, o_sp + llg_sparse_ws_bytes(b->rows), &rc);
+    if (!d_a || !d_x || !d_out) return llg_set_error(d, LLG_E_ARG, "predict_sparse: null pointer");
+    uint8_t *ws = (uint8_t *)llg_ws(d, llg_fused_ws_bytes(wup->rows, wout->rows), &rc);
     if (rc) return rc;
-    rc = llg_predict_enqueue(d, wup, wout, bias, d_a, thr, d_active, d_n_active, nullptr, ws);
-    if (rc) return rc;
-    return llg_sparse_enqueue(d, b->d, b->stride, b->fmt, nullptr, d_x, d_active, d_n_active,
-                              b->rows, act, d_out, ws + o_sp);
+    return llg_fused_enqueue(d, wup, wout, bias, b, d_a, d_x, thr, act, d_out, d_active,
+                             d_n_active, ws);
 }
 
 int llg_hip_ffn_predict_sparse(LlgHipDevice h, int64_t hwup, int64_t hwout, int64_t hbias,
@@ -313,9 +236,8 @@ int llg_hip_ffn_predict_sparse(LlgHipDevice h, int64_t hwup, int64_t hwout, int6
     LlgDevice *d = llg_dev(h);
     if (!d) return LLG_E_NODEV;
     LlgObject *wup, *wout, *bias, *b;
-    int rc = llg_check_predictor(d, hwup, hwout, hbias, &wup, &wout, &bias);
+    int rc = check_fused(d, hwup, hwout, hbias, hb, &wup, &wout, &bias, &b);
     if (rc) return rc;
-    if ((rc = check_bundle(d, hb, &b))) return rc;
     if (!a || !x || !out) return llg_set_error(d, LLG_E_ARG, "predict_sparse: null pointer");
     const int hd = b->fmt.cols, ff = b->rows;
     const long long o_a = 0;
@@ -324,17 +246,14 @@ int llg_hip_ffn_predict_sparse(LlgHipDevice h, int64_t hwup, int64_t hwout, int6
     const long long o_act = o_out + llg_align((long long)hd * 4, 256);
     const long long o_n = o_act + llg_align((long long)ff * 4, 256);
     const long long o_ws = o_n + 256;
-    const long long o_sp = o_ws + llg_align(llg_predict_ws_bytes(wup->rows, ff), 256);
-    uint8_t *ws = (uint8_t *)llg_ws(d, o_sp + llg_sparse_ws_bytes(ff), &rc);
+    uint8_t *ws = (uint8_t *)llg_ws(d, o_ws + llg_fused_ws_bytes(wup->rows, ff), &rc);
     if (rc) return rc;
     if ((rc = llg_h2d(d, ws + o_a, a, (size_t)hd * 4))) return rc;
     if ((rc = llg_h2d(d, ws + o_x, x, (size_t)hd * 4))) return rc;
-    rc = llg_predict_enqueue(d, wup, wout, bias, (const float *)(ws + o_a), thr,
-                             (int32_t *)(ws + o_act), (int32_t *)(ws + o_n), nullptr, ws + o_ws);
-    if (rc) return rc;
-    rc = llg_sparse_enqueue(d, b->d, b->stride, b->fmt, nullptr, (const float *)(ws + o_x),
-                            (const int32_t *)(ws + o_act), (const int32_t *)(ws + o_n), ff, act,
-                            (float *)(ws + o_out), ws + o_sp);
+    rc = llg_fused_enqueue(d, wup, wout, bias, b, (const float *)(ws + o_a),
+                           (const float *)(ws + o_x), thr, act, (float *)(ws + o_out),
+                           active ? (int32_t *)(ws + o_act) : nullptr, (int32_t *)(ws + o_n),
+                           ws + o_ws);
     if (rc) return rc;
     int32_t n = 0;
     if ((rc = llg_d2h(d, out, ws + o_out, (size_t)hd * 4))) return rc;
@@ -395,8 +314,7 @@ int llg_hipd_ffn_dense(LlgHipDevice h, int64_t hu, int64_t hdn, const float *d_x
     if (!d_x || !d_out) return llg_set_error(d, LLG_E_ARG, "ffn_dense: null pointer");
     float *hid = (float *)llg_ws(d, (size_t)up->rows * 4, &rc);
     if (rc) return rc;
-    if ((rc = llg_matvec_enqueue(d, up, d_x, act, hid))) return rc;
-    return llg_matvec_enqueue(d, down, hid, -1, d_out);
+    return dense_enqueue(d, up, down, d_x, act, hid, d_out);
 }
 
 int llg_hip_ffn_dense(LlgHipDevice h, int64_t hu, int64_t hdn, const float *x, int act,
@@ -413,8 +331,8 @@ int llg_hip_ffn_dense(LlgHipDevice h, int64_t hu, int64_t hdn, const float *x, i
     uint8_t *ws = (uint8_t *)llg_ws(d, o_h + (size_t)ff * 4, &rc);
     if (rc) return rc;
     if ((rc = llg_h2d(d, ws, x, (size_t)hd * 4))) return rc;
-    if ((rc = llg_matvec_enqueue(d, up, (const float *)ws, act, (float *)(ws + o_h)))) return rc;
-    if ((rc = llg_matvec_enqueue(d, down, (const float *)(ws + o_h), -1, (float *)(ws + o_out))))
+    if ((rc = dense_enqueue(d, up, down, (const float *)ws, act, (float *)(ws + o_h),
+                            (float *)(ws + o_out))))
         return rc;
     if ((rc = llg_d2h(d, out, ws + o_out, (size_t)hd * 4))) return rc;
     return llg_sync_dev(d);

@@ -9,8 +9,16 @@ int llg_predict_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject
                         float *d_logits, uint8_t *ws);
 int llg_check_predictor(LlgDevice *d, int64_t hwup, int64_t hwout, int64_t hbias,
                         LlgObject **wup, LlgObject **wout, LlgObject **bias);
+// K1 of the predictor: hidden partials into ws; also zeroes the given targets.
+int llg_pred_hidden_enqueue(LlgDevice *d, LlgObject *wup, const float *d_a, uint8_t *ws,
+                            float **partial, unsigned long long **mask, int *psplit,
+                            float *zero_out, int zero_n, int32_t *zero_ctr, int n_ctr,
+                            int32_t *zero_extra);
+// Ascending active list from 64-bit tile masks (one workgroup).
+int llg_compact_enqueue(LlgDevice *d, const unsigned long long *mask, int n_tiles,
+                        int32_t *d_active, int32_t *d_n_active);
 
-// Sparse FFN over bundles (llg_ffn.hip).  Neuron n's bundle is at
+// Sparse FFN over bundles (llg_sparse.hip).  Neuron n's bundle is at
 // base + (slot_of ? slot_of[n] : n) * bstride.  max_active bounds *d_n_active.
 size_t llg_sparse_ws_bytes(int max_active);
 int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, const RowFmt &f,
@@ -20,3 +28,9 @@ int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, con
 
 // Dense quantized matvec y[rows] = act(W . x) (llg_ffn.hip); act < 0 = none.
 int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y);
+
+// Predictor-fused sparse FFN (ffnFlash path 2) (llg_sparse.hip).
+size_t llg_fused_ws_bytes(int rank, int ff);
+int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
+                      LlgObject *b, const float *d_a, const float *d_x, float thr, int act,
+                      float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws);

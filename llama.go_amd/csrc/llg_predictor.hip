@@ -1,98 +1,93 @@
 // llg_predictor.hip -- low-rank activation predictor and active-neuron
 // selection (inference/predictor.go:51-83).
 //
-//   hidden = ReLU(WUp[rank x h] . a)           k_pred_hidden (split over h)
-//   logit  = WOut[ff x rank] . hidden (+bias)   k_pred_logits (64-neuron tiles)
-//   active = {i : logit_i > thr}, ascending     wave ballot per tile -> 64-bit
-//                                               mask, then k_compact (one
-//                                               workgroup: popcount scan + write)
+//   hidden = ReLU(WUp[rank x h] . a)           k_pred_hidden: rank x 8 wavefronts,
+//                                               each one eighth of a row; partials
+//                                               are summed (and ReLU'd) by the reader
+//   logit  = WOut[ff x rank] . hidden (+bias)   k_pred_logits: 64-neuron tiles
+//   active = {i : logit_i > thr}, ascending     wavefront ballot per tile -> 64-bit
+//                                               mask, then k_compact (one workgroup:
+//                                               popcount scan + ordered writes)
 #include "llg_common.hpp"
 #include "llg_internal.hpp"
+#include "llg_pred_tile.hpp"
 
-#define PRED_SPLIT 4
-#define TILE 64
+#define PRED_SPLIT 8
+#define HID_LOADS 4  // float4 loads a lane issues together
 
-// partial[s * rank + r] = sum over the s-th quarter of row r of WUp . a
-__global__ void k_pred_hidden(const uint8_t *__restrict__ wup, long long stride, int h, int rank,
-                              const float *__restrict__ a, float *__restrict__ partial) {
-    const int r = blockIdx.x / PRED_SPLIT;
-    const int s = blockIdx.x % PRED_SPLIT;
-    const int lane = threadIdx.x;
+// partial[s * rank + r] = WUp[r, chunk s] . a[chunk s].  The grid also zeroes
+// `zero_out`, `zero_ctr[0..n_ctr)` and `*zero_extra` (each optional), which
+// the kernels that follow accumulate into.
+__global__ __launch_bounds__(256) void k_pred_hidden(const uint8_t *__restrict__ wup,
+                                                     long long stride, int h, int rank,
+                                                     const float *__restrict__ a,
+                                                     float *__restrict__ partial,
+                                                     float *__restrict__ zero_out, int zero_n,
+                                                     int32_t *__restrict__ zero_ctr, int n_ctr,
+                                                     int32_t *__restrict__ zero_extra) {
+    const int gtid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (zero_out)
+        for (int i = gtid; i < zero_n; i += gridDim.x * blockDim.x) zero_out[i] = 0.0f;
+    if (zero_ctr && gtid < n_ctr) zero_ctr[gtid] = 0;
+    if (zero_extra && gtid == 0) *zero_extra = 0;
+    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= rank * PRED_SPLIT) return;
+    const int r = wid / PRED_SPLIT;
+    const int s = wid % PRED_SPLIT;
+    const int lane = threadIdx.x & 63;
     const float *row = reinterpret_cast<const float *>(wup + (long long)r * stride);
-    const int chunk = (h + PRED_SPLIT - 1) / PRED_SPLIT;
-    const int c0 = s * chunk;
-    const int c1 = min(h, c0 + chunk);
     float acc = 0.0f;
-    if ((h & 3) == 0 && (chunk & 3) == 0) {
+    if ((h & 3) == 0) {
+        const int h4 = h >> 2;
+        const int chunk = (h4 + PRED_SPLIT - 1) / PRED_SPLIT;
+        const int c0 = s * chunk, c1 = min(h4, c0 + chunk);
         const float4 *r4 = reinterpret_cast<const float4 *>(row);
         const float4 *a4 = reinterpret_cast<const float4 *>(a);
-        for (int j = (c0 >> 2) + lane; j < (c1 >> 2); j += 64) {
-            const float4 w = r4[j], v = a4[j];
-            acc += w.x * v.x;
-            acc += w.y * v.y;
-            acc += w.z * v.z;
-            acc += w.w * v.w;
+        for (int j0 = c0 + lane; j0 < c1; j0 += 64 * HID_LOADS) {
+            float4 w[HID_LOADS], v[HID_LOADS];
+#pragma unroll
+            for (int i = 0; i < HID_LOADS; i++) {
+                const int j = j0 + 64 * i;
+                w[i] = j < c1 ? r4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+                v[i] = j < c1 ? a4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int i = 0; i < HID_LOADS; i++) {
+                acc += w[i].x * v[i].x;
+                acc += w[i].y * v[i].y;
+                acc += w[i].z * v[i].z;
+                acc += w[i].w * v[i].w;
+            }
         }
     } else {
+        const int chunk = (h + PRED_SPLIT - 1) / PRED_SPLIT;
+        const int c0 = s * chunk, c1 = min(h, c0 + chunk);
         for (int j = c0 + lane; j < c1; j += 64) acc += row[j] * a[j];
     }
     acc = llg_wave_sum(acc);
     if (lane == 0) partial[s * rank + r] = acc;
 }
 
-// One workgroup of 256 threads per 64-neuron tile.  Writes the tile's
-// 64-bit active mask (bit i <=> logit[tile*64+i] > thr) and, optionally, logits.
-__global__ void k_pred_logits(const uint8_t *__restrict__ wout, long long stride, int ff,
-                              int rank, const float *__restrict__ partial,
-                              const float *__restrict__ bias, float thr,
-                              float *__restrict__ logits, unsigned long long *__restrict__ mask) {
-    extern __shared__ float sh[];  // [rank] hidden, then [TILE] logits
+// One workgroup of 256 threads per 64-neuron tile: logits, optional output,
+// and the tile's 64-bit active mask (bit i <=> logit[tile*64+i] > thr).
+__global__ __launch_bounds__(256) void k_pred_logits(const uint8_t *__restrict__ wout,
+                                                     long long stride, int ff, int rank,
+                                                     const float *__restrict__ partial,
+                                                     const float *__restrict__ bias, float thr,
+                                                     float *__restrict__ logits,
+                                                     unsigned long long *__restrict__ mask) {
+    extern __shared__ float sh[];  // [rank] hidden (16-byte aligned), then [64] logits
     float *hid = sh;
-    float *lg = sh + rank;
-    for (int r = threadIdx.x; r < rank; r += blockDim.x) {
-        float v = 0.0f;
-        for (int s = 0; s < PRED_SPLIT; s++) v += partial[s * rank + r];
-        hid[r] = v < 0.0f ? 0.0f : v;  // predictor.go:61 ReLU
-    }
+    float *lg = sh + ((rank + 3) & ~3);
+    const int tile0 = blockIdx.x * 64;
+    WoutTile t;
+    load_wout_tile(t, wout, stride, ff, rank, tile0);
+    load_hidden<PRED_SPLIT>(hid, partial, rank);
     __syncthreads();
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int tile0 = blockIdx.x * TILE;
-    if ((rank & 3) == 0 && rank <= 256 && (64 % (rank >> 2)) == 0) {
-        // lanes_per_row float4 lanes per row, rows_per_pass rows per wave pass
-        const int lpr = rank >> 2;
-        const int rpp = 64 / lpr;
-        const int sub = lane / lpr;
-        const int c4 = lane % lpr;
-        const float4 hv = reinterpret_cast<const float4 *>(hid)[c4];
-        for (int base = wave * (TILE / 4); base < (wave + 1) * (TILE / 4); base += rpp) {
-            const int i = tile0 + base + sub;
-            float acc = 0.0f;
-            if (i < ff && base + sub < (wave + 1) * (TILE / 4)) {
-                const float4 w =
-                    reinterpret_cast<const float4 *>(wout + (long long)i * stride)[c4];
-                acc = w.x * hv.x;
-                acc += w.y * hv.y;
-                acc += w.z * hv.z;
-                acc += w.w * hv.w;
-            }
-            for (int o = lpr >> 1; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-            if (c4 == 0 && base + sub < (wave + 1) * (TILE / 4)) lg[base + sub] = acc;
-        }
-    } else {
-        for (int t = wave * (TILE / 4); t < (wave + 1) * (TILE / 4); t++) {
-            const int i = tile0 + t;
-            float acc = 0.0f;
-            if (i < ff) {
-                const float *w = reinterpret_cast<const float *>(wout + (long long)i * stride);
-                for (int c = lane; c < rank; c += 64) acc += w[c] * hid[c];
-            }
-            acc = llg_wave_sum(acc);
-            if (lane == 0) lg[t] = acc;
-        }
-    }
+    finish_logits(t, wout, stride, ff, rank, tile0, hid, lg);
     __syncthreads();
-    if (wave == 0) {
+    if ((threadIdx.x >> 6) == 0) {
+        const int lane = threadIdx.x & 63;
         const int i = tile0 + lane;
         bool on = false;
         if (i < ff) {
@@ -118,8 +113,9 @@ __global__ void k_select_mask(const float *__restrict__ logits, int ff, float th
 // Ascending compaction of the tile masks into the active list, by one
 // workgroup of 1024 threads: exclusive scan of popcounts, then each thread
 // writes the set bits of its tile in increasing bit order.
-__global__ void k_compact(const unsigned long long *__restrict__ mask, int n_tiles,
-                          int32_t *__restrict__ active, int32_t *__restrict__ n_active) {
+__global__ __launch_bounds__(1024) void k_compact(const unsigned long long *__restrict__ mask,
+                                                  int n_tiles, int32_t *__restrict__ active,
+                                                  int32_t *__restrict__ n_active) {
     __shared__ int wsum[16];
     __shared__ int carry_sh;
     const int lane = threadIdx.x & 63;
@@ -153,7 +149,7 @@ __global__ void k_compact(const unsigned long long *__restrict__ mask, int n_til
         if (threadIdx.x == 0) carry_sh = total;
         __syncthreads();
     }
-    if (threadIdx.x == 0) *n_active = carry_sh;
+    if (threadIdx.x == 0 && n_active) *n_active = carry_sh;
 }
 
 int llg_predict_ws_bytes(int rank, int ff) {
@@ -161,26 +157,48 @@ int llg_predict_ws_bytes(int rank, int ff) {
                  llg_align((long long)((ff + 63) / 64) * 8, 256));
 }
 
+int llg_pred_hidden_enqueue(LlgDevice *d, LlgObject *wup, const float *d_a, uint8_t *ws,
+                            float **partial, unsigned long long **mask, int *psplit,
+                            float *zero_out, int zero_n, int32_t *zero_ctr, int n_ctr,
+                            int32_t *zero_extra) {
+    const int h = wup->fmt.cols, rank = wup->rows;
+    *partial = reinterpret_cast<float *>(ws);
+    *mask = reinterpret_cast<unsigned long long *>(
+        ws + llg_align((long long)PRED_SPLIT * rank * 4, 256));
+    *psplit = PRED_SPLIT;
+    const int grid = (rank * PRED_SPLIT + 3) / 4;
+    hipLaunchKernelGGL(k_pred_hidden, dim3(grid), dim3(256), 0, llg_dev_stream(d), wup->d,
+                       wup->stride, h, rank, d_a, *partial, zero_out, zero_n, zero_ctr, n_ctr,
+                       zero_extra);
+    LLG_LAUNCH_CHECK(d, "pred_hidden");
+    return 0;
+}
+
+int llg_compact_enqueue(LlgDevice *d, const unsigned long long *mask, int n_tiles,
+                        int32_t *d_active, int32_t *d_n_active) {
+    hipLaunchKernelGGL(k_compact, dim3(1), dim3(1024), 0, llg_dev_stream(d), mask, n_tiles,
+                       d_active, d_n_active);
+    LLG_LAUNCH_CHECK(d, "compact");
+    return 0;
+}
+
 int llg_predict_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
                         const float *d_a, float thr, int32_t *d_active, int32_t *d_n_active,
                         float *d_logits, uint8_t *ws) {
-    const int h = wup->fmt.cols, rank = wup->rows, ff = wout->rows;
-    float *partial = reinterpret_cast<float *>(ws);
-    unsigned long long *mask = reinterpret_cast<unsigned long long *>(
-        ws + llg_align((long long)PRED_SPLIT * rank * 4, 256));
-    hipStream_t st = llg_dev_stream(d);
-    hipLaunchKernelGGL(k_pred_hidden, dim3(rank * PRED_SPLIT), dim3(64), 0, st, wup->d,
-                       wup->stride, h, rank, d_a, partial);
-    LLG_LAUNCH_CHECK(d, "pred_hidden");
-    const int n_tiles = (ff + TILE - 1) / TILE;
+    const int ff = wout->rows, rank = wup->rows;
+    float *partial;
+    unsigned long long *mask;
+    int psplit;
+    int rc = llg_pred_hidden_enqueue(d, wup, d_a, ws, &partial, &mask, &psplit, nullptr, 0,
+                                     nullptr, 0, nullptr);
+    if (rc) return rc;
+    const int n_tiles = (ff + 63) / 64;
     const float *d_bias = bias ? reinterpret_cast<const float *>(bias->d) : nullptr;
-    hipLaunchKernelGGL(k_pred_logits, dim3(n_tiles), dim3(256), (rank + TILE) * sizeof(float),
-                       st, wout->d, wout->stride, ff, rank, partial, d_bias, thr, d_logits, mask);
+    const size_t lds = (size_t)(((rank + 3) & ~3) + 64) * sizeof(float);
+    hipLaunchKernelGGL(k_pred_logits, dim3(n_tiles), dim3(256), lds, llg_dev_stream(d), wout->d,
+                       wout->stride, ff, rank, partial, d_bias, thr, d_logits, mask);
     LLG_LAUNCH_CHECK(d, "pred_logits");
-    hipLaunchKernelGGL(k_compact, dim3(1), dim3(1024), 0, st, mask, n_tiles, d_active,
-                       d_n_active);
-    LLG_LAUNCH_CHECK(d, "compact");
-    return 0;
+    return llg_compact_enqueue(d, mask, n_tiles, d_active, d_n_active);
 }
 
 static int check_predictor(LlgDevice *d, int64_t hwup, int64_t hwout, int64_t hbias,
@@ -197,9 +215,7 @@ static int check_predictor(LlgDevice *d, int64_t hwup, int64_t hwout, int64_t hb
     if ((*wout)->fmt.cols != (*wup)->rows)
         return llg_set_error(d, LLG_E_ARG, "predictor: W_out cols %d != rank %d",
                              (*wout)->fmt.cols, (*wup)->rows);
-    if (*bias && (*bias)->fmt.cols * (*bias)->rows != (*wout)->rows)
-        return llg_set_error(d, LLG_E_ARG, "predictor: bias length != ff");
-    if (*bias && (*bias)->rows != 1)
+    if (*bias && ((*bias)->rows != 1 || (*bias)->fmt.cols != (*wout)->rows))
         return llg_set_error(d, LLG_E_ARG, "predictor: bias must be a [1 x ff] matrix");
     return 0;
 }
@@ -268,14 +284,13 @@ int llg_hip_select(LlgHipDevice h, const float *logits, int ff, float thr, int32
     uint8_t *ws = (uint8_t *)llg_ws(d, o_m + (size_t)n_tiles * 8, &rc);
     if (rc) return rc;
     if ((rc = llg_h2d(d, ws, logits, (size_t)ff * 4))) return rc;
-    hipStream_t st = llg_dev_stream(d);
     unsigned long long *mask = reinterpret_cast<unsigned long long *>(ws + o_m);
-    hipLaunchKernelGGL(k_select_mask, dim3((ff + 255) / 256), dim3(256), 0, st,
+    hipLaunchKernelGGL(k_select_mask, dim3((ff + 255) / 256), dim3(256), 0, llg_dev_stream(d),
                        (const float *)ws, ff, thr, mask);
     LLG_LAUNCH_CHECK(d, "select_mask");
-    hipLaunchKernelGGL(k_compact, dim3(1), dim3(1024), 0, st, mask, n_tiles,
-                       (int32_t *)(ws + o_act), (int32_t *)(ws + o_n));
-    LLG_LAUNCH_CHECK(d, "compact");
+    if ((rc = llg_compact_enqueue(d, mask, n_tiles, (int32_t *)(ws + o_act),
+                                  (int32_t *)(ws + o_n))))
+        return rc;
     int32_t n = 0;
     if ((rc = llg_d2h(d, &n, ws + o_n, 4))) return rc;
     if ((rc = llg_sync_dev(d))) return rc;

@@ -1,0 +1,391 @@
+// llg_sparse.hip -- gathered sparse FFN over row-column bundles
+// (inference/ffn_flash.go:195-299, window.go:143-180).
+//
+// Two ways in:
+//
+//  A. predictor-fused step (ffnFlash path 2, ffn_flash.go:225-231), 3 launches:
+//     K1 k_pred_hidden (llg_predictor.hip): hidden partials; zeroes out/counters
+//     K2 k_tile_up: one workgroup per 64-neuron tile: logits from WOut rows,
+//        strict '>' against the threshold via a wavefront ballot, then the up
+//        dot product of each of the tile's active neurons, u = act(up . x);
+//        nonzero u go to the tile's own 64 pair slots (an LDS counter orders
+//        them), so no two workgroups touch one address
+//     K3 k_sparse_down over the tiles' pairs
+//  B. explicit active list (ffnSparseLoad, NeuronCache.FFNForward), 2 launches:
+//     k_list_up: one wavefront per listed neuron, pair j = (row, u_j)
+//     K3 k_sparse_down
+//
+// x is staged once per workgroup in LDS with a 36-float stride per 32-float
+// block, so the 16-byte reads of 16 consecutive lanes (one block each) hit
+// 64 distinct banks.  Every lane issues the loads of all its blocks before it
+// uses any of them.
+//
+// k_sparse_down: workgroup (slice s of 8 blocks = 256 outputs, pair group g);
+// the four wavefronts split the group's pairs, 8 pairs per wavefront pass
+// (lane = pair sub-index * 8 + block); u == 0 rows are skipped as at
+// ffn_flash.go:290; the per-slice sums are reduced across lanes and waves and
+// added to out with one fp32 atomic per output.  blockIdx -> (s, g) keeps all
+// slices of a group on one XCD (workgroups go round-robin over the 8 XCDs).
+#include "llg_common.hpp"
+#include "llg_internal.hpp"
+#include "llg_pred_tile.hpp"
+
+#define XS_STRIDE 36      // floats per staged 32-float x block (bank-conflict-free)
+#define DN_SLICE 8        // blocks per down slice
+#define BATCH 4           // blocks whose loads a lane issues together
+#define PRED_SPLIT_N 8    // partials per hidden unit written by k_pred_hidden
+
+__device__ __forceinline__ void stage_x(float *xs, const float *__restrict__ x, int nb) {
+    llg_stage_x<XS_STRIDE>(xs, x, nb);
+}
+
+// Up-row dot product of one wavefront: lane l owns blocks l, l+64, ...; the
+// bytes of BATCH of them are loaded before any is used.
+template <int T>
+__device__ __forceinline__ float row_dot(const uint8_t *__restrict__ row, const RowFmt &f,
+                                         const float *xs) {
+    const int lane = threadIdx.x & 63;
+    float s = 0.0f;
+    for (int b0 = lane; b0 < f.nb; b0 += 64 * BATCH) {
+        BlockRaw<T> r[BATCH];
+#pragma unroll
+        for (int i = 0; i < BATCH; i++)
+            if (b0 + 64 * i < f.nb) llg_block_load<T>(r[i], row, f, b0 + 64 * i);
+#pragma unroll
+        for (int i = 0; i < BATCH; i++) {
+            const int b = b0 + 64 * i;
+            if (b < f.nb)
+                s += llg_raw_dot<T>(r[i], reinterpret_cast<const float4 *>(xs + b * XS_STRIDE));
+        }
+    }
+    return llg_wave_sum(s);
+}
+
+// B. explicit list: pair j = (row of active[j], act(up . x)); also zeroes out.
+template <int T>
+__global__ __launch_bounds__(256) void k_list_up(const uint8_t *__restrict__ base,
+                                                 long long bstride, RowFmt f,
+                                                 const int32_t *__restrict__ slot_of,
+                                                 const float *__restrict__ x,
+                                                 const int32_t *__restrict__ active,
+                                                 const int32_t *__restrict__ n_active_p, int act,
+                                                 int2 *__restrict__ pairs,
+                                                 float *__restrict__ out) {
+    extern __shared__ float xs[];
+    const int n_active = *n_active_p;
+    const int gtid = blockIdx.x * blockDim.x + threadIdx.x;
+    for (int i = gtid; i < f.cols; i += gridDim.x * blockDim.x) out[i] = 0.0f;
+    const int first = blockIdx.x * 4;
+    if (first >= n_active) return;  // whole workgroup idle: skip the x staging
+    stage_x(xs, x, f.nb);
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    for (int j = first + (threadIdx.x >> 6); j < n_active; j += gridDim.x * 4) {
+        const int n = active[j];
+        const int row = slot_of ? slot_of[n] : n;
+        float u = 0.0f;  // a non-resident row keeps activation 0 (window.go:150-152)
+        if (row >= 0) u = llg_act(act, row_dot<T>(base + (long long)row * bstride, f, xs));
+        if (lane == 0) pairs[j] = make_int2(row, __float_as_int(u));
+    }
+}
+
+// A. predictor-fused tile kernel.  Tile t writes its nonzero (row, u) pairs
+// to pairs[t*64 + k], k < tile_cnt[t]: fixed slots, so no global counter.
+template <int T>
+__global__ __launch_bounds__(256) void k_tile_up(
+    const uint8_t *__restrict__ wout, long long wstride, int ff, int rank,
+    const float *__restrict__ partial, const float *__restrict__ bias, float thr,
+    const uint8_t *__restrict__ base, long long bstride, RowFmt f, const float *__restrict__ x,
+    int act, unsigned long long *__restrict__ mask, int2 *__restrict__ pairs,
+    int32_t *__restrict__ tile_cnt) {
+    extern __shared__ float sh[];
+    float *xs = sh;                                     // nb * XS_STRIDE
+    float *hid = xs + f.nb * XS_STRIDE;                 // rank (16-byte aligned)
+    float *lg = hid + ((rank + 3) & ~3);                // 64
+    int *tl = reinterpret_cast<int *>(lg + 64);         // 64 tile-local indices, count, nnz
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int tile0 = blockIdx.x * 64;
+    WoutTile t;
+    load_wout_tile(t, wout, wstride, ff, rank, tile0);  // loads first, used after the barrier
+    stage_x(xs, x, f.nb);
+    load_hidden<PRED_SPLIT_N>(hid, partial, rank);
+    __syncthreads();
+    finish_logits(t, wout, wstride, ff, rank, tile0, hid, lg);
+    __syncthreads();
+    if (wave == 0) {
+        const int i = tile0 + lane;
+        bool on = false;
+        if (i < ff) {
+            float v = lg[lane];
+            if (bias) v += bias[i];  // predictor.go:69-73
+            on = v > thr;            // predictor.go:78
+        }
+        const unsigned long long m = __ballot(on);
+        const int before = __popcll(m & ((1ull << lane) - 1ull));
+        if (on) tl[before] = lane;
+        if (lane == 0) {
+            tl[64] = __popcll(m);
+            tl[65] = 0;
+            if (mask) mask[blockIdx.x] = m;
+        }
+    }
+    __syncthreads();
+    const int cnt = tl[64];
+    for (int k = wave; k < cnt; k += 4) {
+        const int n = tile0 + tl[k];
+        const float u = llg_act(act, row_dot<T>(base + (long long)n * bstride, f, xs));
+        if (lane == 0 && u != 0.0f) {  // ffn_flash.go:290 skips zero activations
+            const int pos = atomicAdd(&tl[65], 1);  // LDS atomic, tile-local slot
+            pairs[blockIdx.x * 64 + pos] = make_int2(n, __float_as_int(u));
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) tile_cnt[blockIdx.x] = tl[65];
+}
+
+// Pairs come either as a plain list pairs[0..*count) (TILED = false) or in
+// per-tile slots pairs[t*64 + k], k < tile_cnt[t] (TILED = true); for the
+// latter, group g owns tiles [g*tg, (g+1)*tg) and its workgroups enumerate
+// them through a prefix sum of the counts.  With TILED, workgroup 0 also
+// writes the number of active neurons (popcounts of the tile masks).
+template <int T, bool TILED>
+__global__ __launch_bounds__(256) void k_sparse_down(
+    const uint8_t *__restrict__ base, long long bstride, RowFmt f, const int2 *__restrict__ pairs,
+    const int32_t *__restrict__ count_p, const int32_t *__restrict__ tile_cnt, int n_tiles,
+    const unsigned long long *__restrict__ mask, int32_t *__restrict__ n_active_out,
+    int n_slices, int n_groups, float *__restrict__ out) {
+    __shared__ float red[4][DN_SLICE * 32];
+    __shared__ int pref[65];
+    const int id = blockIdx.x;
+    const int xcd = id & 7;
+    const int k = id >> 3;
+    const int g = xcd + 8 * (k / n_slices);
+    const int s = k % n_slices;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int j0, j1, tg = 0, t0 = 0;
+    if (TILED) {
+        tg = (n_tiles + n_groups - 1) / n_groups;  // <= 64 (checked on the host)
+        t0 = g * tg;
+        if (wave == 0) {
+            const int c = (lane < tg && t0 + lane < n_tiles) ? tile_cnt[t0 + lane] : 0;
+            int incl = c;
+            for (int o = 1; o < 64; o <<= 1) {
+                const int v = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += v;
+            }
+            pref[lane + 1] = incl;
+            if (lane == 0) pref[0] = 0;
+        }
+        if (id == 0 && wave == 1 && n_active_out) {
+            int c = 0;
+            for (int i = lane; i < n_tiles; i += 64) c += __popcll(mask[i]);
+            for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+            if (lane == 0) *n_active_out = c;
+        }
+        __syncthreads();
+        j0 = 0;
+        j1 = pref[64];
+    } else {
+        const int count = *count_p;
+        const int chunk = (count + n_groups - 1) / n_groups;
+        j0 = g * chunk;
+        j1 = min(count, j0 + chunk);
+    }
+    if (j0 >= j1) return;  // uniform over the workgroup: nothing to add
+    const int bl = lane & 7;
+    const int sub = lane >> 3;
+    const int b = s * DN_SLICE + bl;
+    float acc[32];
+#pragma unroll
+    for (int e = 0; e < 32; e++) acc[e] = 0.0f;
+    if (b < f.nb) {
+        for (int j = j0 + wave * 8 + sub; j < j1; j += 64) {
+            // two pairs per pass: both rows' bytes are requested before either is used
+            int2 p0, p1 = make_int2(0, 0);
+            if (TILED) {
+                int t = 0;
+                while (pref[t + 1] <= j) t++;
+                p0 = pairs[(t0 + t) * 64 + (j - pref[t])];
+                if (j + 32 < j1) {
+                    const int jj = j + 32;
+                    while (pref[t + 1] <= jj) t++;
+                    p1 = pairs[(t0 + t) * 64 + (jj - pref[t])];
+                }
+            } else {
+                p0 = pairs[j];
+                if (j + 32 < j1) p1 = pairs[j + 32];
+            }
+            const float u0 = __int_as_float(p0.y), u1 = __int_as_float(p1.y);
+            BlockRaw<T> r0, r1;
+            if (u0 != 0.0f) llg_block_load<T>(r0, base + (long long)p0.x * bstride + f.stride, f, b);
+            if (u1 != 0.0f) llg_block_load<T>(r1, base + (long long)p1.x * bstride + f.stride, f, b);
+            if (u0 != 0.0f) llg_raw_axpy<T>(r0, u0, acc);  // ffn_flash.go:290 skips u == 0
+            if (u1 != 0.0f) llg_raw_axpy<T>(r1, u1, acc);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 32; e++) {  // sum over the 8 pair sub-lanes sharing block bl
+        float v = acc[e];
+        v += llg_dpp<0x128>(v);  // row_ror:8 pairs lanes l and l+8 of each row
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 32, 64);
+        acc[e] = v;
+    }
+    if (sub == 0) {
+#pragma unroll
+        for (int e = 0; e < 32; e++) red[wave][bl * 32 + e] = acc[e];
+    }
+    __syncthreads();
+    const int t = threadIdx.x;
+    const int o = s * DN_SLICE * 32 + t;
+    if (o < f.cols) unsafeAtomicAdd(out + o, red[0][t] + red[1][t] + red[2][t] + red[3][t]);
+}
+
+// ---------------------------------------------------------------------------
+// Host-side enqueue helpers
+// ---------------------------------------------------------------------------
+size_t llg_sparse_ws_bytes(int max_active) {
+    return (size_t)llg_align((long long)(max_active > 0 ? max_active : 1) * 8, 256) + 256;
+}
+
+static size_t xs_bytes(const RowFmt &f) { return (size_t)f.nb * XS_STRIDE * 4; }
+
+// 8 or 16 pair groups (a multiple of the 8 XCDs): enough workgroups to spread
+// the rows, few enough that the atomics per output stay small.
+static int down_groups(int max_pairs) { return max_pairs > 256 ? 16 : 8; }
+
+template <int T>
+static void launch_down(hipStream_t st, const uint8_t *base, long long bstride, const RowFmt &f,
+                        const int2 *pairs, const int32_t *count, int max_pairs, float *out) {
+    const int n_slices = (f.nb + DN_SLICE - 1) / DN_SLICE;
+    const int n_groups = down_groups(max_pairs);
+    hipLaunchKernelGGL((k_sparse_down<T, false>), dim3(n_slices * n_groups), dim3(256), 0, st,
+                       base, bstride, f, pairs, count, (const int32_t *)nullptr, 0,
+                       (const unsigned long long *)nullptr, (int32_t *)nullptr, n_slices,
+                       n_groups, out);
+}
+
+template <int T>
+static void launch_list(hipStream_t st, const uint8_t *base, long long bstride, const RowFmt &f,
+                        const int32_t *slot_of, const float *x, const int32_t *active,
+                        const int32_t *n_active, int max_active, int act, float *out,
+                        int2 *pairs) {
+    int grid = (max_active + 3) / 4;
+    if (grid < 1) grid = 1;
+    if (grid > 2048) grid = 2048;
+    hipLaunchKernelGGL(k_list_up<T>, dim3(grid), dim3(256), xs_bytes(f), st, base, bstride, f,
+                       slot_of, x, active, n_active, act, pairs, out);
+    launch_down<T>(st, base, bstride, f, pairs, n_active, max_active, out);
+}
+
+int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, const RowFmt &f,
+                       const int32_t *slot_of, const float *d_x, const int32_t *d_active,
+                       const int32_t *d_n_active, int max_active, int act, float *d_out,
+                       uint8_t *ws) {
+    if (xs_bytes(f) > 64 * 1024)
+        return llg_set_error(d, LLG_E_ARG, "sparse ffn: hidden size %d too large", f.cols);
+    hipStream_t st = llg_dev_stream(d);
+    int2 *pairs = reinterpret_cast<int2 *>(ws);
+    switch (f.type) {
+    case LLG_TYPE_Q4_0:
+        launch_list<LLG_TYPE_Q4_0>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
+                                   max_active, act, d_out, pairs);
+        break;
+    case LLG_TYPE_Q8_0:
+        launch_list<LLG_TYPE_Q8_0>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
+                                   max_active, act, d_out, pairs);
+        break;
+    case LLG_TYPE_F16:
+        launch_list<LLG_TYPE_F16>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
+                                  max_active, act, d_out, pairs);
+        break;
+    case LLG_TYPE_F32:
+        launch_list<LLG_TYPE_F32>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
+                                  max_active, act, d_out, pairs);
+        break;
+    default:
+        return llg_set_error(d, LLG_E_TYPE, "sparse ffn: unsupported type %d", f.type);
+    }
+    LLG_LAUNCH_CHECK(d, "sparse ffn");
+    return 0;
+}
+
+size_t llg_fused_ws_bytes(int rank, int ff) {
+    const long long n_tiles = (ff + 63) / 64;
+    return (size_t)llg_predict_ws_bytes(rank, ff) + (size_t)llg_align(n_tiles * 64 * 8, 256) +
+           (size_t)llg_align(n_tiles * 4, 256);
+}
+
+template <int T>
+static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial, const float *bias,
+                         float thr, LlgObject *b, const float *x, int act,
+                         unsigned long long *mask, int2 *pairs, int32_t *tile_cnt,
+                         int32_t *n_active, float *out) {
+    const int ff = wout->rows, rank = wout->fmt.cols;
+    const int n_tiles = (ff + 63) / 64;
+    const RowFmt &f = b->fmt;
+    const size_t lds = xs_bytes(f) + (size_t)(((rank + 3) & ~3) + 64 + 66) * 4;
+    hipLaunchKernelGGL(k_tile_up<T>, dim3(n_tiles), dim3(256), lds, st, wout->d, wout->stride, ff,
+                       rank, partial, bias, thr, b->d, b->stride, f, x, act, mask, pairs,
+                       tile_cnt);
+    const int n_slices = (f.nb + DN_SLICE - 1) / DN_SLICE;
+    const int n_groups = down_groups(ff);
+    hipLaunchKernelGGL((k_sparse_down<T, true>), dim3(n_slices * n_groups), dim3(256), 0, st,
+                       b->d, b->stride, f, pairs, (const int32_t *)nullptr, tile_cnt, n_tiles,
+                       mask, n_active, n_slices, n_groups, out);
+}
+
+// ffnFlash path 2 on the device: K1 + K2 + K3, plus the ascending active list
+// through k_compact when d_active is given.  d_n_active (optional) receives
+// the number of active neurons.
+int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
+                      LlgObject *b, const float *d_a, const float *d_x, float thr, int act,
+                      float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws) {
+    const RowFmt &f = b->fmt;
+    const int ff = wout->rows, rank = wup->rows;
+    const int n_tiles = (ff + 63) / 64;
+    if (xs_bytes(f) + (size_t)(rank + 136) * 4 > 64 * 1024)
+        return llg_set_error(d, LLG_E_ARG, "predict_sparse: hidden size %d too large", f.cols);
+    if ((n_tiles + down_groups(ff) - 1) / down_groups(ff) > 64)
+        return llg_set_error(d, LLG_E_ARG, "predict_sparse: d_ff %d too large", ff);
+    hipStream_t st = llg_dev_stream(d);
+    int2 *pairs = reinterpret_cast<int2 *>(ws + llg_predict_ws_bytes(rank, ff));
+    int32_t *tile_cnt = reinterpret_cast<int32_t *>(ws + llg_predict_ws_bytes(rank, ff) +
+                                                    llg_align((long long)n_tiles * 64 * 8, 256));
+    float *partial;
+    unsigned long long *mask;
+    int psplit;
+    // K1 also zeroes out, the atomic target of K3
+    int rc = llg_pred_hidden_enqueue(d, wup, d_a, ws, &partial, &mask, &psplit, d_out, f.cols,
+                                     nullptr, 0, nullptr);
+    if (rc) return rc;
+    if (psplit != PRED_SPLIT_N)
+        return llg_set_error(d, LLG_E_ARG, "predict_sparse: hidden split %d != %d", psplit,
+                             PRED_SPLIT_N);
+    const float *d_bias = bias ? reinterpret_cast<const float *>(bias->d) : nullptr;
+    switch (f.type) {
+    case LLG_TYPE_Q4_0:
+        launch_fused<LLG_TYPE_Q4_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, pairs,
+                                    tile_cnt, d_n_active, d_out);
+        break;
+    case LLG_TYPE_Q8_0:
+        launch_fused<LLG_TYPE_Q8_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, pairs,
+                                    tile_cnt, d_n_active, d_out);
+        break;
+    case LLG_TYPE_F16:
+        launch_fused<LLG_TYPE_F16>(st, wout, partial, d_bias, thr, b, d_x, act, mask, pairs,
+                                   tile_cnt, d_n_active, d_out);
+        break;
+    case LLG_TYPE_F32:
+        launch_fused<LLG_TYPE_F32>(st, wout, partial, d_bias, thr, b, d_x, act, mask, pairs,
+                                   tile_cnt, d_n_active, d_out);
+        break;
+    default:
+        return llg_set_error(d, LLG_E_TYPE, "predict_sparse: unsupported type %d", f.type);
+    }
+    LLG_LAUNCH_CHECK(d, "predict_sparse");
+    if (d_active) return llg_compact_enqueue(d, mask, n_tiles, d_active, nullptr);
+    return 0;
+}
