@@ -369,48 +369,54 @@ __device__ __forceinline__ void llg_block_load<LLG_TYPE_F32>(BlockRaw<LLG_TYPE_F
     for (int i = 0; i < 8; i++) r.q[i] = p[i];
 }
 
-// dot(dequant(block), x[32]) from loaded bytes.
+// dot(dequant(block), x[32]) from loaded bytes; xsum = sum of the 32 x values.
+// Q4_0 sums q * x over the raw nibbles q in [0, 15] (v_cvt_f32_ubyte on
+// nibble-masked words) and subtracts 8 * xsum once; Q8_0 flips the sign bit
+// of every byte (q + 128 in [0, 255]) and subtracts 128 * xsum.  F16/F32
+// ignore xsum.
 template <int T>
-__device__ __forceinline__ float llg_raw_dot(const BlockRaw<T> &r, const float4 *x4);
+__device__ __forceinline__ float llg_raw_dot(const BlockRaw<T> &r, const float4 *x4, float xsum);
 template <>
 __device__ __forceinline__ float llg_raw_dot<LLG_TYPE_Q4_0>(const BlockRaw<LLG_TYPE_Q4_0> &r,
-                                                             const float4 *x4) {
+                                                             const float4 *x4, float xsum) {
     const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const float4 xa = x4[2 * i], xb = x4[2 * i + 1];
-        const uint32_t v = w[i];
-        s += (float)((int)((v >> 0) & 15) - 8) * xa.x;
-        s += (float)((int)((v >> 4) & 15) - 8) * xa.y;
-        s += (float)((int)((v >> 8) & 15) - 8) * xa.z;
-        s += (float)((int)((v >> 12) & 15) - 8) * xa.w;
-        s += (float)((int)((v >> 16) & 15) - 8) * xb.x;
-        s += (float)((int)((v >> 20) & 15) - 8) * xb.y;
-        s += (float)((int)((v >> 24) & 15) - 8) * xb.z;
-        s += (float)((int)((v >> 28) & 15) - 8) * xb.w;
+        const uint32_t lo = w[i] & 0x0F0F0F0Fu;         // elements 8i, 8i+2, 8i+4, 8i+6
+        const uint32_t hi = (w[i] >> 4) & 0x0F0F0F0Fu;  // elements 8i+1, 8i+3, 8i+5, 8i+7
+        s += (float)(lo & 0xFF) * xa.x;
+        s += (float)(hi & 0xFF) * xa.y;
+        s += (float)((lo >> 8) & 0xFF) * xa.z;
+        s += (float)((hi >> 8) & 0xFF) * xa.w;
+        s += (float)((lo >> 16) & 0xFF) * xb.x;
+        s += (float)((hi >> 16) & 0xFF) * xb.y;
+        s += (float)(lo >> 24) * xb.z;
+        s += (float)(hi >> 24) * xb.w;
     }
-    return s * llg_f16(r.d);
+    return (s - 8.0f * xsum) * llg_f16(r.d);
 }
 template <>
 __device__ __forceinline__ float llg_raw_dot<LLG_TYPE_Q8_0>(const BlockRaw<LLG_TYPE_Q8_0> &r,
-                                                             const float4 *x4) {
+                                                             const float4 *x4, float xsum) {
     const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const float4 xv = x4[i];
-        const uint32_t v = w[i];
-        s += (float)(int8_t)(v & 0xFF) * xv.x;
-        s += (float)(int8_t)((v >> 8) & 0xFF) * xv.y;
-        s += (float)(int8_t)((v >> 16) & 0xFF) * xv.z;
-        s += (float)(int8_t)(v >> 24) * xv.w;
+        const uint32_t v = w[i] ^ 0x80808080u;  // byte = q + 128
+        s += (float)(v & 0xFF) * xv.x;
+        s += (float)((v >> 8) & 0xFF) * xv.y;
+        s += (float)((v >> 16) & 0xFF) * xv.z;
+        s += (float)(v >> 24) * xv.w;
     }
-    return s * llg_f16(r.d);
+    return (s - 128.0f * xsum) * llg_f16(r.d);
 }
 template <>
 __device__ __forceinline__ float llg_raw_dot<LLG_TYPE_F16>(const BlockRaw<LLG_TYPE_F16> &r,
-                                                            const float4 *x4) {
+                                                            const float4 *x4, float xsum) {
+    (void)xsum;
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -429,7 +435,8 @@ __device__ __forceinline__ float llg_raw_dot<LLG_TYPE_F16>(const BlockRaw<LLG_TY
 }
 template <>
 __device__ __forceinline__ float llg_raw_dot<LLG_TYPE_F32>(const BlockRaw<LLG_TYPE_F32> &r,
-                                                            const float4 *x4) {
+                                                            const float4 *x4, float xsum) {
+    (void)xsum;
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -442,33 +449,46 @@ __device__ __forceinline__ float llg_raw_dot<LLG_TYPE_F32>(const BlockRaw<LLG_TY
     return s;
 }
 
-// acc[0..31] += u * dequant(block) from loaded bytes.
+// acc[0..31] += u * dequant(block) from loaded bytes, with the block's offset
+// folded into *corr: for Q4_0 acc gets u*d*q (q in [0, 15]) and corr 8*u*d;
+// for Q8_0 acc gets u*d*(q + 128) and corr 128*u*d.  The caller subtracts
+// corr from every acc element once, after its last block.
 template <int T>
-__device__ __forceinline__ void llg_raw_axpy(const BlockRaw<T> &r, float u, float *acc);
+__device__ __forceinline__ void llg_raw_axpy(const BlockRaw<T> &r, float u, float *acc,
+                                             float &corr);
 template <>
 __device__ __forceinline__ void llg_raw_axpy<LLG_TYPE_Q4_0>(const BlockRaw<LLG_TYPE_Q4_0> &r,
-                                                             float u, float *acc) {
+                                                             float u, float *acc, float &corr) {
     const float s = u * llg_f16(r.d);
+    corr += 8.0f * s;
     const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 4; i++) {
+        const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
-        for (int p = 0; p < 8; p++)
-            acc[8 * i + p] += s * (float)((int)((w[i] >> (4 * p)) & 15) - 8);
+        for (int k = 0; k < 4; k++) {
+            acc[8 * i + 2 * k] += s * (float)((lo >> (8 * k)) & 0xFF);
+            acc[8 * i + 2 * k + 1] += s * (float)((hi >> (8 * k)) & 0xFF);
+        }
+    }
 }
 template <>
 __device__ __forceinline__ void llg_raw_axpy<LLG_TYPE_Q8_0>(const BlockRaw<LLG_TYPE_Q8_0> &r,
-                                                             float u, float *acc) {
+                                                             float u, float *acc, float &corr) {
     const float s = u * llg_f16(r.d);
+    corr += 128.0f * s;
     const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (int i = 0; i < 8; i++) {
+        const uint32_t v = w[i] ^ 0x80808080u;
 #pragma unroll
-        for (int p = 0; p < 4; p++) acc[4 * i + p] += s * (float)(int8_t)((w[i] >> (8 * p)) & 0xFF);
+        for (int k = 0; k < 4; k++) acc[4 * i + k] += s * (float)((v >> (8 * k)) & 0xFF);
+    }
 }
 template <>
 __device__ __forceinline__ void llg_raw_axpy<LLG_TYPE_F16>(const BlockRaw<LLG_TYPE_F16> &r,
-                                                            float u, float *acc) {
+                                                            float u, float *acc, float &corr) {
+    (void)corr;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const uint32_t w[4] = {r.q[i].x, r.q[i].y, r.q[i].z, r.q[i].w};
@@ -481,7 +501,8 @@ __device__ __forceinline__ void llg_raw_axpy<LLG_TYPE_F16>(const BlockRaw<LLG_TY
 }
 template <>
 __device__ __forceinline__ void llg_raw_axpy<LLG_TYPE_F32>(const BlockRaw<LLG_TYPE_F32> &r,
-                                                            float u, float *acc) {
+                                                            float u, float *acc, float &corr) {
+    (void)corr;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         acc[4 * i + 0] += u * r.q[i].x;
@@ -491,24 +512,35 @@ __device__ __forceinline__ void llg_raw_axpy<LLG_TYPE_F32>(const BlockRaw<LLG_TY
     }
 }
 
-// Stage x[nb*32] into LDS with XS floats per 32-float block (XS = 36 keeps
-// the 16-byte reads of 16 consecutive lanes on 64 distinct banks).  Each
-// thread issues up to 8 of its float4 loads before storing any.
+// Stage x[nb*32] into LDS, XS (>= 33) floats per block: the block's 32 values
+// then, at offset 32, their sum (the xsum of llg_raw_dot).  Loads are
+// coalesced float4s, 8 consecutive lanes per block, up to 8 per thread issued
+// before any store; each block's sum is reduced over its 8 lanes with DPP
+// (quad steps, then row_half_mirror = 0x141 pairs the two quads of 8 lanes).
+// The loop bound is uniform per wavefront, so every DPP sees full lanes.
 template <int XS>
-__device__ __forceinline__ void llg_stage_x(float *xs, const float *__restrict__ x, int nb) {
+__device__ __forceinline__ void llg_stage_x_sum(float *xs, const float *__restrict__ x, int nb) {
+    static_assert(XS >= 33, "room for the block sum");
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
     const int n4 = nb * 8;
-    for (int i0 = threadIdx.x; i0 < n4; i0 += 8 * blockDim.x) {
+    const int lane = threadIdx.x & 63;
+    for (int base = threadIdx.x - lane; base < n4; base += 8 * blockDim.x) {
         float4 v[8];
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const int i = i0 + k * blockDim.x;
+            const int i = base + k * blockDim.x + lane;
             v[k] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
         for (int k = 0; k < 8; k++) {
-            const int i = i0 + k * blockDim.x;
-            if (i < n4) reinterpret_cast<float4 *>(xs + (i >> 3) * XS)[i & 7] = v[k];
+            const int i = base + k * blockDim.x + lane;
+            float sum = (v[k].x + v[k].y) + (v[k].z + v[k].w);
+            sum = llg_quad_sum(sum);
+            sum += llg_dpp<0x141>(sum);
+            if (i < n4) {
+                reinterpret_cast<float4 *>(xs + (i >> 3) * XS)[i & 7] = v[k];
+                if ((i & 7) == 0) xs[(i >> 3) * XS + 32] = sum;
+            }
         }
     }
 }

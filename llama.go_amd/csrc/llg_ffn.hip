@@ -35,32 +35,35 @@ __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w,
         const int gtid = blockIdx.x * blockDim.x + threadIdx.x;
         for (int i = gtid; i < zero_n; i += gridDim.x * blockDim.x) zero[i] = 0.0f;
     }
-    llg_stage_x<MV_XS>(xs, x + (size_t)cb0 * 32, cnb);
+    llg_stage_x_sum<MV_XS>(xs, x + (size_t)cb0 * 32, cnb);
     __syncthreads();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform per wavefront
     const int r_end = min(rows, (tile + 1) * MV_TILE);
     for (int r0 = tile * MV_TILE + wave * MV_ROWS; r0 < r_end; r0 += 4 * MV_ROWS) {
         float s[MV_ROWS];
 #pragma unroll
         for (int q = 0; q < MV_ROWS; q++) s[q] = 0.0f;
-        for (int bl0 = lane; bl0 < cnb; bl0 += 64 * MV_BATCH) {
-            // request the bytes of all MV_BATCH x MV_ROWS blocks, then use them
+        for (int bb = 0; bb < cnb; bb += 64 * MV_BATCH) {
+            // request the bytes of all MV_BATCH x MV_ROWS blocks, then use them;
+            // loads are never under a per-lane condition (that serialises
+            // them): lanes past the chunk reload its last block and drop it
             BlockRaw<T> r[MV_BATCH][MV_ROWS];
 #pragma unroll
             for (int i = 0; i < MV_BATCH; i++)
 #pragma unroll
-                for (int q = 0; q < MV_ROWS; q++)
-                    if (bl0 + 64 * i < cnb && r0 + q < r_end)
-                        llg_block_load<T>(r[i][q], w + (long long)(r0 + q) * stride, f,
-                                          cb0 + bl0 + 64 * i);
+                for (int q = 0; q < MV_ROWS; q++)  // a row past the end reloads the last row
+                    llg_block_load<T>(r[i][q], w + (long long)min(r0 + q, r_end - 1) * stride, f,
+                                      cb0 + min(bb + lane + 64 * i, cnb - 1));
 #pragma unroll
             for (int i = 0; i < MV_BATCH; i++) {
-                const int bl = bl0 + 64 * i;
+                const int bl = bb + lane + 64 * i;
                 if (bl >= cnb) continue;
-                const float4 *xb = reinterpret_cast<const float4 *>(xs + bl * MV_XS);
+                const float *xb = xs + bl * MV_XS;
+                const float4 *x4 = reinterpret_cast<const float4 *>(xb);
 #pragma unroll
                 for (int q = 0; q < MV_ROWS; q++)
-                    if (r0 + q < r_end) s[q] += llg_raw_dot<T>(r[i][q], xb);
+                    if (r0 + q < r_end) s[q] += llg_raw_dot<T>(r[i][q], x4, xb[32]);
             }
         }
 #pragma unroll

@@ -14,6 +14,12 @@ int llg_pred_hidden_enqueue(LlgDevice *d, LlgObject *wup, const float *d_a, uint
                             float **partial, unsigned long long **mask, int *psplit,
                             float *zero_out, int zero_n, int32_t *zero_ctr, int n_ctr,
                             int32_t *zero_extra);
+// Hidden partials + tile masks (k_pred_hidden, k_pred_logits); also clears
+// zero_out[0..zero_n) and *zero_extra for the kernels that follow.
+int llg_pred_masks_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
+                           const float *d_a, float thr, uint8_t *ws,
+                           unsigned long long **mask_out, float *zero_out, int zero_n,
+                           int32_t *zero_extra);
 // Ascending active list from 64-bit tile masks (one workgroup).
 int llg_compact_enqueue(LlgDevice *d, const unsigned long long *mask, int n_tiles,
                         int32_t *d_active, int32_t *d_n_active);

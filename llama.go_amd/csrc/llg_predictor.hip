@@ -182,6 +182,27 @@ int llg_compact_enqueue(LlgDevice *d, const unsigned long long *mask, int n_tile
     return 0;
 }
 
+// Hidden partials (also clearing zero_out[0..zero_n) and *zero_extra) and the
+// tile masks; *mask_out points into ws.
+int llg_pred_masks_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
+                           const float *d_a, float thr, uint8_t *ws,
+                           unsigned long long **mask_out, float *zero_out, int zero_n,
+                           int32_t *zero_extra) {
+    const int ff = wout->rows, rank = wup->rows;
+    float *partial;
+    int psplit;
+    int rc = llg_pred_hidden_enqueue(d, wup, d_a, ws, &partial, mask_out, &psplit, zero_out,
+                                     zero_n, nullptr, 0, zero_extra);
+    if (rc) return rc;
+    const int n_tiles = (ff + 63) / 64;
+    const float *d_bias = bias ? reinterpret_cast<const float *>(bias->d) : nullptr;
+    const size_t lds = (size_t)(((rank + 3) & ~3) + 64) * sizeof(float);
+    hipLaunchKernelGGL(k_pred_logits, dim3(n_tiles), dim3(256), lds, llg_dev_stream(d), wout->d,
+                       wout->stride, ff, rank, partial, d_bias, thr, (float *)nullptr, *mask_out);
+    LLG_LAUNCH_CHECK(d, "pred_logits");
+    return 0;
+}
+
 int llg_predict_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
                         const float *d_a, float thr, int32_t *d_active, int32_t *d_n_active,
                         float *d_logits, uint8_t *ws) {

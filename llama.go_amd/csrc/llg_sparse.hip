@@ -36,29 +36,59 @@
 #define PRED_SPLIT_N 8    // partials per hidden unit written by k_pred_hidden
 
 __device__ __forceinline__ void stage_x(float *xs, const float *__restrict__ x, int nb) {
-    llg_stage_x<XS_STRIDE>(xs, x, nb);
+    llg_stage_x_sum<XS_STRIDE>(xs, x, nb);
 }
 
-// Up-row dot product of one wavefront: lane l owns blocks l, l+64, ...; the
-// bytes of BATCH of them are loaded before any is used.
+// Up-row dot products of two rows by one wavefront (row < 0: no row, result
+// 0): lane l owns blocks l, l+64, ...; the bytes of up to BATCH blocks of both
+// rows are requested before any is used.  The row indices are made
+// wavefront-uniform and loads are never under a per-lane condition (either
+// makes the compiler wait for each load before issuing the next): a lane past
+// the last block reloads it and drops the result.
 template <int T>
-__device__ __forceinline__ float row_dot(const uint8_t *__restrict__ row, const RowFmt &f,
-                                         const float *xs) {
+__device__ __forceinline__ void row_dot2_pass(const uint8_t *p0, const uint8_t *p1, bool v0,
+                                              bool v1, const RowFmt &f, const float *xs, int b0,
+                                              float &a0, float &a1) {
     const int lane = threadIdx.x & 63;
-    float s = 0.0f;
-    for (int b0 = lane; b0 < f.nb; b0 += 64 * BATCH) {
-        BlockRaw<T> r[BATCH];
+    BlockRaw<T> r0[BATCH], r1[BATCH];
 #pragma unroll
-        for (int i = 0; i < BATCH; i++)
-            if (b0 + 64 * i < f.nb) llg_block_load<T>(r[i], row, f, b0 + 64 * i);
+    for (int i = 0; i < BATCH; i++) {  // straight-line loads (p0/p1 point at row 0 if unused)
+        const int b = min(b0 + lane + 64 * i, f.nb - 1);
+        llg_block_load<T>(r0[i], p0, f, b);
+        llg_block_load<T>(r1[i], p1, f, b);
+    }
 #pragma unroll
-        for (int i = 0; i < BATCH; i++) {
-            const int b = b0 + 64 * i;
-            if (b < f.nb)
-                s += llg_raw_dot<T>(r[i], reinterpret_cast<const float4 *>(xs + b * XS_STRIDE));
+    for (int i = 0; i < BATCH; i++) {
+        const int b = b0 + lane + 64 * i;
+        if (b < f.nb) {
+            const float *xb = xs + b * XS_STRIDE;
+            const float4 *x4 = reinterpret_cast<const float4 *>(xb);
+            const float d0 = llg_raw_dot<T>(r0[i], x4, xb[32]);
+            const float d1 = llg_raw_dot<T>(r1[i], x4, xb[32]);
+            a0 += v0 ? d0 : 0.0f;
+            a1 += v1 ? d1 : 0.0f;
         }
     }
-    return llg_wave_sum(s);
+}
+
+template <int T>
+__device__ __forceinline__ void row_dot2(const uint8_t *__restrict__ base, long long bstride,
+                                         int row0, int row1, const RowFmt &f, const float *xs,
+                                         float &s0, float &s1) {
+    row0 = __builtin_amdgcn_readfirstlane(row0);
+    row1 = __builtin_amdgcn_readfirstlane(row1);
+    const bool v0 = row0 >= 0, v1 = row1 >= 0;
+    const uint8_t *p0 = base + (long long)(v0 ? row0 : 0) * bstride;
+    const uint8_t *p1 = base + (long long)(v1 ? row1 : 0) * bstride;
+    float a0 = 0.0f, a1 = 0.0f;
+    if (f.nb <= 64 * BATCH) {
+        row_dot2_pass<T>(p0, p1, v0, v1, f, xs, 0, a0, a1);
+    } else {
+        for (int b0 = 0; b0 < f.nb; b0 += 64 * BATCH)
+            row_dot2_pass<T>(p0, p1, v0, v1, f, xs, b0, a0, a1);
+    }
+    s0 = llg_wave_sum(a0);
+    s1 = llg_wave_sum(a1);
 }
 
 // B. explicit list: pair j = (row of active[j], act(up . x)); also zeroes out.
@@ -80,12 +110,20 @@ __global__ __launch_bounds__(256) void k_list_up(const uint8_t *__restrict__ bas
     stage_x(xs, x, f.nb);
     __syncthreads();
     const int lane = threadIdx.x & 63;
-    for (int j = first + (threadIdx.x >> 6); j < n_active; j += gridDim.x * 4) {
-        const int n = active[j];
-        const int row = slot_of ? slot_of[n] : n;
-        float u = 0.0f;  // a non-resident row keeps activation 0 (window.go:150-152)
-        if (row >= 0) u = llg_act(act, row_dot<T>(base + (long long)row * bstride, f, xs));
-        if (lane == 0) pairs[j] = make_int2(row, __float_as_int(u));
+    const int stride = gridDim.x * 4;
+    for (int j = first + (threadIdx.x >> 6); j < n_active; j += 2 * stride) {
+        const int j1 = j + stride;
+        const int n0 = active[j];
+        const int n1 = j1 < n_active ? active[j1] : -1;
+        const int row0 = slot_of ? slot_of[n0] : n0;
+        const int row1 = n1 < 0 ? -1 : (slot_of ? slot_of[n1] : n1);
+        float s0, s1;
+        row_dot2<T>(base, bstride, row0, row1, f, xs, s0, s1);
+        if (lane == 0) {  // a non-resident row keeps activation 0 (window.go:150-152)
+            pairs[j] = make_int2(row0, __float_as_int(row0 >= 0 ? llg_act(act, s0) : 0.0f));
+            if (j1 < n_active)
+                pairs[j1] = make_int2(row1, __float_as_int(row1 >= 0 ? llg_act(act, s1) : 0.0f));
+        }
     }
 }
 
@@ -132,12 +170,24 @@ __global__ __launch_bounds__(256) void k_tile_up(
     }
     __syncthreads();
     const int cnt = tl[64];
-    for (int k = wave; k < cnt; k += 4) {
-        const int n = tile0 + tl[k];
-        const float u = llg_act(act, row_dot<T>(base + (long long)n * bstride, f, xs));
-        if (lane == 0 && u != 0.0f) {  // ffn_flash.go:290 skips zero activations
-            const int pos = atomicAdd(&tl[65], 1);  // LDS atomic, tile-local slot
-            pairs[blockIdx.x * 64 + pos] = make_int2(n, __float_as_int(u));
+    for (int k = wave; k < cnt; k += 8) {  // two neurons per wavefront per round
+        const int n0 = tile0 + tl[k];
+        const int n1 = k + 4 < cnt ? tile0 + tl[k + 4] : -1;
+        float s0, s1;
+        row_dot2<T>(base, bstride, n0, n1, f, xs, s0, s1);
+        if (lane == 0) {  // ffn_flash.go:290 skips zero activations
+            const float u0 = llg_act(act, s0);
+            if (u0 != 0.0f) {
+                const int pos = atomicAdd(&tl[65], 1);  // LDS atomic, tile-local slot
+                pairs[blockIdx.x * 64 + pos] = make_int2(n0, __float_as_int(u0));
+            }
+            if (n1 >= 0) {
+                const float u1 = llg_act(act, s1);
+                if (u1 != 0.0f) {
+                    const int pos = atomicAdd(&tl[65], 1);
+                    pairs[blockIdx.x * 64 + pos] = make_int2(n1, __float_as_int(u1));
+                }
+            }
         }
     }
     __syncthreads();
@@ -197,10 +247,12 @@ __global__ __launch_bounds__(256) void k_sparse_down(
     const int bl = lane & 7;
     const int sub = lane >> 3;
     const int b = s * DN_SLICE + bl;
+    const int bc = min(b, f.nb - 1);  // lanes past the last block load it and drop it
     float acc[32];
+    float corr = 0.0f;
 #pragma unroll
     for (int e = 0; e < 32; e++) acc[e] = 0.0f;
-    if (b < f.nb) {
+    {
         for (int j = j0 + wave * 8 + sub; j < j1; j += 64) {
             // two pairs per pass: both rows' bytes are requested before either is used
             int2 p0, p1 = make_int2(0, 0);
@@ -217,14 +269,20 @@ __global__ __launch_bounds__(256) void k_sparse_down(
                 p0 = pairs[j];
                 if (j + 32 < j1) p1 = pairs[j + 32];
             }
-            const float u0 = __int_as_float(p0.y), u1 = __int_as_float(p1.y);
+            float u0 = __int_as_float(p0.y), u1 = __int_as_float(p1.y);
+            if (b >= f.nb) u0 = u1 = 0.0f;
+            // Unconditional loads (a row index of a zero activation may be -1 or
+            // stale: such lanes read row 0); only the use is skipped, as
+            // ffn_flash.go:290 skips u == 0.
             BlockRaw<T> r0, r1;
-            if (u0 != 0.0f) llg_block_load<T>(r0, base + (long long)p0.x * bstride + f.stride, f, b);
-            if (u1 != 0.0f) llg_block_load<T>(r1, base + (long long)p1.x * bstride + f.stride, f, b);
-            if (u0 != 0.0f) llg_raw_axpy<T>(r0, u0, acc);  // ffn_flash.go:290 skips u == 0
-            if (u1 != 0.0f) llg_raw_axpy<T>(r1, u1, acc);
+            llg_block_load<T>(r0, base + (long long)(u0 != 0.0f ? p0.x : 0) * bstride + f.stride, f, bc);
+            llg_block_load<T>(r1, base + (long long)(u1 != 0.0f ? p1.x : 0) * bstride + f.stride, f, bc);
+            if (u0 != 0.0f) llg_raw_axpy<T>(r0, u0, acc, corr);
+            if (u1 != 0.0f) llg_raw_axpy<T>(r1, u1, acc, corr);
         }
     }
+#pragma unroll
+    for (int e = 0; e < 32; e++) acc[e] -= corr;
 #pragma unroll
     for (int e = 0; e < 32; e++) {  // sum over the 8 pair sub-lanes sharing block bl
         float v = acc[e];
