@@ -14,8 +14,8 @@ their average event-timed duration on the library's stream) and a
 `cpu_baseline` object (the oracle's restatement of the reference CPU path,
 timed on a bounded sample on this host).
 
-Other workloads (--workload dense-q4_0 | dense-q8_0 | dense-f16 | window |
-moe-decode | moe-prefill) measure the remaining hot-path configurations.
+Other workloads (--workload dense-q4_0 | dense-q8_0 | dense-f16 | moe-decode |
+moe-prefill) measure the remaining hot-path configurations.
 """
 from __future__ import annotations
 
@@ -251,13 +251,93 @@ def bench_dense(args, torch, llg, dev, t):
                          "alg_bytes_per_launch": alg, "avg_launch_us": ms * 1e3}}
 
 
+MOE_D, MOE_FF, MOE_E, MOE_K, MOE_PREFILL = 4096, 14336, 8, 2, 512
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def bench_moe(args, torch, llg, dev, prefill: bool):
+    """Mixtral-shaped MoE layer (d=4096, 8 SwiGLU experts of 14336, top-2, Q4_0).
+    decode: one token per step (router + 2 experts' gate/up/down matvecs +
+    combine), x fresh per step.  prefill: 512 tokens per step, grouped per
+    expert into MFMA GEMMs."""
+    gg = llg.gguf
+    L = args.layers
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x30E00003)
+    router = torch.randn((MOE_E, MOE_D), generator=g, device="cuda") * 0.02
+    mats = []
+    for rows, cols in [(MOE_E * MOE_FF, MOE_D)] * 2 + [(MOE_E * MOE_D, MOE_FF)]:
+        q = gg.quantize(torch.randn((rows, cols), generator=g, device="cuda") * 0.02, gg.Q4_0)
+        mats.append([dev.upload_matrix(q, gg.Q4_0, rows, cols) for _ in range(L)])
+        del q
+    rh = dev.upload_matrix(router, gg.F32, MOE_E, MOE_D)
+    n_tok = MOE_PREFILL if prefill else 1
+    nx = 4 if prefill else 64
+    X = torch.randn((nx, n_tok, MOE_D), generator=g, device="cuda")
+    out = torch.empty((n_tok, MOE_D), device="cuda")
+    ids = torch.empty((n_tok, MOE_K), dtype=torch.int32, device="cuda")
+    w = torch.empty((n_tok, MOE_K), device="cuda")
+    torch.cuda.synchronize()
+    tm = Timer(torch, dev.stream)
+
+    def step(i):
+        l = i % L
+        rc = dev.lib.llg_hipd_moe_ffn(dev.h, rh.id, mats[0][l].id, mats[1][l].id, mats[2][l].id,
+                                      MOE_E, MOE_K, vp(X[i % nx]), n_tok, vp(out), vp(ids), vp(w))
+        if rc:
+            dev.check(rc, "moe_ffn")
+
+    for i in range(args.warmup):
+        step(i)
+    dev.sync()
+    e0 = tm.event()
+    for i in range(args.steps):
+        step(i)
+    e1 = tm.event()
+    dev.sync()
+    ms = e0.elapsed_time(e1) / args.steps
+    q4 = gg.byte_size(gg.Q4_0, MOE_D)          # per row of gate/up; down rows are eff wide
+    expert_bytes = 2 * MOE_FF * q4 + MOE_D * gg.byte_size(gg.Q4_0, MOE_FF)
+    hit = int(torch.unique(ids).numel())
+    for ms_ in mats:
+        for h_ in ms_:
+            h_.release()
+    rh.release()
+    if prefill:
+        flops = n_tok * MOE_K * 3 * 2 * MOE_D * MOE_FF
+        tf = flops / (ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "kernel": "k_moe_gemm<0> (gate/up+SwiGLU) + k_moe_gemm<1> (down) "
+                "+ grouping/convert/combine (one 512-token step)",
+                "achieved": tf, "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": tf / MFMA_F16_PEAK_TFLOPS, "traffic": None,
+                "alg_flops_per_step": flops, "alg_weight_bytes_per_step": hit * expert_bytes,
+                "avg_step_us": ms * 1e3}
+        wl = "mixtral-moe-layer-q4_0-top2-prefill512"
+        dtype = "f16 x q4_0 -> f32"
+    else:
+        alg = MOE_K * expert_bytes
+        gbs = alg / (ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "kernel": "k_moe_router + k_moe_gateup + k_moe_down (one token)",
+                "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": gbs / HBM_PEAK_GBS, "traffic": None, "alg_bytes_per_step": alg,
+                "avg_step_us": ms * 1e3}
+        wl = "mixtral-moe-layer-q4_0-top2-decode"
+        dtype = "f32"
+    return {"metric": "MoE FFN tokens/s", "value": n_tok * 1000.0 / ms, "unit": "tokens/s",
+            "ms_per_step": ms, "dtype": dtype,
+            "config": {"workload": wl, "d_model": MOE_D, "expert_ff": MOE_FF, "n_experts": MOE_E,
+                       "top_k": MOE_K, "tokens_per_step": n_tok, "layer_copies_rotated": L},
+            "roofline": roof}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="sparse",
-                    choices=["sparse", "dense-q4_0", "dense-q8_0", "dense-f16"])
+                    choices=["sparse", "dense-q4_0", "dense-q8_0", "dense-f16", "moe-decode",
+                             "moe-prefill"])
     ap.add_argument("--layers", type=int, default=0,
                     help="distinct HBM copies rotated per step (0 = enough to defeat the MALL)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -270,7 +350,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     if args.layers <= 0:
-        args.layers = 128 if args.workload == "sparse" else 6
+        args.layers = {"sparse": 128, "moe-decode": 2, "moe-prefill": 1}.get(args.workload, 6)
 
     import torch
     import llg
@@ -282,6 +362,8 @@ def main():
     gg = llg.gguf
     if args.workload == "sparse":
         res = bench_sparse(args, torch, llg, dev)
+    elif args.workload.startswith("moe-"):
+        res = bench_moe(args, torch, llg, dev, args.workload == "moe-prefill")
     else:
         t = {"dense-q4_0": gg.Q4_0, "dense-q8_0": gg.Q8_0, "dense-f16": gg.F16}[args.workload]
         res = bench_dense(args, torch, llg, dev, t)

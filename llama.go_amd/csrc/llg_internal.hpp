@@ -40,3 +40,11 @@ size_t llg_fused_ws_bytes(int rank, int ff);
 int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
                       LlgObject *b, const float *d_a, const float *d_x, float thr, int act,
                       float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws);
+
+// MoE prefill as grouped MFMA GEMMs (llg_moe_gemm.hip).
+bool llg_moe_gemm_supported(int type, int hidden, int eff, int n_tok);
+size_t llg_moe_gemm_ws_bytes(int n_tok, int k, int n_exp, int hidden, int eff);
+int llg_moe_gemm_enqueue(LlgDevice *d, const LlgObject *gate, const LlgObject *up,
+                         const LlgObject *down, int n_exp, int k, int hidden, int eff,
+                         const float *d_x, int n_tok, const int32_t *ids, const float *w,
+                         float *d_out, uint8_t *ws);

@@ -12,6 +12,9 @@
 //                  chosen order, starting from 0 (moe_forward.go:71-77, 141-148)
 // Expert e's rows are e*eff + j of gate/up and e*hidden + d of down, the
 // addressing of ReadContiguousRows (flash/storage.go:72-94).
+// Batches of 16 or more tokens over Q4_0 experts go to the grouped MFMA GEMM
+// path (llg_moe_gemm.hip); smaller batches and other types use the kernels
+// below token by token.
 #include "llg_common.hpp"
 #include "llg_internal.hpp"
 
@@ -204,9 +207,15 @@ static int check_moe(LlgDevice *d, int64_t hr, int64_t hg, int64_t hu, int64_t h
     return 0;
 }
 
+static bool use_gemm(const MoeArgs &a, int n_tok) {
+    return llg_moe_gemm_supported(a.gate->fmt.type, a.hidden, a.eff, n_tok);
+}
+
 static size_t moe_ws_bytes(const MoeArgs &a, int n_tok) {
-    return (size_t)llg_align((long long)n_tok * a.k * 4, 256) * 2 +
-           (size_t)n_tok * a.k * a.eff * 4;
+    const size_t head = (size_t)llg_align((long long)n_tok * a.k * 4, 256) * 2;
+    if (use_gemm(a, n_tok))
+        return head + llg_moe_gemm_ws_bytes(n_tok, a.k, a.n_exp, a.hidden, a.eff);
+    return head + (size_t)n_tok * a.k * a.eff * 4;
 }
 
 template <int T>
@@ -234,6 +243,9 @@ static int moe_enqueue(LlgDevice *d, const MoeArgs &a, const float *d_x, int n_t
     hipLaunchKernelGGL(k_moe_router, dim3(n_tok), dim3(512), 0, st, a.router->d, a.router->stride,
                        a.hidden, a.n_exp, a.k, d_x, (const float *)nullptr, ids, w);
     LLG_LAUNCH_CHECK(d, "moe_router");
+    if (use_gemm(a, n_tok))  // batched tokens: grouped MFMA GEMMs
+        return llg_moe_gemm_enqueue(d, a.gate, a.up, a.down, a.n_exp, a.k, a.hidden, a.eff, d_x,
+                                    n_tok, ids, w, d_out, ws + 2 * kb);
     switch (a.gate->fmt.type) {
     case LLG_TYPE_Q4_0:
         moe_launch_experts<LLG_TYPE_Q4_0>(st, a, n_tok, ids, w, d_x, hbuf, d_out);
@@ -265,6 +277,8 @@ int llg_hipd_moe_ffn(LlgHipDevice h, int64_t hr, int64_t hg, int64_t hu, int64_t
     int rc = check_moe(d, hr, hg, hu, hdn, n_exp, k, &a);
     if (rc) return rc;
     if (!d_x || !d_out || n_tok <= 0) return llg_set_error(d, LLG_E_ARG, "moe: bad arguments");
+    if (((uintptr_t)d_x | (uintptr_t)d_out) & 15)
+        return llg_set_error(d, LLG_E_ALIGN, "moe: x and out must be 16-byte aligned");
     uint8_t *ws = (uint8_t *)llg_ws(d, moe_ws_bytes(a, n_tok), &rc);
     if (rc) return rc;
     return moe_enqueue(d, a, d_x, n_tok, d_out, d_ids, d_w, ws);

@@ -314,6 +314,56 @@ def test_moe_decode_config3(dev, rng):
         hnd.release()
 
 
+@pytest.mark.parametrize("n_tok", [16, 77, 200])
+def test_moe_prefill_gemm(dev, rng, n_tok):
+    """Batches of >= 16 Q4_0 tokens take the grouped MFMA GEMM path (f16
+    operands, fp32 accumulation); every token is checked against the oracle.
+    The router is biased so one expert gets no token and one gets most of
+    them all (empty groups, ragged 64-row tiles, several tiles per expert)."""
+    d, eff, E, k = 256, 384, 8, 2
+    router, gate, up, down = make_moe(rng, d, eff, E, gg.Q4_0)
+    router *= 10
+    hs = upload_moe(dev, router, gate, up, down, d, eff, E, gg.Q4_0)
+    x = normal(rng, (n_tok, d), 1.0)
+    x += 0.5 * router[2] / np.linalg.norm(router[2]) * np.sqrt(d)  # favour expert 2
+    x -= 2.0 * router[5] / np.linalg.norm(router[5]) * np.sqrt(d)  # starve expert 5
+    out, ids, w = llg.moe_ffn(dev, *hs, E, k, x)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    assert counts[5] == 0 and counts[2] == n_tok, counts
+    for i in range(n_tok):
+        ro, rid, rw = R.moe_ffn(router, gate, up, down, gg.Q4_0, d, eff, E, k, x[i])
+        assert np.array_equal(ids[i], rid), i
+        # logits from x are summed in another order than the oracle's, so the
+        # weights agree to rounding (bit-exact routing on equal logits is
+        # test_moe_route_bit_exact)
+        assert np.allclose(w[i], rw, rtol=1e-5, atol=1e-7), i
+        assert max_rel_err(out[i], ro) <= TOL, i
+    for hnd in hs:
+        hnd.release()
+
+
+def test_moe_prefill_config3(dev, rng):
+    """Mixtral-shaped layer, 512-token prefill on the grouped GEMM path: 12
+    sampled tokens against the oracle, and every token against the one-token
+    decode path of the same library (same ids and weights bit for bit)."""
+    d, eff, E, k, n_tok = 4096, 14336, 8, 2, 512
+    router, gate, up, down = make_moe(rng, d, eff, E, gg.Q4_0, seed=61)
+    hs = upload_moe(dev, router, gate, up, down, d, eff, E, gg.Q4_0)
+    x = normal(rng, (n_tok, d), 1.0)
+    out, ids, w = llg.moe_ffn(dev, *hs, E, k, x)
+    assert np.all(np.isfinite(out))
+    for i in np.linspace(0, n_tok - 1, 12).astype(int):
+        ro, rid, rw = R.moe_ffn(router, gate, up, down, gg.Q4_0, d, eff, E, k, x[i])
+        assert np.array_equal(ids[i], rid), i
+        assert max_rel_err(out[i], ro) <= TOL, i
+    for i in range(0, n_tok, 37):
+        o1, id1, w1 = llg.moe_ffn(dev, *hs, E, k, x[i])
+        assert np.array_equal(ids[i], id1) and np.array_equal(w[i], w1), i
+        assert max_rel_err(out[i], o1) <= TOL, i
+    for hnd in hs:
+        hnd.release()
+
+
 def test_moe_invalid_hparams(dev, rng):
     d, eff, E = 64, 96, 4
     router, gate, up, down = make_moe(rng, d, eff, E, gg.Q4_0)
