@@ -15,46 +15,59 @@
 // Batches of 16 or more tokens over Q4_0 experts go to the grouped MFMA GEMM
 // path (llg_moe_gemm.hip); smaller batches and other types use the kernels
 // below token by token.
+#include <algorithm>
+
 #include "llg_common.hpp"
 #include "llg_internal.hpp"
 
 #define MOE_MAX_EXP 64
 #define MOE_MAX_K 8
 
-// Softmax + stable descending top-k over `lg` (n_exp values), one thread.
-__device__ void moe_route_one(const float *lg, int n_exp, int k, int32_t *ids, float *w) {
-    float p[MOE_MAX_EXP];
-    int idx[MOE_MAX_EXP];
-    float mx = lg[0];
-    for (int e = 0; e < n_exp; e++)
-        if (lg[e] > mx) mx = lg[e];
+__device__ __forceinline__ float moe_lane(float v, int e) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), e));
+}
+
+// Softmax + stable descending top-k over `lg` (n_exp <= 64 values), one
+// wavefront, lane e holding expert e.  The sequential parts keep the
+// reference's order: max scan and fp32 sum from expert 0 (forward.go:463-479),
+// wsum from slot 0 (moe_forward.go:62-68).  sort.Slice on n <= 12 is an
+// insertion sort, i.e. stable: expert e's slot is the number of experts with a
+// larger score plus those with an equal score and a lower index.  A NaN or
+// +Inf logit makes every score NaN; the insertion sort then keeps index order.
+__device__ void moe_route_wave(const float *lg, int n_exp, int k, int32_t *ids, float *w) {
+    const int lane = threadIdx.x & 63;
+    const float v = lane < n_exp ? lg[lane] : 0.0f;
+    float mx = moe_lane(v, 0);
+    for (int e = 1; e < n_exp; e++) {
+        const float o = moe_lane(v, e);
+        if (o > mx) mx = o;
+    }
+    float p = (float)exp((double)(v - mx));
     float sum = 0.0f;
+    for (int e = 0; e < n_exp; e++) sum += moe_lane(p, e);
+    p /= sum;
+    int rank = 0;
     for (int e = 0; e < n_exp; e++) {
-        const float v = (float)exp((double)(lg[e] - mx));
-        p[e] = v;
-        sum += v;
+        const float o = moe_lane(p, e);
+        rank += (o > p || (o == p && e < lane)) ? 1 : 0;
     }
-    for (int e = 0; e < n_exp; e++) p[e] /= sum;
-    for (int e = 0; e < n_exp; e++) idx[e] = e;
-    for (int i = 1; i < n_exp; i++) {  // insertion sort: equal scores keep index order
-        const int cur = idx[i];
-        int j = i;
-        while (j > 0 && p[cur] > p[idx[j - 1]]) {
-            idx[j] = idx[j - 1];
-            j--;
-        }
-        idx[j] = cur;
-    }
+    if (p != p) rank = lane;
+    const bool mine = lane < n_exp && rank < k;
     float wsum = 0.0f;
-    for (int s = 0; s < k; s++) wsum += p[idx[s]];
-    if (wsum < 1e-9f) wsum = 1.0f;
     for (int s = 0; s < k; s++) {
-        ids[s] = idx[s];
-        w[s] = p[idx[s]] / wsum;
+        const unsigned long long m = __ballot(lane < n_exp && rank == s);
+        wsum += moe_lane(p, __builtin_ctzll(m));
+    }
+    if (wsum < 1e-9f) wsum = 1.0f;
+    if (mine) {
+        ids[rank] = lane;
+        w[rank] = p / wsum;
     }
 }
 
-// One workgroup per token; wavefront e computes logit e.
+// One workgroup per token; wavefront e computes logit e.  A lane's float4
+// loads of router row and x are issued together (8 per lane per pass, clamped
+// addresses, masked use), so a 4096-wide row costs two round trips.
 __global__ __launch_bounds__(512) void k_moe_router(const uint8_t *__restrict__ router,
                                                     long long stride, int hidden, int n_exp, int k,
                                                     const float *__restrict__ x,
@@ -63,108 +76,400 @@ __global__ __launch_bounds__(512) void k_moe_router(const uint8_t *__restrict__ 
                                                     float *__restrict__ w) {
     __shared__ float lg[MOE_MAX_EXP];
     const int t = blockIdx.x;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (given_logits) {
         for (int e = threadIdx.x; e < n_exp; e += blockDim.x) lg[e] = given_logits[(size_t)t * n_exp + e];
     } else {
-        const float *xt = x + (size_t)t * hidden;
+        const float4 *xt = reinterpret_cast<const float4 *>(x + (size_t)t * hidden);
+        const int n4 = hidden / 4;
         for (int e = wave; e < n_exp; e += nw) {
-            const float *row = reinterpret_cast<const float *>(router + (long long)e * stride);
+            const float4 *row = reinterpret_cast<const float4 *>(router + (long long)e * stride);
             float s = 0.0f;
-            for (int dd = lane; dd < hidden; dd += 64) s += row[dd] * xt[dd];
+            for (int c0 = 0; c0 < n4; c0 += 512) {
+                float4 rv[8], xv[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const int i = min(c0 + lane + 64 * q, n4 - 1);
+                    rv[q] = row[i];
+                    xv[q] = xt[i];
+                }
+#pragma unroll
+                for (int q = 0; q < 8; q++)
+                    if (c0 + lane + 64 * q < n4)
+                        s += rv[q].x * xv[q].x + rv[q].y * xv[q].y + rv[q].z * xv[q].z +
+                             rv[q].w * xv[q].w;
+            }
             s = llg_wave_sum(s);
             if (lane == 0) lg[e] = s;
         }
     }
     __syncthreads();
-    if (threadIdx.x == 0) moe_route_one(lg, n_exp, k, ids + (size_t)t * k, w + (size_t)t * k);
+    if (threadIdx.x < 64) moe_route_wave(lg, n_exp, k, ids + (size_t)t * k, w + (size_t)t * k);
 }
 
-// Wavefront per (token, slot, j): gate and up rows share every x block load.
-template <int T>
+// Dot products of NR rows against the staged vector xs (MOE_XS floats per
+// 32-element block, block sum at [32]) over blocks [0, nb): lane l takes
+// blocks l, l+64, ...; the loads of NB blocks x NR rows are issued together.
+// The first batch is loaded by moe_rows_issue before the caller stages xs.
+#define MOE_XS 36
+template <int T, int NR, int NB>
+struct MoeRows {
+    BlockRaw<T> r[NB][NR];
+    __device__ __forceinline__ void issue(const uint8_t *const (&rp)[NR], const RowFmt &f,
+                                          int b0, int nb) {
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int i = 0; i < NB; i++)
+#pragma unroll
+            for (int q = 0; q < NR; q++)
+                llg_block_load<T>(r[i][q], rp[q], f, b0 + min(lane + 64 * i, nb - 1));
+    }
+    __device__ __forceinline__ void use(const float *xs, int b0, int nb, float (&s)[NR]) const {
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int bl = lane + 64 * i;
+            if (bl >= nb) continue;
+            const float *xb = xs + (b0 + bl) * MOE_XS;
+            const float4 *x4 = reinterpret_cast<const float4 *>(xb);
+#pragma unroll
+            for (int q = 0; q < NR; q++) s[q] += llg_raw_dot<T>(r[i][q], x4, xb[32]);
+        }
+    }
+};
+
+template <int T, int NR, int NB>
+__device__ __forceinline__ void moe_rows_dot(const uint8_t *const (&rp)[NR], const RowFmt &f,
+                                             int nb, const float *xs, float (&s)[NR],
+                                             MoeRows<T, NR, NB> &m) {
+    // m holds the loads of blocks [0, 64*NB); the rest stream in batches
+    m.use(xs, 0, min(nb, 64 * NB), s);
+    for (int b0 = 64 * NB; b0 < nb; b0 += 64 * NB) {
+        m.issue(rp, f, b0, nb - b0);
+        m.use(xs, b0, min(nb - b0, 64 * NB), s);
+    }
+}
+
+// h[ts][j] = silu(gate_e[j] . x_t) * (up_e[j] . x_t), ts = token*k + slot,
+// e = ids[ts] (moe_forward.go:101-132).  Workgroup: one ts, MOE_GU_TILE
+// consecutive j; each wavefront owns MOE_GU_J j (2*MOE_GU_J rows: gate, up)
+// whose loads are issued before x_t is staged.  `zero` (the down kernel's
+// atomic target) is cleared here.
+#define MOE_GU_J 4
+#define MOE_GU_TILE (4 * MOE_GU_J)
+template <int T, int NB>
 __global__ __launch_bounds__(256) void k_moe_gateup(const uint8_t *__restrict__ gate,
                                                     const uint8_t *__restrict__ up,
                                                     long long stride, RowFmt f, int eff, int k,
-                                                    int n_tok, const int32_t *__restrict__ ids,
+                                                    const int32_t *__restrict__ ids,
                                                     const float *__restrict__ x,
-                                                    float *__restrict__ hbuf) {
+                                                    float *__restrict__ hbuf,
+                                                    float *__restrict__ zero, int zero_n) {
+    extern __shared__ float xs[];
+    const int n_tiles = (eff + MOE_GU_TILE - 1) / MOE_GU_TILE;
+    const int ts = blockIdx.x / n_tiles;
+    const int j0 = (blockIdx.x % n_tiles) * MOE_GU_TILE +
+                   MOE_GU_J * __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const long long total = (long long)n_tok * k * eff;
-    const long long nwaves = (long long)gridDim.x * 4;
-    for (long long i = (long long)blockIdx.x * 4 + (threadIdx.x >> 6); i < total; i += nwaves) {
-        const int j = (int)(i % eff);
-        const long long ts = i / eff;  // token * k + slot
-        const int t = (int)(ts / k);
-        const int e = ids[ts];
-        const long long r = (long long)e * eff + j;
-        const uint8_t *gr = gate + r * stride;
-        const uint8_t *ur = up + r * stride;
-        const float *xt = x + (size_t)t * f.cols;
-        float g = 0.0f, u = 0.0f;
-        for (int b = lane; b < f.nb; b += 64) {
-            float4 x4[8];
-            const float4 *xp = reinterpret_cast<const float4 *>(xt + b * 32);
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < zero_n; i += gridDim.x * blockDim.x)
+        zero[i] = 0.0f;
+    const int e = ids[ts];
+    const int t = ts / k;
+    const uint8_t *rp[2 * MOE_GU_J];
 #pragma unroll
-            for (int q = 0; q < 8; q++) x4[q] = xp[q];
-            g += llg_block_dot<T>(gr, f, b, x4);
-            u += llg_block_dot<T>(ur, f, b, x4);
-        }
-        g = llg_wave_sum(g);
-        u = llg_wave_sum(u);
-        if (lane == 0) {
+    for (int q = 0; q < MOE_GU_J; q++) {  // rows past eff reload the last row, dropped
+        const long long r = (long long)e * eff + min(j0 + q, eff - 1);
+        rp[q] = gate + r * stride;
+        rp[MOE_GU_J + q] = up + r * stride;
+    }
+    MoeRows<T, 2 * MOE_GU_J, NB> m;
+    m.issue(rp, f, 0, f.nb);
+    llg_stage_x_sum<MOE_XS>(xs, x + (size_t)t * f.cols, f.nb);
+    __syncthreads();
+    if (j0 >= eff) return;
+    float s[2 * MOE_GU_J];
+#pragma unroll
+    for (int q = 0; q < 2 * MOE_GU_J; q++) s[q] = 0.0f;
+    moe_rows_dot<T, 2 * MOE_GU_J, NB>(rp, f, f.nb, xs, s, m);
+#pragma unroll
+    for (int q = 0; q < 2 * MOE_GU_J; q++) s[q] = llg_wave_sum(s[q]);
+    if (lane == 0) {
+#pragma unroll
+        for (int q = 0; q < MOE_GU_J; q++) {
+            if (j0 + q >= eff) break;
+            const float g = s[q], u = s[MOE_GU_J + q];
             const float silu = g / (1.0f + (float)exp(-(double)g));  // moe_forward.go:130
-            hbuf[i] = silu * u;
+            hbuf[(size_t)ts * eff + j0 + q] = silu * u;
         }
     }
 }
 
-// Wavefront per (token, MOE_DN_ROWS consecutive outputs d); h blocks are
-// loaded once per slot and reused across those rows.
-#define MOE_DN_ROWS 4
-template <int T>
+// out[t][d] += w_s * (down_e[d] . h[ts]) over one column chunk of h
+// (moe_forward.go:71-77, 141-148; chunks and slots meet in fp32 atomics on a
+// zeroed out).  Workgroup: one ts, MOE_DN_TILE consecutive d, one chunk of at
+// most MOE_DN_CHUNK blocks of h staged in LDS; wavefront: MOE_DN_R rows.
+#define MOE_DN_R 4
+#define MOE_DN_TILE (4 * MOE_DN_R)
+#define MOE_DN_CHUNK 160
+template <int T, int NB>
 __global__ __launch_bounds__(256) void k_moe_down(const uint8_t *__restrict__ down,
                                                   long long stride, RowFmt f, int hidden, int k,
-                                                  int n_tok, const int32_t *__restrict__ ids,
+                                                  int chunk_blocks,
+                                                  const int32_t *__restrict__ ids,
                                                   const float *__restrict__ wts,
                                                   const float *__restrict__ hbuf,
                                                   float *__restrict__ out) {
+    extern __shared__ float xs[];
+    const int n_chunks = (f.nb + chunk_blocks - 1) / chunk_blocks;
+    const int n_tiles = (hidden + MOE_DN_TILE - 1) / MOE_DN_TILE;
+    const int ch = blockIdx.x % n_chunks;
+    const int tile = (blockIdx.x / n_chunks) % n_tiles;
+    const int ts = blockIdx.x / (n_chunks * n_tiles);
+    const int d0 = tile * MOE_DN_TILE + MOE_DN_R * __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int groups = (hidden + MOE_DN_ROWS - 1) / MOE_DN_ROWS;
-    const long long total = (long long)n_tok * groups;
-    const long long nwaves = (long long)gridDim.x * 4;
-    const int eff = f.cols;
-    for (long long i = (long long)blockIdx.x * 4 + (threadIdx.x >> 6); i < total; i += nwaves) {
-        const int t = (int)(i / groups);
-        const int d0 = (int)(i % groups) * MOE_DN_ROWS;
-        float res[MOE_DN_ROWS];
+    const int cb0 = ch * chunk_blocks;
+    const int cnb = min(chunk_blocks, f.nb - cb0);
+    const int e = ids[ts];
+    const int t = ts / k;
+    const uint8_t *rp[MOE_DN_R];
 #pragma unroll
-        for (int q = 0; q < MOE_DN_ROWS; q++) res[q] = 0.0f;
-        for (int s = 0; s < k; s++) {
-            const int e = ids[(size_t)t * k + s];
-            const float ws = wts[(size_t)t * k + s];
-            const float *h = hbuf + ((size_t)t * k + s) * eff;
-            float acc[MOE_DN_ROWS];
+    for (int q = 0; q < MOE_DN_R; q++)  // rows past hidden reload the last row, dropped
+        rp[q] = down + ((long long)e * hidden + min(d0 + q, hidden - 1)) * stride;
+    MoeRows<T, MOE_DN_R, NB> m;
+    m.issue(rp, f, cb0, cnb);
+    llg_stage_x_sum<MOE_XS>(xs, hbuf + (size_t)ts * f.cols + (size_t)cb0 * 32, cnb);
+    __syncthreads();
+    if (d0 >= hidden) return;
+    float s[MOE_DN_R];
 #pragma unroll
-            for (int q = 0; q < MOE_DN_ROWS; q++) acc[q] = 0.0f;
-            for (int b = lane; b < f.nb; b += 64) {
-                float4 h4[8];
-                const float4 *hp = reinterpret_cast<const float4 *>(h + b * 32);
+    for (int q = 0; q < MOE_DN_R; q++) s[q] = 0.0f;
+    m.use(xs, 0, min(cnb, 64 * NB), s);
+    for (int b0 = 64 * NB; b0 < cnb; b0 += 64 * NB) {
+        m.issue(rp, f, cb0 + b0, cnb - b0);
+        m.use(xs, b0, min(cnb - b0, 64 * NB), s);
+    }
+    const float ws = wts[ts];
 #pragma unroll
-                for (int q = 0; q < 8; q++) h4[q] = hp[q];
+    for (int q = 0; q < MOE_DN_R; q++) s[q] = llg_wave_sum(s[q]);
+    if (lane == 0) {
 #pragma unroll
-                for (int q = 0; q < MOE_DN_ROWS; q++)
-                    if (d0 + q < hidden)
-                        acc[q] += llg_block_dot<T>(
-                            down + ((long long)e * hidden + d0 + q) * stride, f, b, h4);
-            }
+        for (int q = 0; q < MOE_DN_R; q++)
+            if (d0 + q < hidden) unsafeAtomicAdd(out + (size_t)t * hidden + d0 + q, ws * s[q]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Persistent decode forms (Q4_0/Q8_0, rows of at most 128 blocks for gate/up).
+// A launch fills the chip once (MOE_P_BLOCKS workgroups per CU); wavefront w
+// of W owns the contiguous item range [w*I/W, (w+1)*I/W), so the work is
+// balanced to one item.  Each wavefront keeps its lanes' slice of the input
+// vector in registers (blocks lane and lane+64 of the row, with their sums)
+// and double-buffers the weight bytes: the loads of item i+1 are in flight
+// while item i is reduced.  No LDS and no barriers.
+// ---------------------------------------------------------------------------
+#define MOE_P_BLOCKS 2
+
+// Lane slice of a vector: NBL blocks (lane + 64*b of the chunk starting at
+// block c0), 8 float4 and the 32-element sum each; blocks past nb are zero.
+template <int NBL>
+struct XSlice {
+    float4 v[NBL][8];
+    float sum[NBL];
+};
+template <int NBL>
+__device__ __forceinline__ void xslice_load(XSlice<NBL> &xs, const float *__restrict__ x, int c0,
+                                            int nb) {
+    const int lane = threadIdx.x & 63;
 #pragma unroll
-            for (int q = 0; q < MOE_DN_ROWS; q++) res[q] += ws * llg_wave_sum(acc[q]);
+    for (int b = 0; b < NBL; b++) {
+        const int blk = c0 + lane + 64 * b;
+        const float4 *p = reinterpret_cast<const float4 *>(x + (size_t)min(blk, nb - 1) * 32);
+#pragma unroll
+        for (int q = 0; q < 8; q++) xs.v[b][q] = p[q];
+    }
+#pragma unroll
+    for (int b = 0; b < NBL; b++) {
+        const bool ok = c0 + lane + 64 * b < nb;
+        float t = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            if (!ok) xs.v[b][q] = make_float4(0.f, 0.f, 0.f, 0.f);
+            t += (xs.v[b][q].x + xs.v[b][q].y) + (xs.v[b][q].z + xs.v[b][q].w);
         }
-        if (lane == 0) {
+        xs.sum[b] = t;
+    }
+}
+
+// gate/up item = 2 consecutive j of one ts (4 rows: gate j, j+1, up j, j+1).
+template <int T>
+__device__ __forceinline__ void gu_issue(BlockRaw<T> (&r)[2][4], const uint8_t *__restrict__ gate,
+                                         const uint8_t *__restrict__ up, long long stride,
+                                         const RowFmt &f, long long row, int bl0, int bl1) {
+    const uint8_t *p[4] = {gate + row * stride, gate + (row + 1) * stride, up + row * stride,
+                           up + (row + 1) * stride};
 #pragma unroll
-            for (int q = 0; q < MOE_DN_ROWS; q++)
-                if (d0 + q < hidden) out[(size_t)t * hidden + d0 + q] = res[q];
+    for (int q = 0; q < 4; q++) {
+        llg_block_load<T>(r[0][q], p[q], f, bl0);
+        llg_block_load<T>(r[1][q], p[q], f, bl1);
+    }
+}
+
+template <int T>
+__device__ __forceinline__ void gu_finish(const BlockRaw<T> (&r)[2][4], const XSlice<2> &xs,
+                                          bool ok0, bool ok1, float *__restrict__ h2) {
+    float s[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float d0 = llg_raw_dot<T>(r[0][q], xs.v[0], xs.sum[0]);
+        const float d1 = llg_raw_dot<T>(r[1][q], xs.v[1], xs.sum[1]);
+        s[q] = (ok0 ? d0 : 0.0f) + (ok1 ? d1 : 0.0f);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) s[q] = llg_wave_sum(s[q]);
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const float g = s[q], u = s[2 + q];
+            const float silu = g / (1.0f + (float)exp(-(double)g));  // moe_forward.go:130
+            h2[q] = silu * u;
         }
+    }
+}
+
+// Lanes past the row's nb blocks reload its last block (in-bounds loads, no
+// per-lane branch) and drop the product.
+template <int T>
+__global__ __launch_bounds__(256, MOE_P_BLOCKS) void k_moe_gateup_p(
+    const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up, long long stride, RowFmt f,
+    int eff, int k, int n_items, const int32_t *__restrict__ ids,
+    const float *__restrict__ x, float *__restrict__ hbuf, float *__restrict__ zero, int zero_n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < zero_n; i += gridDim.x * blockDim.x)
+        zero[i] = 0.0f;
+    const int lane = threadIdx.x & 63;
+    const long long W = (long long)gridDim.x * 4;
+    const long long w = (long long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int i0 = (int)(w * n_items / W), i1 = (int)((w + 1) * n_items / W);
+    if (i0 >= i1) return;
+    const int per_ts = eff >> 1;
+    const int bl0 = min(lane, f.nb - 1), bl1 = min(lane + 64, f.nb - 1);
+    const bool ok0 = lane < f.nb, ok1 = lane + 64 < f.nb;
+    BlockRaw<T> ra[2][4], rb[2][4];
+    int ts_a = (int)(i0 / per_ts), ts_b;
+    int e = ids[ts_a], ts_e = ts_a;
+    gu_issue<T>(ra, gate, up, stride, f, (long long)e * eff + 2 * (i0 % per_ts), bl0, bl1);
+    XSlice<2> xs;
+    int t_x = ts_a / k;
+    xslice_load<2>(xs, x + (size_t)t_x * f.cols, 0, f.nb);
+    for (int i = i0;;) {
+        // A holds item i
+        if (i + 1 < i1) {
+            ts_b = (int)((i + 1) / per_ts);
+            if (ts_b != ts_e) e = ids[ts_e = ts_b];
+            gu_issue<T>(rb, gate, up, stride, f, (long long)e * eff + 2 * ((i + 1) % per_ts), bl0, bl1);
+        }
+        if (ts_a / k != t_x) xslice_load<2>(xs, x + (size_t)(t_x = ts_a / k) * f.cols, 0, f.nb);
+        gu_finish<T>(ra, xs, ok0, ok1, hbuf + (size_t)ts_a * eff + 2 * (i % per_ts));
+        if (++i >= i1) break;
+        // B holds item i
+        if (i + 1 < i1) {
+            ts_a = (int)((i + 1) / per_ts);
+            if (ts_a != ts_e) e = ids[ts_e = ts_a];
+            gu_issue<T>(ra, gate, up, stride, f, (long long)e * eff + 2 * ((i + 1) % per_ts), bl0, bl1);
+        }
+        if (ts_b / k != t_x) xslice_load<2>(xs, x + (size_t)(t_x = ts_b / k) * f.cols, 0, f.nb);
+        gu_finish<T>(rb, xs, ok0, ok1, hbuf + (size_t)ts_b * eff + 2 * (i % per_ts));
+        if (++i >= i1) break;
+    }
+}
+
+// down item = MOE_DN_P consecutive d of one (ts, chunk of 64 blocks of h):
+// item index = (ts * n_chunks + chunk) * (hidden / MOE_DN_P) + d / MOE_DN_P,
+// so a wavefront's range mostly shares one h slice.  out[t][d] += w_ts *
+// partial (fp32 atomics on the zeroed out).
+#define MOE_DN_P 8
+template <int T>
+__device__ __forceinline__ void dn_issue(BlockRaw<T> (&r)[MOE_DN_P],
+                                         const uint8_t *__restrict__ down, long long stride,
+                                         const RowFmt &f, long long row, int bl) {
+#pragma unroll
+    for (int q = 0; q < MOE_DN_P; q++) llg_block_load<T>(r[q], down + (row + q) * stride, f, bl);
+}
+
+template <int T>
+__device__ __forceinline__ void dn_finish(const BlockRaw<T> (&r)[MOE_DN_P], const XSlice<1> &hs,
+                                          bool ok, float ws, float *__restrict__ o) {
+    float s[MOE_DN_P];
+#pragma unroll
+    for (int q = 0; q < MOE_DN_P; q++) {
+        const float d = llg_raw_dot<T>(r[q], hs.v[0], hs.sum[0]);
+        s[q] = ok ? d : 0.0f;  // lanes past the row's last block
+    }
+#pragma unroll
+    for (int q = 0; q < MOE_DN_P; q++) s[q] = llg_wave_sum(s[q]);
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int q = 0; q < MOE_DN_P; q++) unsafeAtomicAdd(o + q, ws * s[q]);
+    }
+}
+
+template <int T>
+__global__ __launch_bounds__(256, MOE_P_BLOCKS) void k_moe_down_p(
+    const uint8_t *__restrict__ down, long long stride, RowFmt f, int hidden, int k, int n_items,
+    const int32_t *__restrict__ ids, const float *__restrict__ wts, const float *__restrict__ hbuf,
+    float *__restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const long long W = (long long)gridDim.x * 4;
+    const long long w = (long long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int i0 = (int)(w * n_items / W), i1 = (int)((w + 1) * n_items / W);
+    if (i0 >= i1) return;
+    const int n_chunks = (f.nb + 63) >> 6;
+    const int per_chunk = hidden / MOE_DN_P;
+    BlockRaw<T> ra[MOE_DN_P], rb[MOE_DN_P];
+    // item i -> sc = i / per_chunk = ts * n_chunks + chunk, dg = i % per_chunk
+    int sc_a = i0 / per_chunk, sc_b = 0;
+    int ts_e = sc_a / n_chunks, e = ids[ts_e];
+    dn_issue<T>(ra, down, stride, f, (long long)e * hidden + MOE_DN_P * (i0 - sc_a * per_chunk),
+                min((sc_a - ts_e * n_chunks) * 64 + lane, f.nb - 1));
+    int sc_h = sc_a, ts_h = ts_e;
+    XSlice<1> hs;
+    xslice_load<1>(hs, hbuf + (size_t)ts_h * f.cols, (sc_h - ts_h * n_chunks) * 64, f.nb);
+    float ws = wts[ts_h];
+    for (int i = i0;;) {
+        if (i + 1 < i1) {
+            sc_b = (i + 1) / per_chunk;
+            const int tsb = sc_b / n_chunks;
+            if (tsb != ts_e) e = ids[ts_e = tsb];
+            dn_issue<T>(rb, down, stride, f,
+                        (long long)e * hidden + MOE_DN_P * (i + 1 - sc_b * per_chunk),
+                        min((sc_b - tsb * n_chunks) * 64 + lane, f.nb - 1));
+        }
+        if (sc_a != sc_h) {
+            sc_h = sc_a;
+            ts_h = sc_a / n_chunks;
+            xslice_load<1>(hs, hbuf + (size_t)ts_h * f.cols, (sc_h - ts_h * n_chunks) * 64, f.nb);
+            ws = wts[ts_h];
+        }
+        dn_finish<T>(ra, hs, (sc_h - ts_h * n_chunks) * 64 + lane < f.nb, ws,
+                     out + (size_t)(ts_h / k) * hidden + MOE_DN_P * (i - sc_a * per_chunk));
+        if (++i >= i1) break;
+        if (i + 1 < i1) {
+            sc_a = (i + 1) / per_chunk;
+            const int tsa = sc_a / n_chunks;
+            if (tsa != ts_e) e = ids[ts_e = tsa];
+            dn_issue<T>(ra, down, stride, f,
+                        (long long)e * hidden + MOE_DN_P * (i + 1 - sc_a * per_chunk),
+                        min((sc_a - tsa * n_chunks) * 64 + lane, f.nb - 1));
+        }
+        if (sc_b != sc_h) {
+            sc_h = sc_b;
+            ts_h = sc_b / n_chunks;
+            xslice_load<1>(hs, hbuf + (size_t)ts_h * f.cols, (sc_h - ts_h * n_chunks) * 64, f.nb);
+            ws = wts[ts_h];
+        }
+        dn_finish<T>(rb, hs, (sc_h - ts_h * n_chunks) * 64 + lane < f.nb, ws,
+                     out + (size_t)(ts_h / k) * hidden + MOE_DN_P * (i - sc_b * per_chunk));
+        if (++i >= i1) break;
     }
 }
 
@@ -204,6 +509,8 @@ static int check_moe(LlgDevice *d, int64_t hr, int64_t hg, int64_t hu, int64_t h
         return llg_set_error(d, LLG_E_ARG, "moeFFN: down_exps must be [n_exp*hidden x eff]");
     if (a->hidden % 32 || a->eff % 32)
         return llg_set_error(d, LLG_E_ALIGN, "moeFFN: hidden and expertFF must be multiples of 32");
+    if ((size_t)a->gate->fmt.nb * MOE_XS * 4 > 160 * 1024)  // x is staged whole in LDS
+        return llg_set_error(d, LLG_E_ARG, "moeFFN: hidden=%d too long", a->hidden);
     return 0;
 }
 
@@ -218,19 +525,52 @@ static size_t moe_ws_bytes(const MoeArgs &a, int n_tok) {
     return head + (size_t)n_tok * a.k * a.eff * 4;
 }
 
+template <int T, int NB>
+static void moe_launch_experts_nb(hipStream_t st, const MoeArgs &a, int n_tok, const int32_t *ids,
+                                  const float *w, const float *x, float *hbuf, float *out) {
+    const long long nts = (long long)n_tok * a.k;
+    const long long g1 = nts * ((a.eff + MOE_GU_TILE - 1) / MOE_GU_TILE);
+    hipLaunchKernelGGL((k_moe_gateup<T, NB>), dim3((unsigned)g1), dim3(256),
+                       (size_t)a.gate->fmt.nb * MOE_XS * 4, st, a.gate->d, a.up->d, a.gate->stride,
+                       a.gate->fmt, a.eff, a.k, ids, x, hbuf, out, n_tok * a.hidden);
+    const int nb = a.down->fmt.nb;
+    const int n_chunks = (nb + MOE_DN_CHUNK - 1) / MOE_DN_CHUNK;
+    const int cb = (nb + n_chunks - 1) / n_chunks;
+    const long long g2 = nts * ((a.hidden + MOE_DN_TILE - 1) / MOE_DN_TILE) * n_chunks;
+    hipLaunchKernelGGL((k_moe_down<T, 3>), dim3((unsigned)g2), dim3(256), (size_t)cb * MOE_XS * 4,
+                       st, a.down->d, a.down->stride, a.down->fmt, a.hidden, a.k, cb, ids, w, hbuf,
+                       out);
+}
+
+// Q4_0/Q8_0 with hidden <= 4096 take the persistent kernels; other shapes and
+// types the workgroup-per-tile kernels above.
 template <int T>
-static void moe_launch_experts(hipStream_t st, const MoeArgs &a, int n_tok, const int32_t *ids,
-                               const float *w, const float *x, float *hbuf, float *out) {
-    const long long gu_waves = (long long)n_tok * a.k * a.eff;
-    long long g1 = (gu_waves + 3) / 4;
-    if (g1 > 8192) g1 = 8192;
-    hipLaunchKernelGGL(k_moe_gateup<T>, dim3((unsigned)g1), dim3(256), 0, st, a.gate->d, a.up->d,
-                       a.gate->stride, a.gate->fmt, a.eff, a.k, n_tok, ids, x, hbuf);
-    const long long dn_waves = (long long)n_tok * ((a.hidden + MOE_DN_ROWS - 1) / MOE_DN_ROWS);
-    long long g2 = (dn_waves + 3) / 4;
-    if (g2 > 8192) g2 = 8192;
-    hipLaunchKernelGGL(k_moe_down<T>, dim3((unsigned)g2), dim3(256), 0, st, a.down->d,
-                       a.down->stride, a.down->fmt, a.hidden, a.k, n_tok, ids, w, hbuf, out);
+static void moe_launch_experts(hipStream_t st, int cus, const MoeArgs &a, int n_tok,
+                               const int32_t *ids, const float *w, const float *x, float *hbuf,
+                               float *out) {
+    if constexpr (T == LLG_TYPE_Q4_0 || T == LLG_TYPE_Q8_0) {
+        const long long n_dn = (long long)n_tok * a.k * ((a.down->fmt.nb + 63) / 64) * a.hidden / MOE_DN_P;
+        if (a.gate->fmt.nb <= 128 && a.hidden % MOE_DN_P == 0 && n_dn < (1LL << 31) &&
+            (long long)n_tok * a.k * a.eff < (1LL << 31)) {
+            const long long nts = (long long)n_tok * a.k;
+            const long long gu_items = nts * (a.eff / 2);
+            const int n_chunks = (a.down->fmt.nb + 63) / 64;
+            const long long dn_items = nts * n_chunks * (a.hidden / MOE_DN_P);
+            const long long full = (long long)cus * MOE_P_BLOCKS;
+            const long long g1 = std::min(full, (gu_items + 3) / 4);
+            const long long g2 = std::min(full, (dn_items + 3) / 4);
+            hipLaunchKernelGGL(k_moe_gateup_p<T>, dim3((unsigned)g1), dim3(256), 0, st, a.gate->d,
+                               a.up->d, a.gate->stride, a.gate->fmt, a.eff, a.k, (int)gu_items, ids, x, hbuf,
+                               out, n_tok * a.hidden);
+            hipLaunchKernelGGL(k_moe_down_p<T>, dim3((unsigned)g2), dim3(256), 0, st, a.down->d,
+                               a.down->stride, a.down->fmt, a.hidden, a.k, (int)dn_items, ids, w, hbuf, out);
+            return;
+        }
+    }
+    if (a.gate->fmt.nb <= 64)
+        moe_launch_experts_nb<T, 1>(st, a, n_tok, ids, w, x, hbuf, out);
+    else
+        moe_launch_experts_nb<T, 2>(st, a, n_tok, ids, w, x, hbuf, out);
 }
 
 static int moe_enqueue(LlgDevice *d, const MoeArgs &a, const float *d_x, int n_tok, float *d_out,
@@ -248,16 +588,16 @@ static int moe_enqueue(LlgDevice *d, const MoeArgs &a, const float *d_x, int n_t
                                     n_tok, ids, w, d_out, ws + 2 * kb);
     switch (a.gate->fmt.type) {
     case LLG_TYPE_Q4_0:
-        moe_launch_experts<LLG_TYPE_Q4_0>(st, a, n_tok, ids, w, d_x, hbuf, d_out);
+        moe_launch_experts<LLG_TYPE_Q4_0>(st, llg_cu_count(d), a, n_tok, ids, w, d_x, hbuf, d_out);
         break;
     case LLG_TYPE_Q8_0:
-        moe_launch_experts<LLG_TYPE_Q8_0>(st, a, n_tok, ids, w, d_x, hbuf, d_out);
+        moe_launch_experts<LLG_TYPE_Q8_0>(st, llg_cu_count(d), a, n_tok, ids, w, d_x, hbuf, d_out);
         break;
     case LLG_TYPE_F16:
-        moe_launch_experts<LLG_TYPE_F16>(st, a, n_tok, ids, w, d_x, hbuf, d_out);
+        moe_launch_experts<LLG_TYPE_F16>(st, llg_cu_count(d), a, n_tok, ids, w, d_x, hbuf, d_out);
         break;
     case LLG_TYPE_F32:
-        moe_launch_experts<LLG_TYPE_F32>(st, a, n_tok, ids, w, d_x, hbuf, d_out);
+        moe_launch_experts<LLG_TYPE_F32>(st, llg_cu_count(d), a, n_tok, ids, w, d_x, hbuf, d_out);
         break;
     default:
         return llg_set_error(d, LLG_E_TYPE, "moe: unsupported type");

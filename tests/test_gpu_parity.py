@@ -259,10 +259,23 @@ def test_moe_route_bit_exact(dev, rng):
     lg = normal(rng, (200, 8), 1.5)
     lg[0] = 0.0                          # all tied
     lg[1] = [0, 1, 1, 1, 0, 0, 0, 0]     # three-way tie for first
+    lg[2, 3] = np.nan                    # every score NaN: index order kept
+    lg[3, 5] = np.inf                    # inf - inf: every score NaN
+    lg[4] = [-200, 0, -300, 0, -1e30, 5, 5, -5]  # underflow to exact zeros
     ids, w = dev.moe_route(lg, 2)
     for t in range(lg.shape[0]):
         rid, rw = R.moe_route(lg[t], 2)
-        assert np.array_equal(ids[t], rid)
+        assert np.array_equal(ids[t], rid), t
+        if t in (2, 3):
+            assert np.all(np.isnan(w[t])) and np.all(np.isnan(rw))
+        else:
+            assert np.array_equal(w[t].view(np.uint32), rw.view(np.uint32)), t
+    lg64 = normal(rng, (50, 64), 2.0)
+    lg64[:, 10] = lg64[:, 40]            # ties across a wide expert set
+    ids, w = dev.moe_route(lg64, 8)
+    for t in range(lg64.shape[0]):
+        rid, rw = R.moe_route(lg64[t], 8)
+        assert np.array_equal(ids[t], rid), t
         assert np.array_equal(w[t].view(np.uint32), rw.view(np.uint32)), t
 
 
