@@ -14,8 +14,8 @@ their average event-timed duration on the library's stream) and a
 `cpu_baseline` object (the oracle's restatement of the reference CPU path,
 timed on a bounded sample on this host).
 
-Other workloads (--workload dense-q4_0 | dense-q8_0 | dense-f16 | moe-decode |
-moe-prefill) measure the remaining hot-path configurations.
+Other workloads (--workload dense-q4_0 | dense-q8_0 | dense-f16 | window |
+moe-decode | moe-prefill) measure the remaining hot-path configurations.
 """
 from __future__ import annotations
 
@@ -251,6 +251,123 @@ def bench_dense(args, torch, llg, dev, t):
                          "alg_bytes_per_launch": alg, "avg_launch_us": ms * 1e3}}
 
 
+WIN_K, WIN_SEQ, WIN_KEEP = 5, 64, 0.7
+
+
+def window_sets(seed: int, n_tok: int) -> list:
+    """Active sets of a decode sequence: 909 of 18176 neurons per token, 70%
+    drawn from the previous token's set and the rest uniform over the others,
+    each ascending."""
+    r = np.random.default_rng(seed)
+    sets = [np.sort(r.choice(FF, N_ACTIVE, replace=False))]
+    keep = int(round(WIN_KEEP * N_ACTIVE))
+    for _ in range(n_tok - 1):
+        kept = r.choice(sets[-1], keep, replace=False)
+        rest = np.setdiff1d(np.arange(FF), kept, assume_unique=True)
+        new = r.choice(rest, N_ACTIVE - keep, replace=False)
+        sets.append(np.sort(np.concatenate([kept, new])))
+    return [s.astype(np.int32) for s in sets]
+
+
+def window_loads(sets: list, k: int) -> list:
+    """Neurons each Update must load: active minus the union of the last k
+    sets (the resident set; inference/window.go:71-117)."""
+    loads, ring = [], []
+    for s in sets:
+        res = set().union(*ring) if ring else set()
+        loads.append(len(set(s.tolist()) - res))
+        ring = (ring + [set(s.tolist())])[-k:]
+    return loads
+
+
+def bench_window(args, torch, llg, dev):
+    """Sliding-window decode (window.go Update + FFNForward) over 64-token
+    sequences of the Falcon-7B-shaped Q4_0 layer, k=5: per token the window
+    state update, the gather of newly needed bundles into resident slots, and
+    the gathered FFN over the resident rows (llg_hipd_window_step).  Sequence
+    r runs on its own window over its own bundle copy."""
+    gg = llg.gguf
+    n_seq = (args.steps + WIN_SEQ - 1) // WIN_SEQ
+    n_warm = max(1, (args.warmup + WIN_SEQ - 1) // WIN_SEQ)
+    n_copies = min(args.layers, n_seq + n_warm)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x11A3A002)
+    up = gg.quantize(torch.randn((FF, H), generator=g, device="cuda") * 0.02, gg.Q4_0)
+    dn = gg.quantize(torch.randn((FF, H), generator=g, device="cuda") * 0.02, gg.Q4_0)
+    X = torch.randn((WIN_SEQ, H), generator=g, device="cuda")
+    torch.cuda.synchronize()
+    bundles = [dev.upload_bundle(up, dn, gg.Q4_0, H, FF) for _ in range(n_copies)]
+    sets = window_sets(0x5E7, WIN_SEQ)
+    loads = window_loads(sets, WIN_K)
+    act = torch.tensor(np.stack(sets), device="cuda")
+    nact = torch.full((WIN_SEQ, 1), N_ACTIVE, dtype=torch.int32, device="cuda")
+    out = torch.empty((WIN_SEQ, H), device="cuda")
+    wins = [llg.NeuronCache(dev, bundles[i % n_copies], WIN_K) for i in range(n_warm + n_seq)]
+    lib = dev.lib
+
+    def step(i):
+        w, t = wins[i // WIN_SEQ], i % WIN_SEQ
+        rc = lib.llg_hipd_window_step(dev.h, w.win.id, vp(X[t]), vp(act[t]), vp(nact[t]),
+                                      gg.ACT_RELU, vp(out[t]))
+        if rc:
+            dev.check(rc, "window_step")
+
+    tm = Timer(torch, dev.stream)
+    for i in range(n_warm * WIN_SEQ):
+        step(i)
+    dev.sync()
+    base = n_warm * WIN_SEQ
+    e0 = tm.event()
+    for i in range(args.steps):
+        step(base + i)
+    e1 = tm.event()
+    dev.sync()
+    ms = e0.elapsed_time(e1) / args.steps
+    for w in wins:
+        w.win.release()
+    for b in bundles:
+        b.release()
+    n_load = float(np.mean([loads[i % WIN_SEQ] for i in range(args.steps)]))
+    alg = N_ACTIVE * BUNDLE_ALG + 2 * n_load * BUNDLE_ALG
+    gbs = alg / (ms * 1e-3) / 1e9
+    res = {"metric": "sliding-window sparse-FFN decode tokens/s", "value": 1000.0 / ms,
+           "unit": "tokens/s", "ms_per_step": ms, "dtype": "f32",
+           "config": {"workload": "falcon7b-ffn-layer-q4_0-window5-decode64", "d_model": H,
+                      "d_ff": FF, "window_k": WIN_K, "active": N_ACTIVE, "keep_from_prev": WIN_KEEP,
+                      "tokens_per_sequence": WIN_SEQ, "mean_loaded_per_token": n_load,
+                      "bundle_copies": n_copies},
+           "roofline": {"bound": "hbm", "kernel": "k_window_update + k_window_gather + k_list_up "
+                        "+ k_sparse_down (one token)", "achieved": gbs, "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                        "alg_bytes_per_step": alg, "avg_step_us": ms * 1e3}}
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline_window(args, up.cpu().numpy(), dn.cpu().numpy(),
+                                                  X.cpu().numpy(), sets)
+    return res
+
+
+def cpu_baseline_window(args, up, dn, X, sets):
+    """The oracle's NeuronCache (window.go Update + FFNForward), 1 thread,
+    over the 64-token sequence (repeated on fresh caches up to the time bound)."""
+    from oracle import refcpu as R
+
+    log("cpu baseline: oracle window update + FFNForward, 1 thread")
+    n, t0 = 0, time.perf_counter()
+    while True:
+        nc = R.NeuronCache(FF, H, WIN_K, FF, up, dn, R.Q4_0)
+        for t in range(WIN_SEQ):
+            nc.update(sets[t])
+            nc.ffn_forward(X[t], sets[t])
+            n += 1
+            if time.perf_counter() - t0 >= args.cpu_seconds:
+                break
+        el = time.perf_counter() - t0
+        if el >= args.cpu_seconds or n >= args.cpu_max_tokens:
+            break
+    return {"value": n / el, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{n} window decode tokens (Update + FFNForward, k={WIN_K}), {el:.1f} s"}
+
+
 MOE_D, MOE_FF, MOE_E, MOE_K, MOE_PREFILL = 4096, 14336, 8, 2, 512
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
@@ -336,8 +453,8 @@ def main():
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="sparse",
-                    choices=["sparse", "dense-q4_0", "dense-q8_0", "dense-f16", "moe-decode",
-                             "moe-prefill"])
+                    choices=["sparse", "dense-q4_0", "dense-q8_0", "dense-f16", "window",
+                             "moe-decode", "moe-prefill"])
     ap.add_argument("--layers", type=int, default=0,
                     help="distinct HBM copies rotated per step (0 = enough to defeat the MALL)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -350,7 +467,8 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     if args.layers <= 0:
-        args.layers = {"sparse": 128, "moe-decode": 2, "moe-prefill": 1}.get(args.workload, 6)
+        args.layers = {"sparse": 128, "window": 16, "moe-decode": 2,
+                       "moe-prefill": 1}.get(args.workload, 6)
 
     import torch
     import llg
@@ -362,6 +480,8 @@ def main():
     gg = llg.gguf
     if args.workload == "sparse":
         res = bench_sparse(args, torch, llg, dev)
+    elif args.workload == "window":
+        res = bench_window(args, torch, llg, dev)
     elif args.workload.startswith("moe-"):
         res = bench_moe(args, torch, llg, dev, args.workload == "moe-prefill")
     else:

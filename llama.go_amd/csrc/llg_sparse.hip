@@ -23,8 +23,8 @@
 // k_sparse_down: workgroup (slice s of 8 blocks = 256 outputs, pair group g);
 // the four wavefronts split the group's pairs, 8 pairs per wavefront pass
 // (lane = pair sub-index * 8 + block); u == 0 rows are skipped as at
-// ffn_flash.go:290; the per-slice sums are reduced across lanes and waves and
-// added to out with one fp32 atomic per output.  blockIdx -> (s, g) keeps all
+// ffn_flash.go:290; the per-slice sums are reduced across lanes (one DPP step)
+// and through LDS, and added to out with one fp32 atomic per output.  blockIdx -> (s, g) keeps all
 // slices of a group on one XCD (workgroups go round-robin over the 8 XCDs).
 #include "llg_common.hpp"
 #include "llg_internal.hpp"
@@ -34,6 +34,8 @@
 #define DN_SLICE 8        // blocks per down slice
 #define BATCH 4           // blocks whose loads a lane issues together
 #define PRED_SPLIT_N 8    // partials per hidden unit written by k_pred_hidden
+#define DN_HEAD 8         // pair slots per tile that k_sparse_down reads with the counts
+#define DN_RED_ST 36      // LDS floats per (row, block) partial in the down reduction
 
 __device__ __forceinline__ void stage_x(float *xs, const float *__restrict__ x, int nb) {
     llg_stage_x_sum<XS_STRIDE>(xs, x, nb);
@@ -91,6 +93,78 @@ __device__ __forceinline__ void row_dot2(const uint8_t *__restrict__ base, long 
     s1 = llg_wave_sum(a1);
 }
 
+// Up-row dot products of NR rows (wavefront-uniform indices, < 0: none) by
+// one wavefront, NBATCH blocks per lane per pass, all loads of a pass issued
+// before any is used; same conventions as row_dot2.
+template <int T, int NR, int NBATCH>
+__device__ __forceinline__ void row_dotn(const uint8_t *__restrict__ base, long long bstride,
+                                         const int (&row)[NR], const RowFmt &f, const float *xs,
+                                         float (&s)[NR]) {
+    const int lane = threadIdx.x & 63;
+    const uint8_t *p[NR];
+    bool v[NR];
+#pragma unroll
+    for (int q = 0; q < NR; q++) {
+        const int r = __builtin_amdgcn_readfirstlane(row[q]);
+        v[q] = r >= 0;
+        p[q] = base + (long long)(v[q] ? r : 0) * bstride;
+        s[q] = 0.0f;
+    }
+    for (int b0 = 0; b0 < f.nb; b0 += 64 * NBATCH) {
+        BlockRaw<T> r[NBATCH][NR];
+#pragma unroll
+        for (int i = 0; i < NBATCH; i++)
+#pragma unroll
+            for (int q = 0; q < NR; q++)
+                llg_block_load<T>(r[i][q], p[q], f, min(b0 + lane + 64 * i, f.nb - 1));
+#pragma unroll
+        for (int i = 0; i < NBATCH; i++) {
+            const int b = b0 + lane + 64 * i;
+            if (b < f.nb) {
+                const float *xb = xs + b * XS_STRIDE;
+                const float4 *x4 = reinterpret_cast<const float4 *>(xb);
+#pragma unroll
+                for (int q = 0; q < NR; q++) {
+                    const float d = llg_raw_dot<T>(r[i][q], x4, xb[32]);
+                    s[q] += v[q] ? d : 0.0f;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < NR; q++) s[q] = llg_wave_sum(s[q]);
+}
+
+// One round of the tile's up rows: neuron k0 + wave + 4*i (i < NR) on this
+// wavefront; nonzero u go to the tile's pair slots through the LDS counter.
+template <int T, int NR>
+__device__ __forceinline__ void tile_up_round(const uint8_t *__restrict__ base, long long bstride,
+                                              const RowFmt &f, const float *xs, const int *tl,
+                                              int *ctr, int cnt, int k0, int tile0, int act,
+                                              int2 *__restrict__ tpairs) {
+    const int wave = threadIdx.x >> 6;
+    int rows[NR];
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+        const int k = k0 + wave + 4 * i;
+        rows[i] = k < cnt ? tile0 + tl[k] : -1;
+    }
+    if (rows[0] < 0) return;  // wavefront-uniform: nothing in this round
+    float s[NR];
+    row_dotn<T, NR, NR == 4 ? 3 : 4>(base, bstride, rows, f, xs, s);
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int i = 0; i < NR; i++) {
+            if (rows[i] < 0) break;
+            const float u = llg_act(act, s[i]);
+            if (u != 0.0f) {  // ffn_flash.go:290 skips zero activations
+                const int pos = atomicAdd(ctr, 1);  // LDS atomic, tile-local slot
+                tpairs[pos] = make_int2(rows[i], __float_as_int(u));
+            }
+        }
+    }
+}
+
 // B. explicit list: pair j = (row of active[j], act(up . x)); also zeroes out.
 template <int T>
 __global__ __launch_bounds__(256) void k_list_up(const uint8_t *__restrict__ base,
@@ -142,7 +216,7 @@ __global__ __launch_bounds__(256) void k_tile_up(
     float *lg = hid + ((rank + 3) & ~3);                // 64
     int *tl = reinterpret_cast<int *>(lg + 64);         // 64 tile-local indices, count, nnz
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tile0 = blockIdx.x * 64;
     WoutTile t;
     load_wout_tile(t, wout, wstride, ff, rank, tile0);  // loads first, used after the barrier
@@ -170,25 +244,20 @@ __global__ __launch_bounds__(256) void k_tile_up(
     }
     __syncthreads();
     const int cnt = tl[64];
-    for (int k = wave; k < cnt; k += 8) {  // two neurons per wavefront per round
-        const int n0 = tile0 + tl[k];
-        const int n1 = k + 4 < cnt ? tile0 + tl[k + 4] : -1;
-        float s0, s1;
-        row_dot2<T>(base, bstride, n0, n1, f, xs, s0, s1);
-        if (lane == 0) {  // ffn_flash.go:290 skips zero activations
-            const float u0 = llg_act(act, s0);
-            if (u0 != 0.0f) {
-                const int pos = atomicAdd(&tl[65], 1);  // LDS atomic, tile-local slot
-                pairs[blockIdx.x * 64 + pos] = make_int2(n0, __float_as_int(u0));
-            }
-            if (n1 >= 0) {
-                const float u1 = llg_act(act, s1);
-                if (u1 != 0.0f) {
-                    const int pos = atomicAdd(&tl[65], 1);
-                    pairs[blockIdx.x * 64 + pos] = make_int2(n1, __float_as_int(u1));
-                }
-            }
-        }
+    // up rows of the active neurons, one round of loads for up to 16 (1, 2 or
+    // 4 rows per wavefront by count: sparse tiles request no spare rows)
+    constexpr int UPMAX = T == LLG_TYPE_F32 ? 1 : T == LLG_TYPE_F16 ? 2 : 4;
+    int2 *tpairs = pairs + (size_t)blockIdx.x * 64;
+    if (cnt <= 4 || UPMAX == 1) {
+        for (int k0 = 0; k0 < cnt; k0 += 4)
+            tile_up_round<T, 1>(base, bstride, f, xs, tl, &tl[65], cnt, k0, tile0, act, tpairs);
+    } else if (cnt <= 8 || UPMAX == 2) {
+        for (int k0 = 0; k0 < cnt; k0 += 8)
+            tile_up_round<T, 2>(base, bstride, f, xs, tl, &tl[65], cnt, k0, tile0, act, tpairs);
+    } else {
+        if constexpr (UPMAX == 4)
+            for (int k0 = 0; k0 < cnt; k0 += 16)
+                tile_up_round<T, 4>(base, bstride, f, xs, tl, &tl[65], cnt, k0, tile0, act, tpairs);
     }
     __syncthreads();
     if (threadIdx.x == 0) tile_cnt[blockIdx.x] = tl[65];
@@ -205,8 +274,9 @@ __global__ __launch_bounds__(256) void k_sparse_down(
     const int32_t *__restrict__ count_p, const int32_t *__restrict__ tile_cnt, int n_tiles,
     const unsigned long long *__restrict__ mask, int32_t *__restrict__ n_active_out,
     int n_slices, int n_groups, float *__restrict__ out) {
-    __shared__ float red[4][DN_SLICE * 32];
+    __shared__ __attribute__((aligned(16))) float red[16 * DN_SLICE * DN_RED_ST];
     __shared__ int pref[65];
+    __shared__ int2 head[64 * DN_HEAD];  // the first DN_HEAD pair slots of each tile
     const int id = blockIdx.x;
     const int xcd = id & 7;
     const int k = id >> 3;
@@ -218,6 +288,11 @@ __global__ __launch_bounds__(256) void k_sparse_down(
     if (TILED) {
         tg = (n_tiles + n_groups - 1) / n_groups;  // <= 64 (checked on the host)
         t0 = g * tg;
+        // the counts and the first DN_HEAD slots of every tile, in one round
+        for (int i = threadIdx.x; i < tg * DN_HEAD; i += blockDim.x) {
+            const int tt = min(t0 + i / DN_HEAD, n_tiles - 1);
+            head[i] = pairs[tt * 64 + i % DN_HEAD];
+        }
         if (wave == 0) {
             const int c = (lane < tg && t0 + lane < n_tiles) ? tile_cnt[t0 + lane] : 0;
             int incl = c;
@@ -259,11 +334,13 @@ __global__ __launch_bounds__(256) void k_sparse_down(
             if (TILED) {
                 int t = 0;
                 while (pref[t + 1] <= j) t++;
-                p0 = pairs[(t0 + t) * 64 + (j - pref[t])];
+                int k = j - pref[t];
+                p0 = k < DN_HEAD ? head[t * DN_HEAD + k] : pairs[(t0 + t) * 64 + k];
                 if (j + 32 < j1) {
                     const int jj = j + 32;
                     while (pref[t + 1] <= jj) t++;
-                    p1 = pairs[(t0 + t) * 64 + (jj - pref[t])];
+                    k = jj - pref[t];
+                    p1 = k < DN_HEAD ? head[t * DN_HEAD + k] : pairs[(t0 + t) * 64 + k];
                 }
             } else {
                 p0 = pairs[j];
@@ -281,24 +358,28 @@ __global__ __launch_bounds__(256) void k_sparse_down(
             if (u1 != 0.0f) llg_raw_axpy<T>(r1, u1, acc, corr);
         }
     }
+    // Sum over the 8 pair sub-lanes and 4 wavefronts sharing block bl: one DPP
+    // step folds sub-lanes 2r+1 into 2r (row_ror:8 within each 16-lane row),
+    // then the 16 partial sums per output meet in LDS (row stride 36 floats).
 #pragma unroll
-    for (int e = 0; e < 32; e++) acc[e] -= corr;
-#pragma unroll
-    for (int e = 0; e < 32; e++) {  // sum over the 8 pair sub-lanes sharing block bl
-        float v = acc[e];
-        v += llg_dpp<0x128>(v);  // row_ror:8 pairs lanes l and l+8 of each row
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        acc[e] = v;
+    for (int e = 0; e < 32; e++) {
+        const float v = acc[e] - corr;
+        acc[e] = v + llg_dpp<0x128>(v);
     }
-    if (sub == 0) {
+    if ((lane & 8) == 0) {
+        float *dst = &red[((wave * 4 + (lane >> 4)) * DN_SLICE + bl) * DN_RED_ST];
 #pragma unroll
-        for (int e = 0; e < 32; e++) red[wave][bl * 32 + e] = acc[e];
+        for (int q = 0; q < 8; q++)
+            *reinterpret_cast<float4 *>(dst + 4 * q) =
+                make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
     }
     __syncthreads();
     const int t = threadIdx.x;
     const int o = s * DN_SLICE * 32 + t;
-    if (o < f.cols) unsafeAtomicAdd(out + o, red[0][t] + red[1][t] + red[2][t] + red[3][t]);
+    float sum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) sum += red[(r * DN_SLICE + (t >> 5)) * DN_RED_ST + (t & 31)];
+    if (o < f.cols) unsafeAtomicAdd(out + o, sum);
 }
 
 // ---------------------------------------------------------------------------
