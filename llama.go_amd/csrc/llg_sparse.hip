@@ -7,7 +7,8 @@
 //     K1 k_pred_hidden (llg_predictor.hip): hidden partials; zeroes out/counters
 //     K2 k_tile_up: one workgroup per 64-neuron tile: logits from WOut rows,
 //        strict '>' against the threshold via a wavefront ballot, then the up
-//        dot product of each of the tile's active neurons, u = act(up . x);
+//        dot product of each of the tile's active neurons, u = act(up . x),
+//        one neuron per wavefront of 8 (two when more than 8 are active);
 //        nonzero u go to the tile's own 64 pair slots (an LDS counter orders
 //        them), so no two workgroups touch one address
 //     K3 k_sparse_down over the tiles' pairs
@@ -36,6 +37,7 @@
 #define PRED_SPLIT_N 8    // partials per hidden unit written by k_pred_hidden
 #define DN_HEAD 8         // pair slots per tile that k_sparse_down reads with the counts
 #define DN_RED_ST 36      // LDS floats per (row, block) partial in the down reduction
+#define TILE_THREADS 512  // k_tile_up workgroup: 8 wavefronts for the up rows
 
 __device__ __forceinline__ void stage_x(float *xs, const float *__restrict__ x, int nb) {
     llg_stage_x_sum<XS_STRIDE>(xs, x, nb);
@@ -135,23 +137,23 @@ __device__ __forceinline__ void row_dotn(const uint8_t *__restrict__ base, long 
     for (int q = 0; q < NR; q++) s[q] = llg_wave_sum(s[q]);
 }
 
-// One round of the tile's up rows: neuron k0 + wave + 4*i (i < NR) on this
+// One round of the tile's up rows: neuron k0 + wave + nw*i (i < NR) on this
 // wavefront; nonzero u go to the tile's pair slots through the LDS counter.
 template <int T, int NR>
 __device__ __forceinline__ void tile_up_round(const uint8_t *__restrict__ base, long long bstride,
                                               const RowFmt &f, const float *xs, const int *tl,
                                               int *ctr, int cnt, int k0, int tile0, int act,
                                               int2 *__restrict__ tpairs) {
-    const int wave = threadIdx.x >> 6;
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     int rows[NR];
 #pragma unroll
     for (int i = 0; i < NR; i++) {
-        const int k = k0 + wave + 4 * i;
+        const int k = k0 + wave + nw * i;
         rows[i] = k < cnt ? tile0 + tl[k] : -1;
     }
     if (rows[0] < 0) return;  // wavefront-uniform: nothing in this round
     float s[NR];
-    row_dotn<T, NR, NR == 4 ? 3 : 4>(base, bstride, rows, f, xs, s);
+    row_dotn<T, NR, NR == 1 ? 4 : 3>(base, bstride, rows, f, xs, s);
     if ((threadIdx.x & 63) == 0) {
 #pragma unroll
         for (int i = 0; i < NR; i++) {
@@ -204,7 +206,7 @@ __global__ __launch_bounds__(256) void k_list_up(const uint8_t *__restrict__ bas
 // A. predictor-fused tile kernel.  Tile t writes its nonzero (row, u) pairs
 // to pairs[t*64 + k], k < tile_cnt[t]: fixed slots, so no global counter.
 template <int T>
-__global__ __launch_bounds__(256) void k_tile_up(
+__global__ __launch_bounds__(TILE_THREADS, 2) void k_tile_up(
     const uint8_t *__restrict__ wout, long long wstride, int ff, int rank,
     const float *__restrict__ partial, const float *__restrict__ bias, float thr,
     const uint8_t *__restrict__ base, long long bstride, RowFmt f, const float *__restrict__ x,
@@ -218,12 +220,12 @@ __global__ __launch_bounds__(256) void k_tile_up(
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tile0 = blockIdx.x * 64;
-    WoutTile t;
-    load_wout_tile(t, wout, wstride, ff, rank, tile0);  // loads first, used after the barrier
+    WoutTile t;  // logits: wavefronts 0-3 (16 neurons each)
+    if (wave < 4) load_wout_tile(t, wout, wstride, ff, rank, tile0);  // used after the barrier
     stage_x(xs, x, f.nb);
     load_hidden<PRED_SPLIT_N>(hid, partial, rank);
     __syncthreads();
-    finish_logits(t, wout, wstride, ff, rank, tile0, hid, lg);
+    if (wave < 4) finish_logits(t, wout, wstride, ff, rank, tile0, hid, lg);
     __syncthreads();
     if (wave == 0) {
         const int i = tile0 + lane;
@@ -244,20 +246,18 @@ __global__ __launch_bounds__(256) void k_tile_up(
     }
     __syncthreads();
     const int cnt = tl[64];
-    // up rows of the active neurons, one round of loads for up to 16 (1, 2 or
-    // 4 rows per wavefront by count: sparse tiles request no spare rows)
-    constexpr int UPMAX = T == LLG_TYPE_F32 ? 1 : T == LLG_TYPE_F16 ? 2 : 4;
+    // up rows of the active neurons on all TILE_THREADS/64 wavefronts, one
+    // round of loads for up to 16 (1 or 2 rows per wavefront by count)
+    constexpr int UPMAX = T == LLG_TYPE_F32 ? 1 : 2;
+    const int nw = TILE_THREADS / 64;
     int2 *tpairs = pairs + (size_t)blockIdx.x * 64;
-    if (cnt <= 4 || UPMAX == 1) {
-        for (int k0 = 0; k0 < cnt; k0 += 4)
+    if (cnt <= nw || UPMAX == 1) {
+        for (int k0 = 0; k0 < cnt; k0 += nw)
             tile_up_round<T, 1>(base, bstride, f, xs, tl, &tl[65], cnt, k0, tile0, act, tpairs);
-    } else if (cnt <= 8 || UPMAX == 2) {
-        for (int k0 = 0; k0 < cnt; k0 += 8)
-            tile_up_round<T, 2>(base, bstride, f, xs, tl, &tl[65], cnt, k0, tile0, act, tpairs);
     } else {
-        if constexpr (UPMAX == 4)
-            for (int k0 = 0; k0 < cnt; k0 += 16)
-                tile_up_round<T, 4>(base, bstride, f, xs, tl, &tl[65], cnt, k0, tile0, act, tpairs);
+        if constexpr (UPMAX == 2)
+            for (int k0 = 0; k0 < cnt; k0 += 2 * nw)
+                tile_up_round<T, 2>(base, bstride, f, xs, tl, &tl[65], cnt, k0, tile0, act, tpairs);
     }
     __syncthreads();
     if (threadIdx.x == 0) tile_cnt[blockIdx.x] = tl[65];
@@ -466,7 +466,7 @@ static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial, 
     const int n_tiles = (ff + 63) / 64;
     const RowFmt &f = b->fmt;
     const size_t lds = xs_bytes(f) + (size_t)(((rank + 3) & ~3) + 64 + 66) * 4;
-    hipLaunchKernelGGL(k_tile_up<T>, dim3(n_tiles), dim3(256), lds, st, wout->d, wout->stride, ff,
+    hipLaunchKernelGGL(k_tile_up<T>, dim3(n_tiles), dim3(TILE_THREADS), lds, st, wout->d, wout->stride, ff,
                        rank, partial, bias, thr, b->d, b->stride, f, x, act, mask, pairs,
                        tile_cnt);
     const int n_slices = (f.nb + DN_SLICE - 1) / DN_SLICE;
