@@ -38,6 +38,11 @@ H, FF, RANK, N_ACTIVE = 4544, 18176, 128, 909
 Q4_ROW = H // 32 * 18                # 2556 B per GGUF Q4_0 row
 BUNDLE_ALG = 2 * Q4_ROW              # 5112 B per neuron (unpadded)
 PRED_BYTES = (RANK * H + FF * RANK) * 4
+# HBM bytes per sparse step from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE over
+# k_pred_hidden + k_tile_up + k_sparse_down, each counter scaled by its reading
+# for a 1 GiB streaming copy (FETCH x2.0, WRITE x1.0); the summary with the
+# commands is profiles/sparse_step_falcon7b_q4_0_hbm_traffic.md.
+SPARSE_STEP_TRAFFIC = 16.50e6
 
 
 def log(msg: str):
@@ -169,7 +174,7 @@ def bench_sparse(args, torch, llg, dev):
         "roofline": {"bound": "hbm",
                      "kernel": "k_pred_hidden + k_tile_up + k_sparse_down (one decode step)",
                      "achieved": step_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": step_gbs / HBM_PEAK_GBS, "traffic": None,
+                     "frac": step_gbs / HBM_PEAK_GBS, "traffic": SPARSE_STEP_TRAFFIC,
                      "alg_bytes_per_launch": step_alg, "avg_launch_us": ms_step * 1e3},
         "breakdown": {
             "ffn_list_path_us": ffn_ms * 1e3,
@@ -255,15 +260,15 @@ WIN_K, WIN_SEQ, WIN_KEEP = 5, 64, 0.7
 
 
 def window_sets(seed: int, n_tok: int) -> list:
-    """Active sets of a decode sequence: 909 of 18176 neurons per token, 70%
-    drawn from the previous token's set and the rest uniform over the others,
-    each ascending."""
+    """Active sets of a decode sequence: 909 of 18176 neurons per token, 636
+    drawn from the previous token's set and 273 uniform over the neurons not
+    in it, each set ascending."""
     r = np.random.default_rng(seed)
     sets = [np.sort(r.choice(FF, N_ACTIVE, replace=False))]
     keep = int(round(WIN_KEEP * N_ACTIVE))
     for _ in range(n_tok - 1):
         kept = r.choice(sets[-1], keep, replace=False)
-        rest = np.setdiff1d(np.arange(FF), kept, assume_unique=True)
+        rest = np.setdiff1d(np.arange(FF), sets[-1], assume_unique=True)
         new = r.choice(rest, N_ACTIVE - keep, replace=False)
         sets.append(np.sort(np.concatenate([kept, new])))
     return [s.astype(np.int32) for s in sets]
@@ -460,6 +465,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-max-tokens", type=int, default=2000)
+    ap.add_argument("--calib-mib", type=int, default=0,
+                    help="first run 4 streaming copies of this many MiB (torch elementwise "
+                         "kernel reading and writing the size each), the known-size reference "
+                         "for rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -478,6 +487,15 @@ def main():
         sys.exit(1)
     dev = llg.Device()
     gg = llg.gguf
+    if args.calib_mib > 0:
+        n = args.calib_mib * (1 << 20) // 4
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty(n, device="cuda")
+        for _ in range(4):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        log(f"calibration: 4 copies of {args.calib_mib} MiB (read and write each)")
+        del src, dst
     if args.workload == "sparse":
         res = bench_sparse(args, torch, llg, dev)
     elif args.workload == "window":
