@@ -15,7 +15,9 @@ their average event-timed duration on the library's stream) and a
 timed on a bounded sample on this host).
 
 Other workloads (--workload dense-q4_0 | dense-q8_0 | dense-f16 | window |
-moe-decode | moe-prefill) measure the remaining hot-path configurations.
+moe-decode | moe-prefill | falcon-decode) measure the remaining hot-path
+configurations; falcon-decode is the full 32-layer model around the sparse FFN
+(--steps = generated tokens after the 512-token prompt).
 """
 from __future__ import annotations
 
@@ -373,6 +375,150 @@ def cpu_baseline_window(args, up, dn, X, sets):
             "sample": f"{n} window decode tokens (Update + FFNForward, k={WIN_K}), {el:.1f} s"}
 
 
+F4 = dict(n_layers=32, hidden=H, n_heads=71, n_kv=1, head_dim=64, ff=FF, vocab=65024,
+          max_seq=2048, rank=RANK, rope_base=10000.0, eps=1e-5)
+F4_PROMPT = 512
+
+
+def falcon_weights(torch, gg, d, seed):
+    """Random-init Falcon-7B-architecture weights, generated on the GPU:
+    matrices N(0, 0.02) quantized to Q4_0, LayerNorm weight 1 and bias 0,
+    predictors N(0, 0.05) in f32."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    h, L = d["hidden"], d["n_layers"]
+
+    def q(r, c):
+        return gg.quantize(torch.randn((r, c), generator=g, device="cuda") * 0.02, gg.Q4_0)
+
+    def f(r, c, std):
+        return (torch.randn((r, c), generator=g, device="cuda") * std).contiguous()
+
+    w = {"embed": q(d["vocab"], h), "lm_head": q(d["vocab"], h),
+         "out_w": np.ones(h, np.float32), "out_b": np.zeros(h, np.float32)}
+    for k in ["norm_w", "norm_b", "wq", "wk", "wv", "wo", "pwup", "pwout", "up", "down_t"]:
+        w[k] = []
+    kvd, qd = d["n_kv"] * d["head_dim"], d["n_heads"] * d["head_dim"]
+    for _ in range(L):
+        w["norm_w"].append(np.ones(h, np.float32))
+        w["norm_b"].append(np.zeros(h, np.float32))
+        w["wq"].append(q(qd, h))
+        w["wk"].append(q(kvd, h))
+        w["wv"].append(q(kvd, h))
+        w["wo"].append(q(h, qd))
+        w["pwup"].append(f(d["rank"], h, 0.05))
+        w["pwout"].append(f(d["ff"], d["rank"], 0.05))
+        w["up"].append(q(d["ff"], h))
+        w["down_t"].append(q(d["ff"], h))
+    return w
+
+
+def calibrate_thresholds(model, d, n_tok: int, frac: float, seed: int, rounds: int = 3):
+    """Per-layer thresholds giving a mean active fraction `frac`: each round runs
+    n_tok tokens from position 0 and sets every layer's threshold to the
+    (1 - frac) quantile of its predictor logits (the thresholds of earlier
+    layers change the inputs of later ones, hence the rounds)."""
+    r = np.random.default_rng(seed)
+    toks = r.integers(0, d["vocab"], n_tok)
+    thr = np.full(d["n_layers"], np.float32(3.0e38))
+    for _ in range(rounds):
+        model.set_thresholds(thr)
+        lgs = []
+        for s, t in enumerate(toks):
+            lgs.append(model.forward(int(t), s, pred_logits=True)[3])
+        lg = np.stack(lgs)  # [n_tok, L, ff]
+        thr = np.array([np.quantile(lg[:, l, :], 1.0 - frac) for l in range(d["n_layers"])],
+                       np.float32)
+    model.set_thresholds(thr)
+    return thr
+
+
+def bench_falcon(args, torch, llg, dev):
+    """Full Falcon-7B-architecture decode (32 layers, 71 heads x 64 with one KV
+    head, LayerNorm, NeoX RoPE, per-layer rank-128 predictor at 5%, sparse
+    Q4_0 FFN, LM head over 65024): a 512-token random-id prompt (sequential
+    prefill, as the reference runs it) then greedy decode chained on the
+    device; one step = one generated token through the whole model."""
+    gg = llg.gguf
+    d = dict(F4)
+    n_gen = max(1, min(args.steps, d["max_seq"] - F4_PROMPT))
+    log("falcon: generating weights on the GPU (32 layers, Q4_0)")
+    w = falcon_weights(torch, gg, d, 0x11A3A004)
+    torch.cuda.synchronize()
+    model = llg.FalconModel(dev, d, w, np.zeros(d["n_layers"], np.float32))
+    thr = calibrate_thresholds(model, d, 16, 0.05, 0xCA1)
+    r = np.random.default_rng(0x9707)
+    prompt = r.integers(0, d["vocab"], F4_PROMPT).astype(np.int32)
+    toks = torch.tensor(prompt, device="cuda")
+    gen = torch.zeros(n_gen + 2, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    tm = Timer(torch, dev.stream)
+    p0 = tm.event()
+    for s in range(F4_PROMPT):
+        out = gen.data_ptr() if s == F4_PROMPT - 1 else gen.data_ptr() + 4 * (n_gen + 1)
+        model.step_device(toks.data_ptr() + 4 * s, s, out)
+    p1 = tm.event()
+    for i in range(n_gen):
+        model.step_device(gen.data_ptr() + 4 * i, F4_PROMPT + i, gen.data_ptr() + 4 * (i + 1))
+    p2 = tm.event()
+    dev.sync()
+    prefill_ms = p0.elapsed_time(p1)
+    ms = p1.elapsed_time(p2) / n_gen
+    # active neurons per layer on one more token (host path)
+    _, _, na = model.forward(int(gen[n_gen].item()), F4_PROMPT + n_gen - 1)
+    mean_act = float(na.mean())
+    hd, kvd = d["head_dim"], d["n_kv"] * d["head_dim"]
+    row = gg.byte_size(gg.Q4_0, d["hidden"])
+    mean_pos = F4_PROMPT + n_gen / 2.0
+    per_layer = ((d["n_heads"] * hd + 2 * kvd) * row + d["hidden"] * gg.byte_size(
+        gg.Q4_0, d["n_heads"] * hd) + PRED_BYTES + mean_act * BUNDLE_ALG +
+        2 * kvd * 4 * mean_pos + 2 * d["hidden"] * 4 * 2)
+    alg = d["n_layers"] * per_layer + d["vocab"] * row + row
+    gbs = alg / (ms * 1e-3) / 1e9
+    res = {"metric": "full-model decode tokens/s", "value": 1000.0 / ms, "unit": "tokens/s",
+           "ms_per_step": ms, "dtype": "f32",
+           "config": {"workload": "falcon7b-arch-32layer-q4_0-5pct-sparse-greedy-decode",
+                      "n_layers": 32, "d_model": d["hidden"], "heads": "71 x 64, 1 KV head",
+                      "d_ff": d["ff"], "vocab": d["vocab"], "kv_len": d["max_seq"],
+                      "prompt_tokens": F4_PROMPT, "generated_tokens": n_gen,
+                      "prefill_ms": prefill_ms, "prefill_tokens_per_s": F4_PROMPT / prefill_ms * 1e3,
+                      "mean_active_per_layer": mean_act},
+           "roofline": {"bound": "hbm", "kernel": "one decode token: 32 x (k_resid_norm, "
+                        "k_matvec_q qkv, k_attn, k_matvec_q wo, k_pred_hidden, k_tile_up, "
+                        "k_sparse_down) + k_resid_norm, k_matvec_q lm head, k_argmax",
+                        "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": gbs / HBM_PEAK_GBS, "traffic": None, "alg_bytes_per_step": alg,
+                        "avg_step_us": ms * 1e3}}
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline_falcon(args, d, w, thr, prompt)
+    model.release()
+    return res
+
+
+def cpu_baseline_falcon(args, d, w, thr, prompt):
+    """The oracle's ForwardFlash on one host core, over the first prompt tokens
+    (attention, LM head and embedding dequantized to fp32 at load as the
+    reference does; FFN rows dequantized per token)."""
+    from oracle import refcpu as R
+
+    def host(a):
+        return a.cpu().numpy() if hasattr(a, "is_cuda") else np.asarray(a)
+
+    hw = {k: ([host(x) for x in v] if isinstance(v, list) else host(v)) for k, v in w.items()}
+    log("cpu baseline: oracle ForwardFlash, 1 thread (dequantizing attention/LM head at load)")
+    ref = R.Falcon(d, hw, thr)
+    n, t0 = 0, time.perf_counter()
+    while n < len(prompt):
+        ref.forward(int(prompt[n]), n)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= args.cpu_seconds:
+            break
+    return {"value": n / el, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{n} tokens of the prompt through the 32-layer model (positions 0-{n - 1}), "
+                      f"{el:.1f} s, weights in host memory"}
+
+
 MOE_D, MOE_FF, MOE_E, MOE_K, MOE_PREFILL = 4096, 14336, 8, 2, 512
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
@@ -459,7 +605,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="sparse",
                     choices=["sparse", "dense-q4_0", "dense-q8_0", "dense-f16", "window",
-                             "moe-decode", "moe-prefill"])
+                             "moe-decode", "moe-prefill", "falcon-decode"])
     ap.add_argument("--layers", type=int, default=0,
                     help="distinct HBM copies rotated per step (0 = enough to defeat the MALL)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -500,6 +646,8 @@ def main():
         res = bench_sparse(args, torch, llg, dev)
     elif args.workload == "window":
         res = bench_window(args, torch, llg, dev)
+    elif args.workload == "falcon-decode":
+        res = bench_falcon(args, torch, llg, dev)
     elif args.workload.startswith("moe-"):
         res = bench_moe(args, torch, llg, dev, args.workload == "moe-prefill")
     else:

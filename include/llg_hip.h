@@ -168,6 +168,32 @@ int llg_hip_moe_ffn(LlgHipDevice dev, int64_t router, int64_t gate_exps, int64_t
 int llg_hip_moe_route(LlgHipDevice dev, const float *logits, int n_tok, int n_exp, int k,
                       int32_t *ids, float *weights);
 
+/* ---- Falcon-architecture decode around the sparse FFN ------------------- */
+/* ForwardFlash (inference/ffn_flash.go:115-185) on the Falcon parallel layout
+ * with ffnFlash path 2, attention as forward.go:206-310 (no biases, RoPE with
+ * rope_base, MQA/GQA), KV cache as kvcache/kvcache.go:25-82, greedy argmax as
+ * cmd/generate.go:197-205.  dims = {n_layers, hidden, n_heads, n_kv_heads,
+ * head_dim (64 or 128), ff, vocab, max_seq}.  layer_handles holds 7 handles
+ * per layer: attn_norm weight, attn_norm bias (F32 [1 x hidden]), wqkv (the
+ * rows of Wq, Wk, Wv stacked), wo, predictor WUp, predictor WOut (F32), the
+ * FFN bundle.  thresholds: one per layer.  The model owns its KV cache
+ * (n_layers x max_seq x 2 x n_kv_heads x head_dim floats); the token at
+ * position pos is written to cache row pos (the reference commits after
+ * every token, generate.go:94,119). */
+int llg_hip_falcon_create(LlgHipDevice dev, const int32_t *dims, float rope_base,
+                          float norm_eps, int act, int64_t embed,
+                          const int64_t *layer_handles, const float *thresholds,
+                          int64_t out_norm_w, int64_t out_norm_b, int64_t lm_head,
+                          int64_t *model);
+int llg_hip_falcon_set_thresholds(LlgHipDevice dev, int64_t model, const float *thresholds);
+/* One token (ForwardFlash(token, pos)); logits [vocab], next_token (greedy)
+ * and n_active [n_layers] are optional host outputs.  pred_logits (optional,
+ * [n_layers x ff]) receives every layer's predictor logits (predictor.go:57-73)
+ * from an extra predict-only pass, for calibrating the thresholds. */
+int llg_hip_falcon_forward(LlgHipDevice dev, int64_t model, int32_t token, int pos,
+                           float *logits, int32_t *next_token, int32_t *n_active,
+                           float *pred_logits);
+
 /* ---- device-pointer (async) variants for HBM-resident callers ----------- */
 int llg_hipd_predict(LlgHipDevice dev, int64_t wup, int64_t wout, int64_t bias,
                      const float *d_a, float threshold, int32_t *d_active,
@@ -190,6 +216,11 @@ int llg_hipd_window_step(LlgHipDevice dev, int64_t win, const float *d_x,
 int llg_hipd_moe_ffn(LlgHipDevice dev, int64_t router, int64_t gate_exps, int64_t up_exps,
                      int64_t down_exps, int n_exp, int k, const float *d_x, int n_tok,
                      float *d_out, int32_t *d_ids, float *d_weights);
+/* One token of the Falcon model on the stream: embeds *d_token (device int32),
+ * writes the greedy next token to *d_next_token (may equal d_token) and, if
+ * d_logits is given, the logits.  A decode loop chains calls without waiting. */
+int llg_hipd_falcon_step(LlgHipDevice dev, int64_t model, const int32_t *d_token, int pos,
+                         int32_t *d_next_token, float *d_logits);
 
 #ifdef __cplusplus
 }

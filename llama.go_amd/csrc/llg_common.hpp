@@ -308,6 +308,31 @@ __device__ __forceinline__ void llg_block_axpy<LLG_TYPE_F32>(const uint8_t *__re
     }
 }
 
+// Element c of a row in the row format, bit-exact (tensor/dtype.go:12-82).
+__device__ __forceinline__ float llg_dequant_elem(const uint8_t *row, const RowFmt &f, int c) {
+    switch (f.type) {
+    case LLG_TYPE_Q4_0: {
+        const int b = c >> 5, e = c & 31;
+        const uint8_t byte = row[b * 16 + (e >> 1)];
+        const int q = (e & 1) ? (byte >> 4) : (byte & 15);
+        const uint32_t hb = row[f.d_off + 2 * b] | (row[f.d_off + 2 * b + 1] << 8);
+        return (float)(q - 8) * llg_f16_ref(hb);
+    }
+    case LLG_TYPE_Q8_0: {
+        const int b = c >> 5, e = c & 31;
+        const int8_t q = (int8_t)row[b * 32 + e];
+        const uint32_t hb = row[f.d_off + 2 * b] | (row[f.d_off + 2 * b + 1] << 8);
+        return (float)q * llg_f16_ref(hb);
+    }
+    case LLG_TYPE_F16: {
+        const uint32_t hb = row[2 * c] | (row[2 * c + 1] << 8);
+        return llg_f16_ref(hb);
+    }
+    default:
+        return reinterpret_cast<const float *>(row)[c];
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Split load / compute forms of one 32-element block.  Kernels load the raw
 // bytes of all the blocks a lane owns first (BlockRaw), so their memory
@@ -551,7 +576,7 @@ __device__ __forceinline__ void llg_stage_x_sum(float *xs, const float *__restri
 #ifdef __cplusplus
 #include <string>
 
-enum LlgKind { LLG_KIND_MATRIX = 1, LLG_KIND_BUNDLE = 2, LLG_KIND_WINDOW = 3 };
+enum LlgKind { LLG_KIND_MATRIX = 1, LLG_KIND_BUNDLE = 2, LLG_KIND_WINDOW = 3, LLG_KIND_MODEL = 4 };
 
 struct LlgObject {
     int kind;

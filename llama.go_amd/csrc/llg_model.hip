@@ -1,0 +1,504 @@
+// llg_model.hip -- Falcon-architecture decode around the sparse FFN
+// (inference/ffn_flash.go:115-185 ForwardFlash, inference/forward.go:106-314,
+// kvcache/kvcache.go:25-82, cmd/generate.go:88-121).
+//
+// One token through the model, all on the device stream:
+//   k_embed           x = dequant(embedding row of the token)    (forward.go:449-454)
+//   per layer l:
+//     k_resid_norm    x += attn_out[l-1]; x += ffn_out[l-1] (two separate fp32
+//                     adds, forward.go:170-176); normed = LayerNorm(x) with the
+//                     layer's weight and bias (tensor/ops.go:138-165)
+//     k_matvec_q      qkv = [Wq; Wk; Wv] . normed               (forward.go:211-222)
+//     k_attn          NeoX RoPE of q and k (forward.go:483-497), K/V appended at
+//                     row pos of the layer's cache (kvcache.go:42-52), softmax
+//                     attention of every query head over rows 0..pos of its KV
+//                     head (forward.go:258-301)
+//     k_matvec_q      attn_out = Wo . attn                      (forward.go:305)
+//     sparse step     ffn_out = ffnFlash path 2 with the predictor on attn_out
+//                     and the FFN on normed (ffn_flash.go:157-163, 225-231)
+//   k_resid_norm      final residual adds + output LayerNorm   (ffn_flash.go:126-129)
+//   k_matvec_q        logits = LMHead . x                      (ffn_flash.go:130)
+//   k_argmax          next token = first index of the maximum  (generate.go:197-205)
+// The token comes from device memory, so a greedy decode loop never waits on
+// the host.
+#include <algorithm>
+#include <vector>
+
+#include "llg_common.hpp"
+#include "llg_internal.hpp"
+
+#define NORM_THREADS 1024
+#define ATTN_THREADS 256
+
+struct LlgModelLayer {
+    LlgObject *norm_w, *norm_b, *wqkv, *wo, *pwup, *pwout, *bundle;
+    float thr;
+};
+
+struct LlgModel {
+    int n_layers, hidden, n_heads, n_kv, head_dim, ff, vocab, max_seq, rank, act;
+    float rope_base, eps;
+    LlgObject *embed, *out_w, *out_b, *lm_head;
+    std::vector<LlgModelLayer> layers;
+    // device buffers, carved out of the object's allocation
+    float *x, *normed, *qkv, *attn, *attn_out, *ffn_out, *logits, *kv, *pred_logits;
+    int32_t *token, *n_active, *act_scratch;
+    uint8_t *ws;
+};
+
+void llg_model_destroy(LlgDevice *d, LlgObject *o) {
+    (void)d;
+    delete reinterpret_cast<LlgModel *>(o->ext);
+    o->ext = nullptr;
+}
+
+// ---------------------------------------------------------------------------
+__global__ void k_embed(const uint8_t *__restrict__ emb, long long stride, RowFmt f,
+                        const int32_t *__restrict__ token, int vocab, float *__restrict__ x) {
+    // a token id outside the table would be a slice-bounds panic in the
+    // reference; the host entry points reject it, the device loop only feeds
+    // argmax results (< vocab)
+    const int t = min(max(*token, 0), vocab - 1);
+    const uint8_t *row = emb + (long long)t * stride;
+    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < f.cols; c += gridDim.x * blockDim.x)
+        x[c] = llg_dequant_elem(row, f, c);
+}
+
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = llg_wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();  // red may still be read from a previous call
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = 0; i < nw; i++) s += red[i];
+    return s;
+}
+
+// x = (x + a1) + a2 (either may be null); out = LayerNorm(x) * w + b.
+__global__ __launch_bounds__(NORM_THREADS) void k_resid_norm(
+    float *__restrict__ x, const float *__restrict__ a1, const float *__restrict__ a2,
+    const float *__restrict__ w, const float *__restrict__ b, int n, float eps,
+    float *__restrict__ out) {
+    __shared__ float red[NORM_THREADS / 64];
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v = x[i];
+        if (a1) v = v + a1[i];
+        if (a2) v = v + a2[i];
+        if (a1 || a2) x[i] = v;
+        s += v;
+    }
+    const float mean = block_sum(s, red) / (float)n;
+    float q = 0.0f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float dv = x[i] - mean;
+        q += dv * dv;
+    }
+    const float var = block_sum(q, red) / (float)n;
+    const float std_ = (float)sqrt((double)var + (double)eps);  // ops.go:159
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = (x[i] - mean) / std_ * w[i] + b[i];
+}
+
+// Sum over each 16-lane row (all lanes of the row get the total).
+__device__ __forceinline__ float row16_sum(float v) {
+    v = llg_quad_sum(v);
+    v += llg_dpp<0x124>(v);  // row_ror:4
+    v += llg_dpp<0x128>(v);  // row_ror:8
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// One workgroup per query head; HD = head_dim (64 or 128).  HD/4 lanes hold
+// one key row (a float4 each), so a wavefront scores 256/HD positions per
+// load; each lane requests ATT_U rows before reducing any.  Rows 0..pos-1 come
+// from the layer's cache; row pos is this token's rotated key / value, taken
+// from registers and LDS (the cache row is written by the group's first query
+// head for later tokens, so no workgroup waits on another).  Scores live in
+// LDS (pos + 1 floats).
+#define ATT_U 4
+template <int HD>
+__global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__ qkv, int n_heads,
+                                                       int n_kv, int pos, float rope_base,
+                                                       int max_seq, float *__restrict__ kv,
+                                                       float *__restrict__ out) {
+    constexpr int LP = HD / 4;       // lanes per position
+    constexpr int PW = 64 / LP;      // positions per wavefront per load
+    constexpr int NG = ATTN_THREADS / HD;  // position groups of the value pass
+    extern __shared__ float sc[];    // pos + 1 scores, then probabilities
+    __shared__ __attribute__((aligned(16))) float qh[HD], kh[HD];
+    __shared__ float red[ATTN_THREADS / 64];
+    __shared__ float part[NG][HD];
+    const int h = blockIdx.x;
+    const int kvh = h * n_kv / n_heads;  // forward.go:266
+    const int kv_dim = n_kv * HD;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *q = qkv + (size_t)h * HD;
+    const float *kc = qkv + (size_t)n_heads * HD + (size_t)kvh * HD;
+    const float *vc = qkv + (size_t)n_heads * HD + kv_dim + (size_t)kvh * HD;
+    if (tid < HD / 2) {  // RoPE, pairs (i, i + HD/2) (forward.go:483-497)
+        const int i = tid;
+        const double fr = (double)pos / pow((double)rope_base, (double)(2 * i) / (double)HD);
+        const float c = (float)cos(fr), s = (float)sin(fr);
+        const float q0 = q[i], q1 = q[i + HD / 2], k0 = kc[i], k1 = kc[i + HD / 2];
+        qh[i] = q0 * c - q1 * s;
+        qh[i + HD / 2] = q0 * s + q1 * c;
+        kh[i] = k0 * c - k1 * s;
+        kh[i + HD / 2] = k0 * s + k1 * c;
+    }
+    __syncthreads();
+    const float *kcache = kv;
+    const float *vcache = kv + (size_t)max_seq * kv_dim;
+    if (h == kvh * (n_heads / n_kv) && tid < HD) {  // append row pos (kvcache.go:42-52)
+        kv[(size_t)pos * kv_dim + kvh * HD + tid] = kh[tid];
+        kv[(size_t)max_seq * kv_dim + (size_t)pos * kv_dim + kvh * HD + tid] = vc[tid];
+    }
+    const float scale = (float)(1.0 / sqrt((double)HD));  // forward.go:255
+    const int sub = lane % LP, slot = lane / LP;
+    const float4 qv = reinterpret_cast<const float4 *>(qh)[sub];
+    for (int t0 = wave * PW * ATT_U; t0 < pos; t0 += 4 * PW * ATT_U) {
+        float4 kk[ATT_U];
+#pragma unroll
+        for (int u = 0; u < ATT_U; u++) {
+            const int t = min(t0 + u * PW + slot, pos - 1);
+            kk[u] = reinterpret_cast<const float4 *>(kcache + (size_t)t * kv_dim + kvh * HD)[sub];
+        }
+#pragma unroll
+        for (int u = 0; u < ATT_U; u++) {
+            float dot = qv.x * kk[u].x + qv.y * kk[u].y + qv.z * kk[u].z + qv.w * kk[u].w;
+            dot = row16_sum(dot);
+            if (LP == 32) dot += __shfl_xor(dot, 16, 64);
+            const int t = t0 + u * PW + slot;
+            if (sub == 0 && t < pos) sc[t] = dot * scale;
+        }
+    }
+    if (wave == 0) {  // row pos
+        const float4 k4 = reinterpret_cast<const float4 *>(kh)[sub];
+        float dot = qv.x * k4.x + qv.y * k4.y + qv.z * k4.z + qv.w * k4.w;
+        dot = row16_sum(dot);
+        if (LP == 32) dot += __shfl_xor(dot, 16, 64);
+        if (lane == 0) sc[pos] = dot * scale;
+    }
+    __syncthreads();
+    // softmax (forward.go:463-479): max, exp in double rounded to float, sum, divide
+    const int T = pos + 1;
+    float m = -INFINITY;
+    for (int t = tid; t < T; t += blockDim.x) m = fmaxf(m, sc[t]);
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float s = 0.0f;
+    for (int t = tid; t < T; t += blockDim.x) {
+        const float e = (float)exp((double)(sc[t] - m));
+        sc[t] = e;
+        s += e;
+    }
+    const float sum = block_sum(s, red);  // its barriers also publish sc
+    // out[d] = sum_t p_t * v_t[d]: thread (d, g) takes t = g, g + NG, ... < pos,
+    // ATT_U rows per step; row pos is added last
+    const int dd = tid % HD, g = tid / HD;
+    float acc = 0.0f;
+    for (int t0 = g; t0 < pos; t0 += NG * ATT_U) {
+        float vv[ATT_U];
+#pragma unroll
+        for (int u = 0; u < ATT_U; u++) {
+            const int t = min(t0 + u * NG, pos - 1);
+            vv[u] = vcache[(size_t)t * kv_dim + kvh * HD + dd];
+        }
+#pragma unroll
+        for (int u = 0; u < ATT_U; u++) {
+            const int t = t0 + u * NG;
+            if (t < pos) acc += (sc[t] / sum) * vv[u];
+        }
+    }
+    part[g][dd] = acc;
+    __syncthreads();
+    if (tid < HD) {
+        float r = part[0][tid];
+#pragma unroll
+        for (int i = 1; i < NG; i++) r += part[i][tid];
+        r += (sc[pos] / sum) * vc[tid];
+        out[(size_t)h * HD + tid] = r;
+    }
+}
+
+// First index of the maximum (generate.go:197-205: strict '>' from index 0,
+// so a NaN at index 0 wins and later NaNs never do).
+__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ v, int n,
+                                                 int32_t *__restrict__ out) {
+    __shared__ float bv_s[16];
+    __shared__ int bi_s[16];
+    float bv = -INFINITY;
+    int bi = n;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float x = v[i];
+        if (x == x && (x > bv || (x == bv && i < bi))) {
+            bv = x;
+            bi = i;
+        }
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ov > bv || (ov == bv && oi < bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        bv_s[wave] = bv;
+        bi_s[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+            if (bv_s[w] > bv_s[0] || (bv_s[w] == bv_s[0] && bi_s[w] < bi_s[0])) {
+                bv_s[0] = bv_s[w];
+                bi_s[0] = bi_s[w];
+            }
+        const float v0 = v[0];
+        *out = (v0 != v0 || bi_s[0] >= n) ? 0 : bi_s[0];
+    }
+}
+
+// ---------------------------------------------------------------------------
+static LlgModel *get_model(LlgDevice *d, int64_t h) {
+    LlgObject *o = llg_get(d, h, LLG_KIND_MODEL);
+    return o ? reinterpret_cast<LlgModel *>(o->ext) : nullptr;
+}
+
+static size_t model_ws_bytes(const LlgModel &m) {
+    return std::max(llg_fused_ws_bytes(m.rank, m.ff), (size_t)llg_predict_ws_bytes(m.rank, m.ff));
+}
+
+// One token: embed -> layers -> norm -> LM head -> argmax, on the stream.
+// token_in: device int32 (the token to embed); token_out: device int32 (the
+// greedy next token); n_active_out: device int32[n_layers] or null;
+// pred_logits: device float[n_layers x ff] or null (each layer's predictor
+// logits, from an extra predict-only pass, for threshold calibration).
+static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int pos,
+                      int32_t *token_out, int32_t *n_active_out, float *pred_logits) {
+    hipStream_t st = llg_dev_stream(d);
+    const int qkv_rows = (m.n_heads + 2 * m.n_kv) * m.head_dim;
+    (void)qkv_rows;
+    hipLaunchKernelGGL(k_embed, dim3((m.hidden + 255) / 256), dim3(256), 0, st, m.embed->d,
+                       m.embed->stride, m.embed->fmt, token_in, m.vocab, m.x);
+    const size_t attn_lds = (size_t)(pos + 1) * 4;
+    for (int l = 0; l < m.n_layers; l++) {
+        const LlgModelLayer &L = m.layers[l];
+        hipLaunchKernelGGL(k_resid_norm, dim3(1), dim3(NORM_THREADS), 0, st, m.x,
+                           l ? m.attn_out : (const float *)nullptr,
+                           l ? m.ffn_out : (const float *)nullptr,
+                           reinterpret_cast<const float *>(L.norm_w->d),
+                           reinterpret_cast<const float *>(L.norm_b->d), m.hidden, m.eps, m.normed);
+        int rc = llg_matvec_enqueue(d, L.wqkv, m.normed, -1, m.qkv);
+        if (rc) return rc;
+        float *kvl = m.kv + (size_t)l * 2 * m.max_seq * m.n_kv * m.head_dim;
+        if (m.head_dim == 64)
+            hipLaunchKernelGGL(k_attn<64>, dim3(m.n_heads), dim3(ATTN_THREADS), attn_lds, st, m.qkv,
+                               m.n_heads, m.n_kv, pos, m.rope_base, m.max_seq, kvl, m.attn);
+        else
+            hipLaunchKernelGGL(k_attn<128>, dim3(m.n_heads), dim3(ATTN_THREADS), attn_lds, st, m.qkv,
+                               m.n_heads, m.n_kv, pos, m.rope_base, m.max_seq, kvl, m.attn);
+        LLG_LAUNCH_CHECK(d, "model attention");
+        if ((rc = llg_matvec_enqueue(d, L.wo, m.attn, -1, m.attn_out))) return rc;
+        if (pred_logits &&
+            (rc = llg_predict_enqueue(d, L.pwup, L.pwout, nullptr, m.attn_out, L.thr, m.act_scratch,
+                                      m.act_scratch + m.ff, pred_logits + (size_t)l * m.ff, m.ws)))
+            return rc;
+        // ffnFlash path 2: predictor on the attention output, FFN on normed
+        rc = llg_fused_enqueue(d, L.pwup, L.pwout, nullptr, L.bundle, m.attn_out, m.normed, L.thr,
+                               m.act, m.ffn_out, nullptr, n_active_out ? n_active_out + l : nullptr,
+                               m.ws);
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(k_resid_norm, dim3(1), dim3(NORM_THREADS), 0, st, m.x, m.attn_out,
+                       m.ffn_out, reinterpret_cast<const float *>(m.out_w->d),
+                       reinterpret_cast<const float *>(m.out_b->d), m.hidden, m.eps, m.normed);
+    int rc = llg_matvec_enqueue(d, m.lm_head, m.normed, -1, m.logits);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, m.logits, m.vocab, token_out);
+    LLG_LAUNCH_CHECK(d, "model step");
+    return 0;
+}
+
+static LlgObject *get_f32_vec(LlgDevice *d, int64_t h, int n) {
+    LlgObject *o = llg_get(d, h, LLG_KIND_MATRIX);
+    if (!o || o->fmt.type != LLG_TYPE_F32 || o->rows != 1 || o->fmt.cols != n) return nullptr;
+    return o;
+}
+
+extern "C" {
+
+int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, float norm_eps,
+                          int act, int64_t embed, const int64_t *layer_handles,
+                          const float *thresholds, int64_t out_norm_w, int64_t out_norm_b,
+                          int64_t lm_head, int64_t *model) {
+    LlgDevice *d = llg_dev(h);
+    if (!d) return LLG_E_NODEV;
+    if (!dims || !layer_handles || !thresholds || !model)
+        return llg_set_error(d, LLG_E_ARG, "falcon_create: null argument");
+    LlgModel *m = new LlgModel();
+    m->n_layers = dims[0];
+    m->hidden = dims[1];
+    m->n_heads = dims[2];
+    m->n_kv = dims[3];
+    m->head_dim = dims[4];
+    m->ff = dims[5];
+    m->vocab = dims[6];
+    m->max_seq = dims[7];
+    m->rope_base = rope_base;
+    m->eps = norm_eps;
+    m->act = act;
+    auto fail = [&](int code, const char *msg) {
+        delete m;
+        return llg_set_error(d, code, "falcon_create: %s", msg);
+    };
+    if (m->n_layers < 1 || m->hidden < 32 || m->n_heads < 1 || m->n_kv < 1 ||
+        m->n_heads % m->n_kv || m->vocab < 1 || m->max_seq < 1 || m->ff < 1)
+        return fail(LLG_E_HPARAM, "invalid dimensions");
+    if (m->head_dim != 64 && m->head_dim != 128) return fail(LLG_E_HPARAM, "head_dim must be 64 or 128");
+    if (m->hidden > 64 * 1024) return fail(LLG_E_HPARAM, "hidden too large");
+    if ((size_t)m->max_seq * 4 > 64 * 1024) return fail(LLG_E_HPARAM, "max_seq above 16384");
+    const int qkv_rows = (m->n_heads + 2 * m->n_kv) * m->head_dim;
+    m->embed = llg_get(d, embed, LLG_KIND_MATRIX);
+    m->lm_head = llg_get(d, lm_head, LLG_KIND_MATRIX);
+    m->out_w = get_f32_vec(d, out_norm_w, m->hidden);
+    m->out_b = get_f32_vec(d, out_norm_b, m->hidden);
+    if (!m->embed || m->embed->rows != m->vocab || m->embed->fmt.cols != m->hidden)
+        return fail(LLG_E_ARG, "embedding must be [vocab x hidden]");
+    if (!m->lm_head || m->lm_head->rows != m->vocab || m->lm_head->fmt.cols != m->hidden)
+        return fail(LLG_E_ARG, "lm head must be [vocab x hidden]");
+    if (!m->out_w || !m->out_b) return fail(LLG_E_ARG, "output norm must be F32 [1 x hidden]");
+    m->rank = -1;
+    for (int l = 0; l < m->n_layers; l++) {
+        const int64_t *lh = layer_handles + 7 * l;
+        LlgModelLayer L;
+        L.norm_w = get_f32_vec(d, lh[0], m->hidden);
+        L.norm_b = get_f32_vec(d, lh[1], m->hidden);
+        L.wqkv = llg_get(d, lh[2], LLG_KIND_MATRIX);
+        L.wo = llg_get(d, lh[3], LLG_KIND_MATRIX);
+        L.pwup = llg_get(d, lh[4], LLG_KIND_MATRIX);
+        L.pwout = llg_get(d, lh[5], LLG_KIND_MATRIX);
+        L.bundle = llg_get(d, lh[6], LLG_KIND_BUNDLE);
+        L.thr = thresholds[l];
+        if (!L.norm_w || !L.norm_b) return fail(LLG_E_ARG, "layer norm must be F32 [1 x hidden]");
+        if (!L.wqkv || L.wqkv->rows != qkv_rows || L.wqkv->fmt.cols != m->hidden)
+            return fail(LLG_E_ARG, "wqkv must be [(n_heads + 2 n_kv) head_dim x hidden]");
+        if (!L.wo || L.wo->rows != m->hidden || L.wo->fmt.cols != m->n_heads * m->head_dim)
+            return fail(LLG_E_ARG, "wo must be [hidden x n_heads head_dim]");
+        if (!L.bundle || L.bundle->rows != m->ff || L.bundle->fmt.cols != m->hidden)
+            return fail(LLG_E_ARG, "bundle must hold ff neurons of hidden");
+        if (!L.pwup || !L.pwout || L.pwup->fmt.type != LLG_TYPE_F32 ||
+            L.pwout->fmt.type != LLG_TYPE_F32 || L.pwup->fmt.cols != m->hidden ||
+            L.pwout->rows != m->ff || L.pwout->fmt.cols != L.pwup->rows)
+            return fail(LLG_E_ARG, "predictor must be F32 WUp [rank x hidden], WOut [ff x rank]");
+        if (m->rank < 0) m->rank = L.pwup->rows;
+        if (L.pwup->rows != m->rank) return fail(LLG_E_ARG, "predictor rank differs between layers");
+        m->layers.push_back(L);
+    }
+    // device buffers
+    const size_t kv_dim = (size_t)m->n_kv * m->head_dim;
+    const size_t v_h = llg_align((long long)m->hidden * 4, 256);
+    const size_t v_qkv = llg_align((long long)qkv_rows * 4, 256);
+    const size_t v_att = llg_align((long long)m->n_heads * m->head_dim * 4, 256);
+    const size_t v_log = llg_align((long long)m->vocab * 4, 256);
+    const size_t v_kv = llg_align((long long)m->n_layers * 2 * m->max_seq * kv_dim * 4, 256);
+    const size_t v_i = llg_align((long long)(m->n_layers + 4) * 4, 256);
+    const size_t v_ff = llg_align((long long)(m->ff + 4) * 4, 256);
+    const size_t v_pl = llg_align((long long)m->n_layers * m->ff * 4, 256);
+    const size_t wsb = model_ws_bytes(*m);
+    const size_t total = 5 * v_h + v_qkv + v_att + v_log + v_kv + v_i + v_ff + v_pl + wsb;
+    uint8_t *buf = nullptr;
+    if (hipMalloc(&buf, total) != hipSuccess) return fail(LLG_E_NOMEM, "buffer allocation failed");
+    uint8_t *p = buf;
+    m->x = reinterpret_cast<float *>(p); p += v_h;
+    m->normed = reinterpret_cast<float *>(p); p += v_h;
+    m->attn_out = reinterpret_cast<float *>(p); p += v_h;
+    m->ffn_out = reinterpret_cast<float *>(p); p += v_h;
+    p += v_h;  // spare
+    m->qkv = reinterpret_cast<float *>(p); p += v_qkv;
+    m->attn = reinterpret_cast<float *>(p); p += v_att;
+    m->logits = reinterpret_cast<float *>(p); p += v_log;
+    m->kv = reinterpret_cast<float *>(p); p += v_kv;
+    m->token = reinterpret_cast<int32_t *>(p);
+    m->n_active = m->token + 4;
+    p += v_i;
+    m->act_scratch = reinterpret_cast<int32_t *>(p);
+    p += v_ff;
+    m->pred_logits = reinterpret_cast<float *>(p);
+    p += v_pl;
+    m->ws = p;
+    hipStream_t st = llg_dev_stream(d);
+    LLG_HIP_TRY(d, hipMemsetAsync(buf, 0, total, st));
+    LLG_HIP_TRY(d, hipStreamSynchronize(st));
+    LlgObject *o = new LlgObject();
+    o->kind = LLG_KIND_MODEL;
+    o->d = buf;
+    o->bytes = total;
+    o->rows = m->n_layers;
+    o->fmt = m->embed->fmt;
+    o->stride = 0;
+    o->ext = m;
+    *model = llg_register(d, o);
+    return 0;
+}
+
+int llg_hip_falcon_set_thresholds(LlgHipDevice h, int64_t hm, const float *thresholds) {
+    LlgDevice *d = llg_dev(h);
+    if (!d) return LLG_E_NODEV;
+    LlgModel *m = get_model(d, hm);
+    if (!m) return llg_set_error(d, LLG_E_HANDLE, "falcon: unknown model");
+    if (!thresholds) return llg_set_error(d, LLG_E_ARG, "falcon: null thresholds");
+    for (int l = 0; l < m->n_layers; l++) m->layers[l].thr = thresholds[l];
+    return 0;
+}
+
+int llg_hip_falcon_forward(LlgHipDevice h, int64_t hm, int32_t token, int pos, float *logits,
+                           int32_t *next_token, int32_t *n_active, float *pred_logits) {
+    LlgDevice *d = llg_dev(h);
+    if (!d) return LLG_E_NODEV;
+    LlgModel *m = get_model(d, hm);
+    if (!m) return llg_set_error(d, LLG_E_HANDLE, "falcon: unknown model");
+    if (token < 0 || token >= m->vocab)
+        return llg_set_error(d, LLG_E_RANGE, "falcon: token %d outside [0,%d)", token, m->vocab);
+    if (pos < 0 || pos >= m->max_seq)
+        return llg_set_error(d, LLG_E_RANGE, "falcon: position %d outside [0,%d)", pos, m->max_seq);
+    int rc;
+    if ((rc = llg_h2d(d, m->token, &token, 4))) return rc;
+    if ((rc = model_step(d, *m, m->token, pos, m->token + 1, n_active ? m->n_active : nullptr,
+                         pred_logits ? m->pred_logits : nullptr)))
+        return rc;
+    if (pred_logits &&
+        (rc = llg_d2h(d, pred_logits, m->pred_logits, (size_t)m->n_layers * m->ff * 4)))
+        return rc;
+    if (logits && (rc = llg_d2h(d, logits, m->logits, (size_t)m->vocab * 4))) return rc;
+    if (next_token && (rc = llg_d2h(d, next_token, m->token + 1, 4))) return rc;
+    if (n_active && (rc = llg_d2h(d, n_active, m->n_active, (size_t)m->n_layers * 4))) return rc;
+    return llg_sync_dev(d);
+}
+
+int llg_hipd_falcon_step(LlgHipDevice h, int64_t hm, const int32_t *d_token, int pos,
+                         int32_t *d_next_token, float *d_logits) {
+    LlgDevice *d = llg_dev(h);
+    if (!d) return LLG_E_NODEV;
+    LlgModel *m = get_model(d, hm);
+    if (!m) return llg_set_error(d, LLG_E_HANDLE, "falcon: unknown model");
+    if (!d_token || !d_next_token) return llg_set_error(d, LLG_E_ARG, "falcon: null token pointer");
+    if (pos < 0 || pos >= m->max_seq)
+        return llg_set_error(d, LLG_E_RANGE, "falcon: position %d outside [0,%d)", pos, m->max_seq);
+    int rc = model_step(d, *m, d_token, pos, d_next_token, nullptr, nullptr);
+    if (rc) return rc;
+    if (d_logits)
+        LLG_HIP_TRY(d, hipMemcpyAsync(d_logits, m->logits, (size_t)m->vocab * 4,
+                                      hipMemcpyDeviceToDevice, llg_dev_stream(d)));
+    return 0;
+}
+
+}  // extern "C"

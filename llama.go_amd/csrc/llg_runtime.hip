@@ -199,6 +199,7 @@ static int upload_rows(LlgDevice *d, const void *const *srcs, int nsrc, int from
 }
 
 extern void llg_window_destroy(LlgDevice *d, LlgObject *o);
+extern void llg_model_destroy(LlgDevice *d, LlgObject *o);
 
 extern "C" {
 
@@ -230,6 +231,7 @@ void llg_hip_free(LlgHipDevice h) {
     for (auto &kv : d->objects) {
         LlgObject *o = kv.second;
         if (o->kind == LLG_KIND_WINDOW) llg_window_destroy(d, o);
+        if (o->kind == LLG_KIND_MODEL) llg_model_destroy(d, o);
         if (o->d) hipFree(o->d);
         delete o;
     }
@@ -294,6 +296,7 @@ int llg_hip_release(LlgHipDevice h, int64_t handle) {
     if (!o) return llg_set_error(d, LLG_E_HANDLE, "release: unknown handle %lld", (long long)handle);
     hipStreamSynchronize(d->stream);
     if (o->kind == LLG_KIND_WINDOW) llg_window_destroy(d, o);
+    if (o->kind == LLG_KIND_MODEL) llg_model_destroy(d, o);
     if (o->d) hipFree(o->d);
     d->objects.erase(handle);
     delete o;
@@ -330,33 +333,7 @@ __global__ void k_dequant(const uint8_t *__restrict__ base, long long stride, lo
     const int sub = (int)(rem / f.cols);
     const int c = (int)(rem % f.cols);
     const uint8_t *row = base + r * stride + sub_off + sub * sub_stride;
-    float v;
-    switch (f.type) {
-    case LLG_TYPE_Q4_0: {
-        const int b = c >> 5, e = c & 31;
-        const uint8_t byte = row[b * 16 + (e >> 1)];
-        const int q = (e & 1) ? (byte >> 4) : (byte & 15);
-        const uint32_t hb = row[f.d_off + 2 * b] | (row[f.d_off + 2 * b + 1] << 8);
-        v = (float)(q - 8) * llg_f16_ref(hb);
-        break;
-    }
-    case LLG_TYPE_Q8_0: {
-        const int b = c >> 5, e = c & 31;
-        const int8_t q = (int8_t)row[b * 32 + e];
-        const uint32_t hb = row[f.d_off + 2 * b] | (row[f.d_off + 2 * b + 1] << 8);
-        v = (float)q * llg_f16_ref(hb);
-        break;
-    }
-    case LLG_TYPE_F16: {
-        const uint32_t hb = row[2 * c] | (row[2 * c + 1] << 8);
-        v = llg_f16_ref(hb);
-        break;
-    }
-    default: {
-        v = reinterpret_cast<const float *>(row)[c];
-        break;
-    }
-    }
+    const float v = llg_dequant_elem(row, f, c);
     out[i] = v;
 }
 
@@ -364,7 +341,7 @@ extern "C" int llg_hip_dequant(LlgHipDevice h, int64_t handle, int row0, int nro
     LlgDevice *d = llg_dev(h);
     if (!d) return LLG_E_NODEV;
     LlgObject *o = llg_get(d, handle, 0);
-    if (!o || o->kind == LLG_KIND_WINDOW)
+    if (!o || o->kind == LLG_KIND_WINDOW || o->kind == LLG_KIND_MODEL)
         return llg_set_error(d, LLG_E_HANDLE, "dequant: unknown handle");
     if (!out || nrows < 0 || row0 < 0 || row0 + nrows > o->rows)
         return llg_set_error(d, LLG_E_RANGE, "dequant: rows [%d,%d) outside [0,%d)", row0,

@@ -94,6 +94,11 @@ _SIGS = {
     "llg_hipd_window_step": (C.c_int, [_vp, _i64, _vp, _vp, _vp, C.c_int, _vp]),
     "llg_hipd_moe_ffn": (
         C.c_int, [_vp, _i64, _i64, _i64, _i64, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp, _vp]),
+    "llg_hip_falcon_create": (C.c_int, [_vp, _vp, C.c_float, C.c_float, C.c_int, _i64, _vp, _vp,
+                                        _i64, _i64, _i64, _i64p]),
+    "llg_hip_falcon_set_thresholds": (C.c_int, [_vp, _i64, _vp]),
+    "llg_hip_falcon_forward": (C.c_int, [_vp, _i64, C.c_int32, C.c_int, _vp, _vp, _vp, _vp]),
+    "llg_hipd_falcon_step": (C.c_int, [_vp, _i64, _vp, C.c_int, _vp, _vp]),
 }
 
 _lib = None
@@ -432,3 +437,94 @@ def moe_ffn(dev: Device, router: Handle, gate: Handle, up: Handle, down: Handle,
     if squeeze:
         return out[0], ids[0], w[0]
     return out, ids, w
+
+
+class FalconModel:
+    """The Falcon decode of inference.FlashContext.ForwardFlash
+    (ffn_flash.go:115-185) with its weights in HBM.  `dims`: n_layers, hidden,
+    n_heads, n_kv, head_dim, ff, vocab, max_seq, rope_base, eps.  `w`: embed,
+    lm_head (GGUF rows), out_w, out_b (f32 [hidden]), and per-layer lists
+    norm_w, norm_b (f32), wq, wk, wv, wo (GGUF rows), pwup, pwout (f32
+    predictor), up, down_t (GGUF rows of the bundle halves).  Arrays may be
+    host numpy arrays or CUDA tensors."""
+
+    def __init__(self, dev: Device, dims: dict, w: dict, thresholds, t: int = 2,
+                 act: int = ACT_RELU):
+        self.dev, self.dims = dev, dict(dims)
+        h, nh, nkv, hd = dims["hidden"], dims["n_heads"], dims["n_kv"], dims["head_dim"]
+        ff, V, L = dims["ff"], dims["vocab"], dims["n_layers"]
+        self._h = []
+        up = self._keep
+
+        def vec(a):
+            return up(dev.upload_f32(_as_host_f32(a).reshape(1, -1)))
+
+        def cat_rows(parts):
+            if all(hasattr(p, "is_cuda") for p in parts):
+                import torch
+                return torch.cat([p.reshape(p.shape[0], -1) for p in parts])
+            return np.concatenate([np.asarray(p) for p in parts])
+
+        self.embed = up(dev.upload_matrix(w["embed"], t, V, h))
+        self.lm_head = up(dev.upload_matrix(w["lm_head"], t, V, h))
+        self.out_w, self.out_b = vec(w["out_w"]), vec(w["out_b"])
+        lh = []
+        for l in range(L):
+            wqkv = cat_rows([w["wq"][l], w["wk"][l], w["wv"][l]])
+            hs = [vec(w["norm_w"][l]), vec(w["norm_b"][l]),
+                  up(dev.upload_matrix(wqkv, t, (nh + 2 * nkv) * hd, h)),
+                  up(dev.upload_matrix(w["wo"][l], t, h, nh * hd)),
+                  up(dev.upload_matrix(w["pwup"][l], F32, w["pwup"][l].shape[0], h)),
+                  up(dev.upload_matrix(w["pwout"][l], F32, ff, w["pwout"][l].shape[1])),
+                  up(dev.upload_bundle(w["up"][l], w["down_t"][l], t, h, ff))]
+            lh += [x.id for x in hs]
+        d32 = np.array([L, h, nh, nkv, hd, ff, V, dims["max_seq"]], np.int32)
+        lh = np.array(lh, np.int64)
+        thr = _f32(thresholds)
+        out = C.c_int64()
+        dev.check(dev.lib.llg_hip_falcon_create(
+            dev.h, _ptr(d32), float(dims["rope_base"]), float(dims["eps"]), act, self.embed.id,
+            _ptr(lh), _ptr(thr), self.out_w.id, self.out_b.id, self.lm_head.id, C.byref(out)),
+            "falcon_create")
+        self.model = Handle(dev, out.value, "model")
+
+    def _keep(self, hnd: "Handle") -> "Handle":
+        self._h.append(hnd)
+        return hnd
+
+    def set_thresholds(self, thresholds):
+        thr = _f32(thresholds)
+        self.dev.check(self.dev.lib.llg_hip_falcon_set_thresholds(self.dev.h, self.model.id,
+                                                                  _ptr(thr)), "thresholds")
+
+    def forward(self, token: int, pos: int, pred_logits: bool = False):
+        """ForwardFlash(token, pos) -> (logits, greedy next token, n_active per
+        layer[, predictor logits [n_layers x ff]])."""
+        lg = np.empty(self.dims["vocab"], np.float32)
+        nt = np.zeros(1, np.int32)
+        na = np.empty(self.dims["n_layers"], np.int32)
+        pl = np.empty((self.dims["n_layers"], self.dims["ff"]), np.float32) if pred_logits else None
+        self.dev.check(self.dev.lib.llg_hip_falcon_forward(
+            self.dev.h, self.model.id, int(token), int(pos), _ptr(lg), _ptr(nt), _ptr(na),
+            _ptr(pl) if pl is not None else None), "ForwardFlash")
+        if pred_logits:
+            return lg, int(nt[0]), na, pl
+        return lg, int(nt[0]), na
+
+    def step_device(self, d_token: int, pos: int, d_next: int, d_logits: int = 0):
+        """Enqueue one token on the library stream (device pointers as ints)."""
+        self.dev.check(self.dev.lib.llg_hipd_falcon_step(
+            self.dev.h, self.model.id, C.c_void_p(d_token), int(pos), C.c_void_p(d_next),
+            C.c_void_p(d_logits) if d_logits else None), "falcon_step")
+
+    def release(self):
+        self.model.release()
+        for x in self._h:
+            x.release()
+        self._h = []
+
+
+def _as_host_f32(a) -> np.ndarray:
+    if hasattr(a, "is_cuda"):
+        a = a.detach().float().cpu().numpy()
+    return _f32(a)

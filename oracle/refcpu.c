@@ -541,3 +541,159 @@ int refcpu_moe_ffn(const float *router, const uint8_t *gate_raw, const uint8_t *
     free(hv);
     return 0;
 }
+
+/* ---- Falcon decode on the sparse FFN path ------------------------------- */
+struct refcpu_falcon {
+    refcpu_falcon_params p;
+    float *embed, *wq, *wk, *wv, *wo, *lm; /* dequantized at load (loader/ReadTensor) */
+    float *kcache, *vcache;                 /* [n_layers][max_seq][kv_dim] (kvcache.go:25-37) */
+    int seq_len;                            /* KVCache.SeqLen */
+};
+
+static float *dequant_rows(const uint8_t *raw, int t, int64_t rows, int cols) {
+    const int64_t rb = refcpu_byte_size(t, cols);
+    float *out = (float *)malloc(sizeof(float) * (size_t)(rows * cols));
+    if (!out || rb < 0) {
+        free(out);
+        return NULL;
+    }
+    refcpu_dequantize(raw, rb * rows, t, out);
+    return out;
+}
+
+refcpu_falcon *refcpu_falcon_new(const refcpu_falcon_params *p) {
+    refcpu_falcon *m = (refcpu_falcon *)calloc(1, sizeof(refcpu_falcon));
+    if (!m) return NULL;
+    m->p = *p;
+    const int L = p->n_layers, h = p->hidden, hd = p->head_dim;
+    const int qd = p->n_heads * hd, kvd = p->n_kv * hd;
+    m->embed = dequant_rows(p->embed, p->t, p->vocab, h);
+    m->wq = dequant_rows(p->wq, p->t, (int64_t)L * qd, h);
+    m->wk = dequant_rows(p->wk, p->t, (int64_t)L * kvd, h);
+    m->wv = dequant_rows(p->wv, p->t, (int64_t)L * kvd, h);
+    m->wo = dequant_rows(p->wo, p->t, (int64_t)L * h, qd);
+    m->lm = dequant_rows(p->lm_head, p->t, p->vocab, h);
+    m->kcache = (float *)calloc((size_t)L * p->max_seq * kvd, sizeof(float));
+    m->vcache = (float *)calloc((size_t)L * p->max_seq * kvd, sizeof(float));
+    if (!m->embed || !m->wq || !m->wk || !m->wv || !m->wo || !m->lm || !m->kcache ||
+        !m->vcache) {
+        refcpu_falcon_free(m);
+        return NULL;
+    }
+    return m;
+}
+
+void refcpu_falcon_free(refcpu_falcon *m) {
+    if (!m) return;
+    free(m->embed);
+    free(m->wq);
+    free(m->wk);
+    free(m->wv);
+    free(m->wo);
+    free(m->lm);
+    free(m->kcache);
+    free(m->vcache);
+    free(m);
+}
+
+void refcpu_falcon_commit(refcpu_falcon *m) { m->seq_len++; }
+
+/* inference/forward.go:483-497 */
+static void rope_inplace(float *vec, int n_heads, int head_dim, int pos, float base) {
+    const int half = head_dim / 2;
+    for (int hh = 0; hh < n_heads; hh++) {
+        float *head = vec + (size_t)hh * head_dim;
+        for (int i = 0; i < half; i++) {
+            const double freq = (double)pos / pow((double)base, (double)(2 * i) / (double)head_dim);
+            const float c = (float)cos(freq), s = (float)sin(freq);
+            const float x0 = head[i], x1 = head[i + half];
+            head[i] = x0 * c - x1 * s;
+            head[i + half] = x0 * s + x1 * c;
+        }
+    }
+}
+
+int refcpu_falcon_forward(refcpu_falcon *m, int32_t token, int pos, float *logits,
+                          int32_t *n_active_out) {
+    const refcpu_falcon_params *p = &m->p;
+    const int h = p->hidden, hd = p->head_dim, qd = p->n_heads * hd, kvd = p->n_kv * hd;
+    if (token < 0 || token >= p->vocab || m->seq_len >= p->max_seq) return -1;
+    const int64_t rb_h = refcpu_byte_size(p->t, h);
+    float *x = (float *)malloc(sizeof(float) * (size_t)h);
+    float *normed = (float *)malloc(sizeof(float) * (size_t)h);
+    float *q = (float *)malloc(sizeof(float) * (size_t)qd);
+    float *k = (float *)malloc(sizeof(float) * (size_t)kvd);
+    float *v = (float *)malloc(sizeof(float) * (size_t)kvd);
+    float *att = (float *)malloc(sizeof(float) * (size_t)qd);
+    float *attn_out = (float *)malloc(sizeof(float) * (size_t)h);
+    float *ffn_out = (float *)malloc(sizeof(float) * (size_t)h);
+    float *scores = (float *)malloc(sizeof(float) * (size_t)(m->seq_len + 1));
+    int32_t *active = (int32_t *)malloc(sizeof(int32_t) * (size_t)p->ff);
+    memcpy(x, m->embed + (size_t)token * h, sizeof(float) * (size_t)h); /* forward.go:449-454 */
+    const int seq = m->seq_len + 1;                                     /* forward.go:249 */
+    const float scale = (float)(1.0 / sqrt((double)hd));                /* forward.go:255 */
+    for (int l = 0; l < p->n_layers; l++) {
+        /* ffn_flash.go:142-146: the one LayerNorm of Falcon's parallel block */
+        refcpu_layernorm(x, p->norm_w + (size_t)l * h, p->norm_b + (size_t)l * h, normed, h,
+                         p->eps);
+        /* forward.go:211-222 */
+        refcpu_matmulvec(m->wq + (size_t)l * qd * h, qd, h, normed, q);
+        refcpu_matmulvec(m->wk + (size_t)l * kvd * h, kvd, h, normed, k);
+        refcpu_matmulvec(m->wv + (size_t)l * kvd * h, kvd, h, normed, v);
+        rope_inplace(q, p->n_heads, hd, pos, p->rope_base); /* forward.go:239-242 */
+        rope_inplace(k, p->n_kv, hd, pos, p->rope_base);
+        float *kc = m->kcache + (size_t)l * p->max_seq * kvd;
+        float *vc = m->vcache + (size_t)l * p->max_seq * kvd;
+        memcpy(kc + (size_t)m->seq_len * kvd, k, sizeof(float) * (size_t)kvd); /* :245-246 */
+        memcpy(vc + (size_t)m->seq_len * kvd, v, sizeof(float) * (size_t)kvd);
+        memset(att, 0, sizeof(float) * (size_t)qd);
+        for (int hh = 0; hh < p->n_heads; hh++) { /* forward.go:263-301 */
+            const float *qh = q + (size_t)hh * hd;
+            const int kvh = hh * p->n_kv / p->n_heads;
+            for (int t = 0; t < seq; t++) {
+                const float *kh = kc + (size_t)t * kvd + (size_t)kvh * hd;
+                float dot = 0.0f;
+                for (int d = 0; d < hd; d++) dot += qh[d] * kh[d];
+                scores[t] = dot * scale;
+            }
+            refcpu_softmax_inplace(scores, seq);
+            float *oh = att + (size_t)hh * hd;
+            for (int t = 0; t < seq; t++) {
+                const float *vh = vc + (size_t)t * kvd + (size_t)kvh * hd;
+                for (int d = 0; d < hd; d++) oh[d] += scores[t] * vh[d];
+            }
+        }
+        refcpu_matmulvec(m->wo + (size_t)l * h * qd, h, qd, att, attn_out); /* :305 */
+        /* ffnFlash path 2: predictor on the attention output (ffn_flash.go:157,
+         * 225-231), sparse FFN on the normed input */
+        const int n_act = refcpu_predict(p->pwup + (size_t)l * p->rank * h,
+                                         p->pwout + (size_t)l * p->ff * p->rank, NULL, h, p->rank,
+                                         p->ff, attn_out, p->thr[l], active, NULL);
+        if (n_active_out) n_active_out[l] = n_act;
+        refcpu_ffn_sparse_load(p->up + (size_t)l * p->ff * rb_h,
+                               p->down_t + (size_t)l * p->ff * rb_h, p->t, h, p->ff, normed,
+                               active, n_act, p->act, ffn_out);
+        for (int i = 0; i < h; i++) x[i] += attn_out[i]; /* ffn_flash.go:161-166 */
+        for (int i = 0; i < h; i++) x[i] += ffn_out[i];
+    }
+    refcpu_layernorm(x, p->out_w, p->out_b, normed, h, p->eps); /* ffn_flash.go:126 */
+    refcpu_matmulvec(m->lm, p->vocab, h, normed, logits);       /* ffn_flash.go:130 */
+    free(x);
+    free(normed);
+    free(q);
+    free(k);
+    free(v);
+    free(att);
+    free(attn_out);
+    free(ffn_out);
+    free(scores);
+    free(active);
+    return 0;
+}
+
+int refcpu_argmax(const float *v, int n) { /* cmd/generate.go:197-205 */
+    int best = 0;
+    for (int i = 1; i < n; i++)
+        if (v[i] > v[best]) best = i;
+    return best;
+}

@@ -117,6 +117,41 @@ int refcpu_moe_ffn(const float *router, const uint8_t *gate_raw, const uint8_t *
  * ties to the lower index, top-k, renorm) on given logits. */
 int refcpu_moe_route(const float *logits, int n_exp, int k, int32_t *ids_out, float *w_out);
 
+/* Falcon-architecture decode on the sparse FFN path:
+ * inference/ffn_flash.go:115-185 (ForwardFlash, forwardLayerFlash with the
+ * parallel attention/FFN layout, ffnFlash path 2), inference/forward.go:206-310
+ * (attention without biases or QK norm), :449-497 (embedding, RoPE),
+ * kvcache/kvcache.go:25-82, tensor/ops.go:138-165 (LayerNorm).
+ * Matrices are GGUF rows of type t; per-layer arrays are concatenated layer
+ * after layer.  As the reference does at load, the embedding, attention and
+ * LM-head matrices are dequantized to fp32 once in refcpu_falcon_new; the FFN
+ * rows are dequantized per token (ffnSparseLoad). */
+typedef struct {
+    int n_layers, hidden, n_heads, n_kv, head_dim, ff, vocab, max_seq, rank, act, t;
+    float rope_base, eps;
+    const uint8_t *embed;          /* vocab rows of ByteSize(hidden) */
+    const float *norm_w, *norm_b;  /* [n_layers][hidden] */
+    const uint8_t *wq, *wk, *wv;   /* [n_layers][n_heads*hd | n_kv*hd rows of ByteSize(hidden)] */
+    const uint8_t *wo;             /* [n_layers][hidden rows of ByteSize(n_heads*hd)] */
+    const float *pwup, *pwout;     /* [n_layers][rank x hidden], [n_layers][ff x rank] */
+    const float *thr;              /* [n_layers] */
+    const uint8_t *up, *down_t;    /* [n_layers][ff rows of ByteSize(hidden)] */
+    const float *out_w, *out_b;    /* [hidden] */
+    const uint8_t *lm_head;        /* vocab rows of ByteSize(hidden) */
+} refcpu_falcon_params;
+typedef struct refcpu_falcon refcpu_falcon;
+refcpu_falcon *refcpu_falcon_new(const refcpu_falcon_params *p);
+void refcpu_falcon_free(refcpu_falcon *m);
+/* ForwardFlash(token, pos): logits [vocab]; n_active_out (optional) [n_layers].
+ * The K/V of this token go to cache row SeqLen; returns 0, or -1 if the token
+ * or SeqLen is out of range. */
+int refcpu_falcon_forward(refcpu_falcon *m, int32_t token, int pos, float *logits,
+                          int32_t *n_active_out);
+/* kvcache.go:55-57 (generate.go:94,119 call it after every token). */
+void refcpu_falcon_commit(refcpu_falcon *m);
+/* cmd/generate.go:197-205 */
+int refcpu_argmax(const float *v, int n);
+
 #ifdef __cplusplus
 }
 #endif

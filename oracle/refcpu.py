@@ -271,3 +271,73 @@ def moe_ffn(router, gate_raw, up_raw, down_raw, t: int, hidden: int, eff: int, n
     if rc:
         raise ValueError(f"moeFFN: invalid hparams (rc={rc})")
     return out, ids, w
+
+
+class _FalconParams(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ["n_layers", "hidden", "n_heads", "n_kv", "head_dim", "ff",
+                                       "vocab", "max_seq", "rank", "act", "t"]] + \
+               [("rope_base", C.c_float), ("eps", C.c_float)] + \
+               [(n, C.c_void_p) for n in ["embed", "norm_w", "norm_b", "wq", "wk", "wv", "wo",
+                                          "pwup", "pwout", "thr", "up", "down_t", "out_w",
+                                          "out_b", "lm_head"]]
+
+
+_SIGS.update({
+    "refcpu_falcon_new": (_vp, [C.POINTER(_FalconParams)]),
+    "refcpu_falcon_free": (None, [_vp]),
+    "refcpu_falcon_forward": (C.c_int, [_vp, C.c_int32, C.c_int, _vp, _vp]),
+    "refcpu_falcon_commit": (None, [_vp]),
+    "refcpu_argmax": (C.c_int, [_vp, C.c_int]),
+})
+
+
+class Falcon:
+    """inference/ffn_flash.go:115-185 (ForwardFlash on the Falcon layout, path 2)
+    with kvcache/kvcache.go.  `w` holds the weights: embed, lm_head (vocab GGUF
+    rows), and per-layer lists norm_w, norm_b (f32 [hidden]), wq, wk, wv, wo (GGUF
+    rows), pwup, pwout (f32), up, down_t (GGUF rows of the bundle halves); out_w,
+    out_b (f32).  Per-layer arrays are concatenated here."""
+
+    def __init__(self, dims: dict, w: dict, thr, t: int = Q4_0, act: int = ACT_RELU):
+        cat = lambda k, conv: np.ascontiguousarray(np.concatenate([conv(a).ravel() for a in w[k]]))
+        self._keep = {
+            "embed": _u8(w["embed"]), "lm_head": _u8(w["lm_head"]),
+            "out_w": _f32(w["out_w"]), "out_b": _f32(w["out_b"]),
+            "thr": _f32(np.asarray(thr, np.float32)),
+        }
+        for k in ["norm_w", "norm_b", "pwup", "pwout"]:
+            self._keep[k] = cat(k, _f32)
+        for k in ["wq", "wk", "wv", "wo", "up", "down_t"]:
+            self._keep[k] = cat(k, _u8)
+        p = _FalconParams()
+        for k in ["n_layers", "hidden", "n_heads", "n_kv", "head_dim", "ff", "vocab", "max_seq",
+                  "rank"]:
+            setattr(p, k, int(dims[k]))
+        p.act, p.t = act, t
+        p.rope_base, p.eps = float(dims["rope_base"]), float(dims["eps"])
+        for k, a in self._keep.items():
+            setattr(p, k, a.ctypes.data)
+        self.vocab, self.n_layers = int(dims["vocab"]), int(dims["n_layers"])
+        self.m = lib().refcpu_falcon_new(C.byref(p))
+        if not self.m:
+            raise MemoryError("refcpu_falcon_new failed")
+
+    def forward(self, token: int, pos: int):
+        """ForwardFlash(token, pos) -> (logits, n_active per layer); then commit."""
+        lg = np.empty(self.vocab, np.float32)
+        na = np.empty(self.n_layers, np.int32)
+        if lib().refcpu_falcon_forward(self.m, token, pos, _p(lg), _p(na)):
+            raise ValueError("falcon forward: token or position out of range")
+        lib().refcpu_falcon_commit(self.m)
+        return lg, na
+
+    def __del__(self):
+        if getattr(self, "m", None):
+            lib().refcpu_falcon_free(self.m)
+            self.m = None
+
+
+def argmax(v) -> int:
+    """cmd/generate.go:197-205"""
+    v = _f32(v)
+    return int(lib().refcpu_argmax(_p(v), v.size))

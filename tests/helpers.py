@@ -71,3 +71,94 @@ def window_sets(rng, ff: int, n_active: int, steps: int, carry: float):
         new = rng.choice(comp, n_active - keep, replace=False)
         sets.append(np.sort(np.concatenate([kept, new])).astype(np.int32))
     return sets
+
+
+# ---------------------------------------------------------------- Falcon decode
+def make_falcon(rng, d: dict, t: int = gg.Q4_0) -> dict:
+    """Random Falcon-layout weights (GGUF bytes for the matrices, f32 for the
+    norms and predictors); the norms are random so that weight and bias count."""
+    h, nh, nkv, hd, ff = d["hidden"], d["n_heads"], d["n_kv"], d["head_dim"], d["ff"]
+    V, r, L = d["vocab"], d["rank"], d["n_layers"]
+    w = {"embed": quant(normal(rng, (V, h), 0.5), t), "lm_head": quant(normal(rng, (V, h), 0.05), t),
+         "out_w": 1.0 + normal(rng, h, 0.1), "out_b": normal(rng, h, 0.1)}
+    for k in ["norm_w", "norm_b", "wq", "wk", "wv", "wo", "pwup", "pwout", "up", "down_t"]:
+        w[k] = []
+    for _ in range(L):
+        w["norm_w"].append(1.0 + normal(rng, h, 0.1))
+        w["norm_b"].append(normal(rng, h, 0.1))
+        w["wq"].append(quant(normal(rng, (nh * hd, h), 0.05), t))
+        w["wk"].append(quant(normal(rng, (nkv * hd, h), 0.05), t))
+        w["wv"].append(quant(normal(rng, (nkv * hd, h), 0.05), t))
+        w["wo"].append(quant(normal(rng, (h, nh * hd), 0.05), t))
+        w["pwup"].append(normal(rng, (r, h), 0.05))
+        w["pwout"].append(normal(rng, (ff, r), 0.05))
+        w["up"].append(quant(normal(rng, (ff, h), 0.05), t))
+        w["down_t"].append(quant(normal(rng, (ff, h), 0.05), t))
+    return w
+
+
+def _gap_threshold(lg: np.ndarray, frac: float) -> float:
+    """A float32 threshold near the (1-frac) quantile of lg, at the midpoint of
+    the widest gap between neighbouring values there (so selection does not
+    depend on fp32 rounding)."""
+    s = np.sort(lg.ravel())
+    n = s.size
+    c = int((1.0 - frac) * n)
+    lo, hi = max(1, c - n // 20), min(n - 1, c + n // 20)
+    gaps = s[lo:hi + 1] - s[lo - 1:hi]
+    i = lo + int(np.argmax(gaps))
+    return float(np.float32((s[i - 1] + s[i]) / 2))
+
+
+def ref_falcon_f64(w: dict, d: dict, tokens, frac: float = 0.1, t: int = gg.Q4_0):
+    """float64 ForwardFlash over a token sequence (positions 0..T-1), layer by
+    layer over all tokens; each layer's threshold is picked at a wide gap of its
+    predictor logits.  Returns (logits [T x V], n_active [T x L], thresholds)."""
+    h, nh, nkv, hd, ff = d["hidden"], d["n_heads"], d["n_kv"], d["head_dim"], d["ff"]
+    L, eps, base = d["n_layers"], d["eps"], d["rope_base"]
+    dq = lambda raw, cols: deq(raw, t, cols).astype(np.float64)
+    tokens = np.asarray(tokens)
+    T = tokens.size
+    X = dq(w["embed"], h)[tokens]
+
+    def ln(Z, g, b):
+        mu = Z.mean(1, keepdims=True)
+        var = ((Z - mu) ** 2).mean(1, keepdims=True)
+        return (Z - mu) / np.sqrt(var + eps) * g.astype(np.float64) + b.astype(np.float64)
+
+    def rope(M, nheads):
+        M = M.reshape(T, nheads, hd).copy()
+        half = hd // 2
+        i = np.arange(half)
+        for s in range(T):
+            fr = s / np.power(float(base), 2.0 * i / hd)
+            c, sn = np.cos(fr), np.sin(fr)
+            x0, x1 = M[s, :, :half].copy(), M[s, :, half:].copy()
+            M[s, :, :half] = x0 * c - x1 * sn
+            M[s, :, half:] = x0 * sn + x1 * c
+        return M
+
+    thr, nact = [], np.zeros((T, L), np.int64)
+    for l in range(L):
+        N = ln(X, w["norm_w"][l], w["norm_b"][l])
+        Q = rope(N @ dq(w["wq"][l], h).T, nh)
+        K = rope(N @ dq(w["wk"][l], h).T, nkv)
+        Vv = (N @ dq(w["wv"][l], h).T).reshape(T, nkv, hd)
+        att = np.zeros((T, nh, hd))
+        for s in range(T):
+            for head in range(nh):
+                kvh = head * nkv // nh
+                sc = K[:s + 1, kvh] @ Q[s, head] / np.sqrt(hd)
+                p = np.exp(sc - sc.max())
+                p /= p.sum()
+                att[s, head] = p @ Vv[:s + 1, kvh]
+        A = att.reshape(T, nh * hd) @ dq(w["wo"][l], nh * hd).T
+        lg = np.maximum(A @ w["pwup"][l].T.astype(np.float64), 0.0) @ w["pwout"][l].T.astype(np.float64)
+        th = _gap_threshold(lg, frac)
+        thr.append(th)
+        on = lg > th
+        nact[:, l] = on.sum(1)
+        U = np.maximum(N @ dq(w["up"][l], h).T, 0.0) * on
+        X = X + A + U @ dq(w["down_t"][l], h)
+    out = ln(X, w["out_w"], w["out_b"]) @ dq(w["lm_head"], h).T
+    return out, nact, np.array(thr, np.float32)

@@ -15,8 +15,8 @@ import torch
 import llg
 import llg.gguf as gg
 from oracle import refcpu as R
-from tests.helpers import (make_sparse_layer, max_rel_err, normal, quant, threshold_for,
-                           window_sets)
+from tests.helpers import (make_falcon, make_sparse_layer, max_rel_err, normal, quant,
+                           ref_falcon_f64, threshold_for, window_sets)
 
 pytestmark = pytest.mark.gpu
 
@@ -408,3 +408,70 @@ def test_bad_handles_and_types(dev, rng):
     with pytest.raises(llg.LlgError) as e:
         llg.ffn_sparse_load(dev, fake, np.zeros(64, np.float32), np.array([0], np.int32))
     assert e.value.code == llg.LLG_E_HANDLE
+
+
+# ---------------------------------------------------------------- Falcon decode
+FALCON_GPU = dict(n_layers=2, hidden=256, n_heads=4, n_kv=1, head_dim=64, ff=512, vocab=300,
+                  max_seq=32, rank=16, rope_base=10000.0, eps=1e-5)
+
+
+def _top2_gap(v):
+    s = np.sort(v)
+    return float(s[-1] - s[-2])
+
+
+@pytest.mark.parametrize("n_kv", [1, 2])
+def test_falcon_forward(dev, rng, n_kv):
+    """ForwardFlash token by token against the oracle: logits within the FFN
+    bar, per-layer active counts exact (thresholds sit in wide logit gaps),
+    greedy token equal wherever the top-2 logit gap is clear."""
+    d = dict(FALCON_GPU, n_kv=n_kv)
+    w = make_falcon(rng, d)
+    toks = rng.integers(0, d["vocab"], 10)
+    _, nact, thr = ref_falcon_f64(w, d, toks)
+    ref = R.Falcon(d, w, thr)
+    m = llg.FalconModel(dev, d, w, thr)
+    for s, tk in enumerate(toks):
+        lg, nxt, na = m.forward(int(tk), s)
+        rl, rn = ref.forward(int(tk), s)
+        assert np.array_equal(na, rn) and np.array_equal(na, nact[s]), (s, na, rn)
+        assert max_rel_err(lg, rl) <= TOL, s
+        if _top2_gap(rl) > 1e-3 * np.max(np.abs(rl)):
+            assert nxt == R.argmax(rl), s
+    with pytest.raises(llg.LlgError) as e:
+        m.forward(0, d["max_seq"])
+    assert e.value.code == llg.LLG_E_RANGE
+    with pytest.raises(llg.LlgError) as e:
+        m.forward(d["vocab"], 0)
+    assert e.value.code == llg.LLG_E_RANGE
+    m.release()
+
+
+def test_falcon_device_greedy_loop(dev, rng):
+    """Prompt + greedy decode chained on the device (the next token never goes
+    through the host) against the oracle's greedy continuation."""
+    d = dict(FALCON_GPU)
+    w = make_falcon(rng, d)
+    prompt = rng.integers(0, d["vocab"], 6)
+    n_gen = 8
+    # thresholds from the prompt plus a provisional continuation
+    _, _, thr = ref_falcon_f64(w, d, prompt)
+    ref = R.Falcon(d, w, thr)
+    seq = list(prompt)
+    for s in range(len(prompt) + n_gen - 1):
+        lg, _ = ref.forward(int(seq[s]), s)
+        if s >= len(prompt) - 1:
+            seq.append(R.argmax(lg))
+    m = llg.FalconModel(dev, d, w, thr)
+    toks = torch.tensor(np.array(prompt, np.int32), device="cuda")
+    gen = torch.zeros(n_gen + 1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    for s in range(len(prompt)):
+        out = gen.data_ptr() if s == len(prompt) - 1 else gen.data_ptr() + 4 * n_gen
+        m.step_device(toks.data_ptr() + 4 * s, s, out)
+    for i in range(n_gen - 1):
+        m.step_device(gen.data_ptr() + 4 * i, len(prompt) + i, gen.data_ptr() + 4 * (i + 1))
+    dev.sync()
+    got = gen[:n_gen].cpu().numpy()
+    assert np.array_equal(got, np.array(seq[len(prompt):len(prompt) + n_gen])), (got, seq)
+    m.release()

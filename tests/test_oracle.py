@@ -42,7 +42,8 @@ import pytest
 
 import llg.gguf as gg
 from oracle import refcpu as R
-from tests.helpers import deq, make_sparse_layer, normal, quant, ref_sparse_f64, window_sets
+from tests.helpers import (deq, make_falcon, make_sparse_layer, normal, quant, ref_falcon_f64,
+                           ref_sparse_f64, window_sets)
 
 
 # ---------------------------------------------------------------- f16 -> f32
@@ -346,3 +347,60 @@ def test_moe_invalid_hparams(rng):
     with pytest.raises(ValueError):
         R.moe_ffn(np.zeros((4, 32), np.float32), np.zeros(1, np.uint8), np.zeros(1, np.uint8),
                   np.zeros(1, np.uint8), gg.Q4_0, 32, 32, 4, 0, np.zeros(32, np.float32))
+
+
+# ---------------------------------------------------------------- Falcon decode
+FALCON_TINY = dict(n_layers=2, hidden=64, n_heads=4, n_kv=1, head_dim=16, ff=128, vocab=50,
+                   max_seq=16, rank=8, rope_base=10000.0, eps=1e-5)
+
+
+@pytest.mark.parametrize("n_kv", [1, 2, 4])
+def test_falcon_forward_f64(rng, n_kv):
+    """ForwardFlash restatement against a float64 brute force over 7 tokens:
+    LayerNorm, RoPE at each position, MQA/GQA/MHA head mapping, causal softmax
+    attention over the KV cache, predictor selection on the attention output,
+    the sparse FFN on the normed input, the parallel residual and the LM head."""
+    d = dict(FALCON_TINY, n_kv=n_kv)
+    w = make_falcon(rng, d)
+    toks = rng.integers(0, d["vocab"], 7)
+    ref, nact, thr = ref_falcon_f64(w, d, toks)
+    m = R.Falcon(d, w, thr)
+    for s, tk in enumerate(toks):
+        lg, na = m.forward(int(tk), s)
+        assert np.array_equal(na, nact[s]), (s, na, nact[s])
+        assert np.max(np.abs(lg - ref[s])) <= 1e-4 * np.max(np.abs(ref[s])), s
+    assert 0 < nact.mean() < d["ff"]
+
+
+def test_falcon_pos0_closed_form(rng):
+    """At position 0 softmax over one key is 1, so every head's attention output
+    is its KV head's value and RoPE is the identity: the first logits follow from
+    the embedding row in closed form (no predictor neuron active)."""
+    d = dict(FALCON_TINY, n_layers=1)
+    w = make_falcon(rng, d)
+    m = R.Falcon(d, w, [1e30])
+    lg, na = m.forward(7, 0)
+    assert na[0] == 0
+    h, hd = d["hidden"], d["head_dim"]
+    x = deq(w["embed"], gg.Q4_0, h)[7].astype(np.float64)
+    ln = lambda z, g, b: (z - z.mean()) / np.sqrt(z.var() + d["eps"]) * g + b
+    n = ln(x, w["norm_w"][0], w["norm_b"][0])
+    v = deq(w["wv"][0], gg.Q4_0, h).astype(np.float64) @ n
+    att = np.tile(v, d["n_heads"])
+    x = x + deq(w["wo"][0], gg.Q4_0, d["n_heads"] * hd).astype(np.float64) @ att
+    ref = deq(w["lm_head"], gg.Q4_0, h).astype(np.float64) @ ln(x, w["out_w"], w["out_b"])
+    assert np.max(np.abs(lg - ref)) <= 1e-4 * np.max(np.abs(ref))
+
+
+def test_falcon_kv_and_argmax(rng):
+    """Positions beyond the cache are refused; argmax keeps the first maximum."""
+    d = dict(FALCON_TINY, max_seq=3)
+    w = make_falcon(rng, d)
+    m = R.Falcon(d, w, [0.0, 0.0])
+    for s in range(3):
+        m.forward(1, s)
+    with pytest.raises(ValueError):
+        m.forward(1, 3)
+    assert R.argmax(np.array([1, 3, 3, 2], np.float32)) == 1
+    assert R.argmax(np.array([np.nan, 3, 5], np.float32)) == 0
+    assert R.argmax(np.array([1, np.nan, 5], np.float32)) == 2
