@@ -3,7 +3,8 @@
 // llg_sparse.hip).
 //
 // k_matvec_q: y[r] = act(sum_b block_dot(row r, b, x)).  A workgroup owns a
-// tile of MV_TILE rows and one column chunk of at most MV_CHUNK blocks; it
+// tile of `tile_rows` rows (32, or 8 for matrices under 8192 rows so that the
+// grid still covers the CUs) and one column chunk of at most MV_CHUNK blocks; it
 // stages that chunk of x in LDS (36-float stride per 32-float block, so 16
 // lanes reading one block each hit distinct banks).  Each wavefront takes
 // MV_ROWS rows at a time and issues the loads of all its blocks of those rows
@@ -15,13 +16,16 @@
 
 #define MV_ROWS 2
 #define MV_TILE 32        // rows per workgroup (4 wavefronts x 4 passes x MV_ROWS)
+#define MV_TILE_SMALL 8   // rows per workgroup below MV_SMALL_ROWS rows (one pass)
+#define MV_SMALL_ROWS 8192
 #define MV_CHUNK 160      // max blocks of x staged per workgroup
 #define MV_XS 36          // staged floats per 32-float block
 #define MV_BATCH 3        // blocks per lane whose loads are issued together
 
 template <int T>
 __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w, long long stride,
-                                                  RowFmt f, int rows, int chunk_blocks,
+                                                  RowFmt f, int rows, int tile_rows,
+                                                  int chunk_blocks,
                                                   const float *__restrict__ x, int act,
                                                   float *__restrict__ y, float *__restrict__ zero,
                                                   int zero_n) {
@@ -35,26 +39,29 @@ __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w,
         const int gtid = blockIdx.x * blockDim.x + threadIdx.x;
         for (int i = gtid; i < zero_n; i += gridDim.x * blockDim.x) zero[i] = 0.0f;
     }
-    llg_stage_x_sum<MV_XS>(xs, x + (size_t)cb0 * 32, cnb);
-    __syncthreads();
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform per wavefront
-    const int r_end = min(rows, (tile + 1) * MV_TILE);
-    for (int r0 = tile * MV_TILE + wave * MV_ROWS; r0 < r_end; r0 += 4 * MV_ROWS) {
+    const int r_end = min(rows, (tile + 1) * tile_rows);
+    const int r_first = tile * tile_rows + wave * MV_ROWS;
+    // request the bytes of all MV_BATCH x MV_ROWS blocks, then use them; loads
+    // are never under a per-lane condition (that serialises them): lanes past
+    // the chunk reload its last block and drop it, a row past the end reloads
+    // the last row.  The first batch is requested before x is staged.
+    BlockRaw<T> r[MV_BATCH][MV_ROWS];
+#define MV_ISSUE(r0_, bb_)                                                                      \
+    _Pragma("unroll") for (int i = 0; i < MV_BATCH; i++)                                       \
+        _Pragma("unroll") for (int q = 0; q < MV_ROWS; q++)                                    \
+            llg_block_load<T>(r[i][q], w + (long long)min((r0_) + q, r_end - 1) * stride, f,   \
+                              cb0 + min((bb_) + lane + 64 * i, cnb - 1))
+    MV_ISSUE(min(r_first, r_end - 1), 0);
+    llg_stage_x_sum<MV_XS>(xs, x + (size_t)cb0 * 32, cnb);
+    __syncthreads();
+    for (int r0 = r_first; r0 < r_end; r0 += 4 * MV_ROWS) {
         float s[MV_ROWS];
 #pragma unroll
         for (int q = 0; q < MV_ROWS; q++) s[q] = 0.0f;
         for (int bb = 0; bb < cnb; bb += 64 * MV_BATCH) {
-            // request the bytes of all MV_BATCH x MV_ROWS blocks, then use them;
-            // loads are never under a per-lane condition (that serialises
-            // them): lanes past the chunk reload its last block and drop it
-            BlockRaw<T> r[MV_BATCH][MV_ROWS];
-#pragma unroll
-            for (int i = 0; i < MV_BATCH; i++)
-#pragma unroll
-                for (int q = 0; q < MV_ROWS; q++)  // a row past the end reloads the last row
-                    llg_block_load<T>(r[i][q], w + (long long)min(r0 + q, r_end - 1) * stride, f,
-                                      cb0 + min(bb + lane + 64 * i, cnb - 1));
+            if (r0 != r_first || bb != 0) MV_ISSUE(r0, bb);
 #pragma unroll
             for (int i = 0; i < MV_BATCH; i++) {
                 const int bl = bb + lane + 64 * i;
@@ -77,6 +84,7 @@ __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w,
             }
         }
     }
+#undef MV_ISSUE
 }
 
 static int mv_chunk_blocks(const RowFmt &f, int act) {
@@ -99,23 +107,28 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
     if (n_chunks > 1 && zero != d_y) {
         LLG_HIP_TRY(d, hipMemsetAsync(d_y, 0, (size_t)w->rows * 4, st));
     }
-    const int grid = (w->rows + MV_TILE - 1) / MV_TILE * n_chunks;
+    const int tile_rows = w->rows < MV_SMALL_ROWS ? MV_TILE_SMALL : MV_TILE;
+    const int grid = (w->rows + tile_rows - 1) / tile_rows * n_chunks;
     switch (f.type) {
     case LLG_TYPE_Q4_0:
         hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_Q4_0>, dim3(grid), dim3(256), lds, st, w->d,
-                           w->stride, f, w->rows, cb, d_x, act, d_y, zero, zero_n);
+                           w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, zero,
+                           zero_n);
         break;
     case LLG_TYPE_Q8_0:
         hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_Q8_0>, dim3(grid), dim3(256), lds, st, w->d,
-                           w->stride, f, w->rows, cb, d_x, act, d_y, zero, zero_n);
+                           w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, zero,
+                           zero_n);
         break;
     case LLG_TYPE_F16:
         hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_F16>, dim3(grid), dim3(256), lds, st, w->d,
-                           w->stride, f, w->rows, cb, d_x, act, d_y, zero, zero_n);
+                           w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, zero,
+                           zero_n);
         break;
     case LLG_TYPE_F32:
         hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_F32>, dim3(grid), dim3(256), lds, st, w->d,
-                           w->stride, f, w->rows, cb, d_x, act, d_y, zero, zero_n);
+                           w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, zero,
+                           zero_n);
         break;
     default:
         return llg_set_error(d, LLG_E_TYPE, "matvec: unsupported type %d", f.type);

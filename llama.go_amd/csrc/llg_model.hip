@@ -28,7 +28,7 @@
 #include "llg_internal.hpp"
 
 #define NORM_THREADS 1024
-#define ATTN_THREADS 256
+#define ATTN_THREADS 1024
 
 struct LlgModelLayer {
     LlgObject *norm_w, *norm_b, *wqkv, *wo, *pwup, *pwout, *bundle;
@@ -75,29 +75,49 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
     return s;
 }
 
-// x = (x + a1) + a2 (either may be null); out = LayerNorm(x) * w + b.
+// x = (x + a1) + a2 (either may be null); out = LayerNorm(x) * w + b.  Each
+// thread keeps its NORM_PER elements in registers (hidden <= NORM_THREADS *
+// NORM_PER); all loads of a thread are issued together.
+#define NORM_PER 16
 __global__ __launch_bounds__(NORM_THREADS) void k_resid_norm(
     float *__restrict__ x, const float *__restrict__ a1, const float *__restrict__ a2,
     const float *__restrict__ w, const float *__restrict__ b, int n, float eps,
     float *__restrict__ out) {
     __shared__ float red[NORM_THREADS / 64];
+    float v[NORM_PER], p1[NORM_PER], p2[NORM_PER];
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < NORM_PER; k++) {
+        const int i = min(tid + k * NORM_THREADS, n - 1);
+        v[k] = x[i];
+        p1[k] = a1 ? a1[i] : 0.0f;
+        p2[k] = a2 ? a2[i] : 0.0f;
+    }
     float s = 0.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        float v = x[i];
-        if (a1) v = v + a1[i];
-        if (a2) v = v + a2[i];
-        if (a1 || a2) x[i] = v;
-        s += v;
+#pragma unroll
+    for (int k = 0; k < NORM_PER; k++) {
+        const int i = tid + k * NORM_THREADS;
+        if (a1) v[k] = v[k] + p1[k];
+        if (a2) v[k] = v[k] + p2[k];
+        if (i < n) {
+            if (a1 || a2) x[i] = v[k];
+            s += v[k];
+        }
     }
     const float mean = block_sum(s, red) / (float)n;
     float q = 0.0f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float dv = x[i] - mean;
-        q += dv * dv;
+#pragma unroll
+    for (int k = 0; k < NORM_PER; k++) {
+        const float dv = v[k] - mean;
+        if (tid + k * NORM_THREADS < n) q += dv * dv;
     }
     const float var = block_sum(q, red) / (float)n;
     const float std_ = (float)sqrt((double)var + (double)eps);  // ops.go:159
-    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = (x[i] - mean) / std_ * w[i] + b[i];
+#pragma unroll
+    for (int k = 0; k < NORM_PER; k++) {
+        const int i = tid + k * NORM_THREADS;
+        if (i < n) out[i] = (v[k] - mean) / std_ * w[i] + b[i];
+    }
 }
 
 // Sum over each 16-lane row (all lanes of the row get the total).
@@ -120,7 +140,8 @@ __device__ __forceinline__ float wave_max(float v) {
 // from registers and LDS (the cache row is written by the group's first query
 // head for later tokens, so no workgroup waits on another).  Scores live in
 // LDS (pos + 1 floats).
-#define ATT_U 4
+#define ATT_U 8     // key rows per lane requested together
+#define ATT_VU 8    // value rows per thread requested together
 template <int HD>
 __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__ qkv, int n_heads,
                                                        int n_kv, int pos, float rope_base,
@@ -128,11 +149,10 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
                                                        float *__restrict__ out) {
     constexpr int LP = HD / 4;       // lanes per position
     constexpr int PW = 64 / LP;      // positions per wavefront per load
-    constexpr int NG = ATTN_THREADS / HD;  // position groups of the value pass
     extern __shared__ float sc[];    // pos + 1 scores, then probabilities
     __shared__ __attribute__((aligned(16))) float qh[HD], kh[HD];
     __shared__ float red[ATTN_THREADS / 64];
-    __shared__ float part[NG][HD];
+    __shared__ __attribute__((aligned(16))) float part[ATTN_THREADS / (HD / 4)][HD];
     const int h = blockIdx.x;
     const int kvh = h * n_kv / n_heads;  // forward.go:266
     const int kv_dim = n_kv * HD;
@@ -191,7 +211,7 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
     m = wave_max(m);
     if (lane == 0) red[wave] = m;
     __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int i = 0; i < ATTN_THREADS / 64; i++) m = fmaxf(m, red[i]);
     float s = 0.0f;
     for (int t = tid; t < T; t += blockDim.x) {
         const float e = (float)exp((double)(sc[t] - m));
@@ -199,29 +219,38 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
         s += e;
     }
     const float sum = block_sum(s, red);  // its barriers also publish sc
-    // out[d] = sum_t p_t * v_t[d]: thread (d, g) takes t = g, g + NG, ... < pos,
-    // ATT_U rows per step; row pos is added last
-    const int dd = tid % HD, g = tid / HD;
-    float acc = 0.0f;
-    for (int t0 = g; t0 < pos; t0 += NG * ATT_U) {
-        float vv[ATT_U];
+    // out[d] = sum_t p_t * v_t[d]: thread (c, g) holds float4 column c of the
+    // head and takes t = g, g + VG, ... < pos, ATT_VU rows per step; the groups
+    // meet in LDS and row pos is added last
+    constexpr int VC = HD / 4;               // float4 columns
+    constexpr int VG = ATTN_THREADS / VC;    // position groups
+    const int c4 = tid % VC, g = tid / VC;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int t0 = g; t0 < pos; t0 += VG * ATT_VU) {
+        float4 vv[ATT_VU];
 #pragma unroll
-        for (int u = 0; u < ATT_U; u++) {
-            const int t = min(t0 + u * NG, pos - 1);
-            vv[u] = vcache[(size_t)t * kv_dim + kvh * HD + dd];
+        for (int u = 0; u < ATT_VU; u++) {
+            const int t = min(t0 + u * VG, pos - 1);
+            vv[u] = reinterpret_cast<const float4 *>(vcache + (size_t)t * kv_dim + kvh * HD)[c4];
         }
 #pragma unroll
-        for (int u = 0; u < ATT_U; u++) {
-            const int t = t0 + u * NG;
-            if (t < pos) acc += (sc[t] / sum) * vv[u];
+        for (int u = 0; u < ATT_VU; u++) {
+            const int t = t0 + u * VG;
+            if (t < pos) {
+                const float p = sc[t] / sum;
+                acc.x += p * vv[u].x;
+                acc.y += p * vv[u].y;
+                acc.z += p * vv[u].z;
+                acc.w += p * vv[u].w;
+            }
         }
     }
-    part[g][dd] = acc;
+    reinterpret_cast<float4 *>(&part[g][0])[c4] = acc;
     __syncthreads();
     if (tid < HD) {
         float r = part[0][tid];
 #pragma unroll
-        for (int i = 1; i < NG; i++) r += part[i][tid];
+        for (int i = 1; i < VG; i++) r += part[i][tid];
         r += (sc[pos] / sum) * vc[tid];
         out[(size_t)h * HD + tid] = r;
     }
@@ -235,11 +264,18 @@ __global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ v, in
     __shared__ int bi_s[16];
     float bv = -INFINITY;
     int bi = n;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float x = v[i];
-        if (x == x && (x > bv || (x == bv && i < bi))) {
-            bv = x;
-            bi = i;
+    for (int i0 = threadIdx.x; i0 < n; i0 += 16 * blockDim.x) {
+        float xs[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) xs[k] = v[min(i0 + k * (int)blockDim.x, n - 1)];
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int i = i0 + k * blockDim.x;
+            const float x = xs[k];
+            if (i < n && x == x && (x > bv || (x == bv && i < bi))) {
+                bv = x;
+                bi = i;
+            }
         }
     }
     for (int o = 32; o > 0; o >>= 1) {
@@ -364,7 +400,7 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
         m->n_heads % m->n_kv || m->vocab < 1 || m->max_seq < 1 || m->ff < 1)
         return fail(LLG_E_HPARAM, "invalid dimensions");
     if (m->head_dim != 64 && m->head_dim != 128) return fail(LLG_E_HPARAM, "head_dim must be 64 or 128");
-    if (m->hidden > 64 * 1024) return fail(LLG_E_HPARAM, "hidden too large");
+    if (m->hidden > NORM_THREADS * NORM_PER) return fail(LLG_E_HPARAM, "hidden above 16384");
     if ((size_t)m->max_seq * 4 > 64 * 1024) return fail(LLG_E_HPARAM, "max_seq above 16384");
     const int qkv_rows = (m->n_heads + 2 * m->n_kv) * m->head_dim;
     m->embed = llg_get(d, embed, LLG_KIND_MATRIX);
