@@ -570,6 +570,87 @@ __device__ __forceinline__ void llg_stage_x_sum(float *xs, const float *__restri
     }
 }
 
+// Sum over the workgroup (every thread gets it); red: LDS, one float per
+// wavefront.  Contains two barriers.
+__device__ __forceinline__ float llg_block_sum(float v, float *red) {
+    v = llg_wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();  // red may still be read from a previous call
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = 0; i < nw; i++) s += red[i];
+    return s;
+}
+
+// Residual add + LayerNorm as the prologue of a matvec over the normed row
+// (tensor/ops.go:138-165, residual order of ffn_flash.go:161-166):
+// v = (x_in + a1) + a2 (a1, a2 may be null), normed = (v - mean) / std * w + b
+// with std = sqrt(var + eps) in double.  The normed row is staged in LDS with
+// XS floats per 32-element block and the block sum at [32], like
+// llg_stage_x_sum; workgroup 0 also writes v to x_out and normed to
+// normed_out.  n is a multiple of 32.
+struct LlgLnArgs {
+    const float *x_in, *a1, *a2, *w, *b;
+    float *x_out, *normed_out;
+    float eps;
+    int n;
+};
+
+template <int XS>
+__device__ __forceinline__ void llg_stage_ln(float *xs, const LlgLnArgs &a, float *red) {
+    const int n4 = a.n >> 2;
+    const float4 *x4 = reinterpret_cast<const float4 *>(a.x_in);
+    const float4 *p4 = reinterpret_cast<const float4 *>(a.a1);
+    const float4 *q4 = reinterpret_cast<const float4 *>(a.a2);
+    const bool w0 = blockIdx.x == 0;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+        float4 v = x4[i];
+        if (a.a1) {
+            const float4 p = p4[i];
+            v.x = v.x + p.x; v.y = v.y + p.y; v.z = v.z + p.z; v.w = v.w + p.w;
+        }
+        if (a.a2) {
+            const float4 q = q4[i];
+            v.x = v.x + q.x; v.y = v.y + q.y; v.z = v.z + q.z; v.w = v.w + q.w;
+        }
+        reinterpret_cast<float4 *>(xs + (i >> 3) * XS)[i & 7] = v;
+        if (w0 && a.x_out) reinterpret_cast<float4 *>(a.x_out)[i] = v;
+        s += (v.x + v.y) + (v.z + v.w);
+    }
+    const float mean = llg_block_sum(s, red) / (float)a.n;
+    float q = 0.0f;
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+        const float4 v = reinterpret_cast<const float4 *>(xs + (i >> 3) * XS)[i & 7];
+        const float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
+        q += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+    }
+    const float var = llg_block_sum(q, red) / (float)a.n;
+    const float sd = (float)sqrt((double)var + (double)a.eps);
+    const float4 *w4 = reinterpret_cast<const float4 *>(a.w);
+    const float4 *b4 = reinterpret_cast<const float4 *>(a.b);
+    const int lane = threadIdx.x & 63;
+    for (int base = threadIdx.x - lane; base < n4; base += blockDim.x) {
+        const int i = base + lane;
+        const int ic = min(i, n4 - 1);
+        float4 v = reinterpret_cast<const float4 *>(xs + (ic >> 3) * XS)[ic & 7];
+        const float4 wv = w4[ic], bv = b4[ic];
+        v.x = (v.x - mean) / sd * wv.x + bv.x;
+        v.y = (v.y - mean) / sd * wv.y + bv.y;
+        v.z = (v.z - mean) / sd * wv.z + bv.z;
+        v.w = (v.w - mean) / sd * wv.w + bv.w;
+        float bs = (v.x + v.y) + (v.z + v.w);
+        bs = llg_quad_sum(bs);
+        bs += llg_dpp<0x141>(bs);  // the 8 float4 of one 32-element block
+        if (i < n4) {
+            reinterpret_cast<float4 *>(xs + (i >> 3) * XS)[i & 7] = v;
+            if ((i & 7) == 0) xs[(i >> 3) * XS + 32] = bs;
+            if (w0 && a.normed_out) reinterpret_cast<float4 *>(a.normed_out)[i] = v;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Host-side runtime objects (defined in llg_runtime.hip)
 // ---------------------------------------------------------------------------

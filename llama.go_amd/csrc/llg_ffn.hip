@@ -22,14 +22,15 @@
 #define MV_XS 36          // staged floats per 32-float block
 #define MV_BATCH 3        // blocks per lane whose loads are issued together
 
-template <int T>
+template <int T, bool LN>
 __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w, long long stride,
                                                   RowFmt f, int rows, int tile_rows,
                                                   int chunk_blocks,
                                                   const float *__restrict__ x, int act,
                                                   float *__restrict__ y, float *__restrict__ zero,
-                                                  int zero_n) {
+                                                  int zero_n, LlgLnArgs ln) {
     extern __shared__ float xs[];
+    __shared__ float red[4];
     const int n_chunks = (f.nb + chunk_blocks - 1) / chunk_blocks;
     const int tile = blockIdx.x / n_chunks;
     const int ch = blockIdx.x % n_chunks;
@@ -54,7 +55,10 @@ __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w,
             llg_block_load<T>(r[i][q], w + (long long)min((r0_) + q, r_end - 1) * stride, f,   \
                               cb0 + min((bb_) + lane + 64 * i, cnb - 1))
     MV_ISSUE(min(r_first, r_end - 1), 0);
-    llg_stage_x_sum<MV_XS>(xs, x + (size_t)cb0 * 32, cnb);
+    if (LN)  // x is the LayerNorm of the residual sum (one chunk: cb0 = 0)
+        llg_stage_ln<MV_XS>(xs, ln, red);
+    else
+        llg_stage_x_sum<MV_XS>(xs, x + (size_t)cb0 * 32, cnb);
     __syncthreads();
     for (int r0 = r_first; r0 < r_end; r0 += 4 * MV_ROWS) {
         float s[MV_ROWS];
@@ -95,11 +99,12 @@ static int mv_chunk_blocks(const RowFmt &f, int act) {
 }
 
 // zero/zero_n: a buffer the launch also clears (the next kernel's atomic target).
+// ln (optional): the staged x is the LayerNorm of a residual sum (llg_stage_ln).
 static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y,
-                         float *zero, int zero_n) {
+                         float *zero, int zero_n, const LlgLnArgs *ln = nullptr) {
     hipStream_t st = llg_dev_stream(d);
     const RowFmt &f = w->fmt;
-    const int cb = mv_chunk_blocks(f, act);
+    const int cb = ln ? f.nb : mv_chunk_blocks(f, act);
     const int n_chunks = (f.nb + cb - 1) / cb;
     const size_t lds = (size_t)cb * MV_XS * 4;
     if (lds > 160 * 1024)
@@ -109,32 +114,44 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
     }
     const int tile_rows = w->rows < MV_SMALL_ROWS ? MV_TILE_SMALL : MV_TILE;
     const int grid = (w->rows + tile_rows - 1) / tile_rows * n_chunks;
+    const LlgLnArgs none{};
+    const LlgLnArgs &la = ln ? *ln : none;
+#define MV_LAUNCH(TY)                                                                              \
+    do {                                                                                           \
+        if (ln)                                                                                    \
+            hipLaunchKernelGGL((k_matvec_q<TY, true>), dim3(grid), dim3(256), lds, st, w->d,       \
+                               w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, zero, zero_n,  \
+                               la);                                                                \
+        else                                                                                       \
+            hipLaunchKernelGGL((k_matvec_q<TY, false>), dim3(grid), dim3(256), lds, st, w->d,      \
+                               w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, zero, zero_n,  \
+                               la);                                                                \
+    } while (0)
     switch (f.type) {
     case LLG_TYPE_Q4_0:
-        hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_Q4_0>, dim3(grid), dim3(256), lds, st, w->d,
-                           w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, zero,
-                           zero_n);
+        MV_LAUNCH(LLG_TYPE_Q4_0);
         break;
     case LLG_TYPE_Q8_0:
-        hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_Q8_0>, dim3(grid), dim3(256), lds, st, w->d,
-                           w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, zero,
-                           zero_n);
+        MV_LAUNCH(LLG_TYPE_Q8_0);
         break;
     case LLG_TYPE_F16:
-        hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_F16>, dim3(grid), dim3(256), lds, st, w->d,
-                           w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, zero,
-                           zero_n);
+        MV_LAUNCH(LLG_TYPE_F16);
         break;
     case LLG_TYPE_F32:
-        hipLaunchKernelGGL(k_matvec_q<LLG_TYPE_F32>, dim3(grid), dim3(256), lds, st, w->d,
-                           w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, zero,
-                           zero_n);
+        MV_LAUNCH(LLG_TYPE_F32);
         break;
     default:
         return llg_set_error(d, LLG_E_TYPE, "matvec: unsupported type %d", f.type);
     }
+#undef MV_LAUNCH
     LLG_LAUNCH_CHECK(d, "matvec_q");
     return 0;
+}
+
+int llg_matvec_ln_enqueue(LlgDevice *d, const LlgObject *w, const LlgLnArgs &ln, float *d_y) {
+    if (ln.n != w->fmt.cols)
+        return llg_set_error(d, LLG_E_ARG, "matvec: LayerNorm length %d != %d", ln.n, w->fmt.cols);
+    return matvec_launch(d, w, nullptr, -1, d_y, nullptr, 0, &ln);
 }
 
 int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y) {

@@ -34,6 +34,9 @@ int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, con
 
 // Dense quantized matvec y[rows] = act(W . x) (llg_ffn.hip); act < 0 = none.
 int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y);
+// y = W . LayerNorm((x_in + a1) + a2), the residual sum and the normed row
+// also written to ln.x_out / ln.normed_out (llg_stage_ln).
+int llg_matvec_ln_enqueue(LlgDevice *d, const LlgObject *w, const LlgLnArgs &ln, float *d_y);
 
 // Predictor-fused sparse FFN (ffnFlash path 2) (llg_sparse.hip).
 size_t llg_fused_ws_bytes(int rank, int ff);

@@ -5,10 +5,13 @@
 // One token through the model, all on the device stream:
 //   k_embed           x = dequant(embedding row of the token)    (forward.go:449-454)
 //   per layer l:
-//     k_resid_norm    x += attn_out[l-1]; x += ffn_out[l-1] (two separate fp32
-//                     adds, forward.go:170-176); normed = LayerNorm(x) with the
-//                     layer's weight and bias (tensor/ops.go:138-165)
-//     k_matvec_q      qkv = [Wq; Wk; Wv] . normed               (forward.go:211-222)
+//     k_matvec_q      qkv = [Wq; Wk; Wv] . normed (forward.go:211-222), where
+//                     every workgroup first forms x += attn_out[l-1]; x +=
+//                     ffn_out[l-1] (two separate fp32 adds, ffn_flash.go:161-166)
+//                     and normed = LayerNorm(x) (tensor/ops.go:138-165) itself
+//                     (llg_stage_ln); workgroup 0 stores both.  x alternates
+//                     between two buffers, so no workgroup reads what another
+//                     writes.
 //     k_attn          NeoX RoPE of q and k (forward.go:483-497), K/V appended at
 //                     row pos of the layer's cache (kvcache.go:42-52), softmax
 //                     attention of every query head over rows 0..pos of its KV
@@ -41,7 +44,7 @@ struct LlgModel {
     LlgObject *embed, *out_w, *out_b, *lm_head;
     std::vector<LlgModelLayer> layers;
     // device buffers, carved out of the object's allocation
-    float *x, *normed, *qkv, *attn, *attn_out, *ffn_out, *logits, *kv, *pred_logits;
+    float *x, *x2, *normed, *qkv, *attn, *attn_out, *ffn_out, *logits, *kv, *pred_logits;
     int32_t *token, *n_active, *act_scratch;
     uint8_t *ws;
 };
@@ -64,30 +67,21 @@ __global__ void k_embed(const uint8_t *__restrict__ emb, long long stride, RowFm
         x[c] = llg_dequant_elem(row, f, c);
 }
 
-__device__ __forceinline__ float block_sum(float v, float *red) {
-    v = llg_wave_sum(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();  // red may still be read from a previous call
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float s = 0.0f;
-    for (int i = 0; i < nw; i++) s += red[i];
-    return s;
-}
 
 // x = (x + a1) + a2 (either may be null); out = LayerNorm(x) * w + b.  Each
-// thread keeps its NORM_PER elements in registers (hidden <= NORM_THREADS *
-// NORM_PER); all loads of a thread are issued together.
-#define NORM_PER 16
+// thread keeps NP elements in registers (hidden <= NORM_THREADS * NP); all
+// loads of a thread are issued together.
+#define NORM_PER 16  // largest NP instantiated
+template <int NP>
 __global__ __launch_bounds__(NORM_THREADS) void k_resid_norm(
     float *__restrict__ x, const float *__restrict__ a1, const float *__restrict__ a2,
     const float *__restrict__ w, const float *__restrict__ b, int n, float eps,
     float *__restrict__ out) {
     __shared__ float red[NORM_THREADS / 64];
-    float v[NORM_PER], p1[NORM_PER], p2[NORM_PER];
+    float v[NP], p1[NP], p2[NP];
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < NORM_PER; k++) {
+    for (int k = 0; k < NP; k++) {
         const int i = min(tid + k * NORM_THREADS, n - 1);
         v[k] = x[i];
         p1[k] = a1 ? a1[i] : 0.0f;
@@ -95,7 +89,7 @@ __global__ __launch_bounds__(NORM_THREADS) void k_resid_norm(
     }
     float s = 0.0f;
 #pragma unroll
-    for (int k = 0; k < NORM_PER; k++) {
+    for (int k = 0; k < NP; k++) {
         const int i = tid + k * NORM_THREADS;
         if (a1) v[k] = v[k] + p1[k];
         if (a2) v[k] = v[k] + p2[k];
@@ -104,17 +98,17 @@ __global__ __launch_bounds__(NORM_THREADS) void k_resid_norm(
             s += v[k];
         }
     }
-    const float mean = block_sum(s, red) / (float)n;
+    const float mean = llg_block_sum(s, red) / (float)n;
     float q = 0.0f;
 #pragma unroll
-    for (int k = 0; k < NORM_PER; k++) {
+    for (int k = 0; k < NP; k++) {
         const float dv = v[k] - mean;
         if (tid + k * NORM_THREADS < n) q += dv * dv;
     }
-    const float var = block_sum(q, red) / (float)n;
+    const float var = llg_block_sum(q, red) / (float)n;
     const float std_ = (float)sqrt((double)var + (double)eps);  // ops.go:159
 #pragma unroll
-    for (int k = 0; k < NORM_PER; k++) {
+    for (int k = 0; k < NP; k++) {
         const int i = tid + k * NORM_THREADS;
         if (i < n) out[i] = (v[k] - mean) / std_ * w[i] + b[i];
     }
@@ -218,7 +212,7 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
         sc[t] = e;
         s += e;
     }
-    const float sum = block_sum(s, red);  // its barriers also publish sc
+    const float sum = llg_block_sum(s, red);  // its barriers also publish sc
     // out[d] = sum_t p_t * v_t[d]: thread (c, g) holds float4 column c of the
     // head and takes t = g, g + VG, ... < pos, ATT_VU rows per step; the groups
     // meet in LDS and row pos is added last
@@ -328,12 +322,17 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
     const size_t attn_lds = (size_t)(pos + 1) * 4;
     for (int l = 0; l < m.n_layers; l++) {
         const LlgModelLayer &L = m.layers[l];
-        hipLaunchKernelGGL(k_resid_norm, dim3(1), dim3(NORM_THREADS), 0, st, m.x,
-                           l ? m.attn_out : (const float *)nullptr,
-                           l ? m.ffn_out : (const float *)nullptr,
-                           reinterpret_cast<const float *>(L.norm_w->d),
-                           reinterpret_cast<const float *>(L.norm_b->d), m.hidden, m.eps, m.normed);
-        int rc = llg_matvec_enqueue(d, L.wqkv, m.normed, -1, m.qkv);
+        LlgLnArgs ln;
+        ln.x_in = (l & 1) ? m.x2 : m.x;
+        ln.x_out = (l & 1) ? m.x : m.x2;
+        ln.a1 = l ? m.attn_out : nullptr;
+        ln.a2 = l ? m.ffn_out : nullptr;
+        ln.w = reinterpret_cast<const float *>(L.norm_w->d);
+        ln.b = reinterpret_cast<const float *>(L.norm_b->d);
+        ln.normed_out = m.normed;
+        ln.eps = m.eps;
+        ln.n = m.hidden;
+        int rc = llg_matvec_ln_enqueue(d, L.wqkv, ln, m.qkv);
         if (rc) return rc;
         float *kvl = m.kv + (size_t)l * 2 * m.max_seq * m.n_kv * m.head_dim;
         if (m.head_dim == 64)
@@ -354,9 +353,19 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
                                m.ws);
         if (rc) return rc;
     }
-    hipLaunchKernelGGL(k_resid_norm, dim3(1), dim3(NORM_THREADS), 0, st, m.x, m.attn_out,
-                       m.ffn_out, reinterpret_cast<const float *>(m.out_w->d),
-                       reinterpret_cast<const float *>(m.out_b->d), m.hidden, m.eps, m.normed);
+    float *xf = (m.n_layers & 1) ? m.x2 : m.x;  // the residual after the last layer's input
+    const float *fw = reinterpret_cast<const float *>(m.out_w->d);
+    const float *fb = reinterpret_cast<const float *>(m.out_b->d);
+    const int np = (m.hidden + NORM_THREADS - 1) / NORM_THREADS;
+#define RN(NP)                                                                                    \
+    hipLaunchKernelGGL((k_resid_norm<NP>), dim3(1), dim3(NORM_THREADS), 0, st, xf, m.attn_out,    \
+                       m.ffn_out, fw, fb, m.hidden, m.eps, m.normed)
+    if (np <= 2) RN(2);
+    else if (np <= 4) RN(4);
+    else if (np <= 6) RN(6);
+    else if (np <= 8) RN(8);
+    else RN(16);
+#undef RN
     int rc = llg_matvec_enqueue(d, m.lm_head, m.normed, -1, m.logits);
     if (rc) return rc;
     hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, m.logits, m.vocab, token_out);
@@ -458,7 +467,7 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     m->normed = reinterpret_cast<float *>(p); p += v_h;
     m->attn_out = reinterpret_cast<float *>(p); p += v_h;
     m->ffn_out = reinterpret_cast<float *>(p); p += v_h;
-    p += v_h;  // spare
+    m->x2 = reinterpret_cast<float *>(p); p += v_h;
     m->qkv = reinterpret_cast<float *>(p); p += v_qkv;
     m->attn = reinterpret_cast<float *>(p); p += v_att;
     m->logits = reinterpret_cast<float *>(p); p += v_log;
