@@ -543,30 +543,54 @@ __device__ __forceinline__ void llg_raw_axpy<LLG_TYPE_F32>(const BlockRaw<LLG_TY
 // before any store; each block's sum is reduced over its 8 lanes with DPP
 // (quad steps, then row_half_mirror = 0x141 pairs the two quads of 8 lanes).
 // The loop bound is uniform per wavefront, so every DPP sees full lanes.
+//
+// issue(): called once, right after the first group of x loads is issued and
+// before any of them is used.  Vector loads complete in issue order, so loads
+// a caller issues there (e.g. its weight bytes) stay in flight while x is
+// staged, instead of x waiting behind them.
+struct LlgNoIssue {
+    __device__ void operator()() const {}
+};
+
 template <int XS>
-__device__ __forceinline__ void llg_stage_x_sum(float *xs, const float *__restrict__ x, int nb) {
+__device__ __forceinline__ void llg_x_sum_store(float *xs, const float4 &v, int i, int n4) {
+    float sum = (v.x + v.y) + (v.z + v.w);
+    sum = llg_quad_sum(sum);
+    sum += llg_dpp<0x141>(sum);
+    if (i < n4) {
+        reinterpret_cast<float4 *>(xs + (i >> 3) * XS)[i & 7] = v;
+        if ((i & 7) == 0) xs[(i >> 3) * XS + 32] = sum;
+    }
+}
+
+template <int XS, class Issue = LlgNoIssue>
+__device__ __forceinline__ void llg_stage_x_sum(float *xs, const float *__restrict__ x, int nb,
+                                                Issue &&issue = Issue()) {
     static_assert(XS >= 33, "room for the block sum");
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
     const int n4 = nb * 8;
     const int lane = threadIdx.x & 63;
-    for (int base = threadIdx.x - lane; base < n4; base += 8 * blockDim.x) {
+    const int base0 = threadIdx.x - lane;
+    if (n4 <= 8 * (int)blockDim.x) {
+        // one pass, straight-line: the wait before the stores covers the x
+        // loads only (clamped addresses, so no load sits under a branch)
         float4 v[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int i = base + k * blockDim.x + lane;
-            v[k] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        for (int k = 0; k < 8; k++) v[k] = x4[min(base0 + k * (int)blockDim.x + lane, n4 - 1)];
+        __builtin_amdgcn_sched_barrier(0);  // keep the caller's loads behind these
+        issue();
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int i = base + k * blockDim.x + lane;
-            float sum = (v[k].x + v[k].y) + (v[k].z + v[k].w);
-            sum = llg_quad_sum(sum);
-            sum += llg_dpp<0x141>(sum);
-            if (i < n4) {
-                reinterpret_cast<float4 *>(xs + (i >> 3) * XS)[i & 7] = v[k];
-                if ((i & 7) == 0) xs[(i >> 3) * XS + 32] = sum;
-            }
-        }
+        for (int k = 0; k < 8; k++)
+            llg_x_sum_store<XS>(xs, v[k], base0 + k * blockDim.x + lane, n4);
+        return;
+    }
+    issue();
+    for (int base = base0; base < n4; base += 8 * blockDim.x) {
+        float4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = x4[min(base + k * (int)blockDim.x + lane, n4 - 1)];
+#pragma unroll
+        for (int k = 0; k < 8; k++) llg_x_sum_store<XS>(xs, v[k], base + k * blockDim.x + lane, n4);
     }
 }
 
@@ -597,56 +621,74 @@ struct LlgLnArgs {
     int n;
 };
 
-template <int XS>
-__device__ __forceinline__ void llg_stage_ln(float *xs, const LlgLnArgs &a, float *red) {
+// NP = float4 groups per thread (n <= 4 * NP * blockDim.x): every load of the
+// residual terms and of w and b is issued before the first use, so the
+// prologue costs one memory round trip plus the two block reductions.
+// issue() as in llg_stage_x_sum.
+template <int XS, int NP, class Issue = LlgNoIssue>
+__device__ __forceinline__ void llg_stage_ln(float *xs, const LlgLnArgs &a, float *red,
+                                             Issue &&issue = Issue()) {
     const int n4 = a.n >> 2;
+    const int tid = threadIdx.x, bd = blockDim.x;
     const float4 *x4 = reinterpret_cast<const float4 *>(a.x_in);
     const float4 *p4 = reinterpret_cast<const float4 *>(a.a1);
     const float4 *q4 = reinterpret_cast<const float4 *>(a.a2);
-    const bool w0 = blockIdx.x == 0;
-    float s = 0.0f;
-    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
-        float4 v = x4[i];
-        if (a.a1) {
-            const float4 p = p4[i];
-            v.x = v.x + p.x; v.y = v.y + p.y; v.z = v.z + p.z; v.w = v.w + p.w;
-        }
-        if (a.a2) {
-            const float4 q = q4[i];
-            v.x = v.x + q.x; v.y = v.y + q.y; v.z = v.z + q.z; v.w = v.w + q.w;
-        }
-        reinterpret_cast<float4 *>(xs + (i >> 3) * XS)[i & 7] = v;
-        if (w0 && a.x_out) reinterpret_cast<float4 *>(a.x_out)[i] = v;
-        s += (v.x + v.y) + (v.z + v.w);
-    }
-    const float mean = llg_block_sum(s, red) / (float)a.n;
-    float q = 0.0f;
-    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
-        const float4 v = reinterpret_cast<const float4 *>(xs + (i >> 3) * XS)[i & 7];
-        const float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
-        q += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
-    }
-    const float var = llg_block_sum(q, red) / (float)a.n;
-    const float sd = (float)sqrt((double)var + (double)a.eps);
     const float4 *w4 = reinterpret_cast<const float4 *>(a.w);
     const float4 *b4 = reinterpret_cast<const float4 *>(a.b);
-    const int lane = threadIdx.x & 63;
-    for (int base = threadIdx.x - lane; base < n4; base += blockDim.x) {
-        const int i = base + lane;
-        const int ic = min(i, n4 - 1);
-        float4 v = reinterpret_cast<const float4 *>(xs + (ic >> 3) * XS)[ic & 7];
-        const float4 wv = w4[ic], bv = b4[ic];
-        v.x = (v.x - mean) / sd * wv.x + bv.x;
-        v.y = (v.y - mean) / sd * wv.y + bv.y;
-        v.z = (v.z - mean) / sd * wv.z + bv.z;
-        v.w = (v.w - mean) / sd * wv.w + bv.w;
-        float bs = (v.x + v.y) + (v.z + v.w);
+    const bool w0 = blockIdx.x == 0;
+    float4 v[NP], p[NP], q[NP], wv[NP], bv[NP];
+#pragma unroll
+    for (int k = 0; k < NP; k++) {
+        const int i = min(tid + k * bd, n4 - 1);
+        v[k] = x4[i];
+        if (p4) p[k] = p4[i];
+        if (q4) q[k] = q4[i];
+        wv[k] = w4[i];
+        bv[k] = b4[i];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the caller's loads behind these
+    issue();
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NP; k++) {
+        const int i = tid + k * bd;
+        if (p4) {
+            v[k].x = v[k].x + p[k].x; v[k].y = v[k].y + p[k].y;
+            v[k].z = v[k].z + p[k].z; v[k].w = v[k].w + p[k].w;
+        }
+        if (q4) {
+            v[k].x = v[k].x + q[k].x; v[k].y = v[k].y + q[k].y;
+            v[k].z = v[k].z + q[k].z; v[k].w = v[k].w + q[k].w;
+        }
+        if (i < n4) {
+            s += (v[k].x + v[k].y) + (v[k].z + v[k].w);
+            if (w0 && a.x_out) reinterpret_cast<float4 *>(a.x_out)[i] = v[k];
+        }
+    }
+    const float mean = llg_block_sum(s, red) / (float)a.n;
+    float qs = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NP; k++) {
+        const float d0 = v[k].x - mean, d1 = v[k].y - mean, d2 = v[k].z - mean, d3 = v[k].w - mean;
+        if (tid + k * bd < n4) qs += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+    }
+    const float var = llg_block_sum(qs, red) / (float)a.n;
+    const float sd = (float)sqrt((double)var + (double)a.eps);
+#pragma unroll
+    for (int k = 0; k < NP; k++) {
+        const int i = tid + k * bd;
+        float4 o;
+        o.x = (v[k].x - mean) / sd * wv[k].x + bv[k].x;
+        o.y = (v[k].y - mean) / sd * wv[k].y + bv[k].y;
+        o.z = (v[k].z - mean) / sd * wv[k].z + bv[k].z;
+        o.w = (v[k].w - mean) / sd * wv[k].w + bv[k].w;
+        float bs = (o.x + o.y) + (o.z + o.w);
         bs = llg_quad_sum(bs);
         bs += llg_dpp<0x141>(bs);  // the 8 float4 of one 32-element block
         if (i < n4) {
-            reinterpret_cast<float4 *>(xs + (i >> 3) * XS)[i & 7] = v;
+            reinterpret_cast<float4 *>(xs + (i >> 3) * XS)[i & 7] = o;
             if ((i & 7) == 0) xs[(i >> 3) * XS + 32] = bs;
-            if (w0 && a.normed_out) reinterpret_cast<float4 *>(a.normed_out)[i] = v;
+            if (w0 && a.normed_out) reinterpret_cast<float4 *>(a.normed_out)[i] = o;
         }
     }
 }

@@ -22,7 +22,9 @@
 #define MV_XS 36          // staged floats per 32-float block
 #define MV_BATCH 3        // blocks per lane whose loads are issued together
 
-template <int T, bool LN>
+// LNP > 0: x is the LayerNorm of a residual sum, staged with LNP float4 groups
+// per thread (llg_stage_ln); LNP = 0: x is read from memory.
+template <int T, int LNP>
 __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w, long long stride,
                                                   RowFmt f, int rows, int tile_rows,
                                                   int chunk_blocks,
@@ -47,18 +49,19 @@ __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w,
     // request the bytes of all MV_BATCH x MV_ROWS blocks, then use them; loads
     // are never under a per-lane condition (that serialises them): lanes past
     // the chunk reload its last block and drop it, a row past the end reloads
-    // the last row.  The first batch is requested before x is staged.
+    // the last row.  The first batch is requested right after the loads of x
+    // (or of the LayerNorm inputs), so x is staged while it is in flight.
     BlockRaw<T> r[MV_BATCH][MV_ROWS];
 #define MV_ISSUE(r0_, bb_)                                                                      \
     _Pragma("unroll") for (int i = 0; i < MV_BATCH; i++)                                       \
         _Pragma("unroll") for (int q = 0; q < MV_ROWS; q++)                                    \
             llg_block_load<T>(r[i][q], w + (long long)min((r0_) + q, r_end - 1) * stride, f,   \
                               cb0 + min((bb_) + lane + 64 * i, cnb - 1))
-    MV_ISSUE(min(r_first, r_end - 1), 0);
-    if (LN)  // x is the LayerNorm of the residual sum (one chunk: cb0 = 0)
-        llg_stage_ln<MV_XS>(xs, ln, red);
+    auto issue_first = [&]() { MV_ISSUE(min(r_first, r_end - 1), 0); };
+    if constexpr (LNP > 0)  // x is the LayerNorm of the residual sum (one chunk: cb0 = 0)
+        llg_stage_ln<MV_XS, LNP>(xs, ln, red, issue_first);
     else
-        llg_stage_x_sum<MV_XS>(xs, x + (size_t)cb0 * 32, cnb);
+        llg_stage_x_sum<MV_XS>(xs, x + (size_t)cb0 * 32, cnb, issue_first);
     __syncthreads();
     for (int r0 = r_first; r0 < r_end; r0 += 4 * MV_ROWS) {
         float s[MV_ROWS];
@@ -116,16 +119,18 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
     const int grid = (w->rows + tile_rows - 1) / tile_rows * n_chunks;
     const LlgLnArgs none{};
     const LlgLnArgs &la = ln ? *ln : none;
+    const int lnp = ln ? (ln->n / 4 + 255) / 256 : 0;
+#define MV_GO(TY, NP)                                                                              \
+    hipLaunchKernelGGL((k_matvec_q<TY, NP>), dim3(grid), dim3(256), lds, st, w->d, w->stride, f,   \
+                       w->rows, tile_rows, cb, d_x, act, d_y, zero, zero_n, la)
 #define MV_LAUNCH(TY)                                                                              \
     do {                                                                                           \
-        if (ln)                                                                                    \
-            hipLaunchKernelGGL((k_matvec_q<TY, true>), dim3(grid), dim3(256), lds, st, w->d,       \
-                               w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, zero, zero_n,  \
-                               la);                                                                \
-        else                                                                                       \
-            hipLaunchKernelGGL((k_matvec_q<TY, false>), dim3(grid), dim3(256), lds, st, w->d,      \
-                               w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, zero, zero_n,  \
-                               la);                                                                \
+        if (!ln) MV_GO(TY, 0);                                                                     \
+        else if (lnp <= 2) MV_GO(TY, 2);                                                           \
+        else if (lnp <= 4) MV_GO(TY, 4);                                                           \
+        else if (lnp <= 5) MV_GO(TY, 5);                                                           \
+        else if (lnp <= 8) MV_GO(TY, 8);                                                           \
+        else MV_GO(TY, 16);                                                                        \
     } while (0)
     switch (f.type) {
     case LLG_TYPE_Q4_0:
@@ -144,6 +149,7 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
         return llg_set_error(d, LLG_E_TYPE, "matvec: unsupported type %d", f.type);
     }
 #undef MV_LAUNCH
+#undef MV_GO
     LLG_LAUNCH_CHECK(d, "matvec_q");
     return 0;
 }
@@ -151,6 +157,8 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
 int llg_matvec_ln_enqueue(LlgDevice *d, const LlgObject *w, const LlgLnArgs &ln, float *d_y) {
     if (ln.n != w->fmt.cols)
         return llg_set_error(d, LLG_E_ARG, "matvec: LayerNorm length %d != %d", ln.n, w->fmt.cols);
+    if (ln.n > 256 * 16 * 4)
+        return llg_set_error(d, LLG_E_ARG, "matvec: LayerNorm length %d above 16384", ln.n);
     return matvec_launch(d, w, nullptr, -1, d_y, nullptr, 0, &ln);
 }
 

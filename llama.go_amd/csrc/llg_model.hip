@@ -45,6 +45,7 @@ struct LlgModel {
     std::vector<LlgModelLayer> layers;
     // device buffers, carved out of the object's allocation
     float *x, *x2, *normed, *qkv, *attn, *attn_out, *ffn_out, *logits, *kv, *pred_logits;
+    float2 *rope;  // [max_seq x head_dim/2] (cos, sin)
     int32_t *token, *n_active, *act_scratch;
     uint8_t *ws;
 };
@@ -127,6 +128,17 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// RoPE angles of every position (forward.go:487-489): freq = pos / base^(2i/hd)
+// in double, cos and sin rounded to float.  Built once per model, so the
+// attention kernel reads two floats where it would evaluate pow/cos/sin.
+__global__ void k_rope_table(float2 *__restrict__ tab, int max_seq, int half, float base) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= max_seq * half) return;
+    const int pos = j / half, i = j % half;
+    const double fr = (double)pos / pow((double)base, (double)(2 * i) / (double)(2 * half));
+    tab[j] = make_float2((float)cos(fr), (float)sin(fr));
+}
+
 // One workgroup per query head; HD = head_dim (64 or 128).  HD/4 lanes hold
 // one key row (a float4 each), so a wavefront scores 256/HD positions per
 // load; each lane requests ATT_U rows before reducing any.  Rows 0..pos-1 come
@@ -138,7 +150,8 @@ __device__ __forceinline__ float wave_max(float v) {
 #define ATT_VU 8    // value rows per thread requested together
 template <int HD>
 __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__ qkv, int n_heads,
-                                                       int n_kv, int pos, float rope_base,
+                                                       int n_kv, int pos,
+                                                       const float2 *__restrict__ rope,
                                                        int max_seq, float *__restrict__ kv,
                                                        float *__restrict__ out) {
     constexpr int LP = HD / 4;       // lanes per position
@@ -156,8 +169,8 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
     const float *vc = qkv + (size_t)n_heads * HD + kv_dim + (size_t)kvh * HD;
     if (tid < HD / 2) {  // RoPE, pairs (i, i + HD/2) (forward.go:483-497)
         const int i = tid;
-        const double fr = (double)pos / pow((double)rope_base, (double)(2 * i) / (double)HD);
-        const float c = (float)cos(fr), s = (float)sin(fr);
+        const float2 cs = rope[(size_t)pos * (HD / 2) + i];
+        const float c = cs.x, s = cs.y;
         const float q0 = q[i], q1 = q[i + HD / 2], k0 = kc[i], k1 = kc[i + HD / 2];
         qh[i] = q0 * c - q1 * s;
         qh[i + HD / 2] = q0 * s + q1 * c;
@@ -174,7 +187,7 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
     const float scale = (float)(1.0 / sqrt((double)HD));  // forward.go:255
     const int sub = lane % LP, slot = lane / LP;
     const float4 qv = reinterpret_cast<const float4 *>(qh)[sub];
-    for (int t0 = wave * PW * ATT_U; t0 < pos; t0 += 4 * PW * ATT_U) {
+    for (int t0 = wave * PW * ATT_U; t0 < pos; t0 += (ATTN_THREADS / 64) * PW * ATT_U) {
         float4 kk[ATT_U];
 #pragma unroll
         for (int u = 0; u < ATT_U; u++) {
@@ -337,10 +350,10 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
         float *kvl = m.kv + (size_t)l * 2 * m.max_seq * m.n_kv * m.head_dim;
         if (m.head_dim == 64)
             hipLaunchKernelGGL(k_attn<64>, dim3(m.n_heads), dim3(ATTN_THREADS), attn_lds, st, m.qkv,
-                               m.n_heads, m.n_kv, pos, m.rope_base, m.max_seq, kvl, m.attn);
+                               m.n_heads, m.n_kv, pos, m.rope, m.max_seq, kvl, m.attn);
         else
             hipLaunchKernelGGL(k_attn<128>, dim3(m.n_heads), dim3(ATTN_THREADS), attn_lds, st, m.qkv,
-                               m.n_heads, m.n_kv, pos, m.rope_base, m.max_seq, kvl, m.attn);
+                               m.n_heads, m.n_kv, pos, m.rope, m.max_seq, kvl, m.attn);
         LLG_LAUNCH_CHECK(d, "model attention");
         if ((rc = llg_matvec_enqueue(d, L.wo, m.attn, -1, m.attn_out))) return rc;
         if (pred_logits &&
@@ -458,8 +471,9 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     const size_t v_i = llg_align((long long)(m->n_layers + 4) * 4, 256);
     const size_t v_ff = llg_align((long long)(m->ff + 4) * 4, 256);
     const size_t v_pl = llg_align((long long)m->n_layers * m->ff * 4, 256);
+    const size_t v_rope = llg_align((long long)m->max_seq * m->head_dim / 2 * 8, 256);
     const size_t wsb = model_ws_bytes(*m);
-    const size_t total = 5 * v_h + v_qkv + v_att + v_log + v_kv + v_i + v_ff + v_pl + wsb;
+    const size_t total = 5 * v_h + v_qkv + v_att + v_log + v_kv + v_i + v_ff + v_pl + v_rope + wsb;
     uint8_t *buf = nullptr;
     if (hipMalloc(&buf, total) != hipSuccess) return fail(LLG_E_NOMEM, "buffer allocation failed");
     uint8_t *p = buf;
@@ -479,9 +493,15 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     p += v_ff;
     m->pred_logits = reinterpret_cast<float *>(p);
     p += v_pl;
+    m->rope = reinterpret_cast<float2 *>(p);
+    p += v_rope;
     m->ws = p;
     hipStream_t st = llg_dev_stream(d);
     LLG_HIP_TRY(d, hipMemsetAsync(buf, 0, total, st));
+    const int n_rope = m->max_seq * (m->head_dim / 2);
+    hipLaunchKernelGGL(k_rope_table, dim3((n_rope + 255) / 256), dim3(256), 0, st, m->rope,
+                       m->max_seq, m->head_dim / 2, m->rope_base);
+    LLG_HIP_TRY(d, hipGetLastError());
     LLG_HIP_TRY(d, hipStreamSynchronize(st));
     LlgObject *o = new LlgObject();
     o->kind = LLG_KIND_MODEL;
