@@ -15,9 +15,11 @@ their average event-timed duration on the library's stream) and a
 timed on a bounded sample on this host).
 
 Other workloads (--workload dense-q4_0 | dense-q8_0 | dense-f16 | window |
-moe-decode | moe-prefill | falcon-decode) measure the remaining hot-path
-configurations; falcon-decode is the full 32-layer model around the sparse FFN
-(--steps = generated tokens after the 512-token prompt).
+moe-decode | moe-prefill | falcon-decode | swiglu-q4_0 | swiglu-q8_0 |
+swiglu-f16) measure the remaining hot-path configurations; falcon-decode is
+the full 32-layer model around the sparse FFN (--steps = generated tokens
+after the 512-token prompt); swiglu-* is the SiLU architecture's dense FFN
+(ffnSwiGLU) at a LLaMA-7B layer's shape.
 """
 from __future__ import annotations
 
@@ -253,6 +255,58 @@ def bench_dense(args, torch, llg, dev, t):
             "config": {"workload": f"falcon7b-ffn-layer-{gg.TYPE_NAMES[t].lower()}-dense-decode",
                        "d_model": H, "d_ff": FF, "layer_copies_rotated": L},
             "roofline": {"bound": "hbm", "kernel": "k_matvec_q (up) + k_matvec_q (down)",
+                         "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                         "alg_bytes_per_launch": alg, "avg_launch_us": ms * 1e3}}
+
+
+SW_H, SW_FF = 4096, 11008  # LLaMA-7B layer (the SiLU architecture's dense FFN)
+
+
+def bench_swiglu(args, torch, llg, dev, t):
+    """One decode token through ffnSwiGLU (forward.go:368-389) at a LLaMA-7B
+    layer's shape: gate and up matvecs fused (silu(g) * u), then down."""
+    gg = llg.gguf
+    L = args.layers
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x11A3A006)
+    gate = gg.quantize(torch.randn((SW_FF, SW_H), generator=g, device="cuda") * 0.02, t)
+    up = gg.quantize(torch.randn((SW_FF, SW_H), generator=g, device="cuda") * 0.02, t)
+    down = gg.quantize(torch.randn((SW_H, SW_FF), generator=g, device="cuda") * 0.02, t)
+    torch.cuda.synchronize()
+    gates = [dev.upload_matrix(gate, t, SW_FF, SW_H) for _ in range(L)]
+    ups = [dev.upload_matrix(up, t, SW_FF, SW_H) for _ in range(L)]
+    downs = [dev.upload_matrix(down, t, SW_H, SW_FF) for _ in range(L)]
+    X = torch.randn((64, SW_H), generator=g, device="cuda")
+    out = torch.empty((64, SW_H), device="cuda")
+    torch.cuda.synchronize()
+    tm = Timer(torch, dev.stream)
+
+    def step(i):
+        rc = dev.lib.llg_hipd_ffn_swiglu(dev.h, gates[i % L].id, ups[i % L].id, downs[i % L].id,
+                                         vp(X[i % 64]), vp(out[i % 64]))
+        if rc:
+            dev.check(rc, "ffn_swiglu")
+
+    for i in range(args.warmup):
+        step(i)
+    dev.sync()
+    e0 = tm.event()
+    for i in range(args.steps):
+        step(i)
+    e1 = tm.event()
+    dev.sync()
+    ms = e0.elapsed_time(e1) / args.steps
+    alg = 3 * SW_FF * gg.byte_size(t, SW_H)
+    gbs = alg / (ms * 1e-3) / 1e9
+    for h_ in gates + ups + downs:
+        h_.release()
+    return {"metric": "dense SwiGLU FFN decode tokens/s + achieved HBM GB/s", "value": 1000.0 / ms,
+            "unit": "tokens/s", "ms_per_step": ms, "dtype": "f32",
+            "config": {"workload": f"llama7b-ffn-layer-{gg.TYPE_NAMES[t].lower()}-swiglu-decode",
+                       "d_model": SW_H, "d_ff": SW_FF, "layer_copies_rotated": L},
+            "roofline": {"bound": "hbm",
+                         "kernel": "k_matvec_q gated (gate+up, silu*mul) + k_matvec_q (down)",
                          "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": gbs / HBM_PEAK_GBS, "traffic": None,
                          "alg_bytes_per_launch": alg, "avg_launch_us": ms * 1e3}}
@@ -605,7 +659,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="sparse",
                     choices=["sparse", "dense-q4_0", "dense-q8_0", "dense-f16", "window",
-                             "moe-decode", "moe-prefill", "falcon-decode"])
+                             "moe-decode", "moe-prefill", "falcon-decode", "swiglu-q4_0",
+                             "swiglu-q8_0", "swiglu-f16"])
     ap.add_argument("--layers", type=int, default=0,
                     help="distinct HBM copies rotated per step (0 = enough to defeat the MALL)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -650,6 +705,9 @@ def main():
         res = bench_falcon(args, torch, llg, dev)
     elif args.workload.startswith("moe-"):
         res = bench_moe(args, torch, llg, dev, args.workload == "moe-prefill")
+    elif args.workload.startswith("swiglu-"):
+        t = {"swiglu-q4_0": gg.Q4_0, "swiglu-q8_0": gg.Q8_0, "swiglu-f16": gg.F16}[args.workload]
+        res = bench_swiglu(args, torch, llg, dev, t)
     else:
         t = {"dense-q4_0": gg.Q4_0, "dense-q8_0": gg.Q8_0, "dense-f16": gg.F16}[args.workload]
         res = bench_dense(args, torch, llg, dev, t)

@@ -136,6 +136,11 @@ int llg_hip_matvec_q(LlgHipDevice dev, int64_t mat, const float *x, float *y);
 /* out = down @ act(up @ x); up [ff x h], down [h x ff] (standard GGUF layout). */
 int llg_hip_ffn_dense(LlgHipDevice dev, int64_t up, int64_t down, const float *x, int act,
                       float *out);
+/* ffnSwiGLU (forward.go:368-389), the dense path of SiLU models (forward.go:
+ * 328-329): out = down @ (silu(gate @ x) * (up @ x)); gate and up [ff x h] of
+ * one type, down [h x ff]. */
+int llg_hip_ffn_swiglu(LlgHipDevice dev, int64_t gate, int64_t up, int64_t down, const float *x,
+                       float *out);
 
 /* ---- sliding window: inference/window.go -------------------------------- */
 /* NewNeuronCache (window.go:48-63) over a bundle, window size k >= 1. */
@@ -210,6 +215,8 @@ int llg_hipd_ffn_predict_sparse(LlgHipDevice dev, int64_t wup, int64_t wout, int
 int llg_hipd_matvec_q(LlgHipDevice dev, int64_t mat, const float *d_x, float *d_y);
 int llg_hipd_ffn_dense(LlgHipDevice dev, int64_t up, int64_t down, const float *d_x, int act,
                        float *d_out);
+int llg_hipd_ffn_swiglu(LlgHipDevice dev, int64_t gate, int64_t up, int64_t down,
+                        const float *d_x, float *d_out);
 int llg_hipd_window_step(LlgHipDevice dev, int64_t win, const float *d_x,
                          const int32_t *d_active, const int32_t *d_n_active, int act,
                          float *d_out);

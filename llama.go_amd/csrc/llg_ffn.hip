@@ -11,6 +11,10 @@
 // before using them; every x block read from LDS serves MV_ROWS rows.  With
 // one chunk the row sum is final and the activation is applied; with several
 // chunks each workgroup adds its partial with an fp32 atomic into a zeroed y.
+//
+// Gated (G): y[r] = silu(gate_r . x) * (up_r . x) (ffnSwiGLU, forward.go:
+// 368-389) with gate = w and up = w2; a wavefront's two row slots hold gate
+// row r and up row r, so it takes one output row per pass.
 #include "llg_common.hpp"
 #include "llg_internal.hpp"
 
@@ -24,13 +28,16 @@
 
 // LNP > 0: x is the LayerNorm of a residual sum, staged with LNP float4 groups
 // per thread (llg_stage_ln); LNP = 0: x is read from memory.
-template <int T, int LNP>
+template <int T, int LNP, bool G = false>
 __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w, long long stride,
                                                   RowFmt f, int rows, int tile_rows,
                                                   int chunk_blocks,
                                                   const float *__restrict__ x, int act,
                                                   float *__restrict__ y, float *__restrict__ zero,
-                                                  int zero_n, LlgLnArgs ln) {
+                                                  int zero_n, LlgLnArgs ln,
+                                                  const uint8_t *__restrict__ w2 = nullptr) {
+    static_assert(!G || (LNP == 0 && MV_ROWS == 2), "gated rows pair gate and up");
+    constexpr int RW = G ? 1 : MV_ROWS;  // output rows per wavefront pass
     extern __shared__ float xs[];
     __shared__ float red[4];
     const int n_chunks = (f.nb + chunk_blocks - 1) / chunk_blocks;
@@ -45,25 +52,29 @@ __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w,
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform per wavefront
     const int r_end = min(rows, (tile + 1) * tile_rows);
-    const int r_first = tile * tile_rows + wave * MV_ROWS;
+    const int r_first = tile * tile_rows + wave * RW;
     // request the bytes of all MV_BATCH x MV_ROWS blocks, then use them; loads
     // are never under a per-lane condition (that serialises them): lanes past
     // the chunk reload its last block and drop it, a row past the end reloads
     // the last row.  The first batch is requested right after the loads of x
     // (or of the LayerNorm inputs), so x is staged while it is in flight.
     BlockRaw<T> r[MV_BATCH][MV_ROWS];
+    // row slot q of the pass at r0: row r0 + q of w, or (gated) row r0 of gate / up
+    auto row_ptr = [&](int r0_, int q) {
+        if constexpr (G) return (q ? w2 : w) + (long long)min(r0_, r_end - 1) * stride;
+        else return w + (long long)min(r0_ + q, r_end - 1) * stride;
+    };
 #define MV_ISSUE(r0_, bb_)                                                                      \
     _Pragma("unroll") for (int i = 0; i < MV_BATCH; i++)                                       \
         _Pragma("unroll") for (int q = 0; q < MV_ROWS; q++)                                    \
-            llg_block_load<T>(r[i][q], w + (long long)min((r0_) + q, r_end - 1) * stride, f,   \
-                              cb0 + min((bb_) + lane + 64 * i, cnb - 1))
+            llg_block_load<T>(r[i][q], row_ptr(r0_, q), f, cb0 + min((bb_) + lane + 64 * i, cnb - 1))
     auto issue_first = [&]() { MV_ISSUE(min(r_first, r_end - 1), 0); };
     if constexpr (LNP > 0)  // x is the LayerNorm of the residual sum (one chunk: cb0 = 0)
         llg_stage_ln<MV_XS, LNP>(xs, ln, red, issue_first);
     else
         llg_stage_x_sum<MV_XS>(xs, x + (size_t)cb0 * 32, cnb, issue_first);
     __syncthreads();
-    for (int r0 = r_first; r0 < r_end; r0 += 4 * MV_ROWS) {
+    for (int r0 = r_first; r0 < r_end; r0 += 4 * RW) {
         float s[MV_ROWS];
 #pragma unroll
         for (int q = 0; q < MV_ROWS; q++) s[q] = 0.0f;
@@ -77,8 +88,13 @@ __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w,
                 const float4 *x4 = reinterpret_cast<const float4 *>(xb);
 #pragma unroll
                 for (int q = 0; q < MV_ROWS; q++)
-                    if (r0 + q < r_end) s[q] += llg_raw_dot<T>(r[i][q], x4, xb[32]);
+                    if (r0 + (G ? 0 : q) < r_end) s[q] += llg_raw_dot<T>(r[i][q], x4, xb[32]);
             }
+        }
+        if constexpr (G) {  // silu(gate) * up in fp32 (forward.go:370-383)
+            const float g = llg_wave_sum(s[0]), u = llg_wave_sum(s[1]);
+            if (lane == 0 && r0 < r_end) y[r0] = llg_act(LLG_ACT_SILU, g) * u;
+            continue;
         }
 #pragma unroll
         for (int q = 0; q < MV_ROWS; q++) {
@@ -103,10 +119,13 @@ static int mv_chunk_blocks(const RowFmt &f, int act) {
 
 // zero/zero_n: a buffer the launch also clears (the next kernel's atomic target).
 // ln (optional): the staged x is the LayerNorm of a residual sum (llg_stage_ln).
+// up (optional): gated rows, y = silu(w . x) * (up . x) (act is ignored).
 static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y,
-                         float *zero, int zero_n, const LlgLnArgs *ln = nullptr) {
+                         float *zero, int zero_n, const LlgLnArgs *ln = nullptr,
+                         const LlgObject *up = nullptr) {
     hipStream_t st = llg_dev_stream(d);
     const RowFmt &f = w->fmt;
+    if (up) act = LLG_ACT_SILU;  // whole rows in one workgroup
     const int cb = ln ? f.nb : mv_chunk_blocks(f, act);
     const int n_chunks = (f.nb + cb - 1) / cb;
     const size_t lds = (size_t)cb * MV_XS * 4;
@@ -115,17 +134,22 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
     if (n_chunks > 1 && zero != d_y) {
         LLG_HIP_TRY(d, hipMemsetAsync(d_y, 0, (size_t)w->rows * 4, st));
     }
-    const int tile_rows = w->rows < MV_SMALL_ROWS ? MV_TILE_SMALL : MV_TILE;
+    const int tile_rows = (w->rows < MV_SMALL_ROWS ? MV_TILE_SMALL : MV_TILE) / (up ? 2 : 1);
     const int grid = (w->rows + tile_rows - 1) / tile_rows * n_chunks;
     const LlgLnArgs none{};
     const LlgLnArgs &la = ln ? *ln : none;
     const int lnp = ln ? (ln->n / 4 + 255) / 256 : 0;
 #define MV_GO(TY, NP)                                                                              \
     hipLaunchKernelGGL((k_matvec_q<TY, NP>), dim3(grid), dim3(256), lds, st, w->d, w->stride, f,   \
-                       w->rows, tile_rows, cb, d_x, act, d_y, zero, zero_n, la)
+                       w->rows, tile_rows, cb, d_x, act, d_y, zero, zero_n, la,              \
+                       (const uint8_t *)nullptr)
 #define MV_LAUNCH(TY)                                                                              \
     do {                                                                                           \
-        if (!ln) MV_GO(TY, 0);                                                                     \
+        if (up)                                                                                    \
+            hipLaunchKernelGGL((k_matvec_q<TY, 0, true>), dim3(grid), dim3(256), lds, st, w->d,    \
+                               w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, zero, zero_n, \
+                               la, up->d);                                                         \
+        else if (!ln) MV_GO(TY, 0);                                                                \
         else if (lnp <= 2) MV_GO(TY, 2);                                                           \
         else if (lnp <= 4) MV_GO(TY, 4);                                                           \
         else if (lnp <= 5) MV_GO(TY, 5);                                                           \
@@ -174,6 +198,18 @@ static int dense_enqueue(LlgDevice *d, const LlgObject *up, const LlgObject *dow
                             mv_chunk_blocks(down->fmt, -1);
     int rc = matvec_launch(d, up, d_x, act, hid, down_chunks > 1 ? d_out : nullptr,
                            down->rows);
+    if (rc) return rc;
+    return matvec_launch(d, down, hid, -1, d_out, d_out, 0);
+}
+
+// SwiGLU dense FFN (forward.go:368-389): hid = silu(gate . x) * (up . x),
+// then out = down . hid.
+static int swiglu_enqueue(LlgDevice *d, const LlgObject *gate, const LlgObject *up,
+                          const LlgObject *down, const float *d_x, float *hid, float *d_out) {
+    const int down_chunks = (down->fmt.nb + mv_chunk_blocks(down->fmt, -1) - 1) /
+                            mv_chunk_blocks(down->fmt, -1);
+    int rc = matvec_launch(d, gate, d_x, LLG_ACT_SILU, hid, down_chunks > 1 ? d_out : nullptr,
+                           down->rows, nullptr, up);
     if (rc) return rc;
     return matvec_launch(d, down, hid, -1, d_out, d_out, 0);
 }
@@ -374,6 +410,53 @@ int llg_hip_ffn_dense(LlgHipDevice h, int64_t hu, int64_t hdn, const float *x, i
     if ((rc = llg_h2d(d, ws, x, (size_t)hd * 4))) return rc;
     if ((rc = dense_enqueue(d, up, down, (const float *)ws, act, (float *)(ws + o_h),
                             (float *)(ws + o_out))))
+        return rc;
+    if ((rc = llg_d2h(d, out, ws + o_out, (size_t)hd * 4))) return rc;
+    return llg_sync_dev(d);
+}
+
+static int check_swiglu(LlgDevice *d, int64_t hg, int64_t hu, int64_t hdn, LlgObject **gate,
+                        LlgObject **up, LlgObject **down) {
+    int rc = check_dense(d, hu, hdn, up, down);
+    if (rc) return rc;
+    *gate = llg_get(d, hg, LLG_KIND_MATRIX);
+    if (!*gate) return llg_set_error(d, LLG_E_HANDLE, "ffn_swiglu: unknown gate handle");
+    if ((*gate)->rows != (*up)->rows || (*gate)->fmt.cols != (*up)->fmt.cols ||
+        (*gate)->fmt.type != (*up)->fmt.type || (*gate)->stride != (*up)->stride)
+        return llg_set_error(d, LLG_E_ARG, "ffn_swiglu: gate [%d x %d] differs from up [%d x %d]",
+                             (*gate)->rows, (*gate)->fmt.cols, (*up)->rows, (*up)->fmt.cols);
+    return 0;
+}
+
+int llg_hipd_ffn_swiglu(LlgHipDevice h, int64_t hg, int64_t hu, int64_t hdn, const float *d_x,
+                        float *d_out) {
+    LlgDevice *d = llg_dev(h);
+    if (!d) return LLG_E_NODEV;
+    LlgObject *gate, *up, *down;
+    int rc = check_swiglu(d, hg, hu, hdn, &gate, &up, &down);
+    if (rc) return rc;
+    if (!d_x || !d_out) return llg_set_error(d, LLG_E_ARG, "ffn_swiglu: null pointer");
+    float *hid = (float *)llg_ws(d, (size_t)up->rows * 4, &rc);
+    if (rc) return rc;
+    return swiglu_enqueue(d, gate, up, down, d_x, hid, d_out);
+}
+
+int llg_hip_ffn_swiglu(LlgHipDevice h, int64_t hg, int64_t hu, int64_t hdn, const float *x,
+                       float *out) {
+    LlgDevice *d = llg_dev(h);
+    if (!d) return LLG_E_NODEV;
+    LlgObject *gate, *up, *down;
+    int rc = check_swiglu(d, hg, hu, hdn, &gate, &up, &down);
+    if (rc) return rc;
+    if (!x || !out) return llg_set_error(d, LLG_E_ARG, "ffn_swiglu: null pointer");
+    const int hd = up->fmt.cols, ff = up->rows;
+    const long long o_out = llg_align((long long)hd * 4, 256);
+    const long long o_h = o_out + llg_align((long long)hd * 4, 256);
+    uint8_t *ws = (uint8_t *)llg_ws(d, o_h + (size_t)ff * 4, &rc);
+    if (rc) return rc;
+    if ((rc = llg_h2d(d, ws, x, (size_t)hd * 4))) return rc;
+    if ((rc = swiglu_enqueue(d, gate, up, down, (const float *)ws, (float *)(ws + o_h),
+                             (float *)(ws + o_out))))
         return rc;
     if ((rc = llg_d2h(d, out, ws + o_out, (size_t)hd * 4))) return rc;
     return llg_sync_dev(d);

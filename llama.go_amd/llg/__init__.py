@@ -13,7 +13,8 @@ and tests read like the reference's own code:
   FlashContext.ffnSparseLoad                    ffn_sparse_load(dev, bundle, x, active, act)
     (inference/ffn_flash.go:254-299)
   Context.ffn dense ReLU/GELU                   ffn_dense(dev, up, down, x, act)
-    (inference/forward.go:318-367)
+  Context.ffn dense SiLU (ffnSwiGLU)            ffn_swiglu(dev, gate, up, down, x)
+    (inference/forward.go:318-389)
   NeuronCache.Update / FFNForward / NumCached   NeuronCache(dev, bundle, k).update / ...
     (inference/window.go:48-183)
   moeFFN                                        moe_ffn(dev, router, gate, up, down, ...)
@@ -78,6 +79,7 @@ _SIGS = {
         C.c_int, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, C.c_float, C.c_int, _vp, _vp, _ip]),
     "llg_hip_matvec_q": (C.c_int, [_vp, _i64, _vp, _vp]),
     "llg_hip_ffn_dense": (C.c_int, [_vp, _i64, _i64, _vp, C.c_int, _vp]),
+    "llg_hip_ffn_swiglu": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp]),
     "llg_hip_window_create": (C.c_int, [_vp, _i64, C.c_int, _i64p]),
     "llg_hip_window_update": (C.c_int, [_vp, _i64, _vp, C.c_int, _ip, _ip]),
     "llg_hip_window_ffn": (C.c_int, [_vp, _i64, _vp, _vp, C.c_int, C.c_int, _vp]),
@@ -91,6 +93,7 @@ _SIGS = {
         C.c_int, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, C.c_float, C.c_int, _vp, _vp, _vp]),
     "llg_hipd_matvec_q": (C.c_int, [_vp, _i64, _vp, _vp]),
     "llg_hipd_ffn_dense": (C.c_int, [_vp, _i64, _i64, _vp, C.c_int, _vp]),
+    "llg_hipd_ffn_swiglu": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp]),
     "llg_hipd_window_step": (C.c_int, [_vp, _i64, _vp, _vp, _vp, C.c_int, _vp]),
     "llg_hipd_moe_ffn": (
         C.c_int, [_vp, _i64, _i64, _i64, _i64, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp, _vp]),
@@ -368,6 +371,16 @@ def ffn_dense(dev: Device, up: Handle, down: Handle, x, act: int = ACT_RELU) -> 
     x = _f32(x).ravel()
     out = np.empty_like(x)
     dev.check(dev.lib.llg_hip_ffn_dense(dev.h, up.id, down.id, _ptr(x), act, _ptr(out)), "ffn")
+    return out
+
+
+def ffn_swiglu(dev: Device, gate: Handle, up: Handle, down: Handle, x) -> np.ndarray:
+    """Context.ffn SiLU path, ffnSwiGLU (forward.go:368-389):
+    down @ (silu(gate @ x) * (up @ x))."""
+    x = _f32(x).ravel()
+    out = np.empty_like(x)
+    dev.check(dev.lib.llg_hip_ffn_swiglu(dev.h, gate.id, up.id, down.id, _ptr(x), _ptr(out)),
+              "ffn_swiglu")
     return out
 
 

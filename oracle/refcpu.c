@@ -292,6 +292,32 @@ int refcpu_ffn_dense(const uint8_t *up_raw, const uint8_t *down_raw, int t, int 
     return 0;
 }
 
+/* ffnSwiGLU, inference/forward.go:368-389 (the SiLU model's dense FFN,
+ * forward.go:328-329): gate = MatMulVec(FFNGate, x); SiLU(gate) (ops.go:177-181);
+ * up = MatMulVec(FFNUp, x); Mul(gate, up) (ops.go:223-231, gate[i] *= up[i]);
+ * out = MatMulVec(FFNDown, gate). */
+int refcpu_ffn_swiglu(const uint8_t *gate_raw, const uint8_t *up_raw, const uint8_t *down_raw,
+                      int t, int h, int ff, const float *x, float *out) {
+    int64_t nu = (int64_t)h * ff;
+    int64_t bu = refcpu_byte_size(t, nu);
+    if (bu < 0 || refcpu_byte_size(t, h) < 0 || refcpu_byte_size(t, ff) < 0) return -1;
+    float *w = (float *)malloc(sizeof(float) * (size_t)nu);
+    float *gate = (float *)malloc(sizeof(float) * (size_t)ff);
+    float *up = (float *)malloc(sizeof(float) * (size_t)ff);
+    refcpu_dequantize(gate_raw, bu, t, w);
+    refcpu_matmulvec(w, ff, h, x, gate);
+    refcpu_silu(gate, ff);
+    refcpu_dequantize(up_raw, bu, t, w);
+    refcpu_matmulvec(w, ff, h, x, up);
+    for (int i = 0; i < ff; i++) gate[i] *= up[i];
+    refcpu_dequantize(down_raw, bu, t, w);
+    refcpu_matmulvec(w, h, ff, gate, out);
+    free(w);
+    free(gate);
+    free(up);
+    return 0;
+}
+
 /* ---- inference/window.go ------------------------------------------------ */
 struct refcpu_neuron_cache {
     float *matrix;       /* [max_neurons, 2*hidden] bundled up|down, window.go:23 */

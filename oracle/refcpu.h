@@ -86,6 +86,9 @@ int refcpu_ffn_sparse_load(const uint8_t *up_raw, const uint8_t *down_t_raw, int
  * up_raw: [F rows x h]; down_raw: standard GGUF layout [h rows x F]. */
 int refcpu_ffn_dense(const uint8_t *up_raw, const uint8_t *down_raw, int ggml_type, int h,
                      int ff, const float *x, int act, float *out);
+/* ffnSwiGLU (forward.go:368-389): out = down @ (silu(gate @ x) * (up @ x)). */
+int refcpu_ffn_swiglu(const uint8_t *gate_raw, const uint8_t *up_raw, const uint8_t *down_raw,
+                      int ggml_type, int h, int ff, const float *x, float *out);
 
 /* inference/window.go:21-245 -- NeuronCache. */
 typedef struct refcpu_neuron_cache refcpu_neuron_cache;

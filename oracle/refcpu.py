@@ -35,6 +35,7 @@ _SIGS = {
     "refcpu_ffn_sparse_load": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int,
                                          C.c_int, _vp]),
     "refcpu_ffn_dense": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp]),
+    "refcpu_ffn_swiglu": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "refcpu_nc_new": (_vp, [C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int]),
     "refcpu_nc_free": (None, [_vp]),
     "refcpu_nc_update": (C.c_int, [_vp, _vp, C.c_int, _vp, _vp]),
@@ -206,6 +207,17 @@ def ffn_dense(up_raw, down_raw, t: int, h: int, ff: int, x, act: int = ACT_RELU)
     rc = lib().refcpu_ffn_dense(_p(u), _p(dn), t, h, ff, _p(x), act, _p(out))
     if rc:
         raise ValueError(f"ffn_dense rc={rc}")
+    return out
+
+
+def ffn_swiglu(gate_raw, up_raw, down_raw, t: int, h: int, ff: int, x) -> np.ndarray:
+    """inference/forward.go:368-389 ffnSwiGLU: down @ (silu(gate @ x) * (up @ x))."""
+    g, u, dn = _u8(gate_raw), _u8(up_raw), _u8(down_raw)
+    x = _f32(x).ravel()
+    out = np.empty(h, np.float32)
+    rc = lib().refcpu_ffn_swiglu(_p(g), _p(u), _p(dn), t, h, ff, _p(x), _p(out))
+    if rc:
+        raise ValueError(f"ffn_swiglu rc={rc}")
     return out
 
 

@@ -116,6 +116,20 @@ def moe_tiny(rng):
              route_logits=lg, route_ids=np.stack(r_ids), route_w=np.stack(r_w))
 
 
+def ffn_swiglu_tiny(rng):
+    """ffnSwiGLU (forward.go:368-389) on Q4_0, Q8_0 and F16 weights."""
+    h, ff = 64, 160
+    x = normal(rng, h, 1.0)
+    data = {"x": x}
+    g32, u32, d32 = (normal(rng, (ff, h), 0.1), normal(rng, (ff, h), 0.1),
+                     normal(rng, (h, ff), 0.1))
+    for name, t in (("q4_0", R.Q4_0), ("q8_0", R.Q8_0), ("f16", R.F16)):
+        g, u, d = quant(g32, t), quant(u32, t), quant(d32, t)
+        data.update({f"{name}_gate": g, f"{name}_up": u, f"{name}_down": d,
+                     f"{name}_out": R.ffn_swiglu(g, u, d, t, h, ff, x)})
+    np.savez(HERE / "ffn_swiglu_tiny.npz", **data)
+
+
 def main():
     R.build()
     rng = np.random.default_rng(0x11A3A000)
@@ -125,6 +139,7 @@ def main():
     ffn_dense_tiny(rng)
     window_tiny(rng)
     moe_tiny(rng)
+    ffn_swiglu_tiny(np.random.default_rng(0x11A3A005))  # own stream: earlier fixtures unchanged
     for p in sorted(HERE.glob("*.npz")):
         print(f"{p.name}: {p.stat().st_size} bytes")
 

@@ -33,6 +33,14 @@ def test_oracle_dequant_kat():
         assert np.array_equal(R.dequantize(b, R.Q8_0), o)
 
 
+def test_oracle_ffn_swiglu_tiny():
+    z = load("ffn_swiglu_tiny")
+    h, ff = z["x"].size, z["q4_0_gate"].shape[0]
+    for name, t in (("q4_0", R.Q4_0), ("q8_0", R.Q8_0), ("f16", R.F16)):
+        out = R.ffn_swiglu(z[f"{name}_gate"], z[f"{name}_up"], z[f"{name}_down"], t, h, ff, z["x"])
+        assert np.array_equal(out, z[f"{name}_out"]), name
+
+
 def test_oracle_pred_tiny():
     z = load("pred_tiny")
     act, lg = R.predict(z["wup"], z["wout"], z["bias"], z["a"], float(z["threshold"]))
@@ -117,6 +125,21 @@ def test_gpu_ffn_sparse_tiny(dev):
             out = llg.ffn_sparse_load(dev, b, z["x"], z["active"], act)
             assert rel(out, z[f"{name}_out_{act_name}"]) <= TOL, (name, act_name)
         b.release()
+
+
+@pytest.mark.gpu
+def test_gpu_ffn_swiglu_tiny(dev):
+    import llg
+
+    z = load("ffn_swiglu_tiny")
+    h, ff = z["x"].size, z["q4_0_gate"].shape[0]
+    for name, t in (("q4_0", R.Q4_0), ("q8_0", R.Q8_0), ("f16", R.F16)):
+        g = dev.upload_matrix(z[f"{name}_gate"], t, ff, h)
+        u = dev.upload_matrix(z[f"{name}_up"], t, ff, h)
+        d = dev.upload_matrix(z[f"{name}_down"], t, h, ff)
+        assert rel(llg.ffn_swiglu(dev, g, u, d, z["x"]), z[f"{name}_out"]) <= TOL, name
+        for m in (g, u, d):
+            m.release()
 
 
 @pytest.mark.gpu

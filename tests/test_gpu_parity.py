@@ -8,6 +8,8 @@ Bars (from the hot-path contract):
 Sizes are the configs' real shapes where the oracle finishes in seconds, and
 tiny/ragged shapes for the edge cases.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -193,6 +195,63 @@ def test_ffn_dense_config1(dev, rng, t):
     assert max_rel_err(got, ref) <= TOL
     u.release()
     d.release()
+
+
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16])
+def test_ffn_swiglu_llama7b_shape(dev, rng, t):
+    """ffnSwiGLU (forward.go:368-389) at a LLaMA-7B layer's shape (d = 4096,
+    F = 11008): the down rows are 11008 long, so the down matvec splits
+    columns into chunks and accumulates with atomics."""
+    h, ff = 4096, 11008
+    gate = gpu_quant((ff, h), 0.02, 41, t)
+    up = gpu_quant((ff, h), 0.02, 42, t)
+    down = gpu_quant((h, ff), 0.02, 43, t)
+    x = normal(rng, h, 1.0)
+    g = dev.upload_matrix(gate, t, ff, h)
+    u = dev.upload_matrix(up, t, ff, h)
+    d = dev.upload_matrix(down, t, h, ff)
+    got = llg.ffn_swiglu(dev, g, u, d, x)
+    ref = R.ffn_swiglu(gate, up, down, t, h, ff, x)
+    assert max_rel_err(got, ref) <= TOL
+    # the device-pointer entry point gives the same bits
+    xd = torch.from_numpy(x).cuda()
+    od = torch.empty(h, device="cuda")
+    torch.cuda.synchronize()
+    dev.check(dev.lib.llg_hipd_ffn_swiglu(dev.h, g.id, u.id, d.id, ctypes.c_void_p(xd.data_ptr()),
+                                          ctypes.c_void_p(od.data_ptr())), "ffn_swiglu")
+    dev.sync()
+    assert max_rel_err(od.cpu().numpy(), ref) <= TOL
+    for m in (g, u, d):
+        m.release()
+
+
+@pytest.mark.parametrize("rows", [8192, 8224])
+def test_ffn_swiglu_tall(dev, rng, rows):
+    """gate/up with 8192+ rows take the 16-row workgroup tiles."""
+    h, t = 256, gg.Q4_0
+    g32, u32 = normal(rng, (rows, h), 0.05), normal(rng, (rows, h), 0.05)
+    d32 = normal(rng, (h, rows), 0.05)
+    gate, up, down = quant(g32, t), quant(u32, t), quant(d32, t)
+    x = normal(rng, h, 1.0)
+    g = dev.upload_matrix(gate, t, rows, h)
+    u = dev.upload_matrix(up, t, rows, h)
+    d = dev.upload_matrix(down, t, h, rows)
+    assert max_rel_err(llg.ffn_swiglu(dev, g, u, d, x),
+                       R.ffn_swiglu(gate, up, down, t, h, rows, x)) <= TOL
+    for m in (g, u, d):
+        m.release()
+
+
+def test_ffn_swiglu_gate_mismatch(dev, rng):
+    h, ff = 64, 96
+    up = dev.upload_matrix(quant(normal(rng, (ff, h), 0.02), gg.Q4_0), gg.Q4_0, ff, h)
+    gate = dev.upload_matrix(quant(normal(rng, (ff, h), 0.02), gg.Q8_0), gg.Q8_0, ff, h)
+    down = dev.upload_matrix(quant(normal(rng, (h, ff), 0.02), gg.Q4_0), gg.Q4_0, h, ff)
+    with pytest.raises(llg.LlgError) as e:
+        llg.ffn_swiglu(dev, gate, up, down, normal(rng, h, 1.0))
+    assert e.value.code == llg.LLG_E_ARG
+    for m in (gate, up, down):
+        m.release()
 
 
 def test_ffn_dense_shape_mismatch(dev, rng):

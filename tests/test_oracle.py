@@ -42,8 +42,8 @@ import pytest
 
 import llg.gguf as gg
 from oracle import refcpu as R
-from tests.helpers import (deq, make_falcon, make_sparse_layer, normal, quant, ref_falcon_f64,
-                           ref_sparse_f64, window_sets)
+from tests.helpers import (act_f64, deq, make_falcon, make_sparse_layer, max_rel_err, normal,
+                           quant, ref_falcon_f64, ref_sparse_f64, window_sets)
 
 
 # ---------------------------------------------------------------- f16 -> f32
@@ -266,6 +266,24 @@ def test_all_active_sparse_equals_dense_f32(rng):
     sparse = R.ffn_sparse_load(quant(up, gg.F32), quant(np.ascontiguousarray(down.T), gg.F32),
                                gg.F32, h, ff, x, np.arange(ff, dtype=np.int32))
     assert np.max(np.abs(dense - sparse)) < 1e-6
+
+
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16])
+def test_ffn_swiglu_f64(rng, t):
+    """ffnSwiGLU (forward.go:368-389) against float64 over the exactly
+    dequantized weights; exchanging gate and up must change the result (so a
+    swapped operand cannot pass)."""
+    h, ff = 96, 160
+    g, u, d = (quant(normal(rng, (ff, h), 0.1), t), quant(normal(rng, (ff, h), 0.1), t),
+               quant(normal(rng, (h, ff), 0.1), t))
+    x = normal(rng, h, 1.0)
+    out = R.ffn_swiglu(g, u, d, t, h, ff, x)
+    xd = x.astype(np.float64)
+    gv, uv = deq(g, t, h).astype(np.float64) @ xd, deq(u, t, h).astype(np.float64) @ xd
+    ref = deq(d, t, ff).astype(np.float64) @ (act_f64(gg.ACT_SILU, gv) * uv)
+    assert max_rel_err(out, ref) < 1e-5
+    swapped = R.ffn_swiglu(u, g, d, t, h, ff, x)
+    assert max_rel_err(swapped, ref) > 1e-2
 
 
 # ---------------------------------------------------------------- window
