@@ -130,10 +130,16 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // RoPE angles of every position (forward.go:487-489): freq = pos / base^(2i/hd)
 // in double, cos and sin rounded to float.  Built once per model, so the
-// attention kernel reads two floats where it would evaluate pow/cos/sin.
+// attention kernel reads two floats where it would evaluate pow/cos/sin.  A
+// base <= 0 means no RoPE (forward.go:249): the table holds the identity
+// rotation (cos 1, sin 0).
 __global__ void k_rope_table(float2 *__restrict__ tab, int max_seq, int half, float base) {
     const int j = blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= max_seq * half) return;
+    if (!(base > 0.0f)) {
+        tab[j] = make_float2(1.0f, 0.0f);
+        return;
+    }
     const int pos = j / half, i = j % half;
     const double fr = (double)pos / pow((double)base, (double)(2 * i) / (double)(2 * half));
     tab[j] = make_float2((float)cos(fr), (float)sin(fr));

@@ -459,9 +459,10 @@ class FalconModel:
     lm_head (GGUF rows), out_w, out_b (f32 [hidden]), and per-layer lists
     norm_w, norm_b (f32), wq, wk, wv, wo (GGUF rows), pwup, pwout (f32
     predictor), up, down_t (GGUF rows of the bundle halves).  Arrays may be
-    host numpy arrays or CUDA tensors."""
+    host numpy arrays or CUDA tensors.  `t` is the GGUF type of every matrix,
+    or a dict of types by key (embed, lm_head, wqkv, wo, bundle)."""
 
-    def __init__(self, dev: Device, dims: dict, w: dict, thresholds, t: int = 2,
+    def __init__(self, dev: Device, dims: dict, w: dict, thresholds, t=2,
                  act: int = ACT_RELU):
         self.dev, self.dims = dev, dict(dims)
         h, nh, nkv, hd = dims["hidden"], dims["n_heads"], dims["n_kv"], dims["head_dim"]
@@ -478,18 +479,20 @@ class FalconModel:
                 return torch.cat([p.reshape(p.shape[0], -1) for p in parts])
             return np.concatenate([np.asarray(p) for p in parts])
 
-        self.embed = up(dev.upload_matrix(w["embed"], t, V, h))
-        self.lm_head = up(dev.upload_matrix(w["lm_head"], t, V, h))
+        ty = t if isinstance(t, dict) else dict.fromkeys(
+            ("embed", "lm_head", "wqkv", "wo", "bundle"), t)
+        self.embed = up(dev.upload_matrix(w["embed"], ty["embed"], V, h))
+        self.lm_head = up(dev.upload_matrix(w["lm_head"], ty["lm_head"], V, h))
         self.out_w, self.out_b = vec(w["out_w"]), vec(w["out_b"])
         lh = []
         for l in range(L):
             wqkv = cat_rows([w["wq"][l], w["wk"][l], w["wv"][l]])
             hs = [vec(w["norm_w"][l]), vec(w["norm_b"][l]),
-                  up(dev.upload_matrix(wqkv, t, (nh + 2 * nkv) * hd, h)),
-                  up(dev.upload_matrix(w["wo"][l], t, h, nh * hd)),
+                  up(dev.upload_matrix(wqkv, ty["wqkv"], (nh + 2 * nkv) * hd, h)),
+                  up(dev.upload_matrix(w["wo"][l], ty["wo"], h, nh * hd)),
                   up(dev.upload_matrix(w["pwup"][l], F32, w["pwup"][l].shape[0], h)),
                   up(dev.upload_matrix(w["pwout"][l], F32, ff, w["pwout"][l].shape[1])),
-                  up(dev.upload_bundle(w["up"][l], w["down_t"][l], t, h, ff))]
+                  up(dev.upload_bundle(w["up"][l], w["down_t"][l], ty["bundle"], h, ff))]
             lh += [x.id for x in hs]
         d32 = np.array([L, h, nh, nkv, hd, ff, V, dims["max_seq"]], np.int32)
         lh = np.array(lh, np.int64)

@@ -16,8 +16,13 @@ import torch
 
 F32, F16, Q4_0, Q8_0 = 0, 1, 2, 8
 TYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0"}
-# (block size, bytes per block): gguf/types.go:70-89
-TYPE_INFO = {F32: (1, 4), F16: (1, 2), Q4_0: (32, 18), Q8_0: (32, 34)}
+# (block size, bytes per block) of every type the reference knows
+# (gguf/types.go:70-89); the device path computes on F32, F16, Q4_0 and Q8_0.
+TYPE_INFO = {F32: (1, 4), F16: (1, 2), Q4_0: (32, 18), 3: (32, 20), 6: (32, 22), 7: (32, 24),
+             Q8_0: (32, 34), 9: (32, 36), 10: (256, 84), 11: (256, 110), 12: (256, 144),
+             13: (256, 176), 14: (256, 210), 15: (256, 292), 24: (1, 1), 25: (1, 2),
+             26: (1, 4), 27: (1, 8), 28: (1, 8)}
+DEVICE_TYPES = (F32, F16, Q4_0, Q8_0)
 
 ACT_RELU, ACT_GELU, ACT_SILU = 0, 1, 2  # model/model.go:97-103
 

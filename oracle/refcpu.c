@@ -666,8 +666,10 @@ int refcpu_falcon_forward(refcpu_falcon *m, int32_t token, int pos, float *logit
         refcpu_matmulvec(m->wq + (size_t)l * qd * h, qd, h, normed, q);
         refcpu_matmulvec(m->wk + (size_t)l * kvd * h, kvd, h, normed, k);
         refcpu_matmulvec(m->wv + (size_t)l * kvd * h, kvd, h, normed, v);
-        rope_inplace(q, p->n_heads, hd, pos, p->rope_base); /* forward.go:239-242 */
-        rope_inplace(k, p->n_kv, hd, pos, p->rope_base);
+        if (p->rope_base > 0) { /* forward.go:249-252: no RoPE without a positive base */
+            rope_inplace(q, p->n_heads, hd, pos, p->rope_base);
+            rope_inplace(k, p->n_kv, hd, pos, p->rope_base);
+        }
         float *kc = m->kcache + (size_t)l * p->max_seq * kvd;
         float *vc = m->vcache + (size_t)l * p->max_seq * kvd;
         memcpy(kc + (size_t)m->seq_len * kvd, k, sizeof(float) * (size_t)kvd); /* :245-246 */

@@ -127,6 +127,8 @@ def ref_falcon_f64(w: dict, d: dict, tokens, frac: float = 0.1, t: int = gg.Q4_0
         return (Z - mu) / np.sqrt(var + eps) * g.astype(np.float64) + b.astype(np.float64)
 
     def rope(M, nheads):
+        if not base > 0:  # forward.go:249: no RoPE
+            return M.reshape(T, nheads, hd).copy()
         M = M.reshape(T, nheads, hd).copy()
         half = hd // 2
         i = np.arange(half)

@@ -1,0 +1,114 @@
+"""GPU: models and bundles loaded from files (GGUF via the loader, BNDL bundle
+files) against the same weights uploaded directly, and the no-RoPE model
+against the oracle."""
+import numpy as np
+import pytest
+
+import llg
+import llg.bundle as B
+import llg.gguf as gg
+import llg.gguf_file as G
+import llg.loader as LD
+from oracle import refcpu as R
+from tests.helpers import make_falcon, make_sparse_layer, max_rel_err, normal, ref_falcon_f64
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+FALCON = dict(n_layers=2, hidden=256, n_heads=4, n_kv=1, head_dim=64, ff=512, vocab=300,
+              max_seq=32, rank=16, rope_base=10000.0, eps=1e-5)
+
+
+def _decode_same(a, b, toks):
+    """Same weights on both sides: active counts and greedy tokens equal, logits
+    within fp32 reordering (the down products are summed with fp32 atomics,
+    whose order varies from run to run)."""
+    for s, tk in enumerate(toks):
+        la, ta, na_ = a.forward(int(tk), s)
+        lb, tb, nb_ = b.forward(int(tk), s)
+        assert np.array_equal(na_, nb_), s
+        assert max_rel_err(la, lb.astype(np.float64)) <= 1e-5, s
+        srt = np.sort(lb)
+        if srt[-1] - srt[-2] > 1e-4 * np.max(np.abs(lb)):
+            assert ta == tb, s
+
+
+@pytest.mark.parametrize("act", [gg.ACT_RELU, None])
+def test_load_falcon_matches_direct(dev, rng, tmp_path, act):
+    """Predictors and thresholds read from the file; act None takes the
+    architecture's activation (GELU for falcon, loader.go:56)."""
+    d = dict(FALCON)
+    w = make_falcon(rng, d)
+    toks = rng.integers(0, d["vocab"], 6)
+    _, _, thr = ref_falcon_f64(w, d, toks)
+    p = tmp_path / "falcon.gguf"
+    LD.write_falcon_gguf(p, d, w, gg.Q4_0, thresholds=thr)
+    m, hp = LD.load_falcon(dev, p, act=act)
+    assert hp["n_layers"] == 2 and hp["head_dim"] == 64 and m.dims["max_seq"] == 32
+    direct = llg.FalconModel(dev, d, w, thr, act=gg.ACT_GELU if act is None else act)
+    _decode_same(m, direct, toks)
+    m.release()
+    direct.release()
+
+
+def test_load_falcon_tied_output_external_predictors(dev, rng, tmp_path):
+    d = dict(FALCON)
+    w = make_falcon(rng, d)
+    w["lm_head"] = w["embed"]
+    toks = rng.integers(0, d["vocab"], 5)
+    _, _, thr = ref_falcon_f64(w, d, toks)
+    p = tmp_path / "tied.gguf"
+    LD.write_falcon_gguf(p, d, w, gg.Q4_0, with_predictors=False,
+                         tie_output=True)
+    assert "output.weight" not in G.open_gguf(p).by_name
+    preds = list(zip(w["pwup"], w["pwout"]))
+    m, _ = LD.load_falcon(dev, p, predictors=preds, thresholds=thr, act=gg.ACT_RELU, max_seq=20)
+    direct = llg.FalconModel(dev, dict(d, max_seq=20), w, thr)
+    _decode_same(m, direct, toks)
+    m.release()
+    direct.release()
+
+
+def test_falcon_without_rope(dev, rng):
+    """rope_base 0: no rotation (forward.go:249-252), against the oracle."""
+    d = dict(FALCON, rope_base=0.0)
+    w = make_falcon(rng, d)
+    toks = rng.integers(0, d["vocab"], 6)
+    _, nact, thr = ref_falcon_f64(w, d, toks)
+    ref = R.Falcon(d, w, thr)
+    m = llg.FalconModel(dev, d, w, thr)
+    for s, tk in enumerate(toks):
+        lg, _, na = m.forward(int(tk), s)
+        rl, rn = ref.forward(int(tk), s)
+        assert np.array_equal(na, rn) and np.array_equal(na, nact[s])
+        assert max_rel_err(lg, rl) <= TOL, s
+    m.release()
+
+
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16])
+def test_bundle_file_upload(dev, rng, tmp_path, t):
+    """A typed bundle file uploads to the same device bundle as the rows
+    themselves; the reference's float32 file computes the same FFN."""
+    h, ff = 256, 512
+    up, dn = make_sparse_layer(rng, h, ff, t)
+    p = tmp_path / "l.gguf"
+    G.write_gguf(p, [], [("blk.0.ffn_up.weight", [h, ff], t, up),
+                         ("blk.0.ffn_down.weight", [h, ff], t, dn)])
+    f = G.open_gguf(p)
+    ui, di = f.by_name["blk.0.ffn_up.weight"], f.by_name["blk.0.ffn_down.weight"]
+    B.create_bundle(tmp_path / "q.bundle", f, ui, di, row_type=None)
+    B.create_bundle(tmp_path / "f.bundle", f, ui, di)
+    x = normal(rng, h, 1.0)
+    active = np.sort(rng.choice(ff, 60, replace=False)).astype(np.int32)
+    direct = dev.upload_bundle(up, dn, t, h, ff)
+    from_file = B.open_bundle(tmp_path / "q.bundle").upload(dev)
+    f32 = B.open_bundle(tmp_path / "f.bundle").upload(dev)
+    # the device holds the same rows (bit-exact through the device dequant) ...
+    assert np.array_equal(dev.dequant(from_file, 0, ff), dev.dequant(direct, 0, ff))
+    assert np.array_equal(dev.dequant(f32, 0, ff), dev.dequant(direct, 0, ff))
+    # ... and computes the same FFN (fp32 atomics: reordering only)
+    a = llg.ffn_sparse_load(dev, direct, x, active).astype(np.float64)
+    assert max_rel_err(llg.ffn_sparse_load(dev, from_file, x, active), a) <= 1e-5
+    assert max_rel_err(llg.ffn_sparse_load(dev, f32, x, active), a) <= 1e-5
+    for b in (direct, from_file, f32):
+        b.release()

@@ -390,6 +390,25 @@ def test_falcon_forward_f64(rng, n_kv):
     assert 0 < nact.mean() < d["ff"]
 
 
+def test_falcon_without_rope_f64(rng):
+    """rope.freq_base missing or 0 means no RoPE (forward.go:249-252); the
+    float64 brute force without the rotation must match, and differ from the
+    rotated model after position 0."""
+    d = dict(FALCON_TINY, rope_base=0.0)
+    w = make_falcon(rng, d)
+    toks = rng.integers(0, d["vocab"], 5)
+    ref, nact, thr = ref_falcon_f64(w, d, toks)
+    m = R.Falcon(d, w, thr)
+    rot = R.Falcon(dict(d, rope_base=10000.0), w, thr)
+    for s, tk in enumerate(toks):
+        lg, na = m.forward(int(tk), s)
+        lr, _ = rot.forward(int(tk), s)
+        assert np.array_equal(na, nact[s])
+        assert np.max(np.abs(lg - ref[s])) <= 1e-4 * np.max(np.abs(ref[s])), s
+        if s > 0:
+            assert np.max(np.abs(lr - lg)) > 1e-3 * np.max(np.abs(ref[s]))
+
+
 def test_falcon_pos0_closed_form(rng):
     """At position 0 softmax over one key is 1, so every head's attention output
     is its KV head's value and RoPE is the identity: the first logits follow from
