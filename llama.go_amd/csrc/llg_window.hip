@@ -3,20 +3,19 @@
 // Device state per window (one FFN layer):
 //   slot_of[ff]   resident slot of neuron n, or -1      (the inCache map, window.go:27)
 //   cnt[ff]       how many of the k ring slots hold n
-//   cur[ff]       scratch mark of the current active set
 //   ring[k][ff]   the last k active sets, len/set flags   (lastKActive, window.go:30)
 //   free stack    slots released by evictions; hw = slots ever handed out
 //   resident      cap bundles of bstride bytes            (matrix, window.go:23)
 //
 // Update (window.go:71-117), one workgroup:
 //   A. if the expiring slot is set: cnt[n]-- for its neurons
-//   B. cur[n] = 1 for the active neurons
+//   B. the active neurons are marked in an LDS bitmap (cur)
 //   C. neurons of the expiring slot with cnt == 0 and !cur are evicted
 //      (window.go:89-94): their slot goes on the free stack
 //   D. active neurons without a slot form toLoad, in active order
 //      (window.go:98-103); a block scan gives each its index k, and it takes
 //      free slot top-1-k, or hw + (k - n_free) once the stack is empty
-//   E. cnt[n]++, cur[n] = 0, the set is recorded and the head advances
+//   E. cnt[n]++, the set is recorded and the head advances
 //      (window.go:113-114)
 // then k_window_gather copies only the toLoad bundles from the layer's
 // bundle into their resident slots (loadRows, window.go:207-245).
@@ -35,7 +34,7 @@ struct LlgWindow {
     LlgObject *bundle;  // source bundle (the layer in HBM)
     int k, ff, head;
     int cap;
-    int32_t *slot_of, *cnt, *cur, *ring, *ring_len, *ring_set;
+    int32_t *slot_of, *cnt, *ring, *ring_len, *ring_set;
     int32_t *free_stack;
     int32_t *state;      // [0]=free_top [1]=hw [2]=n_res [3]=n_loaded
     int32_t *load_list;  // [ff] pairs (neuron, slot)
@@ -53,47 +52,89 @@ void llg_window_destroy(LlgDevice *d, LlgObject *o) {
     o->ext = nullptr;
 }
 
+#define WIN_EVCAP 2048  // evicted slots of one update also kept in LDS
+
+// Round trips are the cost of this one-workgroup kernel, so the first 1024
+// entries of both lists are loaded up front (with their slots and the
+// returning decrement of cnt) and kept in registers; the current set is an
+// LDS bitmap (ff bits); this update's evictions go on the global free stack
+// and, up to WIN_EVCAP, into LDS, where the slot assignment reads them.
 __global__ __launch_bounds__(1024) void k_window_update(
-    int32_t *__restrict__ slot_of, int32_t *__restrict__ cnt, int32_t *__restrict__ cur,
-    int32_t *__restrict__ ring, int32_t *__restrict__ ring_len, int32_t *__restrict__ ring_set,
+    int32_t *__restrict__ slot_of, int32_t *__restrict__ cnt, int32_t *__restrict__ ring,
+    int32_t *__restrict__ ring_len, int32_t *__restrict__ ring_set,
     int32_t *__restrict__ free_stack, int32_t *__restrict__ state,
     int32_t *__restrict__ load_list, const int32_t *__restrict__ active,
     const int32_t *__restrict__ n_active_p, int head, int ff) {
+    extern __shared__ uint32_t curbits[];  // [ceil(ff / 32)]: the current active set
     __shared__ int wsum[16];
-    __shared__ int carry_sh;
+    __shared__ int carry_sh, ev_cnt;
+    __shared__ int ev_lds[WIN_EVCAP];
+    const int tid = threadIdx.x, bd = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6, nw = bd >> 6;
+    const int32_t *old = ring + (size_t)head * ff;
+    // round trip 1: sizes and state; the first expiring entry (in bounds whatever old_len is)
     const int n_act = *n_active_p;
     const int old_set = ring_set[head];
-    const int old_len = old_set ? ring_len[head] : 0;
-    const int32_t *old = ring + (size_t)head * ff;
-    const int tid = threadIdx.x;
-    // A + B
-    for (int j = tid; j < old_len; j += blockDim.x) cnt[old[j]] -= 1;
-    for (int j = tid; j < n_act; j += blockDim.x) cur[active[j]] = 1;
-    __syncthreads();
-    // C: evict
-    for (int j = tid; j < old_len; j += blockDim.x) {
-        const int n = old[j];
-        if (cnt[n] == 0 && cur[n] == 0) {
-            const int s = slot_of[n];
-            if (s >= 0) {
-                slot_of[n] = -1;
-                const int pos = atomicAdd(&state[0], 1);
-                free_stack[pos] = s;
-                atomicSub(&state[2], 1);
-            }
-        }
+    const int old_len0 = ring_len[head];
+    const int n_free0 = state[0], hw = state[1], n_res0 = state[2];
+    const int o_pre = old[min(tid, ff - 1)];
+    const int old_len = old_set ? old_len0 : 0;
+    for (int i = tid; i < (ff + 31) / 32; i += bd) curbits[i] = 0;
+    if (tid == 0) {
+        carry_sh = 0;
+        ev_cnt = 0;
+    }
+    // round trip 2: first active entry and its slot; first expiring entry's
+    // slot and count after the decrement (A, window.go:73-80)
+    const int a0 = tid < n_act ? active[tid] : -1;
+    const int sa0 = a0 >= 0 ? slot_of[a0] : 0;
+    const int o0 = tid < old_len ? o_pre : -1;
+    int so0 = -1, c0 = 1;
+    if (o0 >= 0) {
+        so0 = slot_of[o0];
+        c0 = atomicSub(&cnt[o0], 1) - 1;
     }
     __syncthreads();
-    // D: toLoad in active order, via a block-wide exclusive scan
-    const int n_free = state[0];
-    const int hw = state[1];
-    const int lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-    if (tid == 0) carry_sh = 0;
+    // B: mark the current set
+    if (a0 >= 0) atomicOr(&curbits[a0 >> 5], 1u << (a0 & 31));
+    for (int j = tid + bd; j < n_act; j += bd) {
+        const int n = active[j];
+        atomicOr(&curbits[n >> 5], 1u << (n & 31));
+    }
     __syncthreads();
-    for (int j0 = 0; j0 < n_act; j0 += blockDim.x) {
+    // C: an expiring neuron no set holds any more is evicted (window.go:84-95).
+    // Each entry of the expiring set is one thread's, so its decremented count
+    // is final here (the counts of current neurons only grow, in E).
+    auto evict = [&](int n, int s, int c) {
+        if (c == 0 && !((curbits[n >> 5] >> (n & 31)) & 1u) && s >= 0) {
+            slot_of[n] = -1;
+            const int e = atomicAdd(&ev_cnt, 1);
+            free_stack[n_free0 + e] = s;
+            if (e < WIN_EVCAP) ev_lds[e] = s;
+        }
+    };
+    if (o0 >= 0) evict(o0, so0, c0);
+    for (int j = tid + bd; j < old_len; j += bd) {
+        const int n = old[j];
+        const int sn = slot_of[n];
+        evict(n, sn, atomicSub(&cnt[n], 1) - 1);
+    }
+    __syncthreads();
+    // D: toLoad in active order (window.go:98-103) by a block-wide scan; the
+    // k-th needed neuron pops the k-th slot from the top of the free stack
+    // (this update's evictions, then the older entries), then fresh slots.
+    const int n_ev = ev_cnt;
+    const int n_free = n_free0 + n_ev;
+    for (int j0 = 0; j0 < n_act; j0 += bd) {
         const int j = j0 + tid;
-        const int n = j < n_act ? active[j] : -1;
-        const int need = (n >= 0 && slot_of[n] < 0) ? 1 : 0;
+        int n = -1, need = 0;
+        if (j0 == 0) {
+            n = a0;
+            need = (n >= 0 && sa0 < 0) ? 1 : 0;  // evictions never touch current neurons
+        } else if (j < n_act) {
+            n = active[j];
+            need = slot_of[n] < 0 ? 1 : 0;
+        }
         int incl = need;
         for (int o = 1; o < 64; o <<= 1) {
             const int v = __shfl_up(incl, o, 64);
@@ -107,28 +148,39 @@ __global__ __launch_bounds__(1024) void k_window_update(
         for (int w = 0; w < nw; w++) total += wsum[w];
         if (need) {
             const int kidx = before + incl - 1;
-            const int s = kidx < n_free ? free_stack[n_free - 1 - kidx] : hw + (kidx - n_free);
-            slot_of[n] = s;
+            int sl;
+            if (kidx < n_ev) {
+                const int e = n_ev - 1 - kidx;
+                sl = e < WIN_EVCAP ? ev_lds[e] : free_stack[n_free0 + e];
+            } else if (kidx < n_free) {
+                sl = free_stack[n_free - 1 - kidx];
+            } else {
+                sl = hw + (kidx - n_free);
+            }
+            slot_of[n] = sl;
             load_list[2 * kidx] = n;
-            load_list[2 * kidx + 1] = s;
+            load_list[2 * kidx + 1] = sl;
         }
         __syncthreads();
         if (tid == 0) carry_sh = total;
         __syncthreads();
     }
-    // E: record the set
+    // E: counts of the current set, the ring slot, the head (window.go:113-114)
     int32_t *dst = ring + (size_t)head * ff;
-    for (int j = tid; j < n_act; j += blockDim.x) {
+    if (a0 >= 0) {
+        atomicAdd(&cnt[a0], 1);
+        dst[tid] = a0;
+    }
+    for (int j = tid + bd; j < n_act; j += bd) {
         const int n = active[j];
-        cnt[n] += 1;
-        cur[n] = 0;
+        atomicAdd(&cnt[n], 1);
         dst[j] = n;
     }
     if (tid == 0) {
         const int n_load = carry_sh;
         state[0] = n_load < n_free ? n_free - n_load : 0;
         state[1] = hw + (n_load > n_free ? n_load - n_free : 0);
-        state[2] += n_load;
+        state[2] = n_res0 - n_ev + n_load;
         state[3] = n_load;
         ring_len[head] = n_act;
         ring_set[head] = 1;
@@ -161,9 +213,10 @@ static LlgWindow *get_window(LlgDevice *d, int64_t h) {
 static int window_update_enqueue(LlgDevice *d, LlgWindow *w, const int32_t *d_active,
                                  const int32_t *d_n_active, int max_active) {
     hipStream_t st = llg_dev_stream(d);
-    hipLaunchKernelGGL(k_window_update, dim3(1), dim3(1024), 0, st, w->slot_of, w->cnt, w->cur,
-                       w->ring, w->ring_len, w->ring_set, w->free_stack, w->state, w->load_list,
-                       d_active, d_n_active, w->head, w->ff);
+    const size_t bits = (size_t)(w->ff + 31) / 32 * 4;
+    hipLaunchKernelGGL(k_window_update, dim3(1), dim3(1024), bits, st, w->slot_of, w->cnt, w->ring,
+                       w->ring_len, w->ring_set, w->free_stack, w->state, w->load_list, d_active,
+                       d_n_active, w->head, w->ff);
     LLG_LAUNCH_CHECK(d, "window_update");
     int grid = max_active < 1 ? 1 : (max_active > 2048 ? 2048 : max_active);
     hipLaunchKernelGGL(k_window_gather, dim3(grid), dim3(256), 0, st, w->bundle->d, w->resident,
@@ -181,6 +234,8 @@ int llg_hip_window_create(LlgHipDevice h, int64_t hb, int k, int64_t *win) {
     LlgObject *b = llg_get(d, hb, LLG_KIND_BUNDLE);
     if (!b) return llg_set_error(d, LLG_E_HANDLE, "window_create: unknown bundle");
     if (k < 1 || !win) return llg_set_error(d, LLG_E_ARG, "window_create: k must be >= 1");
+    if ((size_t)(b->rows + 31) / 32 * 4 > 48 * 1024)  // the update's LDS bitmap
+        return llg_set_error(d, LLG_E_ARG, "window_create: %d neurons, at most 393216", b->rows);
     LlgWindow *w = new LlgWindow();
     w->bundle = b;
     w->k = k;
@@ -190,7 +245,7 @@ int llg_hip_window_create(LlgHipDevice h, int64_t hb, int k, int64_t *win) {
     w->bstride = b->stride;
     const size_t ff = (size_t)w->ff;
     // one allocation for the int32 state arrays
-    const size_t n_ints = ff * 3 + (size_t)k * ff + 2 * (size_t)k + ff + 4 + 2 * ff;
+    const size_t n_ints = ff * 2 + (size_t)k * ff + 2 * (size_t)k + ff + 4 + 2 * ff;
     int32_t *m = nullptr;
     if (hipMalloc(&m, n_ints * 4) != hipSuccess) {
         delete w;
@@ -198,8 +253,7 @@ int llg_hip_window_create(LlgHipDevice h, int64_t hb, int k, int64_t *win) {
     }
     w->slot_of = m;
     w->cnt = m + ff;
-    w->cur = m + 2 * ff;
-    w->ring = m + 3 * ff;
+    w->ring = m + 2 * ff;
     w->ring_len = w->ring + (size_t)k * ff;
     w->ring_set = w->ring_len + k;
     w->free_stack = w->ring_set + k;
