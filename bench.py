@@ -196,24 +196,73 @@ def bench_sparse(args, torch, llg, dev):
     return res
 
 
-def cpu_baseline_sparse(args, up, dn, wup, wout, X, thr):
-    """The oracle's restatement of ffnFlash path 2 (predictor.go:51-83 +
-    ffn_flash.go:254-299), single-threaded, on a bounded sample of tokens."""
-    from oracle import refcpu as R
+def layer_file(up, dn, t):
+    """Write ffn_up and the transposed ffn_down (GGUF dims [h, F], one row per
+    neuron) to a GGUF file in the temp directory and read it once, so that it
+    sits in the page cache as the reference's weights do after the first
+    token.  Returns (path, up offset, down offset)."""
+    import tempfile
 
-    log("cpu baseline: oracle predict + ffnSparseLoad, 1 thread")
+    from llg import gguf_file as GF
+
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    os.close(fd)
+    GF.write_gguf(path, [("general.architecture", GF.T_STRING, "falcon")],
+                  [("blk.0.ffn_up.weight", [H, FF], t, up),
+                   ("blk.0.ffn_down_t.weight", [H, FF], t, dn)])
+    with open(path, "rb") as f:
+        while f.read(1 << 24):
+            pass
+    gf = GF.open_gguf(path)
+    return (path, gf.by_name["blk.0.ffn_up.weight"].offset,
+            gf.by_name["blk.0.ffn_down_t.weight"].offset)
+
+
+def timed_loop(fn, seconds, max_n):
     n, t0 = 0, time.perf_counter()
     while True:
-        x = X[n % X.shape[0]]
-        active, _ = R.predict(wup, wout, None, x, thr)
-        R.ffn_sparse_load(up, dn, R.Q4_0, H, FF, x, active)
+        fn(n)
         n += 1
         el = time.perf_counter() - t0
-        if el >= args.cpu_seconds or n >= args.cpu_max_tokens:
-            break
-    return {"value": n / el, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"{n} decode tokens of the same layer (predict + sparse FFN), "
-                      f"{el:.1f} s, weights in host memory (no SSD I/O)"}
+        if el >= seconds or n >= max_n:
+            return n, el
+
+
+def cpu_baseline_sparse(args, up, dn, wup, wout, X, thr):
+    """The oracle's restatement of ffnFlash path 2 (predictor.go:51-83 +
+    ffn_flash.go:254-299) on a bounded sample of tokens.  Reported: the
+    reference's own arrangement, rows read from a page-cached GGUF file by a
+    32-thread pread pool that dequantizes them (ReadRowsParallel,
+    storage.go:246-319) and the arithmetic on one thread; alongside it, the
+    same arithmetic on rows already in memory, one thread."""
+    from oracle import refcpu as R
+
+    path, off_up, off_dn = layer_file(up, dn, R.Q4_0)
+    try:
+        log("cpu baseline: oracle predict + ffnSparseLoad, 32-thread pread pool")
+
+        def faithful(i):
+            x = X[i % X.shape[0]]
+            active, _ = R.predict(wup, wout, None, x, thr)
+            R.ffn_sparse_load_file(path, off_up, off_dn, R.Q4_0, H, FF, x, active, nthreads=32)
+
+        n, el = timed_loop(faithful, args.cpu_seconds, args.cpu_max_tokens)
+    finally:
+        os.unlink(path)
+    log("cpu baseline: the same on rows in memory, 1 thread")
+
+    def in_memory(i):
+        x = X[i % X.shape[0]]
+        active, _ = R.predict(wup, wout, None, x, thr)
+        R.ffn_sparse_load(up, dn, R.Q4_0, H, FF, x, active)
+
+    n2, el2 = timed_loop(in_memory, args.cpu_seconds / 3, args.cpu_max_tokens)
+    return {"value": n / el, "unit": "tokens/s", "cores": 32, "kind": "port",
+            "compute_only": n2 / el2,
+            "sample": f"{n} decode tokens of the same layer (predict + sparse FFN), {el:.1f} s: "
+                      f"up/down rows read from a page-cached GGUF file by a 32-thread pread pool "
+                      f"with per-row dequant (ReadRowsParallel), arithmetic on 1 thread; rows in "
+                      f"memory on 1 thread: {n2 / el2:.1f} tokens/s ({n2} tokens)"}
 
 
 def bench_dense(args, torch, llg, dev, t):
@@ -408,25 +457,41 @@ def bench_window(args, torch, llg, dev):
 
 
 def cpu_baseline_window(args, up, dn, X, sets):
-    """The oracle's NeuronCache (window.go Update + FFNForward), 1 thread,
-    over the 64-token sequence (repeated on fresh caches up to the time bound)."""
+    """The oracle's NeuronCache (window.go Update + FFNForward) over the 64-token
+    sequence, repeated on fresh caches up to the time bound.  Reported: new
+    rows loaded from a page-cached GGUF file by the 32-thread pread pool
+    (loadRows, window.go:208-216); alongside it, rows copied from memory."""
     from oracle import refcpu as R
 
-    log("cpu baseline: oracle window update + FFNForward, 1 thread")
-    n, t0 = 0, time.perf_counter()
-    while True:
-        nc = R.NeuronCache(FF, H, WIN_K, FF, up, dn, R.Q4_0)
-        for t in range(WIN_SEQ):
-            nc.update(sets[t])
-            nc.ffn_forward(X[t], sets[t])
-            n += 1
-            if time.perf_counter() - t0 >= args.cpu_seconds:
-                break
-        el = time.perf_counter() - t0
-        if el >= args.cpu_seconds or n >= args.cpu_max_tokens:
-            break
-    return {"value": n / el, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"{n} window decode tokens (Update + FFNForward, k={WIN_K}), {el:.1f} s"}
+    def run(make, seconds):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            nc = make()
+            for t in range(WIN_SEQ):
+                nc.update(sets[t])
+                nc.ffn_forward(X[t], sets[t])
+                n += 1
+                if time.perf_counter() - t0 >= seconds:
+                    break
+            el = time.perf_counter() - t0
+            if el >= seconds or n >= args.cpu_max_tokens:
+                return n, el
+
+    path, off_up, off_dn = layer_file(up, dn, R.Q4_0)
+    try:
+        log("cpu baseline: oracle window update + FFNForward, 32-thread pread pool")
+        n, el = run(lambda: R.NeuronCache.from_file(FF, H, WIN_K, FF, path, off_up, off_dn,
+                                                    R.Q4_0), args.cpu_seconds)
+    finally:
+        os.unlink(path)
+    log("cpu baseline: the same with rows in memory, 1 thread")
+    n2, el2 = run(lambda: R.NeuronCache(FF, H, WIN_K, FF, up, dn, R.Q4_0), args.cpu_seconds / 3)
+    return {"value": n / el, "unit": "tokens/s", "cores": 32, "kind": "port",
+            "compute_only": n2 / el2,
+            "sample": f"{n} window decode tokens (Update + FFNForward, k={WIN_K}), {el:.1f} s: "
+                      f"new rows read from a page-cached GGUF file by a 32-thread pread pool "
+                      f"(loadRows), arithmetic on 1 thread; rows in memory on 1 thread: "
+                      f"{n2 / el2:.1f} tokens/s ({n2} tokens)"}
 
 
 F4 = dict(n_layers=32, hidden=H, n_heads=71, n_kv=1, head_dim=64, ff=FF, vocab=65024,

@@ -15,11 +15,16 @@
  * known-answer vectors, float64 brute force, closed forms or invariants
  * (the header of that file lists which check pins which function).
  */
+#define _POSIX_C_SOURCE 200809L /* pread, strdup */
 #include "refcpu.h"
 
+#include <fcntl.h>
 #include <math.h>
+#include <pthread.h>
+#include <stdatomic.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 /* ---- gguf/types.go:70-102 ------------------------------------------------ */
 static int type_info(int t, int *block, int *tsize) {
@@ -240,7 +245,97 @@ int refcpu_read_rows(const uint8_t *raw, int t, int in_dim, int out_dim, const i
     return 0;
 }
 
+/* ---- flash/storage.go:246-319 ReadRowsParallel --------------------------- */
+typedef struct {
+    const char *path;
+    int64_t offset, rb;
+    int t, in_dim, out_dim, n_rows;
+    const int32_t *rows;
+    float *out;
+    int *errs;          /* per destination row, :259 */
+    atomic_int next;    /* the job queue, :265-270 */
+} rows_job;
+
+static void *rows_worker(void *arg) { /* :278-312 */
+    rows_job *j = (rows_job *)arg;
+    int fd = open(j->path, O_RDONLY); /* its own descriptor, :281 */
+    uint8_t *buf = NULL;
+    for (;;) {
+        int i = atomic_fetch_add(&j->next, 1);
+        if (i >= j->n_rows) break;
+        if (fd < 0) { j->errs[i] = -3; continue; } /* :282-287 */
+        int32_t r = j->rows[i];
+        if (r < 0 || r >= j->out_dim) { j->errs[i] = -2; continue; } /* :291-294 */
+        buf = (uint8_t *)malloc((size_t)j->rb); /* :296-297, a buffer per row */
+        int64_t done = 0, off = j->offset + (int64_t)r * j->rb;
+        while (done < j->rb) {
+            ssize_t n = pread(fd, buf + done, (size_t)(j->rb - done), (off_t)(off + done));
+            if (n <= 0) break;
+            done += n;
+        }
+        if (done < j->rb) j->errs[i] = -4; /* :298-300 */
+        else if (refcpu_dequantize(buf, j->rb, j->t, j->out + (size_t)i * j->in_dim) < 0)
+            j->errs[i] = -1; /* :302-305 */
+        free(buf);
+    }
+    if (fd >= 0) close(fd);
+    return NULL;
+}
+
+int refcpu_read_rows_file(const char *path, int64_t tensor_offset, int t, int in_dim,
+                          int out_dim, const int32_t *rows, int n_rows, int nthreads,
+                          float *out) {
+    int64_t rb = refcpu_byte_size(t, in_dim); /* :253 */
+    if (rb < 0) return -1;
+    if (n_rows <= 0) return 0;
+    if (nthreads <= 0) nthreads = 32; /* :272-274 */
+    rows_job j;
+    j.path = path;
+    j.offset = tensor_offset;
+    j.rb = rb;
+    j.t = t;
+    j.in_dim = in_dim;
+    j.out_dim = out_dim;
+    j.n_rows = n_rows;
+    j.rows = rows;
+    j.out = out;
+    j.errs = (int *)calloc((size_t)n_rows, sizeof(int));
+    atomic_init(&j.next, 0);
+    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)nthreads);
+    int started = 0;
+    for (int i = 0; i < nthreads; i++)
+        if (pthread_create(&th[i], NULL, rows_worker, &j) == 0) started++;
+        else break;
+    if (started == 0) rows_worker(&j); /* no thread could start: read on this one */
+    for (int i = 0; i < started; i++) pthread_join(th[i], NULL); /* :315 */
+    int rc = 0;
+    for (int i = 0; i < n_rows && rc == 0; i++) rc = j.errs[i]; /* :317-321 */
+    free(th);
+    free(j.errs);
+    return rc;
+}
+
 /* ---- inference/ffn_flash.go:254-299 ------------------------------------- */
+/* :272-298 on rows already read and dequantized */
+static void sparse_compute(const float *up_rows, const float *down_rows, int h, const float *x,
+                           int n_active, int act, float *out) {
+    float *inter = (float *)malloc(sizeof(float) * (size_t)n_active);
+    for (int j = 0; j < n_active; j++) { /* :273-281 */
+        const float *row = up_rows + (size_t)j * h;
+        float dot = 0.0f;
+        for (int d = 0; d < h; d++) dot += row[d] * x[d];
+        inter[j] = dot;
+    }
+    refcpu_activation(act, inter, n_active); /* :284-285 */
+    for (int j = 0; j < n_active; j++) {     /* :288-298 */
+        if (inter[j] == 0) continue;
+        const float *row = down_rows + (size_t)j * h;
+        float scale = inter[j];
+        for (int d = 0; d < h; d++) out[d] += scale * row[d];
+    }
+    free(inter);
+}
+
 int refcpu_ffn_sparse_load(const uint8_t *up_raw, const uint8_t *down_t_raw, int t, int h,
                            int ff, const float *x, const int32_t *active, int n_active,
                            int act, float *out) {
@@ -248,27 +343,29 @@ int refcpu_ffn_sparse_load(const uint8_t *up_raw, const uint8_t *down_t_raw, int
     if (n_active == 0) return 0; /* :255-257 */
     float *up_rows = (float *)malloc(sizeof(float) * (size_t)n_active * h);
     float *down_rows = (float *)malloc(sizeof(float) * (size_t)n_active * h);
-    float *inter = (float *)malloc(sizeof(float) * (size_t)n_active);
     int rc = refcpu_read_rows(up_raw, t, h, ff, active, n_active, up_rows); /* :262 */
     if (rc == 0) rc = refcpu_read_rows(down_t_raw, t, h, ff, active, n_active, down_rows);
-    if (rc == 0) {
-        for (int j = 0; j < n_active; j++) { /* :273-281 */
-            const float *row = up_rows + (size_t)j * h;
-            float dot = 0.0f;
-            for (int d = 0; d < h; d++) dot += row[d] * x[d];
-            inter[j] = dot;
-        }
-        refcpu_activation(act, inter, n_active); /* :284-285 */
-        for (int j = 0; j < n_active; j++) {     /* :288-298 */
-            if (inter[j] == 0) continue;
-            const float *row = down_rows + (size_t)j * h;
-            float scale = inter[j];
-            for (int d = 0; d < h; d++) out[d] += scale * row[d];
-        }
-    }
+    if (rc == 0) sparse_compute(up_rows, down_rows, h, x, n_active, act, out);
     free(up_rows);
     free(down_rows);
-    free(inter);
+    return rc;
+}
+
+int refcpu_ffn_sparse_load_file(const char *path, int64_t up_offset, int64_t down_t_offset,
+                                int t, int h, int ff, const float *x, const int32_t *active,
+                                int n_active, int act, int nthreads, float *out) {
+    memset(out, 0, sizeof(float) * (size_t)h);
+    if (n_active == 0) return 0; /* :255-257 */
+    float *up_rows = (float *)malloc(sizeof(float) * (size_t)n_active * h);
+    float *down_rows = (float *)malloc(sizeof(float) * (size_t)n_active * h);
+    int rc = refcpu_read_rows_file(path, up_offset, t, h, ff, active, n_active, nthreads,
+                                   up_rows); /* :262-265 */
+    if (rc == 0)
+        rc = refcpu_read_rows_file(path, down_t_offset, t, h, ff, active, n_active, nthreads,
+                                   down_rows); /* :267-270 */
+    if (rc == 0) sparse_compute(up_rows, down_rows, h, x, n_active, act, out);
+    free(up_rows);
+    free(down_rows);
     return rc;
 }
 
@@ -330,6 +427,9 @@ struct refcpu_neuron_cache {
     int num_used, max_neurons, hidden, window, ff;
     const uint8_t *up_raw, *down_raw;
     int type;
+    char *path; /* file-backed rows when set */
+    int64_t up_off, down_off;
+    int nthreads;
 };
 
 refcpu_neuron_cache *refcpu_nc_new(int max_neurons, int hidden, int window, int ff,
@@ -352,8 +452,20 @@ refcpu_neuron_cache *refcpu_nc_new(int max_neurons, int hidden, int window, int 
     return c;
 }
 
+refcpu_neuron_cache *refcpu_nc_new_file(int max_neurons, int hidden, int window, int ff,
+                                        const char *path, int64_t up_offset,
+                                        int64_t down_t_offset, int t, int nthreads) {
+    refcpu_neuron_cache *c = refcpu_nc_new(max_neurons, hidden, window, ff, NULL, NULL, t);
+    c->path = strdup(path);
+    c->up_off = up_offset;
+    c->down_off = down_t_offset;
+    c->nthreads = nthreads;
+    return c;
+}
+
 void refcpu_nc_free(refcpu_neuron_cache *c) {
     if (!c) return;
+    free(c->path);
     for (int i = 0; i < c->window; i++) free(c->last_k[i]);
     free(c->last_k);
     free(c->last_k_len);
@@ -382,8 +494,17 @@ static int nc_load_rows(refcpu_neuron_cache *c, const int32_t *neurons, int n) {
     int h = c->hidden; /* window.go:207-245 */
     float *up = (float *)malloc(sizeof(float) * (size_t)n * h);
     float *down = (float *)malloc(sizeof(float) * (size_t)n * h);
-    int rc = refcpu_read_rows(c->up_raw, c->type, h, c->ff, neurons, n, up); /* :211 */
-    if (rc == 0) rc = refcpu_read_rows(c->down_raw, c->type, h, c->ff, neurons, n, down);
+    int rc;
+    if (c->path) { /* :211, :216 */
+        rc = refcpu_read_rows_file(c->path, c->up_off, c->type, h, c->ff, neurons, n,
+                                   c->nthreads, up);
+        if (rc == 0)
+            rc = refcpu_read_rows_file(c->path, c->down_off, c->type, h, c->ff, neurons, n,
+                                       c->nthreads, down);
+    } else {
+        rc = refcpu_read_rows(c->up_raw, c->type, h, c->ff, neurons, n, up); /* :211 */
+        if (rc == 0) rc = refcpu_read_rows(c->down_raw, c->type, h, c->ff, neurons, n, down);
+    }
     if (rc == 0) {
         for (int j = 0; j < n; j++) {
             if (c->num_used >= c->max_neurons) { /* grow by 10%: :222-232 */

@@ -76,11 +76,29 @@ int refcpu_predict(const float *wup, const float *wout, const float *bias, int h
 int refcpu_read_rows(const uint8_t *tensor_raw, int ggml_type, int in_dim, int out_dim,
                      const int32_t *rows, int n_rows, float *out);
 
+/* flash/storage.go:246-319 ReadRowsParallel: the rows of the tensor at byte
+ * offset tensor_offset of the file at path, read with pread by nthreads
+ * threads (32 when nthreads <= 0) pulling rows from a shared queue; each
+ * thread opens its own descriptor, reads a row into a buffer of its own and
+ * dequantizes it into out.  Returns 0, or the first failing row's error:
+ * -1 bad type/length, -2 row out of range, -3 open failed, -4 short read. */
+int refcpu_read_rows_file(const char *path, int64_t tensor_offset, int ggml_type, int in_dim,
+                          int out_dim, const int32_t *rows, int n_rows, int nthreads,
+                          float *out);
+
 /* inference/ffn_flash.go:254-299.  up_raw: ffn_up, F rows of ByteSize(h).
  * down_t_raw: ffn_down stored [F rows x h] (GGUF dims [h, F]).  Returns 0 or <0. */
 int refcpu_ffn_sparse_load(const uint8_t *up_raw, const uint8_t *down_t_raw, int ggml_type,
                            int h, int ff, const float *x, const int32_t *active,
                            int n_active, int act, float *out);
+
+/* The same with the rows read from a file as the reference does
+ * (ffn_flash.go:262-270: two ReadRowsParallel calls), tensors at the given
+ * byte offsets. */
+int refcpu_ffn_sparse_load_file(const char *path, int64_t up_offset, int64_t down_t_offset,
+                                int ggml_type, int h, int ff, const float *x,
+                                const int32_t *active, int n_active, int act, int nthreads,
+                                float *out);
 
 /* inference/forward.go:318-353 + 428-445 (dense ReLU/GELU path, no gate).
  * up_raw: [F rows x h]; down_raw: standard GGUF layout [h rows x F]. */
@@ -95,6 +113,11 @@ typedef struct refcpu_neuron_cache refcpu_neuron_cache;
 refcpu_neuron_cache *refcpu_nc_new(int max_neurons, int hidden, int window, int ff,
                                    const uint8_t *up_raw, const uint8_t *down_t_raw,
                                    int ggml_type);
+/* A cache whose loadRows reads the file at path (window.go:208-216, two
+ * ReadRowsParallel calls with 32 threads). */
+refcpu_neuron_cache *refcpu_nc_new_file(int max_neurons, int hidden, int window, int ff,
+                                        const char *path, int64_t up_offset,
+                                        int64_t down_t_offset, int ggml_type, int nthreads);
 void refcpu_nc_free(refcpu_neuron_cache *c);
 /* window.go:71-117.  n_loaded_out (optional) receives |toLoad|; load_list_out
  * (optional, capacity n_active) receives toLoad in the reference's order. */

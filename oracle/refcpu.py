@@ -34,6 +34,13 @@ _SIGS = {
     "refcpu_read_rows": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp]),
     "refcpu_ffn_sparse_load": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int,
                                          C.c_int, _vp]),
+    "refcpu_read_rows_file": (C.c_int, [C.c_char_p, C.c_int64, C.c_int, C.c_int, C.c_int, _vp,
+                                        C.c_int, C.c_int, _vp]),
+    "refcpu_ffn_sparse_load_file": (C.c_int, [C.c_char_p, C.c_int64, C.c_int64, C.c_int, C.c_int,
+                                              C.c_int, _vp, _vp, C.c_int, C.c_int, C.c_int,
+                                              _vp]),
+    "refcpu_nc_new_file": (_vp, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_char_p, C.c_int64,
+                                 C.c_int64, C.c_int, C.c_int]),
     "refcpu_ffn_dense": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp]),
     "refcpu_ffn_swiglu": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, _vp, _vp]),
     "refcpu_nc_new": (_vp, [C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, C.c_int]),
@@ -199,6 +206,39 @@ def ffn_sparse_load(up_raw, down_t_raw, t: int, h: int, ff: int, x, active,
     return out
 
 
+_FILE_ERRORS = {-1: "bad type/length", -2: "row out of range", -3: "open failed",
+                -4: "short read"}
+
+
+def read_rows_file(path, tensor_offset: int, t: int, in_dim: int, out_dim: int, rows,
+                   nthreads: int = 32) -> np.ndarray:
+    """flash/storage.go:246-319 ReadRowsParallel: rows of the tensor at byte
+    offset tensor_offset of the file, read by nthreads threads with pread."""
+    r = np.ascontiguousarray(rows, np.int32)
+    out = np.empty((r.size, in_dim), np.float32)
+    rc = lib().refcpu_read_rows_file(str(path).encode(), tensor_offset, t, in_dim, out_dim,
+                                     _p(r), r.size, nthreads, _p(out))
+    if rc == -2:
+        raise IndexError("row out of range")
+    if rc:
+        raise OSError(f"read_rows_file: {_FILE_ERRORS.get(rc, rc)}")
+    return out
+
+
+def ffn_sparse_load_file(path, up_offset: int, down_t_offset: int, t: int, h: int, ff: int, x,
+                         active, act: int = ACT_RELU, nthreads: int = 32) -> np.ndarray:
+    """inference/ffn_flash.go:254-299 with the up and down rows read from the
+    file as the reference does (two ReadRowsParallel calls, :262-270)."""
+    x = _f32(x).ravel()
+    a = np.ascontiguousarray(active, np.int32)
+    out = np.empty(h, np.float32)
+    rc = lib().refcpu_ffn_sparse_load_file(str(path).encode(), up_offset, down_t_offset, t, h,
+                                           ff, _p(x), _p(a), a.size, act, nthreads, _p(out))
+    if rc:
+        raise OSError(f"ffn_sparse_load_file: {_FILE_ERRORS.get(rc, rc)}")
+    return out
+
+
 def ffn_dense(up_raw, down_raw, t: int, h: int, ff: int, x, act: int = ACT_RELU) -> np.ndarray:
     """inference/forward.go:318-367 dense ReLU/GELU path."""
     u, dn = _u8(up_raw), _u8(down_raw)
@@ -229,6 +269,16 @@ class NeuronCache:
         self._u, self._d = _u8(up_raw), _u8(down_t_raw)  # keep alive
         self.ff = ff
         self.c = lib().refcpu_nc_new(max_neurons, hidden, window, ff, _p(self._u), _p(self._d), t)
+
+    @classmethod
+    def from_file(cls, max_neurons: int, hidden: int, window: int, ff: int, path,
+                  up_offset: int, down_t_offset: int, t: int, nthreads: int = 32):
+        """A cache whose loadRows reads the file (window.go:208-216)."""
+        self = cls.__new__(cls)
+        self.ff = ff
+        self.c = lib().refcpu_nc_new_file(max_neurons, hidden, window, ff, str(path).encode(),
+                                          up_offset, down_t_offset, t, nthreads)
+        return self
 
     def update(self, active):
         a = np.ascontiguousarray(active, np.int32)

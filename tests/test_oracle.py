@@ -20,6 +20,10 @@ check that a plausible restatement mistake would fail:
   select / Predict (predictor.go:51-83)    brute force with strict '>' at ties; float64
                                            logits
   ReadRowsParallel addressing              rows equal slices of the full dequantized tensor
+  ReadRowsParallel from a file             a GGUF file written here, read back by 1, 3 and
+  (storage.go:246-319)                     32 threads: bit-equal to the in-memory rows;
+                                           out-of-range row, missing file and truncated
+                                           tensor errors
   ffnSparseLoad (ffn_flash.go:254-299)     float64 brute force; empty list; zero-skip;
                                            all-active sparse vs dense on F32 weights
   NeuronCache (window.go)                  closed forms toLoad_t = A_t minus the previous k
@@ -231,6 +235,55 @@ def test_read_rows_addressing(rng):
         R.read_rows(raw, R.Q4_0, h, ff, np.array([40], np.int32))
 
 
+def _layer_file(tmp_path, up, dn, t, h, ff):
+    """A GGUF file holding ffn_up and the transposed ffn_down ([h, F] dims,
+    F rows of h) after a small leading tensor, so the offsets are not 0."""
+    from llg import gguf_file as GF
+
+    path = tmp_path / "layer.gguf"
+    pad = np.zeros(7 * 4, np.uint8)
+    GF.write_gguf(path, [("general.architecture", GF.T_STRING, "falcon")],
+                  [("pad", [7], gg.F32, pad), ("blk.0.ffn_up.weight", [h, ff], t, up),
+                   ("blk.0.ffn_down_t.weight", [h, ff], t, dn)])
+    f = GF.open_gguf(path)
+    return path, f.by_name["blk.0.ffn_up.weight"].offset, f.by_name["blk.0.ffn_down_t.weight"].offset
+
+
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16])
+def test_read_rows_file_matches_memory(rng, tmp_path, t):
+    h, ff = 96, 70
+    up, dn = make_sparse_layer(rng, h, ff, t)
+    path, off_up, off_dn = _layer_file(tmp_path, up, dn, t, h, ff)
+    rows = np.array([69, 0, 7, 7, 12, 33, 68], np.int32)
+    for n in (1, 3, 32):
+        assert np.array_equal(R.read_rows_file(path, off_up, t, h, ff, rows, n),
+                              R.read_rows(up, t, h, ff, rows))
+        assert np.array_equal(R.read_rows_file(path, off_dn, t, h, ff, rows, n),
+                              R.read_rows(dn, t, h, ff, rows))
+    with pytest.raises(IndexError):
+        R.read_rows_file(path, off_up, t, h, ff, np.array([3, 70], np.int32))
+    with pytest.raises(OSError, match="open failed"):
+        R.read_rows_file(tmp_path / "missing.gguf", off_up, t, h, ff, rows)
+    with pytest.raises(OSError, match="short read"):  # the last row runs past the end
+        R.read_rows_file(path, off_dn + gg.byte_size(t, h), t, h, ff, np.array([69], np.int32))
+
+
+def test_ffn_sparse_load_file_matches_memory(rng, tmp_path):
+    h, ff = 128, 300
+    up, dn = make_sparse_layer(rng, h, ff, gg.Q4_0)
+    path, off_up, off_dn = _layer_file(tmp_path, up, dn, gg.Q4_0, h, ff)
+    x = normal(rng, h, 1.0)
+    active = np.sort(rng.choice(ff, 45, replace=False)).astype(np.int32)
+    ref = R.ffn_sparse_load(up, dn, gg.Q4_0, h, ff, x, active)
+    assert np.array_equal(
+        R.ffn_sparse_load_file(path, off_up, off_dn, gg.Q4_0, h, ff, x, active), ref)
+    assert np.all(R.ffn_sparse_load_file(path, off_up, off_dn, gg.Q4_0, h, ff, x,
+                                         np.array([], np.int32)) == 0)
+    # rows come from the file: the in-memory arrays are not consulted
+    assert not np.array_equal(
+        R.ffn_sparse_load_file(path, off_dn, off_up, gg.Q4_0, h, ff, x, active), ref)
+
+
 # ---------------------------------------------------------------- sparse FFN
 @pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16])
 def test_ffn_sparse_f64(rng, t):
@@ -304,6 +357,19 @@ def test_neuron_cache_closed_forms(rng, k):
         got = nc.ffn_forward(x, A)
         ref = R.ffn_sparse_load(up, dn, gg.Q4_0, h, ff, x, A)
         assert np.array_equal(got, ref)
+
+
+def test_neuron_cache_from_file(rng, tmp_path):
+    h, ff, k = 64, 96, 3
+    up, dn = make_sparse_layer(rng, h, ff, gg.Q4_0)
+    path, off_up, off_dn = _layer_file(tmp_path, up, dn, gg.Q4_0, h, ff)
+    mem = R.NeuronCache(ff, h, k, ff, up, dn, gg.Q4_0)
+    fil = R.NeuronCache.from_file(ff, h, k, ff, path, off_up, off_dn, gg.Q4_0)
+    for A in window_sets(rng, ff, 10, 24, 0.6):
+        assert np.array_equal(fil.update(A), mem.update(A))
+        assert fil.num_cached() == mem.num_cached()
+        x = normal(rng, h, 1.0)
+        assert np.array_equal(fil.ffn_forward(x, A), mem.ffn_forward(x, A))
 
 
 def test_neuron_cache_grows(rng):
