@@ -27,10 +27,19 @@ int llg_compact_enqueue(LlgDevice *d, const unsigned long long *mask, int n_tile
 // Sparse FFN over bundles (llg_sparse.hip).  Neuron n's bundle is at
 // base + (slot_of ? slot_of[n] : n) * bstride.  max_active bounds *d_n_active.
 size_t llg_sparse_ws_bytes(int max_active);
+// Windowed rows loaded by the current update: a listed neuron n with
+// fresh[n] == epoch is read from row n of src, and its whole bundle is copied
+// into its resident row slot_of[n] of dst (the writable base) on the way.
+struct LlgFreshRows {
+    const uint8_t *src;
+    const int32_t *fresh;
+    int epoch;
+    uint8_t *dst;
+};
 int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, const RowFmt &f,
                        const int32_t *slot_of, const float *d_x, const int32_t *d_active,
                        const int32_t *d_n_active, int max_active, int act, float *d_out,
-                       uint8_t *ws);
+                       uint8_t *ws, const LlgFreshRows *fresh = nullptr);
 
 // Dense quantized matvec y[rows] = act(W . x) (llg_ffn.hip); act < 0 = none.
 int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y);

@@ -49,10 +49,11 @@ __device__ __forceinline__ void stage_x(float *xs, const float *__restrict__ x, 
 // wavefront-uniform and loads are never under a per-lane condition (either
 // makes the compiler wait for each load before issuing the next): a lane past
 // the last block reloads it and drops the result.
-template <int T>
+// issued(): called once the pass's loads are issued, before any is used.
+template <int T, typename Issued = LlgNoIssue>
 __device__ __forceinline__ void row_dot2_pass(const uint8_t *p0, const uint8_t *p1, bool v0,
                                               bool v1, const RowFmt &f, const float *xs, int b0,
-                                              float &a0, float &a1) {
+                                              float &a0, float &a1, Issued &&issued = Issued()) {
     const int lane = threadIdx.x & 63;
     BlockRaw<T> r0[BATCH], r1[BATCH];
 #pragma unroll
@@ -61,6 +62,8 @@ __device__ __forceinline__ void row_dot2_pass(const uint8_t *p0, const uint8_t *
         llg_block_load<T>(r0[i], p0, f, b);
         llg_block_load<T>(r1[i], p1, f, b);
     }
+    __builtin_amdgcn_sched_barrier(0);  // issued() stays behind these loads
+    issued();
 #pragma unroll
     for (int i = 0; i < BATCH; i++) {
         const int b = b0 + lane + 64 * i;
@@ -75,6 +78,24 @@ __device__ __forceinline__ void row_dot2_pass(const uint8_t *p0, const uint8_t *
     }
 }
 
+// p0/p1: the rows (valid when v0/v1; otherwise any readable row).
+// issued(): run once the first pass's loads are issued.
+template <int T, typename Issued = LlgNoIssue>
+__device__ __forceinline__ void row_dot2p(const uint8_t *p0, const uint8_t *p1, bool v0, bool v1,
+                                          const RowFmt &f, const float *xs, float &s0,
+                                          float &s1, Issued &&issued = Issued()) {
+    float a0 = 0.0f, a1 = 0.0f;
+    if (f.nb <= 64 * BATCH) {
+        row_dot2_pass<T>(p0, p1, v0, v1, f, xs, 0, a0, a1, issued);
+    } else {
+        row_dot2_pass<T>(p0, p1, v0, v1, f, xs, 0, a0, a1, issued);
+        for (int b0 = 64 * BATCH; b0 < f.nb; b0 += 64 * BATCH)
+            row_dot2_pass<T>(p0, p1, v0, v1, f, xs, b0, a0, a1);
+    }
+    s0 = llg_wave_sum(a0);
+    s1 = llg_wave_sum(a1);
+}
+
 template <int T>
 __device__ __forceinline__ void row_dot2(const uint8_t *__restrict__ base, long long bstride,
                                          int row0, int row1, const RowFmt &f, const float *xs,
@@ -82,17 +103,40 @@ __device__ __forceinline__ void row_dot2(const uint8_t *__restrict__ base, long 
     row0 = __builtin_amdgcn_readfirstlane(row0);
     row1 = __builtin_amdgcn_readfirstlane(row1);
     const bool v0 = row0 >= 0, v1 = row1 >= 0;
-    const uint8_t *p0 = base + (long long)(v0 ? row0 : 0) * bstride;
-    const uint8_t *p1 = base + (long long)(v1 ? row1 : 0) * bstride;
-    float a0 = 0.0f, a1 = 0.0f;
-    if (f.nb <= 64 * BATCH) {
-        row_dot2_pass<T>(p0, p1, v0, v1, f, xs, 0, a0, a1);
-    } else {
-        for (int b0 = 0; b0 < f.nb; b0 += 64 * BATCH)
-            row_dot2_pass<T>(p0, p1, v0, v1, f, xs, b0, a0, a1);
-    }
-    s0 = llg_wave_sum(a0);
-    s1 = llg_wave_sum(a1);
+    row_dot2p<T>(base + (long long)(v0 ? row0 : 0) * bstride,
+                 base + (long long)(v1 ? row1 : 0) * bstride, v0, v1, f, xs, s0, s1);
+}
+
+// Copy of one bundle (n16 16-byte units) by a wavefront: bc_issue loads the
+// first 64 * N units (N <= 5), bc_store stores them (the caller issues other
+// loads in between, so that one wait covers both), bc_rest copies the rest.
+typedef unsigned int bc_u4 __attribute__((ext_vector_type(4)));
+template <int N>
+struct BundleCopy {
+    bc_u4 v[N];
+};
+template <int N>
+__device__ __forceinline__ void bc_issue(BundleCopy<N> &c, const bc_u4 *__restrict__ sp, int n16) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < N; k++) c.v[k] = sp[min(lane + 64 * k, n16 - 1)];
+}
+template <int N>
+__device__ __forceinline__ void bc_store(const BundleCopy<N> &c, bc_u4 *__restrict__ dp, int n16) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < N; k++)
+        if (lane + 64 * k < n16) dp[lane + 64 * k] = c.v[k];
+}
+template <int N>
+__device__ __forceinline__ void bc_rest(const bc_u4 *__restrict__ sp, bc_u4 *__restrict__ dp,
+                                        int n16) {
+    for (int u = 64 * N + (int)(threadIdx.x & 63); u < n16; u += 64) dp[u] = sp[u];
+}
+// units held across the dot: a whole Q4_0/Q8_0 bundle of up to 5120 bytes
+template <int T>
+constexpr int bc_first() {
+    return T == LLG_TYPE_Q4_0 || T == LLG_TYPE_Q8_0 ? 5 : 1;
 }
 
 // Up-row dot products of NR rows (wavefront-uniform indices, < 0: none) by
@@ -168,15 +212,21 @@ __device__ __forceinline__ void tile_up_round(const uint8_t *__restrict__ base, 
 }
 
 // B. explicit list: pair j = (row of active[j], act(up . x)); also zeroes out.
-template <int T>
-__global__ __launch_bounds__(256) void k_list_up(const uint8_t *__restrict__ base,
-                                                 long long bstride, RowFmt f,
+// With src (windowed rows): a neuron n with fresh[n] == epoch (loaded by this
+// token's update) is read from row n of src, and its whole bundle is copied
+// to its resident row on the way (the gather of loadRows, window.go:207-245,
+// done by the first reader).
+// (base and dst are the same buffer then: base is not __restrict__.)  FR
+// selects that form (fr.src set), which holds the copies in registers.
+template <int T, bool FR>
+__global__ __launch_bounds__(256) void k_list_up(
+    const uint8_t *base, long long bstride, RowFmt f,
                                                  const int32_t *__restrict__ slot_of,
                                                  const float *__restrict__ x,
                                                  const int32_t *__restrict__ active,
                                                  const int32_t *__restrict__ n_active_p, int act,
                                                  int2 *__restrict__ pairs,
-                                                 float *__restrict__ out) {
+                                                 float *__restrict__ out, LlgFreshRows fr) {
     extern __shared__ float xs[];
     const int n_active = *n_active_p;
     const int gtid = blockIdx.x * blockDim.x + threadIdx.x;
@@ -194,7 +244,34 @@ __global__ __launch_bounds__(256) void k_list_up(const uint8_t *__restrict__ bas
         const int row0 = slot_of ? slot_of[n0] : n0;
         const int row1 = n1 < 0 ? -1 : (slot_of ? slot_of[n1] : n1);
         float s0, s1;
-        row_dot2<T>(base, bstride, row0, row1, f, xs, s0, s1);
+        if constexpr (FR) {
+            const int r0 = __builtin_amdgcn_readfirstlane(row0);
+            const int r1 = __builtin_amdgcn_readfirstlane(row1);
+            const bool f0 = __builtin_amdgcn_readfirstlane(r0 >= 0 && fr.fresh[n0] == fr.epoch);
+            const bool f1 = __builtin_amdgcn_readfirstlane(r1 >= 0 && fr.fresh[n1] == fr.epoch);
+            const uint8_t *p0 = f0 ? fr.src + (long long)n0 * bstride
+                                   : base + (long long)(r0 >= 0 ? r0 : 0) * bstride;
+            const uint8_t *p1 = f1 ? fr.src + (long long)n1 * bstride
+                                   : base + (long long)(r1 >= 0 ? r1 : 0) * bstride;
+            const int n16 = (int)(bstride >> 4);
+            constexpr int NC = bc_first<T>();
+            const bc_u4 *sp0 = reinterpret_cast<const bc_u4 *>(p0);
+            const bc_u4 *sp1 = reinterpret_cast<const bc_u4 *>(p1);
+            bc_u4 *dp0 = reinterpret_cast<bc_u4 *>(fr.dst + (long long)(f0 ? r0 : 0) * bstride);
+            bc_u4 *dp1 = reinterpret_cast<bc_u4 *>(fr.dst + (long long)(f1 ? r1 : 0) * bstride);
+            BundleCopy<NC> c0, c1;
+            if (f0) bc_issue(c0, sp0, n16);
+            if (f1) bc_issue(c1, sp1, n16);
+            // the copies are stored once the dot's loads are in flight
+            row_dot2p<T>(p0, p1, r0 >= 0, r1 >= 0, f, xs, s0, s1, [&]() {
+                if (f0) bc_store(c0, dp0, n16);
+                if (f1) bc_store(c1, dp1, n16);
+            });
+            if (f0) bc_rest<NC>(sp0, dp0, n16);
+            if (f1) bc_rest<NC>(sp1, dp1, n16);
+        } else {
+            row_dot2<T>(base, bstride, row0, row1, f, xs, s0, s1);
+        }
         if (lane == 0) {  // a non-resident row keeps activation 0 (window.go:150-152)
             pairs[j] = make_int2(row0, __float_as_int(row0 >= 0 ? llg_act(act, s0) : 0.0f));
             if (j1 < n_active)
@@ -410,19 +487,26 @@ template <int T>
 static void launch_list(hipStream_t st, const uint8_t *base, long long bstride, const RowFmt &f,
                         const int32_t *slot_of, const float *x, const int32_t *active,
                         const int32_t *n_active, int max_active, int act, float *out,
-                        int2 *pairs) {
+                        int2 *pairs, const LlgFreshRows &fr) {
     int grid = (max_active + 3) / 4;
     if (grid < 1) grid = 1;
     if (grid > 2048) grid = 2048;
-    hipLaunchKernelGGL(k_list_up<T>, dim3(grid), dim3(256), xs_bytes(f), st, base, bstride, f,
-                       slot_of, x, active, n_active, act, pairs, out);
+    if (fr.src)
+        hipLaunchKernelGGL((k_list_up<T, true>), dim3(grid), dim3(256), xs_bytes(f), st, base,
+                           bstride, f, slot_of, x, active, n_active, act, pairs, out, fr);
+    else
+        hipLaunchKernelGGL((k_list_up<T, false>), dim3(grid), dim3(256), xs_bytes(f), st, base,
+                           bstride, f, slot_of, x, active, n_active, act, pairs, out, fr);
     launch_down<T>(st, base, bstride, f, pairs, n_active, max_active, out);
 }
 
 int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, const RowFmt &f,
                        const int32_t *slot_of, const float *d_x, const int32_t *d_active,
                        const int32_t *d_n_active, int max_active, int act, float *d_out,
-                       uint8_t *ws) {
+                       uint8_t *ws, const LlgFreshRows *fresh) {
+    const LlgFreshRows fr = fresh ? *fresh : LlgFreshRows{nullptr, nullptr, 0, nullptr};
+    if (fr.src && (!slot_of || !fr.fresh || !fr.dst || (bstride & 15)))
+        return llg_set_error(d, LLG_E_ARG, "sparse ffn: windowed rows need slots and tags");
     if (xs_bytes(f) > 64 * 1024)
         return llg_set_error(d, LLG_E_ARG, "sparse ffn: hidden size %d too large", f.cols);
     hipStream_t st = llg_dev_stream(d);
@@ -430,19 +514,19 @@ int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, con
     switch (f.type) {
     case LLG_TYPE_Q4_0:
         launch_list<LLG_TYPE_Q4_0>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                   max_active, act, d_out, pairs);
+                                   max_active, act, d_out, pairs, fr);
         break;
     case LLG_TYPE_Q8_0:
         launch_list<LLG_TYPE_Q8_0>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                   max_active, act, d_out, pairs);
+                                   max_active, act, d_out, pairs, fr);
         break;
     case LLG_TYPE_F16:
         launch_list<LLG_TYPE_F16>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                  max_active, act, d_out, pairs);
+                                  max_active, act, d_out, pairs, fr);
         break;
     case LLG_TYPE_F32:
         launch_list<LLG_TYPE_F32>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                  max_active, act, d_out, pairs);
+                                  max_active, act, d_out, pairs, fr);
         break;
     default:
         return llg_set_error(d, LLG_E_TYPE, "sparse ffn: unsupported type %d", f.type);

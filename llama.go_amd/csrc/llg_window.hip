@@ -5,6 +5,7 @@
 //   cnt[ff]       how many of the k ring slots hold n
 //   ring[k][ff]   the last k active sets, len/set flags   (lastKActive, window.go:30)
 //   free stack    slots released by evictions; hw = slots ever handed out
+//   fresh[ff]     the number of the update that last loaded n
 //   resident      cap bundles of bstride bytes            (matrix, window.go:23)
 //
 // Update (window.go:71-117), one workgroup:
@@ -17,8 +18,11 @@
 //      free slot top-1-k, or hw + (k - n_free) once the stack is empty
 //   E. cnt[n]++, the set is recorded and the head advances
 //      (window.go:113-114)
-// then k_window_gather copies only the toLoad bundles from the layer's
-// bundle into their resident slots (loadRows, window.go:207-245).
+// then the toLoad bundles are copied from the layer's bundle into their
+// resident slots (loadRows, window.go:207-245): by k_window_gather after a
+// plain update, or, in the update + FFN step, by k_list_up as it reads each
+// loaded neuron's up row (fresh[n] == this update's number), so the step
+// takes no separate copy launch and reads no copied row back.
 //
 // Physical slot order differs from the reference's swap-with-last order
 // (window.go:188-204); it is unobservable, because FFNForward walks the
@@ -34,8 +38,9 @@ struct LlgWindow {
     LlgObject *bundle;  // source bundle (the layer in HBM)
     int k, ff, head;
     int cap;
+    int epoch;  // number of the last update (fresh tags); starts at 1
     int32_t *slot_of, *cnt, *ring, *ring_len, *ring_set;
-    int32_t *free_stack;
+    int32_t *free_stack, *fresh;
     int32_t *state;      // [0]=free_top [1]=hw [2]=n_res [3]=n_loaded
     int32_t *load_list;  // [ff] pairs (neuron, slot)
     uint8_t *resident;
@@ -63,8 +68,9 @@ __global__ __launch_bounds__(1024) void k_window_update(
     int32_t *__restrict__ slot_of, int32_t *__restrict__ cnt, int32_t *__restrict__ ring,
     int32_t *__restrict__ ring_len, int32_t *__restrict__ ring_set,
     int32_t *__restrict__ free_stack, int32_t *__restrict__ state,
-    int32_t *__restrict__ load_list, const int32_t *__restrict__ active,
-    const int32_t *__restrict__ n_active_p, int head, int ff) {
+    int32_t *__restrict__ load_list, int32_t *__restrict__ fresh, int epoch,
+    const int32_t *__restrict__ active, const int32_t *__restrict__ n_active_p, int head,
+    int ff) {
     extern __shared__ uint32_t curbits[];  // [ceil(ff / 32)]: the current active set
     __shared__ int wsum[16];
     __shared__ int carry_sh, ev_cnt;
@@ -158,6 +164,7 @@ __global__ __launch_bounds__(1024) void k_window_update(
                 sl = hw + (kidx - n_free);
             }
             slot_of[n] = sl;
+            fresh[n] = epoch;
             load_list[2 * kidx] = n;
             load_list[2 * kidx + 1] = sl;
         }
@@ -210,18 +217,23 @@ static LlgWindow *get_window(LlgDevice *d, int64_t h) {
     return o ? reinterpret_cast<LlgWindow *>(o->ext) : nullptr;
 }
 
+// gather = false: the caller's FFN launch copies the loaded bundles (the
+// k_list_up form that reads fresh tags).
 static int window_update_enqueue(LlgDevice *d, LlgWindow *w, const int32_t *d_active,
-                                 const int32_t *d_n_active, int max_active) {
+                                 const int32_t *d_n_active, int max_active, bool gather) {
     hipStream_t st = llg_dev_stream(d);
     const size_t bits = (size_t)(w->ff + 31) / 32 * 4;
+    w->epoch = w->epoch == 0x7FFFFFFF ? 1 : w->epoch + 1;
     hipLaunchKernelGGL(k_window_update, dim3(1), dim3(1024), bits, st, w->slot_of, w->cnt, w->ring,
-                       w->ring_len, w->ring_set, w->free_stack, w->state, w->load_list, d_active,
-                       d_n_active, w->head, w->ff);
+                       w->ring_len, w->ring_set, w->free_stack, w->state, w->load_list, w->fresh,
+                       w->epoch, d_active, d_n_active, w->head, w->ff);
     LLG_LAUNCH_CHECK(d, "window_update");
-    int grid = max_active < 1 ? 1 : (max_active > 2048 ? 2048 : max_active);
-    hipLaunchKernelGGL(k_window_gather, dim3(grid), dim3(256), 0, st, w->bundle->d, w->resident,
-                       w->bstride, w->load_list, w->state);
-    LLG_LAUNCH_CHECK(d, "window_gather");
+    if (gather) {
+        int grid = max_active < 1 ? 1 : (max_active > 2048 ? 2048 : max_active);
+        hipLaunchKernelGGL(k_window_gather, dim3(grid), dim3(256), 0, st, w->bundle->d,
+                           w->resident, w->bstride, w->load_list, w->state);
+        LLG_LAUNCH_CHECK(d, "window_gather");
+    }
     w->head = (w->head + 1) % w->k;
     return 0;
 }
@@ -245,7 +257,7 @@ int llg_hip_window_create(LlgHipDevice h, int64_t hb, int k, int64_t *win) {
     w->bstride = b->stride;
     const size_t ff = (size_t)w->ff;
     // one allocation for the int32 state arrays
-    const size_t n_ints = ff * 2 + (size_t)k * ff + 2 * (size_t)k + ff + 4 + 2 * ff;
+    const size_t n_ints = ff * 2 + (size_t)k * ff + 2 * (size_t)k + ff + 4 + 2 * ff + ff;
     int32_t *m = nullptr;
     if (hipMalloc(&m, n_ints * 4) != hipSuccess) {
         delete w;
@@ -259,6 +271,8 @@ int llg_hip_window_create(LlgHipDevice h, int64_t hb, int k, int64_t *win) {
     w->free_stack = w->ring_set + k;
     w->state = w->free_stack + ff;
     w->load_list = w->state + 4;
+    w->fresh = w->load_list + 2 * ff;  // 0: never loaded (updates are numbered from 1)
+    w->epoch = 0;
     if (hipMalloc(&w->resident, (size_t)w->cap * w->bstride) != hipSuccess) {
         hipFree(m);
         delete w;
@@ -304,7 +318,7 @@ int llg_hip_window_update(LlgHipDevice h, int64_t hw, const int32_t *active, int
     if ((rc = llg_h2d(d, ws, active, (size_t)n_active * 4))) return rc;
     if ((rc = llg_h2d(d, ws + o_n, &n32, 4))) return rc;
     if ((rc = window_update_enqueue(d, w, (const int32_t *)ws, (const int32_t *)(ws + o_n),
-                                    n_active)))
+                                    n_active, true)))
         return rc;
     int32_t st[4];
     if ((rc = llg_d2h(d, st, w->state, sizeof st))) return rc;
@@ -361,9 +375,10 @@ int llg_hipd_window_step(LlgHipDevice h, int64_t hw, const float *d_x, const int
     int rc;
     uint8_t *ws = (uint8_t *)llg_ws(d, llg_sparse_ws_bytes(w->ff), &rc);
     if (rc) return rc;
-    if ((rc = window_update_enqueue(d, w, d_active, d_n_active, w->ff))) return rc;
+    if ((rc = window_update_enqueue(d, w, d_active, d_n_active, w->ff, false))) return rc;
+    const LlgFreshRows fr{w->bundle->d, w->fresh, w->epoch, w->resident};
     return llg_sparse_enqueue(d, w->resident, w->bstride, w->bundle->fmt, w->slot_of, d_x,
-                              d_active, d_n_active, w->ff, act, d_out, ws);
+                              d_active, d_n_active, w->ff, act, d_out, ws, &fr);
 }
 
 int llg_hip_window_resident(LlgHipDevice h, int64_t hw, uint8_t *resident, int *n_resident) {

@@ -418,6 +418,17 @@ class NeuronCache:
             _ptr(out)), "NeuronCache.FFNForward")
         return out
 
+    def step_device(self, d_x: int, d_active: int, d_n_active: int, d_out: int,
+                    act: int = ACT_RELU) -> None:
+        """Update + FFNForward of one token on device buffers (x f32[h], the
+        active list int32[n] and its count int32[1], out f32[h]), enqueued on
+        the device's stream without waiting: the bundles that the update
+        loads are copied into their resident rows by the FFN's first read.
+        num_cached() is refreshed by resident()."""
+        self.dev.check(self.dev.lib.llg_hipd_window_step(self.dev.h, self.win.id, d_x, d_active,
+                                                         d_n_active, act, d_out),
+                       "NeuronCache.step")
+
     def num_cached(self) -> int:
         """NumCached (window.go:183)."""
         return self._num

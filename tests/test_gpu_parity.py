@@ -304,6 +304,63 @@ def test_window_config2(dev, rng):
     b.release()
 
 
+def _window_steps_vs_oracle(dev, rng, t, h, ff, k, n_active, steps, carry, check_every,
+                            host_update_at=()):
+    """Device steps (llg_hipd_window_step: update, then the list FFN that
+    copies the loaded bundles into their resident rows) against the oracle's
+    NeuronCache, token by token; host updates (separate gather launch) may be
+    interleaved.  Ends by running the FFN over every resident neuron with
+    GELU (no zero activations, so every up and down row is read back from its
+    resident row) against the oracle on the source rows."""
+    up = gpu_quant((ff, h), 0.02, 51, t)
+    dn = gpu_quant((ff, h), 0.02, 52, t)
+    b = dev.upload_bundle(up, dn, t, h, ff)
+    nc = llg.NeuronCache(dev, b, k)
+    ref = R.NeuronCache(ff, h, k, ff, up, dn, t)
+    sets = window_sets(rng, ff, n_active, steps, carry)
+    sets.insert(3, np.array([], np.int32))  # an empty active set
+    d_out = torch.empty(h, device="cuda")
+    d_n = torch.empty(1, dtype=torch.int32, device="cuda")
+    for i, A in enumerate(sets):
+        x = normal(rng, h, 1.0)
+        if i in host_update_at:
+            assert nc.update(A) == ref.update(A).size
+            got = nc.ffn_forward(x, A)
+        else:
+            d_x = torch.from_numpy(x).cuda()
+            d_a = torch.from_numpy(np.ascontiguousarray(A, np.int32)).cuda() if A.size else \
+                torch.zeros(1, dtype=torch.int32, device="cuda")
+            d_n.fill_(A.size)
+            torch.cuda.synchronize()
+            nc.step_device(d_x.data_ptr(), d_a.data_ptr(), d_n.data_ptr(), d_out.data_ptr())
+            dev.sync()
+            got = d_out.cpu().numpy()
+            ref.update(A)
+        exp = ref.ffn_forward(x, A)
+        if i % check_every == 0 or i in host_update_at:
+            assert max_rel_err(got, exp) <= TOL, f"token {i}"
+        if i % check_every == 0:
+            assert np.array_equal(nc.resident(), ref.resident()), f"token {i}"
+            assert nc.num_cached() == ref.num_cached()
+    res = nc.resident()
+    assert np.array_equal(res, ref.resident())
+    x = normal(rng, h, 1.0)
+    got = nc.ffn_forward(x, res, llg.gguf.ACT_GELU)
+    exp = R.ffn_sparse_load(up, dn, t, h, ff, x, res, R.ACT_GELU)
+    assert max_rel_err(got, exp) <= TOL
+    b.release()
+
+
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16, gg.F32])
+def test_window_step_device(dev, rng, t):
+    _window_steps_vs_oracle(dev, rng, t, 512, 1024, 3, 120, 20, 0.6, 1, host_update_at=(7, 8))
+
+
+def test_window_step_device_config2(dev, rng):
+    """64 device steps at the config-2 shape (k=5, 909 active, 70% carried)."""
+    _window_steps_vs_oracle(dev, rng, gg.Q4_0, 4544, 18176, 5, 909, 64, 0.7, 8)
+
+
 def test_window_rejects_duplicates(dev, rng):
     up, dn = make_sparse_layer(rng, 32, 32, gg.Q4_0)
     b = dev.upload_bundle(up, dn, gg.Q4_0, 32, 32)
