@@ -5,8 +5,7 @@
 //   1. k_moe_router (llg_moe.hip): ids / weights per token
 //   2. k_moe_group: counting sort of the (token, slot) pairs by expert, the
 //      pair <-> row maps, and a list of 64-row M-tiles (expert, first row, rows)
-//   3. k_moe_x16: X -> f16, each 8-group of K stored in the order
-//      [0,4,1,5,2,6,3,7] (the order in which the Q4_0 B fragment unpacks)
+//   3. k_moe_x16: X -> f16 in the MFMA K order (k_order)
 //   4. k_moe_gemm<0>: G = X_e . gate_e^T, U = X_e . up_e^T on v_mfma_f32_16x16x32_f16,
 //      epilogue H = silu(G) * U (moe_forward.go:128-132) stored f16, same K order
 //   5. k_moe_gemm<1>: Y = H_e . down_e^T
@@ -16,26 +15,31 @@
 // MFMA operands (16x16x32 f16): lane l holds 8 halves of A row l%16 and of B
 // column l%16 for the K-group l/16; C lane l holds column l%16, rows
 // 4*(l/16) .. +3.  A and B use the same K permutation, so the dot products are
-// unchanged.  B is a Q4_0 block per K step: lane (column j, group g) takes
-// 32-bit word g of the block (nibble p = element 8g + p), forms the f16 pairs
-// (1024 + q_p, 1024 + q_{p+4}) with one and/or, subtracts 1032 (exact) and
-// multiplies by the block scale.  Tiles: 64 rows x 128 columns per workgroup
-// (per weight matrix), 4 wavefronts of 64 x 32, K chunks of 128 staged in LDS
-// (double buffered; the next chunk is loaded into registers while the current
-// one is multiplied).
+// unchanged: in each 128-wide chunk (4 Q4_0 blocks), MFMA step j gives lane
+// group g word j of block g, so a lane's 16-byte load of one block holds its
+// B fragments for all 4 steps of the chunk.  The B fragment is built from the
+// word with two and-or's per nibble pair (q4_frag), an exact subtraction of
+// the offset and a multiply by the block scale.  Tiles: 64 rows x 128 columns
+// per workgroup (per weight matrix), 4 wavefronts of 64 x 32; A in K chunks of
+// 128 staged in LDS (double buffered; the next chunk is loaded into registers
+// while the current one is multiplied); B straight into registers, one chunk
+// ahead.
 #include "llg_common.hpp"
 #include "llg_internal.hpp"
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 #define GM_BM 64
 #define GM_BN 128
 #define GM_KC 128                 // K per chunk
 #define GM_KB (GM_KC / 32)        // Q4_0 blocks per chunk
 #define GM_AST (GM_KC + 8)        // LDS A row stride (halves)
-#define GM_BST 80                 // LDS B nibble row stride (bytes): conflict-free reads
+#ifndef GM_BD
+#define GM_BD 1                   // chunks of B loads in flight ahead of use
+#endif
 
 // ---------------------------------------------------------------------------
 // Grouping: pairs p = t*k + s sorted by expert (order within an expert is not
@@ -76,7 +80,10 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int32_t *__restrict__ 
     }
 }
 
-// X (fp32, [n_tok x K]) -> f16 with each 8-group in the order [0,4,1,5,2,6,3,7].
+// X (fp32, [n_tok x K]) -> f16 in the MFMA K order (k_order; K is a
+// multiple of 128, so chunks never straddle rows): 8-group i goes to 8-group
+// (i & ~15) | (i & 3) << 2 | (i >> 2) & 3, its elements in the order
+// [0,4,1,5,2,6,3,7].
 __global__ void k_moe_x16(const float *__restrict__ x, long long n8, _Float16 *__restrict__ x16) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;  // 8-group index
     if (i >= n8) return;
@@ -91,54 +98,89 @@ __global__ void k_moe_x16(const float *__restrict__ x, long long n8, _Float16 *_
     h[5] = (_Float16)b.z;
     h[6] = (_Float16)a.w;
     h[7] = (_Float16)b.w;
-    reinterpret_cast<half8_t *>(x16)[i] = h;
+    const long long dst = (i & ~15ll) | ((i & 3) << 2) | ((i >> 2) & 3);
+    reinterpret_cast<half8_t *>(x16)[dst] = h;
 }
 
-// B fragment: word g of a Q4_0 block (nibble p = element 8g+p) times scale d,
-// as f16 in the order [e0,e4,e1,e5,e2,e6,e3,e7].
-__device__ __forceinline__ half8_t q4_frag(uint32_t w, _Float16 d) {
-    const half2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
-    const half2_t dd = {d, d};
-    half8_t r;
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const uint32_t bits = ((w >> (4 * t)) & 0x000F000Fu) | 0x64006400u;  // 1024 + q
-        half2_t v = __builtin_bit_cast(half2_t, bits);
-        v = (v - off) * dd;
-        r[2 * t] = v[0];
-        r[2 * t + 1] = v[1];
-    }
+// (a & m) | o in one instruction
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
     return r;
 }
 
-// MODE 0: gate+up with SwiGLU epilogue -> H (f16, permuted K order, [rows x N]).
-// MODE 1: down -> Y (f32, [rows x N]).
+// B fragment: word g of a Q4_0 block (nibble p = element 8g+p) times scale d,
+// as f16 in the order [e0,e4,e1,e5,e2,e6,e3,e7].  A nibble at bits 0-3 of an
+// f16 under exponent bits 0x6400 is the exact value 1024 + q; one at bits 4-7
+// under 0x5400 is 64 + q (ulp 1/16).  So the two nibble pairs of each byte
+// pair need one shift between them, and subtracting 1032 or 72 gives q - 8
+// exactly before the scale.
+__device__ __forceinline__ half8_t q4_frag(uint32_t w, _Float16 d) {
+    const half2_t off_lo = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const half2_t off_hi = {(_Float16)72.0f, (_Float16)72.0f};
+    const half2_t dd = {d, d};
+    const uint32_t w8 = w >> 8;
+    const uint32_t m_lo = 0x000F000Fu, m_hi = 0x00F000F0u, e_lo = 0x64006400u, e_hi = 0x54005400u;
+    const half2_t v0 = (__builtin_bit_cast(half2_t, and_or(w, m_lo, e_lo)) - off_lo) * dd;
+    const half2_t v1 = (__builtin_bit_cast(half2_t, and_or(w, m_hi, e_hi)) - off_hi) * dd;
+    const half2_t v2 = (__builtin_bit_cast(half2_t, and_or(w8, m_lo, e_lo)) - off_lo) * dd;
+    const half2_t v3 = (__builtin_bit_cast(half2_t, and_or(w8, m_hi, e_hi)) - off_hi) * dd;
+    half8_t r;
+    r[0] = v0[0];
+    r[1] = v0[1];
+    r[2] = v1[0];
+    r[3] = v1[1];
+    r[4] = v2[0];
+    r[5] = v2[1];
+    r[6] = v3[0];
+    r[7] = v3[1];
+    return r;
+}
+
+// Position of element k of a row in the MFMA K order: within each 128-wide
+// chunk, MFMA step j (0..3) takes word j (elements 8j..8j+7) of block g for
+// lane group g, so the 8-group of word j of block g sits at 8-group j*4 + g;
+// inside it, nibble order [0,4,1,5,2,6,3,7] (q4_frag's).
+__device__ __forceinline__ int k_order(int k) {
+    const int gi = k >> 3;  // 8-group
+    const int dst = (gi & ~15) | ((gi & 3) << 2) | ((gi >> 2) & 3);
+    const int p = k & 7;
+    return dst * 8 + ((p & 3) << 1) + (p >> 2);
+}
+
+// MODE 0: gate+up with SwiGLU epilogue -> H (f16, MFMA K order, [rows x N]).
+// MODE 1: down -> Y (f32, [rows x N]), K split into ksplit equal slices: slice
+// q writes its partial product to Y + q * ystride (the combine adds them).
+// blockIdx = (M tile * N tiles + N tile) * ksplit + slice.
 // A rows: MODE 0 gathers X16 row row_pair[r] / k (the pair's token); MODE 1
-// reads H row r.
+// reads H row r.  A goes through LDS (every wavefront reads all 64 rows); B
+// is private to a wavefront (its 32 columns), so each lane loads its own
+// block of each column straight into registers: lane (column n, group g)
+// takes the 16 quant bytes and the scale of block 4c + g of chunk c, whose
+// word j is the lane's B fragment at MFMA step j.
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void k_moe_gemm(
     const int4 *__restrict__ tiles, const int32_t *__restrict__ n_tiles_p,
     const int32_t *__restrict__ row_pair, int k_slots, const _Float16 *__restrict__ A,
     const uint8_t *__restrict__ W0, const uint8_t *__restrict__ W1, long long wstride,
     int d_off, int rows_per_expert, int K, int N, _Float16 *__restrict__ H,
-    float *__restrict__ Y) {
+    float *__restrict__ Y, int ksplit, long long ystride) {
     constexpr int NM = MODE == 0 ? 2 : 1;  // weight matrices
-    constexpr int BROWS = GM_BN * NM;      // B rows per chunk
+    constexpr int NF = NM * 2;             // B fragments per wavefront per K step
     __shared__ __attribute__((aligned(16))) _Float16 As[2][GM_BM * GM_AST];
-    __shared__ __attribute__((aligned(16))) uint8_t Bq[2][BROWS * GM_BST];
-    __shared__ __attribute__((aligned(16))) _Float16 Bd[2][BROWS * GM_KB];
     const int n_ntiles = N / GM_BN;
-    const int nt = blockIdx.x % n_ntiles;
-    const int mt = blockIdx.x / n_ntiles;
+    const int ks = blockIdx.x % ksplit;
+    const int nt = (blockIdx.x / ksplit) % n_ntiles;
+    const int mt = blockIdx.x / ksplit / n_ntiles;
     if (mt >= *n_tiles_p) return;
     const int4 tile = tiles[mt];
     const int e = tile.x, row0 = tile.y, nrows = tile.z;
     const int n0 = nt * GM_BN;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lg = lane >> 4;
 
-    // Per-thread load assignment.  A: 64 rows x 16 uint4 per chunk -> 4 per
-    // thread (rows past the tile reload the tile's last row; results dropped).
-    constexpr int BQ = BROWS * GM_KB / 256;  // B nibble uint4 per thread (4 or 2)
+    // A: 64 rows x 16 uint4 per chunk -> 4 per thread (rows past the tile
+    // reload the tile's last row; their results are dropped).
     long long a_off[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -148,43 +190,35 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
         const long long arow = MODE == 0 ? row_pair[row0 + rr] / k_slots : row0 + rr;
         a_off[q] = arow * K + part * 8;
     }
-    long long b_off[BQ];
+    // B: fragment f = (matrix m, 16-column group ns) -> column
+    // n0 + wave*32 + ns*16 + li of matrix m; the lane's block of chunk c is 4c + lg.
+    const uint8_t *brow[NF];
 #pragma unroll
-    for (int q = 0; q < BQ; q++) {
-        const int idx = tid + 256 * q;
-        const int rb = idx / GM_KB, blk = idx % GM_KB;
-        const int n = rb % GM_BN;
-        b_off[q] = ((long long)e * rows_per_expert + n0 + n) * wstride + blk * 16;
+    for (int f = 0; f < NF; f++) {
+        const int m = f / 2, ns = f % 2;
+        const uint8_t *W = (MODE == 0 && m == 1) ? W1 : W0;
+        brow[f] = W + ((long long)e * rows_per_expert + n0 + wave * 32 + ns * 16 + li) * wstride;
     }
-    const uint8_t *W0b = W0, *W1b = MODE == 0 ? W1 : W0;
-    const long long d_row = ((long long)e * rows_per_expert + n0 + (tid % GM_BN)) * wstride + d_off;
-    const uint8_t *Wd = (MODE == 0 && tid >= GM_BN) ? W1b : W0b;
 
-    uint4 ra[4], rbq[BQ];
-    uint2 rd = make_uint2(0, 0);
-#define GM_LOAD(c)                                                                               \
-    do {                                                                                         \
-        _Pragma("unroll") for (int q = 0; q < 4; q++) ra[q] =                                   \
-            *reinterpret_cast<const uint4 *>(A + a_off[q] + (long long)(c) * GM_KC);             \
-        _Pragma("unroll") for (int q = 0; q < BQ; q++) {                                         \
-            const uint8_t *W = (MODE == 0 && (tid + 256 * q) / GM_KB >= GM_BN) ? W1b : W0b;      \
-            rbq[q] = *reinterpret_cast<const uint4 *>(W + b_off[q] + (long long)(c) * GM_KB * 16); \
-        }                                                                                        \
-        if (tid < BROWS) rd = *reinterpret_cast<const uint2 *>(Wd + d_row + (c) * GM_KB * 2);    \
-    } while (0)
-#define GM_STORE(buf)                                                                            \
-    do {                                                                                         \
-        _Pragma("unroll") for (int q = 0; q < 4; q++) {                                         \
-            const int idx = tid + 256 * q;                                                       \
-            *reinterpret_cast<uint4 *>(&As[buf][(idx >> 4) * GM_AST + (idx & 15) * 8]) = ra[q];  \
-        }                                                                                        \
-        _Pragma("unroll") for (int q = 0; q < BQ; q++) {                                         \
-            const int idx = tid + 256 * q;                                                       \
-            *reinterpret_cast<uint4 *>(&Bq[buf][(idx / GM_KB) * GM_BST + (idx % GM_KB) * 16]) =  \
-                rbq[q];                                                                          \
-        }                                                                                        \
-        if (tid < BROWS) *reinterpret_cast<uint2 *>(&Bd[buf][tid * GM_KB]) = rd;                \
-    } while (0)
+    constexpr int NB = GM_BD + 1;                  // B register slots
+    constexpr int UNR = NB % 2 == 0 ? NB : 2 * NB;  // loop unroll: static A buffer and B slot
+    u32x4_t ra[4];
+    u32x4_t bq[NB][NF];
+    uint32_t bd[NB][NF];
+#define GM_LOAD_A(c)                                                                             \
+    _Pragma("unroll") for (int q = 0; q < 4; q++) ra[q] =                                       \
+        *reinterpret_cast<const u32x4_t *>(A + a_off[q] + (long long)(c) * GM_KC)
+#define GM_LOAD_B(c, slot)                                                                       \
+    _Pragma("unroll") for (int f = 0; f < NF; f++) {                                             \
+        const int blk = 4 * (c) + lg;                                                            \
+        bq[slot][f] = *reinterpret_cast<const u32x4_t *>(brow[f] + blk * 16);                    \
+        bd[slot][f] = *reinterpret_cast<const unsigned short *>(brow[f] + d_off + blk * 2);      \
+    }
+#define GM_STORE_A(buf)                                                                          \
+    _Pragma("unroll") for (int q = 0; q < 4; q++) {                                             \
+        const int idx = tid + 256 * q;                                                           \
+        *reinterpret_cast<u32x4_t *>(&As[buf][(idx >> 4) * GM_AST + (idx & 15) * 8]) = ra[q];    \
+    }
 
     floatx4_t acc[NM][4][2];
 #pragma unroll
@@ -194,40 +228,48 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
 #pragma unroll
             for (int j = 0; j < 2; j++) acc[m][i][j] = {0.f, 0.f, 0.f, 0.f};
 
-    const int nc = K / GM_KC;
-    GM_LOAD(0);
-    GM_STORE(0);
-    __syncthreads();
-    const int li = lane & 15, lg = lane >> 4;
-    for (int c = 0; c < nc; c++) {
-        const int buf = c & 1;
-        GM_LOAD(min(c + 1, nc - 1));  // the last iteration reloads its own chunk (unused)
+    const int ncs = K / GM_KC / ksplit;  // chunks of this slice: c0 .. ce - 1
+    const int c0 = ks * ncs, ce = c0 + ncs;
+    GM_LOAD_A(c0);
 #pragma unroll
-        for (int s = 0; s < GM_KB; s++) {
+    for (int i = 0; i < GM_BD; i++) GM_LOAD_B(min(c0 + i, ce - 1), i);
+    GM_STORE_A(0);
+    __syncthreads();
+    // chunk c (the i-th of the slice): A in As[i & 1], B in slot i % NB.  First
+    // the loads of A for chunk c + 1 and of B for chunk c + GM_BD are issued
+    // (past the end, the last chunk is reloaded and not used).
+    auto chunk = [&](int c, int buf, int slot) __attribute__((always_inline)) {
+        GM_LOAD_A(min(c + 1, ce - 1));
+        GM_LOAD_B(min(c + GM_BD, ce - 1), (slot + GM_BD) % NB);
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
             half8_t a[4];
 #pragma unroll
             for (int ms = 0; ms < 4; ms++)
                 a[ms] = *reinterpret_cast<const half8_t *>(
                     &As[buf][(ms * 16 + li) * GM_AST + s * 32 + lg * 8]);
 #pragma unroll
-            for (int m = 0; m < NM; m++)
+            for (int f = 0; f < NF; f++) {
+                const uint32_t w = bq[slot][f][s];
+                const half8_t b =
+                    q4_frag(w, __builtin_bit_cast(_Float16, (unsigned short)bd[slot][f]));
 #pragma unroll
-                for (int ns = 0; ns < 2; ns++) {
-                    const int rb = m * GM_BN + wave * 32 + ns * 16 + li;
-                    const uint32_t w =
-                        *reinterpret_cast<const uint32_t *>(&Bq[buf][rb * GM_BST + s * 16 + lg * 4]);
-                    const half8_t b = q4_frag(w, Bd[buf][rb * GM_KB + s]);
-#pragma unroll
-                    for (int ms = 0; ms < 4; ms++)
-                        acc[m][ms][ns] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                            a[ms], b, acc[m][ms][ns], 0, 0, 0);
-                }
+                for (int ms = 0; ms < 4; ms++)
+                    acc[f / 2][ms][f % 2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        a[ms], b, acc[f / 2][ms][f % 2], 0, 0, 0);
+            }
         }
-        if (c + 1 < nc) GM_STORE(buf ^ 1);
+        if (c + 1 < ce) GM_STORE_A(buf ^ 1);
         __syncthreads();
+    };
+    for (int c = c0; c < ce; c += UNR) {
+#pragma unroll
+        for (int i = 0; i < UNR; i++)
+            if (c + i < ce) chunk(c + i, i & 1, i % NB);
     }
-#undef GM_LOAD
-#undef GM_STORE
+#undef GM_LOAD_A
+#undef GM_LOAD_B
+#undef GM_STORE_A
 
     // epilogue
 #pragma unroll
@@ -243,19 +285,19 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
                 if (MODE == 0) {
                     const float g = acc[0][ms][ns][v], u = acc[1][ms][ns][v];
                     const float h = g / (1.0f + (float)exp(-(double)g)) * u;  // moe_forward.go:130
-                    const int slot = (n & ~7) | ((n & 3) << 1) | ((n >> 2) & 1);
-                    H[r * N + slot] = (_Float16)h;
+                    H[r * N + k_order(n)] = (_Float16)h;
                 } else {
-                    Y[r * N + n] = acc[0][ms][ns][v];
+                    Y[ks * ystride + r * N + n] = acc[0][ms][ns][v];
                 }
             }
         }
 }
 
-// out[t][d] = sum_s w[t][s] * Y[pair_row[t*k+s]][d], summed from 0 in slot order.
+// out[t][d] = sum_s w[t][s] * Y[pair_row[t*k+s]][d], summed from 0 in slot order;
+// Y of a pair is the sum of its ksplit K-slice partials, in slice order.
 __global__ void k_moe_combine(const float *__restrict__ Y, const int32_t *__restrict__ pair_row,
                               const float *__restrict__ w, int k, int n_tok, int hidden,
-                              float *__restrict__ out) {
+                              int ksplit, long long ystride, float *__restrict__ out) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;  // float4 index
     const long long n4 = (long long)n_tok * hidden / 4;
     if (i >= n4) return;
@@ -264,7 +306,15 @@ __global__ void k_moe_combine(const float *__restrict__ Y, const int32_t *__rest
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s = 0; s < k; s++) {
         const float ws = w[t * k + s];
-        const float4 y = reinterpret_cast<const float4 *>(Y + (long long)pair_row[t * k + s] * hidden)[d4];
+        const float *yr = Y + (long long)pair_row[t * k + s] * hidden;
+        float4 y = reinterpret_cast<const float4 *>(yr)[d4];
+        for (int q = 1; q < ksplit; q++) {
+            const float4 p = reinterpret_cast<const float4 *>(yr + q * ystride)[d4];
+            y.x += p.x;
+            y.y += p.y;
+            y.z += p.z;
+            y.w += p.w;
+        }
         acc.x += ws * y.x;
         acc.y += ws * y.y;
         acc.z += ws * y.z;
@@ -273,13 +323,20 @@ __global__ void k_moe_combine(const float *__restrict__ Y, const int32_t *__rest
     reinterpret_cast<float4 *>(out)[i] = acc;
 }
 
+// K slices of the down GEMM: 4 (or 2) when the chunks divide evenly, so that
+// the launch has enough independent workgroups to keep loads in flight.
+static int down_split(int eff) {
+    const int nc = eff / GM_KC;
+    return nc % 4 == 0 ? 4 : nc % 2 == 0 ? 2 : 1;
+}
+
 // ---------------------------------------------------------------------------
 size_t llg_moe_gemm_ws_bytes(int n_tok, int k, int n_exp, int hidden, int eff) {
     const long long np = (long long)n_tok * k;
     const long long nt = np / GM_BM + n_exp + 1;
     return (size_t)(llg_align(np * 4, 256) * 2 + llg_align(nt * 16, 256) + 256 +
                     llg_align((long long)n_tok * hidden * 2, 256) +
-                    llg_align(np * eff * 2, 256) + llg_align(np * hidden * 4, 256));
+                    llg_align(np * eff * 2, 256) + down_split(eff) * llg_align(np * hidden * 4, 256));
 }
 
 bool llg_moe_gemm_supported(int type, int hidden, int eff, int n_tok) {
@@ -316,13 +373,16 @@ int llg_moe_gemm_enqueue(LlgDevice *d, const LlgObject *gate, const LlgObject *u
                        x16);
     hipLaunchKernelGGL((k_moe_gemm<0>), dim3((unsigned)(nt_max * (eff / GM_BN))), dim3(256), 0, st,
                        tiles, n_tiles, row_pair, k, x16, gate->d, up->d, gate->stride,
-                       gate->fmt.d_off, eff, hidden, eff, H, (float *)nullptr);
-    hipLaunchKernelGGL((k_moe_gemm<1>), dim3((unsigned)(nt_max * (hidden / GM_BN))), dim3(256), 0,
-                       st, tiles, n_tiles, row_pair, k, H, down->d, (const uint8_t *)nullptr,
-                       down->stride, down->fmt.d_off, hidden, eff, hidden, (_Float16 *)nullptr, Y);
+                       gate->fmt.d_off, eff, hidden, eff, H, (float *)nullptr, 1, 0ll);
+    const int ksplit = down_split(eff);
+    const long long ystride = llg_align(np * hidden * 4, 256) / 4;
+    hipLaunchKernelGGL((k_moe_gemm<1>), dim3((unsigned)(nt_max * (hidden / GM_BN) * ksplit)),
+                       dim3(256), 0, st, tiles, n_tiles, row_pair, k, H, down->d,
+                       (const uint8_t *)nullptr, down->stride, down->fmt.d_off, hidden, eff,
+                       hidden, (_Float16 *)nullptr, Y, ksplit, ystride);
     const long long n4 = (long long)n_tok * hidden / 4;
     hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, Y,
-                       pair_row, w, k, n_tok, hidden, d_out);
+                       pair_row, w, k, n_tok, hidden, ksplit, ystride, d_out);
     LLG_LAUNCH_CHECK(d, "moe grouped gemm");
     return 0;
 }
