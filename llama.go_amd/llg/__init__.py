@@ -555,3 +555,6 @@ def _as_host_f32(a) -> np.ndarray:
     if hasattr(a, "is_cuda"):
         a = a.detach().float().cpu().numpy()
     return _f32(a)
+
+
+from .flash import FlashFFN, FlashFFNConfig, FlashLayer, PredictorSet  # noqa: E402,F401
