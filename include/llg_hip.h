@@ -98,6 +98,10 @@ int llg_hip_upload_bundle(LlgHipDevice dev, const void *up_raw, const void *down
                           int ggml_type, int h, int ff, int64_t *bundle);
 int llg_hipd_upload_bundle(LlgHipDevice dev, const void *d_up_raw, const void *d_down_t_raw,
                            int ggml_type, int h, int ff, int64_t *bundle);
+/* Retires a handle (LLG_E_HANDLE if unknown or already retired).  An object
+ * that a window or model still reads (a window's bundle, a model's weights)
+ * stays in device memory until the last of those is released; any other
+ * object is freed now.  llg_hip_free frees everything. */
 int llg_hip_release(LlgHipDevice dev, int64_t handle);
 /* Per-neuron byte stride of a bundle and per-row stride of a matrix in HBM. */
 int llg_hip_object_info(LlgHipDevice dev, int64_t handle, int *ggml_type, int *rows,

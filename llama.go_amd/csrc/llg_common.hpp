@@ -701,15 +701,20 @@ __device__ __forceinline__ void llg_stage_ln(float *xs, const LlgLnArgs &a, floa
 
 enum LlgKind { LLG_KIND_MATRIX = 1, LLG_KIND_BUNDLE = 2, LLG_KIND_WINDOW = 3, LLG_KIND_MODEL = 4 };
 
+// Objects are value-initialized (new LlgObject()).  A window or model holds
+// the objects it reads (llg_ref); releasing a held object only retires its
+// handle, and its memory goes when the last holder does (llg_unref).
 struct LlgObject {
     int kind;
-    int id_self;
+    int64_t id_self;
     uint8_t *d;          // device bytes
     size_t bytes;
     RowFmt fmt;          // row format (matrix rows, or each half of a bundle)
     int rows;            // matrix rows, or bundle neurons (ff)
     long long stride;    // matrix: bytes per row; bundle: bytes per neuron (2 * fmt.stride)
-    void *ext;           // kind-specific state (window)
+    void *ext;           // kind-specific state (window, model)
+    int refs;            // windows / models holding this object
+    bool released;       // handle retired; freed when refs reaches 0
 };
 
 struct LlgDevice;
@@ -719,8 +724,10 @@ LlgDevice *llg_dev(LlgHipDevice h);
 hipStream_t llg_dev_stream(LlgDevice *d);
 int llg_set_error(LlgDevice *d, int code, const char *fmt, ...);
 int llg_hip_error(LlgDevice *d, hipError_t e, const char *what);
-LlgObject *llg_get(LlgDevice *d, int64_t h, int kind);
+LlgObject *llg_get(LlgDevice *d, int64_t h, int kind);  // live handles only
 int64_t llg_register(LlgDevice *d, LlgObject *o);
+void llg_ref(LlgObject *o);
+void llg_unref(LlgDevice *d, LlgObject *o);
 // Device workspace of at least `bytes`, valid until the next llg_ws call that
 // grows it (growth synchronises the device before freeing the old buffer).
 void *llg_ws(LlgDevice *d, size_t bytes, int *rc);

@@ -50,9 +50,22 @@ struct LlgModel {
     uint8_t *ws;
 };
 
+// The objects a model reads, each once per use (llg_ref / llg_unref pairs).
+template <class F>
+static void model_objects(LlgModel *m, F &&f) {
+    f(m->embed);
+    f(m->lm_head);
+    f(m->out_w);
+    f(m->out_b);
+    for (LlgModelLayer &L : m->layers)
+        for (LlgObject *o : {L.norm_w, L.norm_b, L.wqkv, L.wo, L.pwup, L.pwout, L.bundle}) f(o);
+}
+
 void llg_model_destroy(LlgDevice *d, LlgObject *o) {
-    (void)d;
-    delete reinterpret_cast<LlgModel *>(o->ext);
+    LlgModel *m = reinterpret_cast<LlgModel *>(o->ext);
+    if (!m) return;
+    model_objects(m, [&](LlgObject *x) { llg_unref(d, x); });
+    delete m;
     o->ext = nullptr;
 }
 
@@ -503,12 +516,20 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     p += v_rope;
     m->ws = p;
     hipStream_t st = llg_dev_stream(d);
-    LLG_HIP_TRY(d, hipMemsetAsync(buf, 0, total, st));
+    hipError_t e = hipMemsetAsync(buf, 0, total, st);
     const int n_rope = m->max_seq * (m->head_dim / 2);
-    hipLaunchKernelGGL(k_rope_table, dim3((n_rope + 255) / 256), dim3(256), 0, st, m->rope,
-                       m->max_seq, m->head_dim / 2, m->rope_base);
-    LLG_HIP_TRY(d, hipGetLastError());
-    LLG_HIP_TRY(d, hipStreamSynchronize(st));
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(k_rope_table, dim3((n_rope + 255) / 256), dim3(256), 0, st, m->rope,
+                           m->max_seq, m->head_dim / 2, m->rope_base);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        hipFree(buf);
+        delete m;
+        return llg_hip_error(d, e, "falcon_create");
+    }
+    model_objects(m, [](LlgObject *x) { llg_ref(x); });
     LlgObject *o = new LlgObject();
     o->kind = LLG_KIND_MODEL;
     o->d = buf;

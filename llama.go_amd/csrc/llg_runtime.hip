@@ -19,6 +19,7 @@ struct LlgDevice {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     std::string last_error;
+    bool tearing_down = false;  // llg_hip_free: every object is freed in one sweep
 };
 
 LlgDevice *llg_dev(LlgHipDevice h) { return reinterpret_cast<LlgDevice *>(h); }
@@ -44,16 +45,41 @@ int llg_hip_error(LlgDevice *d, hipError_t e, const char *what) {
 
 LlgObject *llg_get(LlgDevice *d, int64_t h, int kind) {
     auto it = d->objects.find(h);
-    if (it == d->objects.end()) return nullptr;
+    if (it == d->objects.end() || it->second->released) return nullptr;
     if (kind && it->second->kind != kind) return nullptr;
     return it->second;
 }
 
 int64_t llg_register(LlgDevice *d, LlgObject *o) {
     int64_t id = d->next_id++;
-    o->id_self = (int)id;
+    o->id_self = id;
     d->objects[id] = o;
     return id;
+}
+
+extern void llg_window_destroy(LlgDevice *d, LlgObject *o);
+extern void llg_model_destroy(LlgDevice *d, LlgObject *o);
+
+// Frees an object's state and memory (the caller has taken it out of the
+// registry, or is sweeping the registry).
+static void destroy_object(LlgDevice *d, LlgObject *o) {
+    if (o->kind == LLG_KIND_WINDOW) llg_window_destroy(d, o);
+    if (o->kind == LLG_KIND_MODEL) llg_model_destroy(d, o);
+    if (o->d) hipFree(o->d);
+    delete o;
+}
+
+void llg_ref(LlgObject *o) {
+    if (o) o->refs++;
+}
+
+void llg_unref(LlgDevice *d, LlgObject *o) {
+    // during llg_hip_free the sweep frees every object (o may already be gone)
+    if (!o || d->tearing_down) return;
+    if (--o->refs == 0 && o->released) {
+        d->objects.erase(o->id_self);
+        destroy_object(d, o);
+    }
 }
 
 void *llg_ws(LlgDevice *d, size_t bytes, int *rc) {
@@ -155,7 +181,10 @@ static int upload_rows(LlgDevice *d, const void *const *srcs, int nsrc, int from
     uint8_t *dmem = nullptr;
     if (hipMalloc(&dmem, bytes) != hipSuccess)
         return llg_set_error(d, LLG_E_NOMEM, "upload: hipMalloc(%zu) failed", bytes);
-    LLG_HIP_TRY(d, hipMemsetAsync(dmem, 0, bytes, d->stream));
+    if (hipError_t e = hipMemsetAsync(dmem, 0, bytes, d->stream); e != hipSuccess) {
+        hipFree(dmem);
+        return llg_hip_error(d, e, "upload memset");
+    }
     uint8_t *tmp = nullptr;
     const size_t src_bytes = (size_t)row_bytes * rows;
     if (!from_device) {
@@ -198,9 +227,6 @@ static int upload_rows(LlgDevice *d, const void *const *srcs, int nsrc, int from
     return 0;
 }
 
-extern void llg_window_destroy(LlgDevice *d, LlgObject *o);
-extern void llg_model_destroy(LlgDevice *d, LlgObject *o);
-
 extern "C" {
 
 int llg_hip_available(void) {
@@ -228,13 +254,9 @@ void llg_hip_free(LlgHipDevice h) {
     LlgDevice *d = llg_dev(h);
     if (!d) return;
     hipStreamSynchronize(d->stream);
-    for (auto &kv : d->objects) {
-        LlgObject *o = kv.second;
-        if (o->kind == LLG_KIND_WINDOW) llg_window_destroy(d, o);
-        if (o->kind == LLG_KIND_MODEL) llg_model_destroy(d, o);
-        if (o->d) hipFree(o->d);
-        delete o;
-    }
+    d->tearing_down = true;  // holders' unrefs free nothing: the sweep frees all
+    for (auto &kv : d->objects) destroy_object(d, kv.second);
+    d->objects.clear();
     if (d->ws) hipFree(d->ws);
     hipStreamDestroy(d->stream);
     delete d;
@@ -295,11 +317,12 @@ int llg_hip_release(LlgHipDevice h, int64_t handle) {
     LlgObject *o = llg_get(d, handle, 0);
     if (!o) return llg_set_error(d, LLG_E_HANDLE, "release: unknown handle %lld", (long long)handle);
     hipStreamSynchronize(d->stream);
-    if (o->kind == LLG_KIND_WINDOW) llg_window_destroy(d, o);
-    if (o->kind == LLG_KIND_MODEL) llg_model_destroy(d, o);
-    if (o->d) hipFree(o->d);
+    if (o->refs > 0) {  // a window or model still reads it: retire the handle only
+        o->released = true;
+        return 0;
+    }
     d->objects.erase(handle);
-    delete o;
+    destroy_object(d, o);
     return 0;
 }
 

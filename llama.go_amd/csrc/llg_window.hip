@@ -48,11 +48,11 @@ struct LlgWindow {
 };
 
 void llg_window_destroy(LlgDevice *d, LlgObject *o) {
-    (void)d;
     LlgWindow *w = reinterpret_cast<LlgWindow *>(o->ext);
     if (!w) return;
     hipFree(w->slot_of);
     hipFree(w->resident);
+    llg_unref(d, w->bundle);
     delete w;
     o->ext = nullptr;
 }
@@ -279,9 +279,16 @@ int llg_hip_window_create(LlgHipDevice h, int64_t hb, int k, int64_t *win) {
         return llg_set_error(d, LLG_E_NOMEM, "window_create: resident buffer allocation failed");
     }
     hipStream_t st = llg_dev_stream(d);
-    LLG_HIP_TRY(d, hipMemsetAsync(m, 0, n_ints * 4, st));
-    LLG_HIP_TRY(d, hipMemsetAsync(w->slot_of, 0xFF, ff * 4, st));  // -1: nothing resident
-    LLG_HIP_TRY(d, hipStreamSynchronize(st));
+    hipError_t e = hipMemsetAsync(m, 0, n_ints * 4, st);
+    if (e == hipSuccess) e = hipMemsetAsync(w->slot_of, 0xFF, ff * 4, st);  // -1: nothing resident
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        hipFree(m);
+        hipFree(w->resident);
+        delete w;
+        return llg_hip_error(d, e, "window_create");
+    }
+    llg_ref(b);  // the window reads the bundle until it is destroyed
     LlgObject *o = new LlgObject();
     o->kind = LLG_KIND_WINDOW;
     o->d = nullptr;

@@ -361,6 +361,29 @@ def test_window_step_device_config2(dev, rng):
     _window_steps_vs_oracle(dev, rng, gg.Q4_0, 4544, 18176, 5, 909, 64, 0.7, 8)
 
 
+def test_released_bundle_stays_alive_for_its_window(dev, rng):
+    """Releasing a bundle that a window reads retires the handle only; the
+    window keeps working on it, and destroying the window frees it."""
+    h, ff, k = 64, 96, 2
+    up, dn = make_sparse_layer(rng, h, ff, gg.Q4_0)
+    b = dev.upload_bundle(up, dn, gg.Q4_0, h, ff)
+    nc = llg.NeuronCache(dev, b, k)
+    ref = R.NeuronCache(256, h, k, ff, up, dn, gg.Q4_0)
+    bid = b.id
+    b.release()
+    with pytest.raises(llg.LlgError) as e:  # a retired handle is unknown
+        dev.check(dev.lib.llg_hip_release(dev.h, bid), "release")
+    assert e.value.code == llg.LLG_E_HANDLE
+    with pytest.raises(llg.LlgError) as e:
+        llg.NeuronCache(dev, llg.Handle(dev, bid, "bundle"), k)
+    assert e.value.code == llg.LLG_E_HANDLE
+    for A in window_sets(rng, ff, 16, 8, 0.5):
+        assert nc.update(A) == ref.update(A).size
+        x = normal(rng, h, 1.0)
+        assert max_rel_err(nc.ffn_forward(x, A), ref.ffn_forward(x, A)) <= TOL
+    nc.win.release()
+
+
 def test_window_rejects_duplicates(dev, rng):
     up, dn = make_sparse_layer(rng, 32, 32, gg.Q4_0)
     b = dev.upload_bundle(up, dn, gg.Q4_0, 32, 32)
@@ -560,6 +583,25 @@ def test_falcon_forward(dev, rng, n_kv):
     with pytest.raises(llg.LlgError) as e:
         m.forward(d["vocab"], 0)
     assert e.value.code == llg.LLG_E_RANGE
+    m.release()
+
+
+def test_released_weights_stay_alive_for_their_model(dev, rng):
+    """Every weight handle released before the model: the model still reads
+    them (the handles are retired, the memory is kept until the model goes)."""
+    d = dict(FALCON_GPU)
+    w = make_falcon(rng, d)
+    toks = rng.integers(0, d["vocab"], 4)
+    _, _, thr = ref_falcon_f64(w, d, toks)
+    ref = R.Falcon(d, w, thr)
+    m = llg.FalconModel(dev, d, w, thr)
+    for hnd in m._h:
+        hnd.release()
+    m._h = []
+    for s, tk in enumerate(toks):
+        lg, _, _ = m.forward(int(tk), s)
+        rl, _ = ref.forward(int(tk), s)
+        assert max_rel_err(lg, rl) <= TOL, s
     m.release()
 
 
