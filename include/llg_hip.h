@@ -48,6 +48,8 @@ enum {
     LLG_TYPE_Q8_0 = 8,
 };
 
+/* model.ActivationType (model.go:97-103).  Every `act` argument takes one of
+ * these; any other value is LLG_E_ARG. */
 enum { LLG_ACT_RELU = 0, LLG_ACT_GELU = 1, LLG_ACT_SILU = 2 };
 
 enum {

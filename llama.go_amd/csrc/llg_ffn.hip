@@ -194,6 +194,7 @@ int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int a
 // launch clears `out` when the down matvec accumulates over column chunks.
 static int dense_enqueue(LlgDevice *d, const LlgObject *up, const LlgObject *down,
                          const float *d_x, int act, float *hid, float *d_out) {
+    if (int rc = llg_check_act(d, act)) return rc;
     const int down_chunks = (down->fmt.nb + mv_chunk_blocks(down->fmt, -1) - 1) /
                             mv_chunk_blocks(down->fmt, -1);
     int rc = matvec_launch(d, up, d_x, act, hid, down_chunks > 1 ? d_out : nullptr,
@@ -255,6 +256,7 @@ int llg_hip_ffn_sparse(LlgHipDevice h, int64_t hb, const float *x, const int32_t
     if (rc) return rc;
     if (!x || !out || n_active < 0 || (n_active > 0 && !active))
         return llg_set_error(d, LLG_E_ARG, "ffn_sparse: bad arguments");
+    if ((rc = llg_check_act(d, act))) return rc;
     const int hd = b->fmt.cols, ff = b->rows;
     for (int j = 0; j < n_active; j++)  // storage.go:292-294
         if (active[j] < 0 || active[j] >= ff)

@@ -27,6 +27,15 @@ int llg_compact_enqueue(LlgDevice *d, const unsigned long long *mask, int n_tile
 // Sparse FFN over bundles (llg_sparse.hip).  Neuron n's bundle is at
 // base + (slot_of ? slot_of[n] : n) * bstride.  max_active bounds *d_n_active.
 size_t llg_sparse_ws_bytes(int max_active);
+// The activations of model.ActivationType (model.go:97-103) an entry point
+// accepts; anything else is an argument error.
+inline bool llg_act_ok(int act) {
+    return act == LLG_ACT_RELU || act == LLG_ACT_GELU || act == LLG_ACT_SILU;
+}
+inline int llg_check_act(LlgDevice *d, int act) {
+    return llg_act_ok(act) ? 0 : llg_set_error(d, LLG_E_ARG, "activation %d is not ReLU, GELU or SiLU", act);
+}
+
 // Windowed rows loaded by the current update: a listed neuron n with
 // fresh[n] == epoch is read from row n of src, and its whole bundle is copied
 // into its resident row slot_of[n] of dst (the writable base) on the way.

@@ -441,6 +441,7 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
         m->n_heads % m->n_kv || m->vocab < 1 || m->max_seq < 1 || m->ff < 1)
         return fail(LLG_E_HPARAM, "invalid dimensions");
     if (m->head_dim != 64 && m->head_dim != 128) return fail(LLG_E_HPARAM, "head_dim must be 64 or 128");
+    if (!llg_act_ok(m->act)) return fail(LLG_E_ARG, "activation must be ReLU, GELU or SiLU");
     if (m->hidden > NORM_THREADS * NORM_PER) return fail(LLG_E_HPARAM, "hidden above 16384");
     if ((size_t)m->max_seq * 4 > 64 * 1024) return fail(LLG_E_HPARAM, "max_seq above 16384");
     const int qkv_rows = (m->n_heads + 2 * m->n_kv) * m->head_dim;

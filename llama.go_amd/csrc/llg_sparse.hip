@@ -504,6 +504,7 @@ int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, con
                        const int32_t *slot_of, const float *d_x, const int32_t *d_active,
                        const int32_t *d_n_active, int max_active, int act, float *d_out,
                        uint8_t *ws, const LlgFreshRows *fresh) {
+    if (int rc = llg_check_act(d, act)) return rc;
     const LlgFreshRows fr = fresh ? *fresh : LlgFreshRows{nullptr, nullptr, 0, nullptr};
     if (fr.src && (!slot_of || !fr.fresh || !fr.dst || (bstride & 15)))
         return llg_set_error(d, LLG_E_ARG, "sparse ffn: windowed rows need slots and tags");
@@ -566,6 +567,7 @@ static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial, 
 int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
                       LlgObject *b, const float *d_a, const float *d_x, float thr, int act,
                       float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws) {
+    if (int rc = llg_check_act(d, act)) return rc;
     const RowFmt &f = b->fmt;
     const int ff = wout->rows, rank = wup->rows;
     const int n_tiles = (ff + 63) / 64;

@@ -344,6 +344,7 @@ int llg_hip_window_ffn(LlgHipDevice h, int64_t hw, const float *x, const int32_t
     const int hd = w->bundle->fmt.cols;
     if (!x || !out || n_active < 0 || (n_active > 0 && !active))
         return llg_set_error(d, LLG_E_ARG, "window_ffn: bad arguments");
+    if (int rc = llg_check_act(d, act)) return rc;
     for (int j = 0; j < n_active; j++)
         if (active[j] < 0 || active[j] >= w->ff)
             return llg_set_error(d, LLG_E_RANGE, "row %d out of range [0,%d)", active[j], w->ff);

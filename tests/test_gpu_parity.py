@@ -384,6 +384,29 @@ def test_released_bundle_stays_alive_for_its_window(dev, rng):
     nc.win.release()
 
 
+@pytest.mark.parametrize("act", [-1, 3])
+def test_bad_activation_rejected(dev, rng, act):
+    h, ff = 64, 64
+    up, dn = make_sparse_layer(rng, h, ff, gg.Q4_0)
+    b = dev.upload_bundle(up, dn, gg.Q4_0, h, ff)
+    m_up = dev.upload_matrix(up, gg.Q4_0, ff, h)
+    m_dn = dev.upload_matrix(quant(normal(rng, (h, ff), 0.02), gg.Q4_0), gg.Q4_0, h, ff)
+    x = normal(rng, h, 1.0)
+    for call in (lambda: llg.ffn_sparse_load(dev, b, x, np.array([1, 2], np.int32), act),
+                 lambda: llg.ffn_sparse_load(dev, b, x, np.array([], np.int32), act),
+                 lambda: llg.ffn_dense(dev, m_up, m_dn, x, act)):
+        with pytest.raises(llg.LlgError) as e:
+            call()
+        assert e.value.code == llg.LLG_E_ARG
+    nc = llg.NeuronCache(dev, b, 2)
+    nc.update(np.array([1, 2], np.int32))
+    with pytest.raises(llg.LlgError) as e:
+        nc.ffn_forward(x, np.array([1, 2], np.int32), act)
+    assert e.value.code == llg.LLG_E_ARG
+    for hnd in (nc.win, m_up, m_dn, b):
+        hnd.release()
+
+
 def test_window_rejects_duplicates(dev, rng):
     up, dn = make_sparse_layer(rng, 32, 32, gg.Q4_0)
     b = dev.upload_bundle(up, dn, gg.Q4_0, 32, 32)
