@@ -209,8 +209,12 @@ int llg_hip_falcon_forward(LlgHipDevice dev, int64_t model, int32_t token, int p
 int llg_hipd_predict(LlgHipDevice dev, int64_t wup, int64_t wout, int64_t bias,
                      const float *d_a, float threshold, int32_t *d_active,
                      int32_t *d_n_active, float *d_logits);
-/* n_active is read on the device from d_n_active; indices are not range-checked
- * on this path (they come from llg_hipd_predict or a checked caller). */
+/* n_active is read on the device from d_n_active; d_active must hold that
+ * many entries.  Indices are not checked on the host on this path (they come
+ * from llg_hipd_predict or a checked caller); the kernels clamp the count to
+ * ff and treat an index outside [0, ff) as an inactive neuron, so such a list
+ * gives meaningless results but no out-of-bounds access.  The same holds for
+ * llg_hipd_window_step, whose window state such a list leaves meaningless. */
 int llg_hipd_ffn_sparse(LlgHipDevice dev, int64_t bundle, const float *d_x,
                         const int32_t *d_active, const int32_t *d_n_active, int act,
                         float *d_out);

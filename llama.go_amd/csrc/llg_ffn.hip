@@ -244,7 +244,7 @@ int llg_hipd_ffn_sparse(LlgHipDevice h, int64_t hb, const float *d_x, const int3
     uint8_t *ws = (uint8_t *)llg_ws(d, llg_sparse_ws_bytes(b->rows), &rc);
     if (rc) return rc;
     return llg_sparse_enqueue(d, b->d, b->stride, b->fmt, nullptr, d_x, d_active, d_n_active,
-                              b->rows, act, d_out, ws);
+                              b->rows, b->rows, act, d_out, ws);
 }
 
 int llg_hip_ffn_sparse(LlgHipDevice h, int64_t hb, const float *x, const int32_t *active,
@@ -278,7 +278,7 @@ int llg_hip_ffn_sparse(LlgHipDevice h, int64_t hb, const float *x, const int32_t
     if ((rc = llg_h2d(d, ws + o_n, &n32, 4))) return rc;
     rc = llg_sparse_enqueue(d, b->d, b->stride, b->fmt, nullptr, (const float *)(ws + o_x),
                             (const int32_t *)(ws + o_act), (const int32_t *)(ws + o_n), n_active,
-                            act, (float *)(ws + o_out), ws + o_ws);
+                            b->rows, act, (float *)(ws + o_out), ws + o_ws);
     if (rc) return rc;
     if ((rc = llg_d2h(d, out, ws + o_out, (size_t)hd * 4))) return rc;
     return llg_sync_dev(d);

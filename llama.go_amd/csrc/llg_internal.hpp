@@ -45,10 +45,13 @@ struct LlgFreshRows {
     int epoch;
     uint8_t *dst;
 };
+// max_active: capacity of the list and of the pair workspace (the count read
+// on the device is clamped to it); n_rows: the neurons of the bundle or window
+// (an index outside [0, n_rows) counts as absent).
 int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, const RowFmt &f,
                        const int32_t *slot_of, const float *d_x, const int32_t *d_active,
-                       const int32_t *d_n_active, int max_active, int act, float *d_out,
-                       uint8_t *ws, const LlgFreshRows *fresh = nullptr);
+                       const int32_t *d_n_active, int max_active, int n_rows, int act,
+                       float *d_out, uint8_t *ws, const LlgFreshRows *fresh = nullptr);
 
 // Dense quantized matvec y[rows] = act(W . x) (llg_ffn.hip); act < 0 = none.
 int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y);

@@ -218,17 +218,17 @@ __device__ __forceinline__ void tile_up_round(const uint8_t *__restrict__ base, 
 // done by the first reader).
 // (base and dst are the same buffer then: base is not __restrict__.)  FR
 // selects that form (fr.src set), which holds the copies in registers.
+// The count read on the device is clamped to the pair capacity `cap`, and a
+// neuron outside [0, n_rows) counts as absent (activation 0), so no list
+// makes the kernel read or write out of bounds.
 template <int T, bool FR>
 __global__ __launch_bounds__(256) void k_list_up(
-    const uint8_t *base, long long bstride, RowFmt f,
-                                                 const int32_t *__restrict__ slot_of,
-                                                 const float *__restrict__ x,
-                                                 const int32_t *__restrict__ active,
-                                                 const int32_t *__restrict__ n_active_p, int act,
-                                                 int2 *__restrict__ pairs,
-                                                 float *__restrict__ out, LlgFreshRows fr) {
+    const uint8_t *base, long long bstride, RowFmt f, const int32_t *__restrict__ slot_of,
+    const float *__restrict__ x, const int32_t *__restrict__ active,
+    const int32_t *__restrict__ n_active_p, int cap, int n_rows, int act,
+    int2 *__restrict__ pairs, float *__restrict__ out, LlgFreshRows fr) {
     extern __shared__ float xs[];
-    const int n_active = *n_active_p;
+    const int n_active = min(max(*n_active_p, 0), cap);
     const int gtid = blockIdx.x * blockDim.x + threadIdx.x;
     for (int i = gtid; i < f.cols; i += gridDim.x * blockDim.x) out[i] = 0.0f;
     const int first = blockIdx.x * 4;
@@ -239,9 +239,13 @@ __global__ __launch_bounds__(256) void k_list_up(
     const int stride = gridDim.x * 4;
     for (int j = first + (threadIdx.x >> 6); j < n_active; j += 2 * stride) {
         const int j1 = j + stride;
-        const int n0 = active[j];
-        const int n1 = j1 < n_active ? active[j1] : -1;
-        const int row0 = slot_of ? slot_of[n0] : n0;
+        auto neuron = [&](int jj) {
+            const int n = active[jj];
+            return n >= 0 && n < n_rows ? n : -1;
+        };
+        const int n0 = neuron(j);
+        const int n1 = j1 < n_active ? neuron(j1) : -1;
+        const int row0 = n0 < 0 ? -1 : (slot_of ? slot_of[n0] : n0);
         const int row1 = n1 < 0 ? -1 : (slot_of ? slot_of[n1] : n1);
         float s0, s1;
         if constexpr (FR) {
@@ -340,7 +344,8 @@ __global__ __launch_bounds__(TILE_THREADS, 2) void k_tile_up(
     if (threadIdx.x == 0) tile_cnt[blockIdx.x] = tl[65];
 }
 
-// Pairs come either as a plain list pairs[0..*count) (TILED = false) or in
+// Pairs come either as a plain list pairs[0..*count) (TILED = false; the
+// count is clamped to the capacity n_tiles) or in
 // per-tile slots pairs[t*64 + k], k < tile_cnt[t] (TILED = true); for the
 // latter, group g owns tiles [g*tg, (g+1)*tg) and its workgroups enumerate
 // them through a prefix sum of the counts.  With TILED, workgroup 0 also
@@ -390,7 +395,7 @@ __global__ __launch_bounds__(256) void k_sparse_down(
         j0 = 0;
         j1 = pref[64];
     } else {
-        const int count = *count_p;
+        const int count = min(max(*count_p, 0), n_tiles);
         const int chunk = (count + n_groups - 1) / n_groups;
         j0 = g * chunk;
         j1 = min(count, j0 + chunk);
@@ -478,7 +483,7 @@ static void launch_down(hipStream_t st, const uint8_t *base, long long bstride, 
     const int n_slices = (f.nb + DN_SLICE - 1) / DN_SLICE;
     const int n_groups = down_groups(max_pairs);
     hipLaunchKernelGGL((k_sparse_down<T, false>), dim3(n_slices * n_groups), dim3(256), 0, st,
-                       base, bstride, f, pairs, count, (const int32_t *)nullptr, 0,
+                       base, bstride, f, pairs, count, (const int32_t *)nullptr, max_pairs,
                        (const unsigned long long *)nullptr, (int32_t *)nullptr, n_slices,
                        n_groups, out);
 }
@@ -486,24 +491,26 @@ static void launch_down(hipStream_t st, const uint8_t *base, long long bstride, 
 template <int T>
 static void launch_list(hipStream_t st, const uint8_t *base, long long bstride, const RowFmt &f,
                         const int32_t *slot_of, const float *x, const int32_t *active,
-                        const int32_t *n_active, int max_active, int act, float *out,
-                        int2 *pairs, const LlgFreshRows &fr) {
+                        const int32_t *n_active, int max_active, int n_rows, int act,
+                        float *out, int2 *pairs, const LlgFreshRows &fr) {
     int grid = (max_active + 3) / 4;
     if (grid < 1) grid = 1;
     if (grid > 2048) grid = 2048;
     if (fr.src)
         hipLaunchKernelGGL((k_list_up<T, true>), dim3(grid), dim3(256), xs_bytes(f), st, base,
-                           bstride, f, slot_of, x, active, n_active, act, pairs, out, fr);
+                           bstride, f, slot_of, x, active, n_active, max_active, n_rows, act,
+                           pairs, out, fr);
     else
         hipLaunchKernelGGL((k_list_up<T, false>), dim3(grid), dim3(256), xs_bytes(f), st, base,
-                           bstride, f, slot_of, x, active, n_active, act, pairs, out, fr);
+                           bstride, f, slot_of, x, active, n_active, max_active, n_rows, act,
+                           pairs, out, fr);
     launch_down<T>(st, base, bstride, f, pairs, n_active, max_active, out);
 }
 
 int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, const RowFmt &f,
                        const int32_t *slot_of, const float *d_x, const int32_t *d_active,
-                       const int32_t *d_n_active, int max_active, int act, float *d_out,
-                       uint8_t *ws, const LlgFreshRows *fresh) {
+                       const int32_t *d_n_active, int max_active, int n_rows, int act,
+                       float *d_out, uint8_t *ws, const LlgFreshRows *fresh) {
     if (int rc = llg_check_act(d, act)) return rc;
     const LlgFreshRows fr = fresh ? *fresh : LlgFreshRows{nullptr, nullptr, 0, nullptr};
     if (fr.src && (!slot_of || !fr.fresh || !fr.dst || (bstride & 15)))
@@ -515,19 +522,19 @@ int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, con
     switch (f.type) {
     case LLG_TYPE_Q4_0:
         launch_list<LLG_TYPE_Q4_0>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                   max_active, act, d_out, pairs, fr);
+                                   max_active, n_rows, act, d_out, pairs, fr);
         break;
     case LLG_TYPE_Q8_0:
         launch_list<LLG_TYPE_Q8_0>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                   max_active, act, d_out, pairs, fr);
+                                   max_active, n_rows, act, d_out, pairs, fr);
         break;
     case LLG_TYPE_F16:
         launch_list<LLG_TYPE_F16>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                  max_active, act, d_out, pairs, fr);
+                                  max_active, n_rows, act, d_out, pairs, fr);
         break;
     case LLG_TYPE_F32:
         launch_list<LLG_TYPE_F32>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                  max_active, act, d_out, pairs, fr);
+                                  max_active, n_rows, act, d_out, pairs, fr);
         break;
     default:
         return llg_set_error(d, LLG_E_TYPE, "sparse ffn: unsupported type %d", f.type);

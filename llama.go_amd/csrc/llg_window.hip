@@ -64,6 +64,11 @@ void llg_window_destroy(LlgDevice *d, LlgObject *o) {
 // returning decrement of cnt) and kept in registers; the current set is an
 // LDS bitmap (ff bits); this update's evictions go on the global free stack
 // and, up to WIN_EVCAP, into LDS, where the slot assignment reads them.
+// A device list is not checked on the host, so every access stays in bounds
+// whatever it holds: the count is clamped to [0, ff], an index outside
+// [0, ff) is recorded as -1 and skipped, the free stack never grows past ff
+// entries and no slot at or past ff is handed out (such a neuron stays
+// non-resident).  The results of such a list are meaningless, but safe.
 __global__ __launch_bounds__(1024) void k_window_update(
     int32_t *__restrict__ slot_of, int32_t *__restrict__ cnt, int32_t *__restrict__ ring,
     int32_t *__restrict__ ring_len, int32_t *__restrict__ ring_set,
@@ -79,12 +84,14 @@ __global__ __launch_bounds__(1024) void k_window_update(
     const int lane = tid & 63, wave = tid >> 6, nw = bd >> 6;
     const int32_t *old = ring + (size_t)head * ff;
     // round trip 1: sizes and state; the first expiring entry (in bounds whatever old_len is)
-    const int n_act = *n_active_p;
+    const int n_act = min(max(*n_active_p, 0), ff);
     const int old_set = ring_set[head];
     const int old_len0 = ring_len[head];
-    const int n_free0 = state[0], hw = state[1], n_res0 = state[2];
+    const int n_free0 = min(max(state[0], 0), ff), hw = min(max(state[1], 0), ff);
+    const int n_res0 = state[2];
     const int o_pre = old[min(tid, ff - 1)];
-    const int old_len = old_set ? old_len0 : 0;
+    const int old_len = old_set ? min(max(old_len0, 0), ff) : 0;
+    auto nid = [&](int v) { return v >= 0 && v < ff ? v : -1; };  // an index, or -1
     for (int i = tid; i < (ff + 31) / 32; i += bd) curbits[i] = 0;
     if (tid == 0) {
         carry_sh = 0;
@@ -92,9 +99,9 @@ __global__ __launch_bounds__(1024) void k_window_update(
     }
     // round trip 2: first active entry and its slot; first expiring entry's
     // slot and count after the decrement (A, window.go:73-80)
-    const int a0 = tid < n_act ? active[tid] : -1;
+    const int a0 = tid < n_act ? nid(active[tid]) : -1;
     const int sa0 = a0 >= 0 ? slot_of[a0] : 0;
-    const int o0 = tid < old_len ? o_pre : -1;
+    const int o0 = tid < old_len ? nid(o_pre) : -1;
     int so0 = -1, c0 = 1;
     if (o0 >= 0) {
         so0 = slot_of[o0];
@@ -104,8 +111,8 @@ __global__ __launch_bounds__(1024) void k_window_update(
     // B: mark the current set
     if (a0 >= 0) atomicOr(&curbits[a0 >> 5], 1u << (a0 & 31));
     for (int j = tid + bd; j < n_act; j += bd) {
-        const int n = active[j];
-        atomicOr(&curbits[n >> 5], 1u << (n & 31));
+        const int n = nid(active[j]);
+        if (n >= 0) atomicOr(&curbits[n >> 5], 1u << (n & 31));
     }
     __syncthreads();
     // C: an expiring neuron no set holds any more is evicted (window.go:84-95).
@@ -115,13 +122,14 @@ __global__ __launch_bounds__(1024) void k_window_update(
         if (c == 0 && !((curbits[n >> 5] >> (n & 31)) & 1u) && s >= 0) {
             slot_of[n] = -1;
             const int e = atomicAdd(&ev_cnt, 1);
-            free_stack[n_free0 + e] = s;
+            if (n_free0 + e < ff) free_stack[n_free0 + e] = s;
             if (e < WIN_EVCAP) ev_lds[e] = s;
         }
     };
     if (o0 >= 0) evict(o0, so0, c0);
     for (int j = tid + bd; j < old_len; j += bd) {
-        const int n = old[j];
+        const int n = nid(old[j]);
+        if (n < 0) continue;
         const int sn = slot_of[n];
         evict(n, sn, atomicSub(&cnt[n], 1) - 1);
     }
@@ -129,7 +137,7 @@ __global__ __launch_bounds__(1024) void k_window_update(
     // D: toLoad in active order (window.go:98-103) by a block-wide scan; the
     // k-th needed neuron pops the k-th slot from the top of the free stack
     // (this update's evictions, then the older entries), then fresh slots.
-    const int n_ev = ev_cnt;
+    const int n_ev = min(ev_cnt, ff - n_free0);  // evictions kept on the stack
     const int n_free = n_free0 + n_ev;
     for (int j0 = 0; j0 < n_act; j0 += bd) {
         const int j = j0 + tid;
@@ -138,8 +146,8 @@ __global__ __launch_bounds__(1024) void k_window_update(
             n = a0;
             need = (n >= 0 && sa0 < 0) ? 1 : 0;  // evictions never touch current neurons
         } else if (j < n_act) {
-            n = active[j];
-            need = slot_of[n] < 0 ? 1 : 0;
+            n = nid(active[j]);
+            need = (n >= 0 && slot_of[n] < 0) ? 1 : 0;
         }
         int incl = need;
         for (int o = 1; o < 64; o <<= 1) {
@@ -162,9 +170,10 @@ __global__ __launch_bounds__(1024) void k_window_update(
                 sl = free_stack[n_free - 1 - kidx];
             } else {
                 sl = hw + (kidx - n_free);
+                if (sl >= ff) sl = -1;  // no room (only a list with repeats gets here)
             }
             slot_of[n] = sl;
-            fresh[n] = epoch;
+            if (sl >= 0) fresh[n] = epoch;
             load_list[2 * kidx] = n;
             load_list[2 * kidx + 1] = sl;
         }
@@ -174,19 +183,17 @@ __global__ __launch_bounds__(1024) void k_window_update(
     }
     // E: counts of the current set, the ring slot, the head (window.go:113-114)
     int32_t *dst = ring + (size_t)head * ff;
-    if (a0 >= 0) {
-        atomicAdd(&cnt[a0], 1);
-        dst[tid] = a0;
-    }
+    if (tid < n_act) dst[tid] = a0;
+    if (a0 >= 0) atomicAdd(&cnt[a0], 1);
     for (int j = tid + bd; j < n_act; j += bd) {
-        const int n = active[j];
-        atomicAdd(&cnt[n], 1);
+        const int n = nid(active[j]);
+        if (n >= 0) atomicAdd(&cnt[n], 1);
         dst[j] = n;
     }
     if (tid == 0) {
         const int n_load = carry_sh;
         state[0] = n_load < n_free ? n_free - n_load : 0;
-        state[1] = hw + (n_load > n_free ? n_load - n_free : 0);
+        state[1] = min(ff, hw + (n_load > n_free ? n_load - n_free : 0));
         state[2] = n_res0 - n_ev + n_load;
         state[3] = n_load;
         ring_len[head] = n_act;
@@ -206,6 +213,7 @@ __global__ __launch_bounds__(256) void k_window_gather(const uint8_t *__restrict
     for (int i = blockIdx.x; i < n_load; i += gridDim.x) {
         const int n = load_list[2 * i];
         const int s = load_list[2 * i + 1];
+        if (s < 0) continue;  // left non-resident (the update found no slot)
         const uint4 *sp = reinterpret_cast<const uint4 *>(src + (long long)n * bstride);
         uint4 *dp = reinterpret_cast<uint4 *>(dst + (long long)s * bstride);
         for (int c = threadIdx.x; c < n16; c += blockDim.x) dp[c] = sp[c];
@@ -365,8 +373,8 @@ int llg_hip_window_ffn(LlgHipDevice h, int64_t hw, const float *x, const int32_t
     if ((rc = llg_h2d(d, ws + o_n, &n32, 4))) return rc;
     rc = llg_sparse_enqueue(d, w->resident, w->bstride, w->bundle->fmt, w->slot_of,
                             (const float *)ws, (const int32_t *)(ws + o_act),
-                            (const int32_t *)(ws + o_n), n_active, act, (float *)(ws + o_out),
-                            ws + o_ws);
+                            (const int32_t *)(ws + o_n), n_active, w->ff, act,
+                            (float *)(ws + o_out), ws + o_ws);
     if (rc) return rc;
     if ((rc = llg_d2h(d, out, ws + o_out, (size_t)hd * 4))) return rc;
     return llg_sync_dev(d);
@@ -386,7 +394,7 @@ int llg_hipd_window_step(LlgHipDevice h, int64_t hw, const float *d_x, const int
     if ((rc = window_update_enqueue(d, w, d_active, d_n_active, w->ff, false))) return rc;
     const LlgFreshRows fr{w->bundle->d, w->fresh, w->epoch, w->resident};
     return llg_sparse_enqueue(d, w->resident, w->bstride, w->bundle->fmt, w->slot_of, d_x,
-                              d_active, d_n_active, w->ff, act, d_out, ws, &fr);
+                              d_active, d_n_active, w->ff, w->ff, act, d_out, ws, &fr);
 }
 
 int llg_hip_window_resident(LlgHipDevice h, int64_t hw, uint8_t *resident, int *n_resident) {

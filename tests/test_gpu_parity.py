@@ -407,6 +407,46 @@ def test_bad_activation_rejected(dev, rng, act):
         hnd.release()
 
 
+def test_window_step_device_list_out_of_contract(dev, rng):
+    """Device lists are not checked on the host; the kernels keep every access
+    in bounds whatever such a list holds (indices outside [0, ff), repeats, a
+    count above ff or below 0, within a buffer of ff entries).  The window is
+    then discarded; a fresh window on the same bundle still matches the oracle."""
+    h, ff, k = 128, 256, 2
+    up, dn = make_sparse_layer(rng, h, ff, gg.Q4_0)
+    b = dev.upload_bundle(up, dn, gg.Q4_0, h, ff)
+    bad = llg.NeuronCache(dev, b, k)
+    d_out = torch.empty(h, device="cuda")
+    d_n = torch.empty(1, dtype=torch.int32, device="cuda")
+    d_x = torch.from_numpy(normal(rng, h, 1.0)).cuda()
+    lists = [np.array([-5, ff, ff + 100, 3, 3, 7, 2 ** 31 - 1], np.int32),
+             np.repeat(np.arange(0, ff, 2, dtype=np.int32), 2)[:ff]]
+    for A, count in [(lists[0], 7), (lists[1], ff + 50), (lists[1], -3), (lists[1], ff)] * 3:
+        buf = np.full(ff, 1, np.int32)
+        buf[:A.size] = A
+        d_a = torch.from_numpy(buf).cuda()
+        d_n.fill_(count)
+        torch.cuda.synchronize()
+        bad.step_device(d_x.data_ptr(), d_a.data_ptr(), d_n.data_ptr(), d_out.data_ptr())
+        dev.sync()
+        assert np.all(np.isfinite(d_out.cpu().numpy()))
+    bad.win.release()
+    nc = llg.NeuronCache(dev, b, k)
+    ref = R.NeuronCache(ff, h, k, ff, up, dn, gg.Q4_0)
+    for A in window_sets(rng, ff, 40, 6, 0.5):
+        x = normal(rng, h, 1.0)
+        d_a = torch.from_numpy(A).cuda()
+        d_xx = torch.from_numpy(x).cuda()
+        d_n.fill_(A.size)
+        torch.cuda.synchronize()
+        nc.step_device(d_xx.data_ptr(), d_a.data_ptr(), d_n.data_ptr(), d_out.data_ptr())
+        dev.sync()
+        ref.update(A)
+        assert max_rel_err(d_out.cpu().numpy(), ref.ffn_forward(x, A)) <= TOL
+    nc.win.release()
+    b.release()
+
+
 def test_window_rejects_duplicates(dev, rng):
     up, dn = make_sparse_layer(rng, 32, 32, gg.Q4_0)
     b = dev.upload_bundle(up, dn, gg.Q4_0, 32, 32)
