@@ -213,6 +213,9 @@ class Device:
     def upload_matrix(self, raw, ggml_type: int, rows: int, cols: int) -> "Handle":
         """GGUF bytes of a [rows x cols] tensor (host numpy/torch-CPU or a CUDA tensor)."""
         out = C.c_int64()
+        rb = _row_bytes(ggml_type, cols)
+        if rb and rows > 0:
+            _need(_nbytes(raw), rows * rb, "upload_matrix bytes")
         if _is_device_tensor(raw):
             rc = self.lib.llg_hipd_upload_matrix(self.h, C.c_void_p(raw.data_ptr()), ggml_type,
                                                  rows, cols, C.byref(out))
@@ -232,6 +235,10 @@ class Device:
     def upload_bundle(self, up_raw, down_t_raw, ggml_type: int, h: int, ff: int) -> "Handle":
         """flash.CreateBundle (flash/bundle.go:37-111) into HBM, bytes kept quantized."""
         out = C.c_int64()
+        rb = _row_bytes(ggml_type, h)
+        if rb and ff > 0:
+            _need(_nbytes(up_raw), ff * rb, "upload_bundle up bytes")
+            _need(_nbytes(down_t_raw), ff * rb, "upload_bundle down bytes")
         if _is_device_tensor(up_raw):
             rc = self.lib.llg_hipd_upload_bundle(self.h, C.c_void_p(up_raw.data_ptr()),
                                                  C.c_void_p(down_t_raw.data_ptr()), ggml_type, h,
@@ -262,6 +269,7 @@ class Device:
     def matvec_q(self, mat: "Handle", x) -> np.ndarray:
         info = mat.info()
         x = _f32(x).ravel()
+        _need(x.size, info["cols"], "matvec_q x")
         y = np.empty(info["rows"], np.float32)
         self.check(self.lib.llg_hip_matvec_q(self.h, mat.id, _ptr(x), _ptr(y)), "matvec_q")
         return y
@@ -270,6 +278,8 @@ class Device:
         lg = _f32(logits)
         if lg.ndim == 1:
             lg = lg.reshape(1, -1)
+        if lg.ndim != 2:
+            raise LlgError(LLG_E_ARG, "moe_route: logits must be [n_tok x n_exp]")
         n_tok, n_exp = lg.shape
         ids = np.empty((n_tok, k), np.int32)
         w = np.empty((n_tok, k), np.float32)
@@ -280,6 +290,28 @@ class Device:
 
 def _is_device_tensor(a) -> bool:
     return hasattr(a, "is_cuda") and bool(getattr(a, "is_cuda"))
+
+
+def _nbytes(a) -> int:
+    if hasattr(a, "element_size"):
+        return a.numel() * a.element_size()
+    return np.asarray(a).nbytes
+
+
+def _row_bytes(ggml_type: int, cols: int) -> int:
+    """ByteSize of a row, or 0 when the C ABI will reject the type or length
+    itself (with its own error code)."""
+    try:
+        return gguf.byte_size(ggml_type, cols) if ggml_type in gguf.DEVICE_TYPES and cols > 0 else 0
+    except ValueError:
+        return 0
+
+
+def _need(n_have: int, n_want: int, what: str):
+    """The C ABI reads exactly n_want elements (or bytes): a shorter buffer
+    is an argument error here, before any copy."""
+    if n_have != n_want:
+        raise LlgError(LLG_E_ARG, f"{what}: {n_have} given, {n_want} expected")
 
 
 def _host_bytes(a) -> np.ndarray:
@@ -297,11 +329,14 @@ class Handle:
         self.kind = kind
 
     def info(self) -> dict:
-        t, r, c, s = C.c_int(), C.c_int(), C.c_int(), C.c_int64()
-        self.dev.check(self.dev.lib.llg_hip_object_info(self.dev.h, self.id, C.byref(t),
-                                                        C.byref(r), C.byref(c), C.byref(s)),
-                       "object_info")
-        return {"type": t.value, "rows": r.value, "cols": c.value, "stride": s.value}
+        """type, rows, cols, stride of the object (queried once; objects never change shape)."""
+        if getattr(self, "_info", None) is None:
+            t, r, c, s = C.c_int(), C.c_int(), C.c_int(), C.c_int64()
+            self.dev.check(self.dev.lib.llg_hip_object_info(self.dev.h, self.id, C.byref(t),
+                                                            C.byref(r), C.byref(c), C.byref(s)),
+                           "object_info")
+            self._info = {"type": t.value, "rows": r.value, "cols": c.value, "stride": s.value}
+        return self._info
 
     @property
     def is_bundle(self) -> bool:
@@ -333,6 +368,7 @@ class Predictor:
     def predict(self, attn_out, return_logits: bool = False):
         """Predict (predictor.go:51-83): ascending indices with logit > Threshold."""
         a = _f32(attn_out).ravel()
+        _need(a.size, self.h, "Predict attn_out")
         act = np.empty(self.ff, np.int32)
         n = C.c_int()
         logits = np.empty(self.ff, np.float32) if return_logits else None
@@ -346,6 +382,7 @@ class Predictor:
 def ffn_sparse_load(dev: Device, bundle: Handle, x, active, act: int = ACT_RELU) -> np.ndarray:
     """ffnSparseLoad (ffn_flash.go:254-299) over an HBM bundle."""
     x = _f32(x).ravel()
+    _need(x.size, bundle.info()["cols"], "ffnSparseLoad x")
     a = _i32(active).ravel()
     out = np.empty_like(x)
     dev.check(dev.lib.llg_hip_ffn_sparse(dev.h, bundle.id, _ptr(x), _ptr(a) if a.size else None,
@@ -357,6 +394,8 @@ def ffn_predict_sparse(dev: Device, pred: Predictor, bundle: Handle, attn_out, x
                        act: int = ACT_RELU):
     """ffnFlash path 2 (ffn_flash.go:225-231): Predict then ffnSparseLoad, on the device."""
     a, x = _f32(attn_out).ravel(), _f32(x).ravel()
+    _need(a.size, pred.h, "ffnFlash attn_out")
+    _need(x.size, bundle.info()["cols"], "ffnFlash x")
     out = np.empty_like(x)
     idx = np.empty(pred.ff, np.int32)
     n = C.c_int()
@@ -369,7 +408,8 @@ def ffn_predict_sparse(dev: Device, pred: Predictor, bundle: Handle, attn_out, x
 def ffn_dense(dev: Device, up: Handle, down: Handle, x, act: int = ACT_RELU) -> np.ndarray:
     """Context.ffn ReLU/GELU path (forward.go:342-367): down @ act(up @ x)."""
     x = _f32(x).ravel()
-    out = np.empty_like(x)
+    _need(x.size, up.info()["cols"], "ffn x")
+    out = np.empty(down.info()["rows"], np.float32)
     dev.check(dev.lib.llg_hip_ffn_dense(dev.h, up.id, down.id, _ptr(x), act, _ptr(out)), "ffn")
     return out
 
@@ -378,7 +418,8 @@ def ffn_swiglu(dev: Device, gate: Handle, up: Handle, down: Handle, x) -> np.nda
     """Context.ffn SiLU path, ffnSwiGLU (forward.go:368-389):
     down @ (silu(gate @ x) * (up @ x))."""
     x = _f32(x).ravel()
-    out = np.empty_like(x)
+    _need(x.size, gate.info()["cols"], "ffn_swiglu x")
+    out = np.empty(down.info()["rows"], np.float32)
     dev.check(dev.lib.llg_hip_ffn_swiglu(dev.h, gate.id, up.id, down.id, _ptr(x), _ptr(out)),
               "ffn_swiglu")
     return out
@@ -391,6 +432,8 @@ class NeuronCache:
         self.dev = dev
         self.bundle = bundle
         self.window_size = window_size
+        info = bundle.info()  # kept: the window outlives a released bundle handle
+        self.hidden, self.ff = info["cols"], info["rows"]
         out = C.c_int64()
         dev.check(dev.lib.llg_hip_window_create(dev.h, bundle.id, window_size, C.byref(out)),
                   "NewNeuronCache")
@@ -411,6 +454,7 @@ class NeuronCache:
     def ffn_forward(self, x, active_neurons, act: int = ACT_RELU) -> np.ndarray:
         """FFNForward (window.go:143-180)."""
         x = _f32(x).ravel()
+        _need(x.size, self.hidden, "FFNForward x")
         a = _i32(active_neurons).ravel()
         out = np.empty_like(x)
         self.dev.check(self.dev.lib.llg_hip_window_ffn(
@@ -434,8 +478,7 @@ class NeuronCache:
         return self._num
 
     def resident(self) -> np.ndarray:
-        ff = self.bundle.info()["rows"]
-        flags = np.empty(ff, np.uint8)
+        flags = np.empty(self.ff, np.uint8)
         n = C.c_int()
         self.dev.check(self.dev.lib.llg_hip_window_resident(self.dev.h, self.win.id,
                                                             _ptr(flags), C.byref(n)), "resident")
@@ -453,6 +496,9 @@ def moe_ffn(dev: Device, router: Handle, gate: Handle, up: Handle, down: Handle,
     if squeeze:
         x = x.reshape(1, -1)
     n_tok = x.shape[0]
+    if x.ndim != 2:
+        raise LlgError(LLG_E_ARG, "moeFFN: x must be [hidden] or [n_tok x hidden]")
+    _need(x.shape[1], gate.info()["cols"], "moeFFN x width")
     out = np.empty_like(x)
     ids = np.empty((n_tok, k), np.int32)
     w = np.empty((n_tok, k), np.float32)

@@ -447,6 +447,31 @@ def test_window_step_device_list_out_of_contract(dev, rng):
     b.release()
 
 
+def test_short_host_buffers_rejected(dev, rng):
+    """A host array shorter than the shape it is passed with is an argument
+    error before any copy (the C ABI would read past its end)."""
+    h, ff = 64, 64
+    up, dn = make_sparse_layer(rng, h, ff, gg.Q4_0)
+    calls = [lambda: dev.upload_matrix(up[:-1], gg.Q4_0, ff, h),
+             lambda: dev.upload_bundle(up, dn[:-1], gg.Q4_0, h, ff)]
+    b = dev.upload_bundle(up, dn, gg.Q4_0, h, ff)
+    m = dev.upload_matrix(up, gg.Q4_0, ff, h)
+    pred = llg.Predictor(dev, normal(rng, (8, h), 0.05), normal(rng, (ff, 8), 0.05))
+    nc = llg.NeuronCache(dev, b, 2)
+    short = normal(rng, h - 1, 1.0)
+    calls += [lambda: llg.ffn_sparse_load(dev, b, short, np.array([1], np.int32)),
+              lambda: llg.ffn_predict_sparse(dev, pred, b, short, normal(rng, h, 1.0)),
+              lambda: pred.predict(short),
+              lambda: dev.matvec_q(m, short),
+              lambda: nc.ffn_forward(short, np.array([1], np.int32))]
+    for call in calls:
+        with pytest.raises(llg.LlgError) as e:
+            call()
+        assert e.value.code == llg.LLG_E_ARG
+    for hnd in (nc.win, m, b):
+        hnd.release()
+
+
 def test_window_rejects_duplicates(dev, rng):
     up, dn = make_sparse_layer(rng, 32, 32, gg.Q4_0)
     b = dev.upload_bundle(up, dn, gg.Q4_0, 32, 32)
