@@ -24,6 +24,8 @@
 
 #include "../../include/llg_hip.h"
 
+typedef _Float16 half2_llg __attribute__((ext_vector_type(2)));
+
 #define LLG_ROW_ALIGN 128
 
 struct RowFmt {
@@ -401,26 +403,41 @@ __device__ __forceinline__ void llg_block_load<LLG_TYPE_F32>(BlockRaw<LLG_TYPE_F
 // ignore xsum.
 template <int T>
 __device__ __forceinline__ float llg_raw_dot(const BlockRaw<T> &r, const float4 *x4, float xsum);
+// (a & m) | o in one instruction
+__device__ __forceinline__ uint32_t llg_and_or(uint32_t a, uint32_t m, uint32_t o) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
+    return r;
+}
+
 template <>
 __device__ __forceinline__ float llg_raw_dot<LLG_TYPE_Q4_0>(const BlockRaw<LLG_TYPE_Q4_0> &r,
                                                              const float4 *x4, float xsum) {
+    // Nibble p of word i is element 8i + p.  A nibble at bits 4-7 of an f16
+    // whose other bits are 0x5400 is exactly 64 + q, so one shift and one
+    // and-or give the pair (64 + q_p, 64 + q_{p+4}) of a word, and the f16
+    // values multiply fp32 x directly (v_fma_mix_f32).  The sum of
+    // (64 + q) x less 72 xsum is the sum of (q - 8) x.
     const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    const uint32_t m = 0x00F000F0u, e = 0x54005400u;
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const float4 xa = x4[2 * i], xb = x4[2 * i + 1];
-        const uint32_t lo = w[i] & 0x0F0F0F0Fu;         // elements 8i, 8i+2, 8i+4, 8i+6
-        const uint32_t hi = (w[i] >> 4) & 0x0F0F0F0Fu;  // elements 8i+1, 8i+3, 8i+5, 8i+7
-        s += (float)(lo & 0xFF) * xa.x;
-        s += (float)(hi & 0xFF) * xa.y;
-        s += (float)((lo >> 8) & 0xFF) * xa.z;
-        s += (float)((hi >> 8) & 0xFF) * xa.w;
-        s += (float)((lo >> 16) & 0xFF) * xb.x;
-        s += (float)((hi >> 16) & 0xFF) * xb.y;
-        s += (float)(lo >> 24) * xb.z;
-        s += (float)(hi >> 24) * xb.w;
+        const half2_llg p0 = __builtin_bit_cast(half2_llg, llg_and_or(w[i] << 4, m, e));
+        const half2_llg p1 = __builtin_bit_cast(half2_llg, llg_and_or(w[i], m, e));
+        const half2_llg p2 = __builtin_bit_cast(half2_llg, llg_and_or(w[i] >> 4, m, e));
+        const half2_llg p3 = __builtin_bit_cast(half2_llg, llg_and_or(w[i] >> 8, m, e));
+        s = __builtin_fmaf((float)p0[0], xa.x, s);
+        s = __builtin_fmaf((float)p1[0], xa.y, s);
+        s = __builtin_fmaf((float)p2[0], xa.z, s);
+        s = __builtin_fmaf((float)p3[0], xa.w, s);
+        s = __builtin_fmaf((float)p0[1], xb.x, s);
+        s = __builtin_fmaf((float)p1[1], xb.y, s);
+        s = __builtin_fmaf((float)p2[1], xb.z, s);
+        s = __builtin_fmaf((float)p3[1], xb.w, s);
     }
-    return (s - 8.0f * xsum) * llg_f16(r.d);
+    return (s - 72.0f * xsum) * llg_f16(r.d);
 }
 template <>
 __device__ __forceinline__ float llg_raw_dot<LLG_TYPE_Q8_0>(const BlockRaw<LLG_TYPE_Q8_0> &r,
@@ -698,6 +715,7 @@ __device__ __forceinline__ void llg_stage_ln(float *xs, const LlgLnArgs &a, floa
 // ---------------------------------------------------------------------------
 #ifdef __cplusplus
 #include <string>
+
 
 enum LlgKind { LLG_KIND_MATRIX = 1, LLG_KIND_BUNDLE = 2, LLG_KIND_WINDOW = 3, LLG_KIND_MODEL = 4 };
 
