@@ -10,10 +10,11 @@ int llg_predict_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject
 int llg_check_predictor(LlgDevice *d, int64_t hwup, int64_t hwout, int64_t hbias,
                         LlgObject **wup, LlgObject **wout, LlgObject **bias);
 // K1 of the predictor: hidden partials into ws; also zeroes the given targets.
+// zero_out[0..zero_n) is cleared, or, with add_to, accumulated (+= add_to[i]).
 int llg_pred_hidden_enqueue(LlgDevice *d, LlgObject *wup, const float *d_a, uint8_t *ws,
                             float **partial, unsigned long long **mask, int *psplit,
                             float *zero_out, int zero_n, int32_t *zero_ctr, int n_ctr,
-                            int32_t *zero_extra);
+                            int32_t *zero_extra, const float *add_to = nullptr);
 // Hidden partials + tile masks (k_pred_hidden, k_pred_logits); also clears
 // zero_out[0..zero_n) and *zero_extra for the kernels that follow.
 int llg_pred_masks_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
@@ -63,7 +64,8 @@ int llg_matvec_ln_enqueue(LlgDevice *d, const LlgObject *w, const LlgLnArgs &ln,
 size_t llg_fused_ws_bytes(int rank, int ff);
 int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
                       LlgObject *b, const float *d_a, const float *d_x, float thr, int act,
-                      float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws);
+                      float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws,
+                      const float *d_out_add = nullptr);
 
 // MoE prefill as grouped MFMA GEMMs (llg_moe_gemm.hip).
 bool llg_moe_gemm_supported(int type, int hidden, int eff, int n_tok);

@@ -2,25 +2,25 @@
 // (inference/ffn_flash.go:115-185 ForwardFlash, inference/forward.go:106-314,
 // kvcache/kvcache.go:25-82, cmd/generate.go:88-121).
 //
-// One token through the model, all on the device stream:
-//   k_embed           x = dequant(embedding row of the token)    (forward.go:449-454)
+// One token through the model, all on the device stream.  The residual
+// stream lives in one buffer r:
+//   k_embed           r = dequant(embedding row of the token)    (forward.go:449-454)
 //   per layer l:
 //     k_matvec_q      qkv = [Wq; Wk; Wv] . normed (forward.go:211-222), where
-//                     every workgroup first forms x += attn_out[l-1]; x +=
-//                     ffn_out[l-1] (two separate fp32 adds, ffn_flash.go:161-166)
-//                     and normed = LayerNorm(x) (tensor/ops.go:138-165) itself
-//                     (llg_stage_ln); workgroup 0 stores both.  x alternates
-//                     between two buffers, so no workgroup reads what another
-//                     writes.
+//                     every workgroup first forms normed = LayerNorm(r)
+//                     (tensor/ops.go:138-165) itself (llg_stage_ln)
 //     k_attn          NeoX RoPE of q and k (forward.go:483-497), K/V appended at
 //                     row pos of the layer's cache (kvcache.go:42-52), softmax
 //                     attention of every query head over rows 0..pos of its KV
 //                     head (forward.go:258-301)
 //     k_matvec_q      attn_out = Wo . attn                      (forward.go:305)
-//     sparse step     ffn_out = ffnFlash path 2 with the predictor on attn_out
-//                     and the FFN on normed (ffn_flash.go:157-163, 225-231)
-//   k_resid_norm      final residual adds + output LayerNorm   (ffn_flash.go:126-129)
-//   k_matvec_q        logits = LMHead . x                      (ffn_flash.go:130)
+//     sparse step     ffnFlash path 2 with the predictor on attn_out and the FFN
+//                     on normed (ffn_flash.go:157-163, 225-231); its first
+//                     kernel adds attn_out to r (x += attnOut, ffn_flash.go:161),
+//                     and its down sums are added into r (x += ffnOut, :164-166),
+//                     so r ends as the next layer's residual
+//   k_resid_norm      output LayerNorm of r                    (ffn_flash.go:126-129)
+//   k_matvec_q        logits = LMHead . normed                 (ffn_flash.go:130)
 //   k_argmax          next token = first index of the maximum  (generate.go:197-205)
 // The token comes from device memory, so a greedy decode loop never waits on
 // the host.
@@ -44,7 +44,7 @@ struct LlgModel {
     LlgObject *embed, *out_w, *out_b, *lm_head;
     std::vector<LlgModelLayer> layers;
     // device buffers, carved out of the object's allocation
-    float *x, *x2, *normed, *qkv, *attn, *attn_out, *ffn_out, *logits, *kv, *pred_logits;
+    float *x, *normed, *qkv, *attn, *attn_out, *logits, *kv, *pred_logits;  // x: the residual
     float2 *rope;  // [max_seq x head_dim/2] (cos, sin)
     int32_t *token, *n_active, *act_scratch;
     uint8_t *ws;
@@ -349,16 +349,17 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
     hipStream_t st = llg_dev_stream(d);
     const int qkv_rows = (m.n_heads + 2 * m.n_kv) * m.head_dim;
     (void)qkv_rows;
+    float *r = m.x;  // the residual stream
     hipLaunchKernelGGL(k_embed, dim3((m.hidden + 255) / 256), dim3(256), 0, st, m.embed->d,
-                       m.embed->stride, m.embed->fmt, token_in, m.vocab, m.x);
+                       m.embed->stride, m.embed->fmt, token_in, m.vocab, r);
     const size_t attn_lds = (size_t)(pos + 1) * 4;
     for (int l = 0; l < m.n_layers; l++) {
         const LlgModelLayer &L = m.layers[l];
         LlgLnArgs ln;
-        ln.x_in = (l & 1) ? m.x2 : m.x;
-        ln.x_out = (l & 1) ? m.x : m.x2;
-        ln.a1 = l ? m.attn_out : nullptr;
-        ln.a2 = l ? m.ffn_out : nullptr;
+        ln.x_in = r;
+        ln.x_out = nullptr;
+        ln.a1 = nullptr;
+        ln.a2 = nullptr;
         ln.w = reinterpret_cast<const float *>(L.norm_w->d);
         ln.b = reinterpret_cast<const float *>(L.norm_b->d);
         ln.normed_out = m.normed;
@@ -380,18 +381,19 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
                                       m.act_scratch + m.ff, pred_logits + (size_t)l * m.ff, m.ws)))
             return rc;
         // ffnFlash path 2: predictor on the attention output, FFN on normed
+        // r += attn_out by its first kernel, then r += the FFN output
         rc = llg_fused_enqueue(d, L.pwup, L.pwout, nullptr, L.bundle, m.attn_out, m.normed, L.thr,
-                               m.act, m.ffn_out, nullptr, n_active_out ? n_active_out + l : nullptr,
-                               m.ws);
+                               m.act, r, nullptr, n_active_out ? n_active_out + l : nullptr, m.ws,
+                               m.attn_out);
         if (rc) return rc;
     }
-    float *xf = (m.n_layers & 1) ? m.x2 : m.x;  // the residual after the last layer's input
     const float *fw = reinterpret_cast<const float *>(m.out_w->d);
     const float *fb = reinterpret_cast<const float *>(m.out_b->d);
     const int np = (m.hidden + NORM_THREADS - 1) / NORM_THREADS;
 #define RN(NP)                                                                                    \
-    hipLaunchKernelGGL((k_resid_norm<NP>), dim3(1), dim3(NORM_THREADS), 0, st, xf, m.attn_out,    \
-                       m.ffn_out, fw, fb, m.hidden, m.eps, m.normed)
+    hipLaunchKernelGGL((k_resid_norm<NP>), dim3(1), dim3(NORM_THREADS), 0, st, r,                 \
+                       (const float *)nullptr, (const float *)nullptr, fw, fb, m.hidden, m.eps,   \
+                       m.normed)
     if (np <= 2) RN(2);
     else if (np <= 4) RN(4);
     else if (np <= 6) RN(6);
@@ -493,15 +495,13 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     const size_t v_pl = llg_align((long long)m->n_layers * m->ff * 4, 256);
     const size_t v_rope = llg_align((long long)m->max_seq * m->head_dim / 2 * 8, 256);
     const size_t wsb = model_ws_bytes(*m);
-    const size_t total = 5 * v_h + v_qkv + v_att + v_log + v_kv + v_i + v_ff + v_pl + v_rope + wsb;
+    const size_t total = 3 * v_h + v_qkv + v_att + v_log + v_kv + v_i + v_ff + v_pl + v_rope + wsb;
     uint8_t *buf = nullptr;
     if (hipMalloc(&buf, total) != hipSuccess) return fail(LLG_E_NOMEM, "buffer allocation failed");
     uint8_t *p = buf;
     m->x = reinterpret_cast<float *>(p); p += v_h;
     m->normed = reinterpret_cast<float *>(p); p += v_h;
     m->attn_out = reinterpret_cast<float *>(p); p += v_h;
-    m->ffn_out = reinterpret_cast<float *>(p); p += v_h;
-    m->x2 = reinterpret_cast<float *>(p); p += v_h;
     m->qkv = reinterpret_cast<float *>(p); p += v_qkv;
     m->attn = reinterpret_cast<float *>(p); p += v_att;
     m->logits = reinterpret_cast<float *>(p); p += v_log;

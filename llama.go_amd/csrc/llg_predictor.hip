@@ -24,10 +24,13 @@ __global__ __launch_bounds__(256) void k_pred_hidden(const uint8_t *__restrict__
                                                      float *__restrict__ partial,
                                                      float *__restrict__ zero_out, int zero_n,
                                                      int32_t *__restrict__ zero_ctr, int n_ctr,
-                                                     int32_t *__restrict__ zero_extra) {
+                                                     int32_t *__restrict__ zero_extra,
+                                                     const float *__restrict__ add_to) {
     const int gtid = blockIdx.x * blockDim.x + threadIdx.x;
-    if (zero_out)
-        for (int i = gtid; i < zero_n; i += gridDim.x * blockDim.x) zero_out[i] = 0.0f;
+    if (zero_out) {  // cleared, or (add_to) accumulated: zero_out[i] += add_to[i]
+        for (int i = gtid; i < zero_n; i += gridDim.x * blockDim.x)
+            zero_out[i] = add_to ? zero_out[i] + add_to[i] : 0.0f;
+    }
     if (zero_ctr && gtid < n_ctr) zero_ctr[gtid] = 0;
     if (zero_extra && gtid == 0) *zero_extra = 0;
     const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -160,7 +163,7 @@ int llg_predict_ws_bytes(int rank, int ff) {
 int llg_pred_hidden_enqueue(LlgDevice *d, LlgObject *wup, const float *d_a, uint8_t *ws,
                             float **partial, unsigned long long **mask, int *psplit,
                             float *zero_out, int zero_n, int32_t *zero_ctr, int n_ctr,
-                            int32_t *zero_extra) {
+                            int32_t *zero_extra, const float *add_to) {
     const int h = wup->fmt.cols, rank = wup->rows;
     *partial = reinterpret_cast<float *>(ws);
     *mask = reinterpret_cast<unsigned long long *>(
@@ -169,7 +172,7 @@ int llg_pred_hidden_enqueue(LlgDevice *d, LlgObject *wup, const float *d_a, uint
     const int grid = (rank * PRED_SPLIT + 3) / 4;
     hipLaunchKernelGGL(k_pred_hidden, dim3(grid), dim3(256), 0, llg_dev_stream(d), wup->d,
                        wup->stride, h, rank, d_a, *partial, zero_out, zero_n, zero_ctr, n_ctr,
-                       zero_extra);
+                       zero_extra, add_to);
     LLG_LAUNCH_CHECK(d, "pred_hidden");
     return 0;
 }

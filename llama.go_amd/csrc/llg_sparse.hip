@@ -573,7 +573,8 @@ static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial, 
 // the number of active neurons.
 int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
                       LlgObject *b, const float *d_a, const float *d_x, float thr, int act,
-                      float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws) {
+                      float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws,
+                      const float *d_out_add) {
     if (int rc = llg_check_act(d, act)) return rc;
     const RowFmt &f = b->fmt;
     const int ff = wout->rows, rank = wup->rows;
@@ -589,9 +590,10 @@ int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *
     float *partial;
     unsigned long long *mask;
     int psplit;
-    // K1 also zeroes out, the atomic target of K3
+    // K1 also clears out, the atomic target of K3 (or, with d_out_add, adds
+    // d_out_add to it: out then ends as out + d_out_add + the FFN output)
     int rc = llg_pred_hidden_enqueue(d, wup, d_a, ws, &partial, &mask, &psplit, d_out, f.cols,
-                                     nullptr, 0, nullptr);
+                                     nullptr, 0, nullptr, d_out_add);
     if (rc) return rc;
     if (psplit != PRED_SPLIT_N)
         return llg_set_error(d, LLG_E_ARG, "predict_sparse: hidden split %d != %d", psplit,
