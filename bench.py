@@ -738,7 +738,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the sparse-FFN path runs on a single MI355X; see DESIGN.md for sharding)",
+              "(the sparse-FFN path is measured on a single MI355X; a sharded layer would "
+              "split the neurons across GPUs and all-reduce the 18 KB output per layer)",
               file=sys.stderr)
         sys.exit(2)
     if args.layers <= 0:
