@@ -4,7 +4,7 @@
  * TEST INFRASTRUCTURE ONLY.  This file restates the reference's Go CPU code
  * (AndersHsueh/llama.go) in C so that the HIP path can be checked against it
  * on the same inputs.  Only tests/, __graft_entry__.smoke() and bench.py's
- * cpu_baseline leg load it, and only as the checker or the timed CPU
+ * cpu_baseline leg load it, and only as the reference result or the timed CPU
  * baseline; the product library never links or calls it.
  *
  * Build: see oracle/Makefile (gcc -O2 -ffp-contract=off, no fast-math), so

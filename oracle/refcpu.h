@@ -1,6 +1,6 @@
 /*
  * refcpu.h -- CPU oracle: a plain-C restatement of llama.go's sparse-FFN
- * path (AndersHsueh/llama.go), used ONLY as the checker by tests/, the smoke
+ * path (AndersHsueh/llama.go), used ONLY as the reference result by tests/, the smoke
  * check and bench.py's cpu_baseline leg.  It is never linked into, loaded by
  * or called from the product library.
  *
