@@ -168,10 +168,10 @@ int llg_hip_window_resident(LlgHipDevice dev, int64_t win, uint8_t *resident, in
  * n_exp*hidden rows x eff (dims [eff, hidden, n_exp]).  x: [n_tok x hidden];
  * out: [n_tok x hidden].  ids/weights (optional, [n_tok x k]) receive the
  * chosen experts in accumulation order (descending probability, ties to the
- * lower index) and p/wsum.  Batches of n_tok >= 16 Q4_0 tokens with hidden
- * and expert width multiples of 128 are grouped per expert and run as grouped
- * MFMA GEMMs (f16 operands, fp32 accumulation); other batches run the
- * per-token decode kernels. */
+ * lower index) and p/wsum.  Batches of n_tok >= 16 Q4_0 tokens with hidden a
+ * multiple of 256 and expert width a multiple of 128 are grouped per expert
+ * and run as grouped MFMA GEMMs (f16 operands, fp32 accumulation); other
+ * batches run the per-token decode kernels. */
 int llg_hip_moe_ffn(LlgHipDevice dev, int64_t router, int64_t gate_exps, int64_t up_exps,
                     int64_t down_exps, int n_exp, int k, const float *x, int n_tok, float *out,
                     int32_t *ids, float *weights);

@@ -19,11 +19,12 @@
 // group g word j of block g, so a lane's 16-byte load of one block holds its
 // B fragments for all 4 steps of the chunk.  The B fragment is built from the
 // word with two and-or's per nibble pair (q4_frag), an exact subtraction of
-// the offset and a multiply by the block scale.  Tiles: 64 rows x 128 columns
-// per workgroup (per weight matrix), 4 wavefronts of 64 x 32; A in K chunks of
-// 128 staged in LDS (double buffered; the next chunk is loaded into registers
-// while the current one is multiplied); B straight into registers, one chunk
-// ahead.
+// the offset and a multiply by the block scale.  Tiles: 64 rows per
+// workgroup, 4 wavefronts of 64 rows each; a gate/up wavefront owns 32 columns
+// of gate and the same 32 of up, a down wavefront 64 columns, so each A
+// fragment feeds 4 MFMAs.  A in K chunks of 128 staged in LDS (double
+// buffered; the next chunk is loaded into registers while the current one is
+// multiplied); B straight into registers, one chunk ahead.
 #include "llg_common.hpp"
 #include "llg_internal.hpp"
 
@@ -33,7 +34,6 @@ typedef float floatx4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 #define GM_BM 64
-#define GM_BN 128
 #define GM_KC 128                 // K per chunk
 #define GM_KB (GM_KC / 32)        // Q4_0 blocks per chunk
 #define GM_AST (GM_KC + 8)        // LDS A row stride (halves)
@@ -154,10 +154,18 @@ __device__ __forceinline__ int k_order(int k) {
 // blockIdx = (M tile * N tiles + N tile) * ksplit + slice.
 // A rows: MODE 0 gathers X16 row row_pair[r] / k (the pair's token); MODE 1
 // reads H row r.  A goes through LDS (every wavefront reads all 64 rows); B
-// is private to a wavefront (its 32 columns), so each lane loads its own
+// is private to a wavefront (its columns), so each lane loads its own
 // block of each column straight into registers: lane (column n, group g)
 // takes the 16 quant bytes and the scale of block 4c + g of chunk c, whose
 // word j is the lane's B fragment at MFMA step j.
+// Columns per wavefront of each weight matrix: gate/up 32 of gate and 32 of
+// up, down 64, so both take 4 B fragments per K step and every A fragment read
+// from LDS feeds 4 MFMAs.
+template <int MODE>
+constexpr int gm_wave_cols() {
+    return MODE == 0 ? 32 : 64;
+}
+
 template <int MODE>
 __global__ __launch_bounds__(256, 2) void k_moe_gemm(
     const int4 *__restrict__ tiles, const int32_t *__restrict__ n_tiles_p,
@@ -165,17 +173,17 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
     const uint8_t *__restrict__ W0, const uint8_t *__restrict__ W1, long long wstride,
     int d_off, int rows_per_expert, int K, int N, _Float16 *__restrict__ H,
     float *__restrict__ Y, int ksplit, long long ystride) {
-    constexpr int NM = MODE == 0 ? 2 : 1;  // weight matrices
-    constexpr int NF = NM * 2;             // B fragments per wavefront per K step
+    constexpr int NF = 4;                     // B fragments per wavefront per K step
+    constexpr int WC = gm_wave_cols<MODE>();  // columns per wavefront per matrix
     __shared__ __attribute__((aligned(16))) _Float16 As[2][GM_BM * GM_AST];
-    const int n_ntiles = N / GM_BN;
+    const int n_ntiles = N / (4 * WC);
     const int ks = blockIdx.x % ksplit;
     const int nt = (blockIdx.x / ksplit) % n_ntiles;
     const int mt = blockIdx.x / ksplit / n_ntiles;
     if (mt >= *n_tiles_p) return;
     const int4 tile = tiles[mt];
     const int e = tile.x, row0 = tile.y, nrows = tile.z;
-    const int n0 = nt * GM_BN;
+    const int n0 = nt * 4 * WC;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
 
@@ -191,13 +199,14 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
         a_off[q] = arow * K + part * 8;
     }
     // B: fragment f = (matrix m, 16-column group ns) -> column
-    // n0 + wave*32 + ns*16 + li of matrix m; the lane's block of chunk c is 4c + lg.
+    // n0 + wave*WC + ns*16 + li of matrix m (gate/up: m = f / 2, ns = f % 2;
+    // down: m = 0, ns = f); the lane's block of chunk c is 4c + lg.
     const uint8_t *brow[NF];
 #pragma unroll
     for (int f = 0; f < NF; f++) {
-        const int m = f / 2, ns = f % 2;
-        const uint8_t *W = (MODE == 0 && m == 1) ? W1 : W0;
-        brow[f] = W + ((long long)e * rows_per_expert + n0 + wave * 32 + ns * 16 + li) * wstride;
+        const int m = MODE == 0 ? f / 2 : 0, ns = MODE == 0 ? f % 2 : f;
+        const uint8_t *W = m == 1 ? W1 : W0;
+        brow[f] = W + ((long long)e * rows_per_expert + n0 + wave * WC + ns * 16 + li) * wstride;
     }
 
     constexpr int NB = GM_BD + 1;                  // B register slots
@@ -220,13 +229,11 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
         *reinterpret_cast<u32x4_t *>(&As[buf][(idx >> 4) * GM_AST + (idx & 15) * 8]) = ra[q];    \
     }
 
-    floatx4_t acc[NM][4][2];
+    floatx4_t acc[NF][4];  // [fragment][16-row group]
 #pragma unroll
-    for (int m = 0; m < NM; m++)
+    for (int f = 0; f < NF; f++)
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 2; j++) acc[m][i][j] = {0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < 4; i++) acc[f][i] = {0.f, 0.f, 0.f, 0.f};
 
     const int ncs = K / GM_KC / ksplit;  // chunks of this slice: c0 .. ce - 1
     const int c0 = ks * ncs, ce = c0 + ncs;
@@ -255,8 +262,7 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
                     q4_frag(w, __builtin_bit_cast(_Float16, (unsigned short)bd[slot][f]));
 #pragma unroll
                 for (int ms = 0; ms < 4; ms++)
-                    acc[f / 2][ms][f % 2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        a[ms], b, acc[f / 2][ms][f % 2], 0, 0, 0);
+                    acc[f][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ms], b, acc[f][ms], 0, 0, 0);
             }
         }
         if (c + 1 < ce) GM_STORE_A(buf ^ 1);
@@ -271,23 +277,24 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
 #undef GM_LOAD_B
 #undef GM_STORE_A
 
-    // epilogue
+    // epilogue: gate/up pairs fragment ns (gate) with ns + 2 (up)
+    constexpr int NS = MODE == 0 ? 2 : 4;  // 16-column groups per wavefront
 #pragma unroll
     for (int ms = 0; ms < 4; ms++)
 #pragma unroll
-        for (int ns = 0; ns < 2; ns++) {
-            const int n = n0 + wave * 32 + ns * 16 + li;
+        for (int ns = 0; ns < NS; ns++) {
+            const int n = n0 + wave * WC + ns * 16 + li;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int m = ms * 16 + lg * 4 + v;
                 if (m >= nrows) continue;
                 const long long r = row0 + m;
                 if (MODE == 0) {
-                    const float g = acc[0][ms][ns][v], u = acc[1][ms][ns][v];
+                    const float g = acc[ns][ms][v], u = acc[ns + 2][ms][v];
                     const float h = g / (1.0f + (float)exp(-(double)g)) * u;  // moe_forward.go:130
                     H[r * N + k_order(n)] = (_Float16)h;
                 } else {
-                    Y[ks * ystride + r * N + n] = acc[0][ms][ns][v];
+                    Y[ks * ystride + r * N + n] = acc[ns][ms][v];
                 }
             }
         }
@@ -340,7 +347,8 @@ size_t llg_moe_gemm_ws_bytes(int n_tok, int k, int n_exp, int hidden, int eff) {
 }
 
 bool llg_moe_gemm_supported(int type, int hidden, int eff, int n_tok) {
-    return type == LLG_TYPE_Q4_0 && n_tok >= 16 && hidden % GM_BN == 0 && eff % GM_BN == 0 &&
+    return type == LLG_TYPE_Q4_0 && n_tok >= 16 && hidden % (4 * gm_wave_cols<1>()) == 0 &&
+           eff % (4 * gm_wave_cols<0>()) == 0 &&
            hidden % GM_KC == 0 && eff % GM_KC == 0;
 }
 
@@ -371,12 +379,14 @@ int llg_moe_gemm_enqueue(LlgDevice *d, const LlgObject *gate, const LlgObject *u
     const long long n8 = (long long)n_tok * hidden / 8;
     hipLaunchKernelGGL(k_moe_x16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st, d_x, n8,
                        x16);
-    hipLaunchKernelGGL((k_moe_gemm<0>), dim3((unsigned)(nt_max * (eff / GM_BN))), dim3(256), 0, st,
+    hipLaunchKernelGGL((k_moe_gemm<0>), dim3((unsigned)(nt_max * (eff / (4 * gm_wave_cols<0>())))),
+                       dim3(256), 0, st,
                        tiles, n_tiles, row_pair, k, x16, gate->d, up->d, gate->stride,
                        gate->fmt.d_off, eff, hidden, eff, H, (float *)nullptr, 1, 0ll);
     const int ksplit = down_split(eff);
     const long long ystride = llg_align(np * hidden * 4, 256) / 4;
-    hipLaunchKernelGGL((k_moe_gemm<1>), dim3((unsigned)(nt_max * (hidden / GM_BN) * ksplit)),
+    hipLaunchKernelGGL((k_moe_gemm<1>),
+                       dim3((unsigned)(nt_max * (hidden / (4 * gm_wave_cols<1>())) * ksplit)),
                        dim3(256), 0, st, tiles, n_tiles, row_pair, k, H, down->d,
                        (const uint8_t *)nullptr, down->stride, down->fmt.d_off, hidden, eff,
                        hidden, (_Float16 *)nullptr, Y, ksplit, ystride);
