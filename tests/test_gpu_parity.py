@@ -169,6 +169,33 @@ def test_ffn_predict_sparse_config0(dev, rng):
     b.release()
 
 
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0])
+def test_ffn_predict_sparse_densities(dev, rng, t):
+    """The fused predictor -> selection -> gathered FFN at the extremes of
+    density: no neuron (a zero output), about half of them (tiles with more
+    active neurons than one round of up rows covers) and every neuron."""
+    h, ff, rank = 256, 1024, 32
+    up, dn = make_sparse_layer(rng, h, ff, t)
+    wup, wout = normal(rng, (rank, h), 0.05), normal(rng, (ff, rank), 0.05)
+    x, a = normal(rng, h, 1.0), normal(rng, h, 1.0)
+    _, lg = R.predict(wup, wout, None, a, 0.0)
+    b = dev.upload_bundle(up, dn, t, h, ff)
+    for n_target in (0, ff // 2, ff):
+        thr = float(np.max(lg)) + 1.0 if n_target == 0 else (
+            float(np.min(lg)) - 1.0 if n_target == ff else threshold_for(lg, n_target))
+        ref_act, _ = R.predict(wup, wout, None, a, thr)
+        assert ref_act.size == n_target
+        p = llg.Predictor(dev, wup, wout, None, thr)
+        out, act = llg.ffn_predict_sparse(dev, p, b, a, x)
+        assert np.array_equal(act, ref_act), n_target
+        ref = R.ffn_sparse_load(up, dn, t, h, ff, x, ref_act)
+        if n_target == 0:
+            assert np.all(out == 0)
+        else:
+            assert max_rel_err(out, ref) <= TOL, n_target
+    b.release()
+
+
 # ---------------------------------------------------------------- dense path
 @pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16, gg.F32])
 def test_matvec_q_small(dev, rng, t):
