@@ -61,7 +61,7 @@ void llg_window_destroy(LlgDevice *d, LlgObject *o) {
 
 // Round trips are the cost of this one-workgroup kernel, so the first 1024
 // entries of both lists are loaded up front (with their slots and the
-// returning decrement of cnt) and kept in registers; the current set is an
+// decrement of cnt) and kept in registers; the current set is an
 // LDS bitmap (ff bits); this update's evictions go on the global free stack
 // and, up to WIN_EVCAP, into LDS, where the slot assignment reads them.
 // A device list is not checked on the host, so every access stays in bounds
@@ -102,10 +102,13 @@ __global__ __launch_bounds__(1024) void k_window_update(
     const int a0 = tid < n_act ? nid(active[tid]) : -1;
     const int sa0 = a0 >= 0 ? slot_of[a0] : 0;
     const int o0 = tid < old_len ? nid(o_pre) : -1;
+    // cnt belongs to this one workgroup, so the decrement is a plain load and
+    // store (a returning atomic takes a longer round trip)
     int so0 = -1, c0 = 1;
     if (o0 >= 0) {
         so0 = slot_of[o0];
-        c0 = atomicSub(&cnt[o0], 1) - 1;
+        c0 = cnt[o0] - 1;
+        cnt[o0] = c0;
     }
     __syncthreads();
     // B: mark the current set
@@ -131,7 +134,9 @@ __global__ __launch_bounds__(1024) void k_window_update(
         const int n = nid(old[j]);
         if (n < 0) continue;
         const int sn = slot_of[n];
-        evict(n, sn, atomicSub(&cnt[n], 1) - 1);
+        const int c = cnt[n] - 1;
+        cnt[n] = c;
+        evict(n, sn, c);
     }
     __syncthreads();
     // D: toLoad in active order (window.go:98-103) by a block-wide scan; the
