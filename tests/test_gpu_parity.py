@@ -170,11 +170,12 @@ def test_ffn_predict_sparse_config0(dev, rng):
 
 
 @pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0])
-def test_ffn_predict_sparse_densities(dev, rng, t):
+@pytest.mark.parametrize("h,ff,rank", [(256, 1024, 32), (160, 1000, 20)])
+def test_ffn_predict_sparse_densities(dev, rng, t, h, ff, rank):
     """The fused predictor -> selection -> gathered FFN at the extremes of
     density: no neuron (a zero output), about half of them (tiles with more
-    active neurons than one round of up rows covers) and every neuron."""
-    h, ff, rank = 256, 1024, 32
+    active neurons than one round of up rows covers) and every neuron; the
+    second shape has a partial last tile and a hidden size of 5 blocks."""
     up, dn = make_sparse_layer(rng, h, ff, t)
     wup, wout = normal(rng, (rank, h), 0.05), normal(rng, (ff, rank), 0.05)
     x, a = normal(rng, h, 1.0), normal(rng, h, 1.0)
