@@ -582,6 +582,27 @@ def test_moe_decode_config3(dev, rng):
         hnd.release()
 
 
+@pytest.mark.parametrize("d,eff,E,k,n_tok", [(64, 96, 64, 8, 3),      # the most experts and slots
+                                           (64, 96, 5, 1, 4),       # top-1
+                                           (256, 128, 16, 4, 40)])  # the GEMM path, k = 4
+def test_moe_expert_and_slot_limits(dev, rng, d, eff, E, k, n_tok):
+    """Routing and combine at the limits of the expert count (64) and slots
+    per token (8), top-1, and a 4-slot batch on the grouped GEMM."""
+    router, gate, up, down = make_moe(rng, d, eff, E, gg.Q4_0)
+    router *= 10
+    hs = upload_moe(dev, router, gate, up, down, d, eff, E, gg.Q4_0)
+    x = normal(rng, (n_tok, d), 1.0)
+    out, ids, w = llg.moe_ffn(dev, *hs, E, k, x)
+    assert ids.shape == (n_tok, k)
+    for i in range(n_tok):
+        ro, rid, rw = R.moe_ffn(router, gate, up, down, gg.Q4_0, d, eff, E, k, x[i])
+        assert np.array_equal(ids[i], rid), i
+        assert np.allclose(w[i], rw, rtol=1e-5, atol=1e-7), i
+        assert max_rel_err(out[i], ro) <= TOL, i
+    for hnd in hs:
+        hnd.release()
+
+
 @pytest.mark.parametrize("n_tok", [16, 77, 200])
 def test_moe_prefill_gemm(dev, rng, n_tok):
     """Batches of >= 16 Q4_0 tokens take the grouped MFMA GEMM path (f16
