@@ -475,6 +475,34 @@ def test_window_step_device_list_out_of_contract(dev, rng):
     b.release()
 
 
+def test_size_limits(dev, rng):
+    """Maximum sizes: a hidden size whose staged x overflows the sparse
+    kernels' LDS, and a row too long for one workgroup when the activation
+    needs it whole, are argument errors; the same long rows without an
+    activation run in column chunks (Q4_0 and the flat Q8_0 layout)."""
+    h, ff = 16384, 64  # 512 blocks of x: more than the sparse kernels stage
+    up, dn = make_sparse_layer(rng, h, ff, gg.Q4_0)
+    b = dev.upload_bundle(up, dn, gg.Q4_0, h, ff)
+    with pytest.raises(llg.LlgError) as e:
+        llg.ffn_sparse_load(dev, b, normal(rng, h, 1.0), np.array([1, 5], np.int32))
+    assert e.value.code == llg.LLG_E_ARG
+    b.release()
+    cols, rows = 36864, 32  # 1152 blocks: 166 KB of staged x for a whole row
+    for t in (gg.Q4_0, gg.Q8_0):
+        w = quant(normal(rng, (rows, cols), 0.02), t)
+        wd = quant(normal(rng, (cols, rows), 0.02), t)
+        mu = dev.upload_matrix(w, t, rows, cols)
+        md = dev.upload_matrix(wd, t, cols, rows)
+        x = normal(rng, cols, 1.0)
+        with pytest.raises(llg.LlgError) as e:
+            llg.ffn_dense(dev, mu, md, x)
+        assert e.value.code == llg.LLG_E_ARG
+        ref = R.matmulvec(np.stack([R.dequantize(w[r], t) for r in range(rows)]), x)
+        assert max_rel_err(dev.matvec_q(mu, x), ref) <= 1e-5
+        mu.release()
+        md.release()
+
+
 def test_short_host_buffers_rejected(dev, rng):
     """A host array shorter than the shape it is passed with is an argument
     error before any copy (the C ABI would read past its end)."""
