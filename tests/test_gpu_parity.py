@@ -724,17 +724,18 @@ def _top2_gap(v):
     return float(s[-1] - s[-2])
 
 
-@pytest.mark.parametrize("n_kv", [1, 2])
-def test_falcon_forward(dev, rng, n_kv):
+@pytest.mark.parametrize("n_kv,t", [(1, gg.Q4_0), (2, gg.Q4_0), (1, gg.Q8_0)])
+def test_falcon_forward(dev, rng, n_kv, t):
     """ForwardFlash token by token against the oracle: logits within the FFN
     bar, per-layer active counts exact (thresholds sit in wide logit gaps),
-    greedy token equal wherever the top-2 logit gap is clear."""
+    greedy token equal wherever the top-2 logit gap is clear.  Q8_0 weights
+    take the flat matvec layout under the LayerNorm prologue."""
     d = dict(FALCON_GPU, n_kv=n_kv)
-    w = make_falcon(rng, d)
+    w = make_falcon(rng, d, t)
     toks = rng.integers(0, d["vocab"], 10)
-    _, nact, thr = ref_falcon_f64(w, d, toks)
-    ref = R.Falcon(d, w, thr)
-    m = llg.FalconModel(dev, d, w, thr)
+    _, nact, thr = ref_falcon_f64(w, d, toks, t=t)
+    ref = R.Falcon(d, w, thr, t)
+    m = llg.FalconModel(dev, d, w, thr, t=t)
     for s, tk in enumerate(toks):
         lg, nxt, na = m.forward(int(tk), s)
         rl, rn = ref.forward(int(tk), s)
