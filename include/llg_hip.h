@@ -62,6 +62,8 @@ enum {
     LLG_E_NOMEM = -6,   /* device or pinned allocation failed */
     LLG_E_HPARAM = -7,  /* invalid MoE hparams (moe_forward.go:38-40) */
     LLG_E_NODEV = -8,   /* null device handle */
+    LLG_E_SCRATCH = -9, /* workload needs more than the fixed scratch of the
+                           allocation-free entry points */
 };
 
 /* ---- device lifecycle: metal_bridge.h:7-10 ------------------------------ */
@@ -222,6 +224,22 @@ int llg_hipd_ffn_predict_sparse(LlgHipDevice dev, int64_t wup, int64_t wout, int
                                 int64_t bundle, const float *d_a, const float *d_x,
                                 float threshold, int act, float *d_out, int32_t *d_active,
                                 int32_t *d_n_active);
+/* Allocation-free form of llg_hipd_ffn_predict_sparse: no counterpart in the
+ * reference.  It is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, results and errors; its kernels take their pair lists,
+ * counts and partials from a fixed array in each GPU's memory (512 KiB per
+ * GPU, held until the process ends) instead of the handle's growable
+ * workspace, and it calls no hipMalloc, hipFree or hipMemset.  A predictor and
+ * bundle whose workspace exceeds the array give LLG_E_SCRATCH (the Falcon-7B
+ * layer, rank 128 x d_ff 18176, needs 150 KiB).  Every call on one GPU shares
+ * the array: calls that overlap on one GPU (from several handles or streams)
+ * race; calls ordered on one stream do not. */
+int llg_hipd_ffn_predict_sparse_noalloc(LlgHipDevice dev, int64_t wup, int64_t wout,
+                                        int64_t bias, int64_t bundle, const float *d_a,
+                                        const float *d_x, float threshold, int act,
+                                        float *d_out, int32_t *d_active,
+                                        int32_t *d_n_active);
 int llg_hipd_matvec_q(LlgHipDevice dev, int64_t mat, const float *d_x, float *d_y);
 int llg_hipd_ffn_dense(LlgHipDevice dev, int64_t up, int64_t down, const float *d_x, int act,
                        float *d_out);

@@ -351,6 +351,25 @@ int llg_hipd_ffn_predict_sparse(LlgHipDevice h, int64_t hwup, int64_t hwout, int
                              d_n_active, ws);
 }
 
+// The same path with its workspace in the GPU's fixed scratch array: no
+// allocation, and nothing in the scratch needs clearing (every slot the
+// kernels read is written earlier in the same call).
+int llg_hipd_ffn_predict_sparse_noalloc(LlgHipDevice h, int64_t hwup, int64_t hwout,
+                                        int64_t hbias, int64_t hb, const float *d_a,
+                                        const float *d_x, float thr, int act, float *d_out,
+                                        int32_t *d_active, int32_t *d_n_active) {
+    LlgDevice *d = llg_dev(h);
+    if (!d) return LLG_E_NODEV;
+    LlgObject *wup, *wout, *bias, *b;
+    int rc = check_fused(d, hwup, hwout, hbias, hb, &wup, &wout, &bias, &b);
+    if (rc) return rc;
+    if (!d_a || !d_x || !d_out) return llg_set_error(d, LLG_E_ARG, "predict_sparse: null pointer");
+    uint8_t *ws = llg_dev_scratch(d, llg_fused_ws_bytes(wup->rows, wout->rows), &rc);
+    if (!ws) return rc;
+    return llg_fused_enqueue(d, wup, wout, bias, b, d_a, d_x, thr, act, d_out, d_active,
+                             d_n_active, ws);
+}
+
 int llg_hip_ffn_predict_sparse(LlgHipDevice h, int64_t hwup, int64_t hwout, int64_t hbias,
                                int64_t hb, const float *a, const float *x, float thr, int act,
                                float *out, int32_t *active, int *n_active) {

@@ -14,6 +14,10 @@ struct LlgDevice {
     int device = 0;
     int cus = 0;
     hipStream_t stream = nullptr;
+    // device address of this GPU's `scratch` array (null if the lookup failed;
+    // scratch_err then holds its error)
+    uint8_t *scratch = nullptr;
+    hipError_t scratch_err = hipSuccess;
     std::unordered_map<int64_t, LlgObject *> objects;
     int64_t next_id = 1;
     void *ws = nullptr;
@@ -22,7 +26,31 @@ struct LlgDevice {
     bool tearing_down = false;  // llg_hip_free: every object is freed in one sweep
 };
 
+// Scratch of the allocation-free entry points: a fixed array in each GPU's
+// memory, held until the process ends.  Host code never passes `scratch`
+// itself to a kernel or copy (in host code the name is only a stand-in): it
+// uses the address hipGetSymbolAddress returns for the current device, kept
+// per device handle (LlgDevice::scratch).  Every call on one GPU shares the
+// array, so calls that overlap on one GPU (several handles or streams) race.
+static __device__ __align__(256) uint8_t scratch[LLG_SCRATCH_BYTES];
+
 LlgDevice *llg_dev(LlgHipDevice h) { return reinterpret_cast<LlgDevice *>(h); }
+
+uint8_t *llg_dev_scratch(LlgDevice *d, size_t bytes, int *rc) {
+    *rc = 0;
+    if (!d->scratch) {
+        *rc = llg_hip_error(d, d->scratch_err, "scratch address lookup at init");
+        return nullptr;
+    }
+    if (bytes > (size_t)LLG_SCRATCH_BYTES) {
+        *rc = llg_set_error(d, LLG_E_SCRATCH,
+                            "needs %zu bytes of scratch, above the fixed %zu of the "
+                            "allocation-free entry points",
+                            bytes, (size_t)LLG_SCRATCH_BYTES);
+        return nullptr;
+    }
+    return d->scratch;
+}
 hipStream_t llg_dev_stream(LlgDevice *d) { return d->stream; }
 int llg_device_id(LlgDevice *d) { return d->device; }
 int llg_cu_count(LlgDevice *d) { return d->cus; }
@@ -247,6 +275,9 @@ LlgHipDevice llg_hip_init(void) {
     if (hipGetDeviceProperties(&prop, d->device) == hipSuccess)
         d->cus = prop.multiProcessorCount;
     if (d->cus <= 0) d->cus = 256;
+    // this device's copy of the scratch array (the device is current here)
+    d->scratch_err = hipGetSymbolAddress(reinterpret_cast<void **>(&d->scratch), HIP_SYMBOL(scratch));
+    if (d->scratch_err != hipSuccess) d->scratch = nullptr;
     return reinterpret_cast<LlgHipDevice>(d);
 }
 

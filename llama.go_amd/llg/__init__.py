@@ -47,6 +47,7 @@ LLG_E_HANDLE = -5
 LLG_E_NOMEM = -6
 LLG_E_HPARAM = -7
 LLG_E_NODEV = -8
+LLG_E_SCRATCH = -9
 
 _i32p = C.POINTER(C.c_int32)
 _f32p = C.POINTER(C.c_float)
@@ -90,6 +91,8 @@ _SIGS = {
     "llg_hipd_predict": (C.c_int, [_vp, _i64, _i64, _i64, _vp, C.c_float, _vp, _vp, _vp]),
     "llg_hipd_ffn_sparse": (C.c_int, [_vp, _i64, _vp, _vp, _vp, C.c_int, _vp]),
     "llg_hipd_ffn_predict_sparse": (
+        C.c_int, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, C.c_float, C.c_int, _vp, _vp, _vp]),
+    "llg_hipd_ffn_predict_sparse_noalloc": (
         C.c_int, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, C.c_float, C.c_int, _vp, _vp, _vp]),
     "llg_hipd_matvec_q": (C.c_int, [_vp, _i64, _vp, _vp]),
     "llg_hipd_ffn_dense": (C.c_int, [_vp, _i64, _i64, _vp, C.c_int, _vp]),

@@ -45,6 +45,6 @@ def test_missing_library_raises(tmp_path):
 def test_error_codes_match_header():
     text = HEADER.read_text()
     for name in ["LLG_E_ARG", "LLG_E_TYPE", "LLG_E_ALIGN", "LLG_E_RANGE", "LLG_E_HANDLE",
-                 "LLG_E_NOMEM", "LLG_E_HPARAM", "LLG_E_NODEV"]:
+                 "LLG_E_NOMEM", "LLG_E_HPARAM", "LLG_E_NODEV", "LLG_E_SCRATCH"]:
         m = re.search(rf"{name}\s*=\s*(-?\d+)", text)
         assert m and int(m.group(1)) == getattr(llg, name)
