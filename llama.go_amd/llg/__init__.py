@@ -527,6 +527,8 @@ class FalconModel:
         self.dev, self.dims = dev, dict(dims)
         h, nh, nkv, hd = dims["hidden"], dims["n_heads"], dims["n_kv"], dims["head_dim"]
         ff, V, L = dims["ff"], dims["vocab"], dims["n_layers"]
+        thr = _f32(thresholds).ravel()
+        _need(thr.size, L, "falcon thresholds")  # the C ABI reads one per layer
         self._h = []
         up = self._keep
 
@@ -556,7 +558,6 @@ class FalconModel:
             lh += [x.id for x in hs]
         d32 = np.array([L, h, nh, nkv, hd, ff, V, dims["max_seq"]], np.int32)
         lh = np.array(lh, np.int64)
-        thr = _f32(thresholds)
         out = C.c_int64()
         dev.check(dev.lib.llg_hip_falcon_create(
             dev.h, _ptr(d32), float(dims["rope_base"]), float(dims["eps"]), act, self.embed.id,
@@ -569,7 +570,8 @@ class FalconModel:
         return hnd
 
     def set_thresholds(self, thresholds):
-        thr = _f32(thresholds)
+        thr = _f32(thresholds).ravel()
+        _need(thr.size, self.dims["n_layers"], "falcon thresholds")
         self.dev.check(self.dev.lib.llg_hip_falcon_set_thresholds(self.dev.h, self.model.id,
                                                                   _ptr(thr)), "thresholds")
 

@@ -130,12 +130,53 @@ int64_t refcpu_dequantize(const uint8_t *raw, int64_t nbytes, int t, float *out)
 }
 
 /* ---- tensor/ops.go ------------------------------------------------------ */
-void refcpu_matmulvec(const float *w, int out_dim, int in_dim, const float *x, float *y) {
-    for (int i = 0; i < out_dim; i++) { /* ops.go:51-58 */
+/* Threads that refcpu_matmulvec splits its rows over (1: the reference's one
+ * goroutine).  Each row's sum keeps its sequential order on whichever thread
+ * computes it, so the results are bit-identical for every setting; more
+ * threads only shorten the tests that run long sequences through the oracle. */
+static int g_threads = 1;
+
+void refcpu_set_threads(int n) { g_threads = n < 1 ? 1 : (n > 64 ? 64 : n); }
+
+static void matmulvec_rows(const float *w, int r0, int r1, int in_dim, const float *x, float *y) {
+    for (int i = r0; i < r1; i++) { /* ops.go:51-58 */
         float sum = 0.0f;
         const float *row = w + (size_t)i * in_dim;
         for (int j = 0; j < in_dim; j++) sum += row[j] * x[j];
         y[i] = sum;
+    }
+}
+
+typedef struct {
+    const float *w, *x;
+    float *y;
+    int r0, r1, in_dim;
+} mv_part;
+
+static void *mv_worker(void *arg) {
+    mv_part *p = (mv_part *)arg;
+    matmulvec_rows(p->w, p->r0, p->r1, p->in_dim, p->x, p->y);
+    return NULL;
+}
+
+void refcpu_matmulvec(const float *w, int out_dim, int in_dim, const float *x, float *y) {
+    const int nt = g_threads;
+    if (nt <= 1 || (int64_t)out_dim * in_dim < (1 << 20) || out_dim < nt) {
+        matmulvec_rows(w, 0, out_dim, in_dim, x, y);
+        return;
+    }
+    mv_part parts[64];
+    pthread_t th[64];
+    int started[64];
+    for (int k = 0; k < nt; k++) {
+        parts[k] = (mv_part){w, x, y, (int)((int64_t)out_dim * k / nt),
+                             (int)((int64_t)out_dim * (k + 1) / nt), in_dim};
+        started[k] = k > 0 && pthread_create(&th[k], NULL, mv_worker, &parts[k]) == 0;
+    }
+    mv_worker(&parts[0]);
+    for (int k = 1; k < nt; k++) {
+        if (started[k]) pthread_join(th[k], NULL);
+        else mv_worker(&parts[k]); /* no thread: this one computes those rows */
     }
 }
 
@@ -762,6 +803,11 @@ static void rope_inplace(float *vec, int n_heads, int head_dim, int pos, float b
 
 int refcpu_falcon_forward(refcpu_falcon *m, int32_t token, int pos, float *logits,
                           int32_t *n_active_out) {
+    return refcpu_falcon_forward_ex(m, token, pos, logits, n_active_out, NULL);
+}
+
+int refcpu_falcon_forward_ex(refcpu_falcon *m, int32_t token, int pos, float *logits,
+                             int32_t *n_active_out, float *pred_logits_out) {
     const refcpu_falcon_params *p = &m->p;
     const int h = p->hidden, hd = p->head_dim, qd = p->n_heads * hd, kvd = p->n_kv * hd;
     if (token < 0 || token >= p->vocab || m->seq_len >= p->max_seq) return -1;
@@ -817,7 +863,9 @@ int refcpu_falcon_forward(refcpu_falcon *m, int32_t token, int pos, float *logit
          * 225-231), sparse FFN on the normed input */
         const int n_act = refcpu_predict(p->pwup + (size_t)l * p->rank * h,
                                          p->pwout + (size_t)l * p->ff * p->rank, NULL, h, p->rank,
-                                         p->ff, attn_out, p->thr[l], active, NULL);
+                                         p->ff, attn_out, p->thr[l], active,
+                                         pred_logits_out ? pred_logits_out + (size_t)l * p->ff
+                                                         : NULL);
         if (n_active_out) n_active_out[l] = n_act;
         refcpu_ffn_sparse_load(p->up + (size_t)l * p->ff * rb_h,
                                p->down_t + (size_t)l * p->ff * rb_h, p->t, h, p->ff, normed,

@@ -47,6 +47,8 @@ int64_t refcpu_dequantize(const uint8_t *raw, int64_t nbytes, int ggml_type, flo
 
 /* tensor/ops.go:39-60 -- y[i] = sum_j w[i*in+j]*x[j], sequential j. */
 void refcpu_matmulvec(const float *w, int out_dim, int in_dim, const float *x, float *y);
+/* Row threads of refcpu_matmulvec (default 1); results are identical for any n. */
+void refcpu_set_threads(int n);
 
 /* tensor/ops.go:168-189 and inference/ffn_flash.go:303-312 */
 void refcpu_relu(float *x, int n);
@@ -173,6 +175,10 @@ void refcpu_falcon_free(refcpu_falcon *m);
  * or SeqLen is out of range. */
 int refcpu_falcon_forward(refcpu_falcon *m, int32_t token, int pos, float *logits,
                           int32_t *n_active_out);
+/* The same, also writing every layer's predictor logits (predictor.go:57-73)
+ * to pred_logits_out [n_layers x ff] when it is not NULL. */
+int refcpu_falcon_forward_ex(refcpu_falcon *m, int32_t token, int pos, float *logits,
+                             int32_t *n_active_out, float *pred_logits_out);
 /* kvcache.go:55-57 (generate.go:94,119 call it after every token). */
 void refcpu_falcon_commit(refcpu_falcon *m);
 /* cmd/generate.go:197-205 */

@@ -12,8 +12,12 @@ from pathlib import Path
 
 import numpy as np
 
+import os
+
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "librefcpu.so"
+# REFCPU_LIB selects another build of the same source (the sanitizer builds of
+# oracle/Makefile, loaded by oracle/sanitize.sh)
+LIB_PATH = Path(os.environ.get("REFCPU_LIB", HERE / "librefcpu.so"))
 
 F32, F16, Q4_0, Q8_0 = 0, 1, 2, 8
 ACT_RELU, ACT_GELU, ACT_SILU = 0, 1, 2
@@ -24,6 +28,7 @@ _SIGS = {
     "refcpu_f16_to_f32": (C.c_float, [C.c_uint16]),
     "refcpu_dequantize": (C.c_int64, [_vp, C.c_int64, C.c_int, _vp]),
     "refcpu_matmulvec": (None, [_vp, C.c_int, C.c_int, _vp, _vp]),
+    "refcpu_set_threads": (None, [C.c_int]),
     "refcpu_activation": (None, [C.c_int, _vp, C.c_int]),
     "refcpu_rmsnorm": (None, [_vp, _vp, _vp, C.c_int, C.c_float]),
     "refcpu_layernorm": (None, [_vp, _vp, _vp, _vp, C.c_int, C.c_float]),
@@ -89,6 +94,13 @@ def _u8(a):
     if hasattr(a, "numpy"):
         a = a.contiguous().cpu().numpy()
     return np.ascontiguousarray(a).view(np.uint8).ravel()
+
+
+def set_threads(n: int) -> None:
+    """Row threads of the oracle's MatMulVec (1 = the reference's single
+    goroutine, the default and what the CPU baseline uses).  Every row keeps
+    its sequential sum, so any n gives bit-identical results."""
+    lib().refcpu_set_threads(int(n))
 
 
 def byte_size(t: int, n: int) -> int:
@@ -304,8 +316,8 @@ class NeuronCache:
                         np.int32)
 
     def __del__(self):
-        if getattr(self, "c", None):
-            lib().refcpu_nc_free(self.c)
+        if getattr(self, "c", None) and _lib is not None:  # the module may be gone at exit
+            _lib.refcpu_nc_free(self.c)
             self.c = None
 
 
@@ -348,6 +360,7 @@ _SIGS.update({
     "refcpu_falcon_new": (_vp, [C.POINTER(_FalconParams)]),
     "refcpu_falcon_free": (None, [_vp]),
     "refcpu_falcon_forward": (C.c_int, [_vp, C.c_int32, C.c_int, _vp, _vp]),
+    "refcpu_falcon_forward_ex": (C.c_int, [_vp, C.c_int32, C.c_int, _vp, _vp, _vp]),
     "refcpu_falcon_commit": (None, [_vp]),
     "refcpu_argmax": (C.c_int, [_vp, C.c_int]),
 })
@@ -379,23 +392,25 @@ class Falcon:
         p.rope_base, p.eps = float(dims["rope_base"]), float(dims["eps"])
         for k, a in self._keep.items():
             setattr(p, k, a.ctypes.data)
-        self.vocab, self.n_layers = int(dims["vocab"]), int(dims["n_layers"])
+        self.vocab, self.n_layers, self.ff = int(dims["vocab"]), int(dims["n_layers"]), int(dims["ff"])
         self.m = lib().refcpu_falcon_new(C.byref(p))
         if not self.m:
             raise MemoryError("refcpu_falcon_new failed")
 
-    def forward(self, token: int, pos: int):
-        """ForwardFlash(token, pos) -> (logits, n_active per layer); then commit."""
+    def forward(self, token: int, pos: int, pred_logits: bool = False):
+        """ForwardFlash(token, pos) -> (logits, n_active per layer[, predictor
+        logits [n_layers x ff]]); then commit."""
         lg = np.empty(self.vocab, np.float32)
         na = np.empty(self.n_layers, np.int32)
-        if lib().refcpu_falcon_forward(self.m, token, pos, _p(lg), _p(na)):
+        pl = np.empty((self.n_layers, self.ff), np.float32) if pred_logits else None
+        if lib().refcpu_falcon_forward_ex(self.m, token, pos, _p(lg), _p(na), _p(pl)):
             raise ValueError("falcon forward: token or position out of range")
         lib().refcpu_falcon_commit(self.m)
-        return lg, na
+        return (lg, na, pl) if pred_logits else (lg, na)
 
     def __del__(self):
-        if getattr(self, "m", None):
-            lib().refcpu_falcon_free(self.m)
+        if getattr(self, "m", None) and _lib is not None:  # the module may be gone at exit
+            _lib.refcpu_falcon_free(self.m)
             self.m = None
 
 

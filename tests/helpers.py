@@ -74,9 +74,10 @@ def window_sets(rng, ff: int, n_active: int, steps: int, carry: float):
 
 
 # ---------------------------------------------------------------- Falcon decode
-def make_falcon(rng, d: dict, t: int = gg.Q4_0) -> dict:
+def make_falcon(rng, d: dict, t: int = gg.Q4_0, std: float = 0.05) -> dict:
     """Random Falcon-layout weights (GGUF bytes for the matrices, f32 for the
-    norms and predictors); the norms are random so that weight and bias count."""
+    norms and predictors); the norms are random so that weight and bias count.
+    `std`: the attention and FFN matrices are N(0, std)."""
     h, nh, nkv, hd, ff = d["hidden"], d["n_heads"], d["n_kv"], d["head_dim"], d["ff"]
     V, r, L = d["vocab"], d["rank"], d["n_layers"]
     w = {"embed": quant(normal(rng, (V, h), 0.5), t), "lm_head": quant(normal(rng, (V, h), 0.05), t),
@@ -86,14 +87,14 @@ def make_falcon(rng, d: dict, t: int = gg.Q4_0) -> dict:
     for _ in range(L):
         w["norm_w"].append(1.0 + normal(rng, h, 0.1))
         w["norm_b"].append(normal(rng, h, 0.1))
-        w["wq"].append(quant(normal(rng, (nh * hd, h), 0.05), t))
-        w["wk"].append(quant(normal(rng, (nkv * hd, h), 0.05), t))
-        w["wv"].append(quant(normal(rng, (nkv * hd, h), 0.05), t))
-        w["wo"].append(quant(normal(rng, (h, nh * hd), 0.05), t))
+        w["wq"].append(quant(normal(rng, (nh * hd, h), std), t))
+        w["wk"].append(quant(normal(rng, (nkv * hd, h), std), t))
+        w["wv"].append(quant(normal(rng, (nkv * hd, h), std), t))
+        w["wo"].append(quant(normal(rng, (h, nh * hd), std), t))
         w["pwup"].append(normal(rng, (r, h), 0.05))
         w["pwout"].append(normal(rng, (ff, r), 0.05))
-        w["up"].append(quant(normal(rng, (ff, h), 0.05), t))
-        w["down_t"].append(quant(normal(rng, (ff, h), 0.05), t))
+        w["up"].append(quant(normal(rng, (ff, h), std), t))
+        w["down_t"].append(quant(normal(rng, (ff, h), std), t))
     return w
 
 
@@ -110,10 +111,12 @@ def _gap_threshold(lg: np.ndarray, frac: float) -> float:
     return float(np.float32((s[i - 1] + s[i]) / 2))
 
 
-def ref_falcon_f64(w: dict, d: dict, tokens, frac: float = 0.1, t: int = gg.Q4_0):
+def ref_falcon_f64(w: dict, d: dict, tokens, frac: float = 0.1, t: int = gg.Q4_0,
+                   pred_logits: bool = False):
     """float64 ForwardFlash over a token sequence (positions 0..T-1), layer by
     layer over all tokens; each layer's threshold is picked at a wide gap of its
-    predictor logits.  Returns (logits [T x V], n_active [T x L], thresholds)."""
+    predictor logits.  Returns (logits [T x V], n_active [T x L], thresholds),
+    and with pred_logits also the predictor logits [T x L x ff]."""
     h, nh, nkv, hd, ff = d["hidden"], d["n_heads"], d["n_kv"], d["head_dim"], d["ff"]
     L, eps, base = d["n_layers"], d["eps"], d["rope_base"]
     dq = lambda raw, cols: deq(raw, t, cols).astype(np.float64)
@@ -140,7 +143,7 @@ def ref_falcon_f64(w: dict, d: dict, tokens, frac: float = 0.1, t: int = gg.Q4_0
             M[s, :, half:] = x0 * sn + x1 * c
         return M
 
-    thr, nact = [], np.zeros((T, L), np.int64)
+    thr, nact, plg = [], np.zeros((T, L), np.int64), []
     for l in range(L):
         N = ln(X, w["norm_w"][l], w["norm_b"][l])
         Q = rope(N @ dq(w["wq"][l], h).T, nh)
@@ -156,6 +159,7 @@ def ref_falcon_f64(w: dict, d: dict, tokens, frac: float = 0.1, t: int = gg.Q4_0
                 att[s, head] = p @ Vv[:s + 1, kvh]
         A = att.reshape(T, nh * hd) @ dq(w["wo"][l], nh * hd).T
         lg = np.maximum(A @ w["pwup"][l].T.astype(np.float64), 0.0) @ w["pwout"][l].T.astype(np.float64)
+        plg.append(lg)
         th = _gap_threshold(lg, frac)
         thr.append(th)
         on = lg > th
@@ -163,4 +167,6 @@ def ref_falcon_f64(w: dict, d: dict, tokens, frac: float = 0.1, t: int = gg.Q4_0
         U = np.maximum(N @ dq(w["up"][l], h).T, 0.0) * on
         X = X + A + U @ dq(w["down_t"][l], h)
     out = ln(X, w["out_w"], w["out_b"]) @ dq(w["lm_head"], h).T
+    if pred_logits:
+        return out, nact, np.array(thr, np.float32), np.stack(plg, 1)
     return out, nact, np.array(thr, np.float32)

@@ -48,3 +48,19 @@ def test_error_codes_match_header():
                  "LLG_E_NOMEM", "LLG_E_HPARAM", "LLG_E_NODEV", "LLG_E_SCRATCH"]:
         m = re.search(rf"{name}\s*=\s*(-?\d+)", text)
         assert m and int(m.group(1)) == getattr(llg, name)
+
+
+def test_falcon_thresholds_length_checked():
+    """The C ABI reads one threshold per layer: a shorter or longer list (or a
+    scalar for a multi-layer model) is rejected before any device call."""
+    dims = dict(n_layers=2, hidden=64, n_heads=1, n_kv=1, head_dim=64, ff=128, vocab=8,
+                max_seq=4, rope_base=10000.0, eps=1e-5)
+    for bad in ([0.5], [0.1, 0.2, 0.3], 0.5):
+        with pytest.raises(llg.LlgError) as e:
+            llg.FalconModel(None, dims, {}, bad)
+        assert e.value.code == llg.LLG_E_ARG
+    m = llg.FalconModel.__new__(llg.FalconModel)
+    m.dev, m.dims = None, dims
+    with pytest.raises(llg.LlgError) as e:
+        m.set_thresholds([0.5])
+    assert e.value.code == llg.LLG_E_ARG

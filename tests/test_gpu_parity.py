@@ -125,10 +125,18 @@ def test_ffn_sparse_config0(dev, rng, t):
     got = llg.ffn_sparse_load(dev, b, x, active)
     ref = R.ffn_sparse_load(up, dn, t, h, ff, x, active)
     assert max_rel_err(got, ref) <= TOL
-    # unsorted and repeated indices are accepted like the reference's []int
+    # unsorted indices are accepted like the reference's []int, and a
+    # repeated index adds its neuron once per occurrence (ffn_flash.go:262-298
+    # reads and accumulates every listed row)
     perm = active[::-1].copy()
     assert max_rel_err(llg.ffn_sparse_load(dev, b, x, perm),
                        R.ffn_sparse_load(up, dn, t, h, ff, x, perm)) <= TOL
+    rep = np.concatenate([active[:300], active[100:200], active[:50], active[300:]])
+    rep = rep[rng.permutation(rep.size)].astype(np.int32)
+    got = llg.ffn_sparse_load(dev, b, x, rep)
+    ref_rep = R.ffn_sparse_load(up, dn, t, h, ff, x, rep)
+    assert max_rel_err(got, ref_rep) <= TOL
+    assert max_rel_err(ref_rep, ref) > 10 * TOL  # the repeats do count
     b.release()
 
 
@@ -210,16 +218,19 @@ def test_matvec_q_small(dev, rng, t):
 
 
 @pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16])
-def test_ffn_dense_config1(dev, rng, t):
-    """Dense naive path (window=0): full up matvec, ReLU, full down matvec."""
+@pytest.mark.parametrize("act", [gg.ACT_RELU, gg.ACT_GELU])
+def test_ffn_dense_config1(dev, rng, t, act):
+    """Dense naive path (window=0): full up matvec, the activation, full down
+    matvec; ReLU (ffnReLU, forward.go:342-353) and GELU (ffnGELU, :355-366,
+    the activation Falcon's loader picks, loader.go:57-58)."""
     h, ff = 4544, 18176
     up = gpu_quant((ff, h), 0.02, 31, t)
     down = gpu_quant((h, ff), 0.02, 32, t)
     x = normal(rng, h, 1.0)
     u = dev.upload_matrix(up, t, ff, h)
     d = dev.upload_matrix(down, t, h, ff)
-    got = llg.ffn_dense(dev, u, d, x)
-    ref = R.ffn_dense(up, down, t, h, ff, x)
+    got = llg.ffn_dense(dev, u, d, x, act)
+    ref = R.ffn_dense(up, down, t, h, ff, x, act)
     assert max_rel_err(got, ref) <= TOL
     u.release()
     d.release()

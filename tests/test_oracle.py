@@ -443,16 +443,19 @@ def test_falcon_forward_f64(rng, n_kv):
     """ForwardFlash restatement against a float64 brute force over 7 tokens:
     LayerNorm, RoPE at each position, MQA/GQA/MHA head mapping, causal softmax
     attention over the KV cache, predictor selection on the attention output,
-    the sparse FFN on the normed input, the parallel residual and the LM head."""
+    the sparse FFN on the normed input, the parallel residual and the LM head.
+    The predictor logits it reports (every layer's) match the brute force's."""
     d = dict(FALCON_TINY, n_kv=n_kv)
     w = make_falcon(rng, d)
     toks = rng.integers(0, d["vocab"], 7)
-    ref, nact, thr = ref_falcon_f64(w, d, toks)
+    ref, nact, thr, plg = ref_falcon_f64(w, d, toks, pred_logits=True)
     m = R.Falcon(d, w, thr)
     for s, tk in enumerate(toks):
-        lg, na = m.forward(int(tk), s)
+        lg, na, pl = m.forward(int(tk), s, pred_logits=True)
         assert np.array_equal(na, nact[s]), (s, na, nact[s])
         assert np.max(np.abs(lg - ref[s])) <= 1e-4 * np.max(np.abs(ref[s])), s
+        assert np.max(np.abs(pl - plg[s])) <= 1e-5 * np.max(np.abs(plg[s])), s
+        assert np.array_equal((pl > thr[:, None]).sum(1), na)
     assert 0 < nact.mean() < d["ff"]
 
 
@@ -507,3 +510,20 @@ def test_falcon_kv_and_argmax(rng):
     assert R.argmax(np.array([1, 3, 3, 2], np.float32)) == 1
     assert R.argmax(np.array([np.nan, 3, 5], np.float32)) == 0
     assert R.argmax(np.array([1, np.nan, 5], np.float32)) == 2
+
+
+def test_matmulvec_threads_bit_identical():
+    """set_threads splits MatMulVec's rows over threads; each row keeps its
+    sequential sum (ops.go:51-58), so every thread count gives the same bits."""
+    rng = np.random.default_rng(5)
+    w = rng.standard_normal((2053, 1031)).astype(np.float32)
+    x = rng.standard_normal(1031).astype(np.float32)
+    one = R.matmulvec(w, x)
+    try:
+        for n in (2, 7, 16):
+            R.set_threads(n)
+            assert np.array_equal(R.matmulvec(w, x), one)
+    finally:
+        R.set_threads(1)
+    ref = (w.astype(np.float64) @ x.astype(np.float64))
+    assert np.max(np.abs(one - ref)) <= 1e-4 * np.max(np.abs(ref))
