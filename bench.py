@@ -70,11 +70,6 @@ class Timer:
         return e
 
 
-def threshold_for(logits: np.ndarray, n: int) -> float:
-    s = np.sort(logits.astype(np.float32))[::-1]
-    return float(np.float32((np.float64(s[n - 1]) + np.float64(s[n])) / 2))
-
-
 def bench_sparse(args, torch, llg, dev):
     gg = llg.gguf
     L = args.layers
@@ -86,11 +81,7 @@ def bench_sparse(args, torch, llg, dev):
     wup = (torch.randn((RANK, H), generator=g, device="cuda") * 0.05).contiguous()
     wout = (torch.randn((FF, RANK), generator=g, device="cuda") * 0.05).contiguous()
     n_x = 64
-    X = torch.randn((n_x, H), generator=g, device="cuda").contiguous()
-    # threshold: midpoint of the 909th/910th largest logit for the first token
-    hid = torch.relu(wup.double() @ X[0].double())
-    lg = (wout.double() @ hid).float().cpu().numpy()
-    thr = threshold_for(lg, N_ACTIVE)
+    X, thrs = exact_active_inputs(torch, g, wup, wout, n_x)
     torch.cuda.synchronize()  # the library's stream does not wait on torch's
     bundles, wups, wouts = [], [], []
     for _ in range(L):
@@ -108,8 +99,8 @@ def bench_sparse(args, torch, llg, dev):
         l = i % L
         x = X[i % n_x]
         rc = lib.llg_hipd_ffn_predict_sparse(dev.h, wups[l].id, wouts[l].id, 0, bundles[l].id,
-                                             vp(x), vp(x), thr, gg.ACT_RELU, vp(out[i % n_x]),
-                                             None, vp(nstep[i]))
+                                             vp(x), vp(x), float(thrs[i % n_x]), gg.ACT_RELU,
+                                             vp(out[i % n_x]), None, vp(nstep[i]))
         if rc:
             dev.check(rc, "ffn_predict_sparse")
 
@@ -124,8 +115,8 @@ def bench_sparse(args, torch, llg, dev):
     def pred_only(i):
         """Predictor.Predict with the ascending active list (3 launches)."""
         l = i % L
-        rc = lib.llg_hipd_predict(dev.h, wups[l].id, wouts[l].id, 0, vp(X[l % n_x]), thr,
-                                  vp(act[l]), vp(nact[l]), None)
+        rc = lib.llg_hipd_predict(dev.h, wups[l].id, wouts[l].id, 0, vp(X[l % n_x]),
+                                  float(thrs[l % n_x]), vp(act[l]), vp(nact[l]), None)
         if rc:
             dev.check(rc, "predict")
 
@@ -173,7 +164,9 @@ def bench_sparse(args, torch, llg, dev):
         "dtype": "f32",
         "config": {"workload": "falcon7b-ffn-layer-q4_0-5pct-sparse-decode", "d_model": H,
                    "d_ff": FF, "predictor_rank": RANK, "weights": "Q4_0 bundled",
-                   "target_active": N_ACTIVE, "mean_active": mean_active, "batch": 1,
+                   "target_active": N_ACTIVE, "mean_active": mean_active,
+                   "threshold": "per token: fp32 midpoint of its 909th and 910th largest "
+                                "predictor logit", "batch": 1,
                    "layer_copies_rotated": L, "step": "predict+select+gathered up/down FFN"},
         "roofline": {"bound": "hbm",
                      "kernel": "k_pred_hidden + k_tile_up + k_sparse_down (one decode step)",
@@ -192,8 +185,41 @@ def bench_sparse(args, torch, llg, dev):
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline_sparse(args, up.cpu().numpy(), dn.cpu().numpy(),
                                                   wup.cpu().numpy(), wout.cpu().numpy(),
-                                                  X.cpu().numpy(), thr)
+                                                  X.cpu().numpy(), thrs)
     return res
+
+
+def exact_active_inputs(torch, g, wup, wout, n_x):
+    """n_x inputs x ~ N(0, 1) and, per input, the threshold that activates
+    exactly N_ACTIVE neurons: the fp32 midpoint of its N_ACTIVE-th and
+    (N_ACTIVE+1)-th largest predictor logit (float64 on the device).  Inputs
+    whose two logits lie closer than 1e-4 of the logits' standard deviation
+    are skipped, so that fp32 reordering in the kernels cannot move a neuron
+    across the threshold."""
+    cand = torch.randn((2 * n_x, H), generator=g, device="cuda")
+    hid = torch.relu(wup.double() @ cand.double().T)        # [rank, 2 n_x]
+    lg = wout.double() @ hid                                 # [FF, 2 n_x]
+    top = torch.topk(lg, N_ACTIVE + 1, dim=0).values
+    a, b = top[N_ACTIVE - 1], top[N_ACTIVE]
+    keep = torch.nonzero((a - b) > 1e-4 * lg.std(dim=0)).flatten()[:n_x]
+    if keep.numel() < n_x:
+        raise RuntimeError("too few inputs with a clear 909/910 logit gap")
+    thrs = ((a + b) / 2)[keep].float().cpu().numpy()
+    return cand[keep].contiguous(), thrs
+
+
+def host_cpu() -> dict:
+    """The host's CPU model, its logical CPUs and those this process may use."""
+    model = "unknown"
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "usable_cpus": len(os.sched_getaffinity(0)),
+            "cpu_model": model}
 
 
 def layer_file(up, dn, t):
@@ -228,7 +254,7 @@ def timed_loop(fn, seconds, max_n):
             return n, el
 
 
-def cpu_baseline_sparse(args, up, dn, wup, wout, X, thr):
+def cpu_baseline_sparse(args, up, dn, wup, wout, X, thrs):
     """The oracle's restatement of ffnFlash path 2 (predictor.go:51-83 +
     ffn_flash.go:254-299) on a bounded sample of tokens.  Reported: the
     reference's own arrangement, rows read from a page-cached GGUF file by a
@@ -243,7 +269,7 @@ def cpu_baseline_sparse(args, up, dn, wup, wout, X, thr):
 
         def faithful(i):
             x = X[i % X.shape[0]]
-            active, _ = R.predict(wup, wout, None, x, thr)
+            active, _ = R.predict(wup, wout, None, x, float(thrs[i % X.shape[0]]))
             R.ffn_sparse_load_file(path, off_up, off_dn, R.Q4_0, H, FF, x, active, nthreads=32)
 
         n, el = timed_loop(faithful, args.cpu_seconds, args.cpu_max_tokens)
@@ -253,12 +279,13 @@ def cpu_baseline_sparse(args, up, dn, wup, wout, X, thr):
 
     def in_memory(i):
         x = X[i % X.shape[0]]
-        active, _ = R.predict(wup, wout, None, x, thr)
+        active, _ = R.predict(wup, wout, None, x, float(thrs[i % X.shape[0]]))
         R.ffn_sparse_load(up, dn, R.Q4_0, H, FF, x, active)
 
     n2, el2 = timed_loop(in_memory, args.cpu_seconds / 3, args.cpu_max_tokens)
     return {"value": n / el, "unit": "tokens/s", "cores": 32, "kind": "port",
-            "compute_only": n2 / el2,
+            "threads": "32 row-read threads (pread + dequant) and 1 arithmetic thread",
+            **host_cpu(), "compute_only": n2 / el2,
             "sample": f"{n} decode tokens of the same layer (predict + sparse FFN), {el:.1f} s: "
                       f"up/down rows read from a page-cached GGUF file by a 32-thread pread pool "
                       f"with per-row dequant (ReadRowsParallel), arithmetic on 1 thread; rows in "
@@ -487,7 +514,8 @@ def cpu_baseline_window(args, up, dn, X, sets):
     log("cpu baseline: the same with rows in memory, 1 thread")
     n2, el2 = run(lambda: R.NeuronCache(FF, H, WIN_K, FF, up, dn, R.Q4_0), args.cpu_seconds / 3)
     return {"value": n / el, "unit": "tokens/s", "cores": 32, "kind": "port",
-            "compute_only": n2 / el2,
+            "threads": "32 row-read threads (pread + dequant) and 1 arithmetic thread",
+            **host_cpu(), "compute_only": n2 / el2,
             "sample": f"{n} window decode tokens (Update + FFNForward, k={WIN_K}), {el:.1f} s: "
                       f"new rows read from a page-cached GGUF file by a 32-thread pread pool "
                       f"(loadRows), arithmetic on 1 thread; rows in memory on 1 thread: "
@@ -633,7 +661,7 @@ def cpu_baseline_falcon(args, d, w, thr, prompt):
         el = time.perf_counter() - t0
         if el >= args.cpu_seconds:
             break
-    return {"value": n / el, "unit": "tokens/s", "cores": 1, "kind": "port",
+    return {"value": n / el, "unit": "tokens/s", "cores": 1, "kind": "port", **host_cpu(),
             "sample": f"{n} tokens of the prompt through the 32-layer model (positions 0-{n - 1}), "
                       f"{el:.1f} s, weights in host memory"}
 
@@ -743,7 +771,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     if args.layers <= 0:
-        args.layers = {"sparse": 128, "window": 16, "moe-decode": 2,
+        args.layers = {"sparse": 128, "window": 16, "moe-decode": 8,
                        "moe-prefill": 1}.get(args.workload, 6)
 
     import torch

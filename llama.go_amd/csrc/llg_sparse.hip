@@ -4,13 +4,15 @@
 // Two ways in:
 //
 //  A. predictor-fused step (ffnFlash path 2, ffn_flash.go:225-231), 3 launches:
-//     K1 k_pred_hidden (llg_predictor.hip): hidden partials; zeroes out/counters
+//     K1 k_pred_hidden (llg_predictor.hip): hidden partials (and x += attn_out
+//        for a caller that accumulates into a residual)
 //     K2 k_tile_up: one workgroup per 64-neuron tile: logits from WOut rows,
 //        strict '>' against the threshold via a wavefront ballot, then the up
 //        dot product of each of the tile's active neurons, u = act(up . x),
 //        one neuron per wavefront of 8 (two when more than 8 are active);
-//        nonzero u go to the tile's own 64 pair slots (an LDS counter orders
-//        them), so no two workgroups touch one address
+//        active neuron k of the tile (ascending) goes to the tile's pair
+//        slot k, so no two workgroups touch one address and the slot order
+//        is fixed
 //     K3 k_sparse_down over the tiles' pairs
 //  B. explicit active list (ffnSparseLoad, NeuronCache.FFNForward), 2 launches:
 //     k_list_up: one wavefront per listed neuron, pair j = (row, u_j)
@@ -21,23 +23,24 @@
 // 64 distinct banks.  Every lane issues the loads of all its blocks before it
 // uses any of them.
 //
-// k_sparse_down: workgroup (slice s of 8 blocks = 256 outputs, pair group g);
-// the four wavefronts split the group's pairs, 8 pairs per wavefront pass
-// (lane = pair sub-index * 8 + block); u == 0 rows are skipped as at
-// ffn_flash.go:290; the per-slice sums are reduced across lanes (one DPP step)
-// and through LDS, and added to out with one fp32 atomic per output.  blockIdx -> (s, g) keeps all
-// slices of a group on one XCD (workgroups go round-robin over the 8 XCDs).
+// k_sparse_down: one workgroup per output block of 32 outputs reads every
+// pair (thread = tile, or a stride of the list), so no output is summed
+// across workgroups: no atomics, and the summation order is fixed (each
+// thread adds its pairs in slot order, then a fixed shuffle/DPP transpose
+// reduction per wavefront and an ordered sum over the wavefronts).  Results
+// are bit-identical from run to run.  u == 0 rows are skipped as at
+// ffn_flash.go:290.  blockIdx -> block keeps neighbouring blocks (which
+// share the rows' cache lines) on one XCD (workgroups go round-robin over
+// the 8 XCDs).
 #include "llg_common.hpp"
 #include "llg_internal.hpp"
 #include "llg_pred_tile.hpp"
 
 #define XS_STRIDE 36      // floats per staged 32-float x block (bank-conflict-free)
-#define DN_SLICE 8        // blocks per down slice
 #define BATCH 4           // blocks whose loads a lane issues together
 #define PRED_SPLIT_N 8    // partials per hidden unit written by k_pred_hidden
-#define DN_HEAD 8         // pair slots per tile that k_sparse_down reads with the counts
-#define DN_RED_ST 36      // LDS floats per (row, block) partial in the down reduction
 #define TILE_THREADS 512  // k_tile_up workgroup: 8 wavefronts for the up rows
+#define DN_THREADS 512    // k_sparse_down workgroup: one tile (or list stride) per thread
 
 __device__ __forceinline__ void stage_x(float *xs, const float *__restrict__ x, int nb) {
     llg_stage_x_sum<XS_STRIDE>(xs, x, nb);
@@ -181,12 +184,13 @@ __device__ __forceinline__ void row_dotn(const uint8_t *__restrict__ base, long 
     for (int q = 0; q < NR; q++) s[q] = llg_wave_sum(s[q]);
 }
 
-// One round of the tile's up rows: neuron k0 + wave + nw*i (i < NR) on this
-// wavefront; nonzero u go to the tile's pair slots through the LDS counter.
+// One round of the tile's up rows: active neuron k = k0 + wave + nw*i (i <
+// NR) of the tile on this wavefront; its pair (row, u) goes to the tile's
+// slot k (a zero activation is kept, and k_sparse_down skips it).
 template <int T, int NR>
 __device__ __forceinline__ void tile_up_round(const uint8_t *__restrict__ base, long long bstride,
                                               const RowFmt &f, const float *xs, const int *tl,
-                                              int *ctr, int cnt, int k0, int tile0, int act,
+                                              int cnt, int k0, int tile0, int act,
                                               int2 *__restrict__ tpairs) {
     const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     int rows[NR];
@@ -202,16 +206,12 @@ __device__ __forceinline__ void tile_up_round(const uint8_t *__restrict__ base, 
 #pragma unroll
         for (int i = 0; i < NR; i++) {
             if (rows[i] < 0) break;
-            const float u = llg_act(act, s[i]);
-            if (u != 0.0f) {  // ffn_flash.go:290 skips zero activations
-                const int pos = atomicAdd(ctr, 1);  // LDS atomic, tile-local slot
-                tpairs[pos] = make_int2(rows[i], __float_as_int(u));
-            }
+            tpairs[k0 + wave + nw * i] = make_int2(rows[i], __float_as_int(llg_act(act, s[i])));
         }
     }
 }
 
-// B. explicit list: pair j = (row of active[j], act(up . x)); also zeroes out.
+// B. explicit list: pair j = (row of active[j], act(up . x)).
 // With src (windowed rows): a neuron n with fresh[n] == epoch (loaded by this
 // token's update) is read from row n of src, and its whole bundle is copied
 // to its resident row on the way (the gather of loadRows, window.go:207-245,
@@ -226,11 +226,9 @@ __global__ __launch_bounds__(256) void k_list_up(
     const uint8_t *base, long long bstride, RowFmt f, const int32_t *__restrict__ slot_of,
     const float *__restrict__ x, const int32_t *__restrict__ active,
     const int32_t *__restrict__ n_active_p, int cap, int n_rows, int act,
-    int2 *__restrict__ pairs, float *__restrict__ out, LlgFreshRows fr) {
+    int2 *__restrict__ pairs, LlgFreshRows fr) {
     extern __shared__ float xs[];
     const int n_active = min(max(*n_active_p, 0), cap);
-    const int gtid = blockIdx.x * blockDim.x + threadIdx.x;
-    for (int i = gtid; i < f.cols; i += gridDim.x * blockDim.x) out[i] = 0.0f;
     const int first = blockIdx.x * 4;
     if (first >= n_active) return;  // whole workgroup idle: skip the x staging
     stage_x(xs, x, f.nb);
@@ -284,20 +282,48 @@ __global__ __launch_bounds__(256) void k_list_up(
     }
 }
 
-// A. predictor-fused tile kernel.  Tile t writes its nonzero (row, u) pairs
-// to pairs[t*64 + k], k < tile_cnt[t]: fixed slots, so no global counter.
+// Sum of v[0..31] over the wavefront by halving exchanges: at each step a
+// lane keeps half of its values and adds the partner's copy of that half.
+// The partners are lane ^ 32, ^ 16, ^ 8, ^ 7, ^ 2 and ^ 1: each step's
+// partner agrees in the lane bits that already chose the half (so it holds
+// the same elements) and covers a disjoint set of lanes.  Lane l returns the
+// total of element l >> 1.  The exchange pattern is fixed, so the result is
+// the same on every run.
+__device__ __forceinline__ float dn_wave_transpose_sum(const float (&v)[32]) {
+    const int lane = threadIdx.x & 63;
+    float a[16], b[8], c[4], d[2];
+    const bool h5 = lane & 32, h4 = lane & 16, h3 = lane & 8, h2 = lane & 4, h1 = lane & 2;
+#pragma unroll
+    for (int m = 0; m < 16; m++)
+        a[m] = (h5 ? v[m + 16] : v[m]) + __shfl_xor(h5 ? v[m] : v[m + 16], 32, 64);
+#pragma unroll
+    for (int m = 0; m < 8; m++)
+        b[m] = (h4 ? a[m + 8] : a[m]) + __shfl_xor(h4 ? a[m] : a[m + 8], 16, 64);
+#pragma unroll
+    for (int m = 0; m < 4; m++)  // row_ror:8 pairs lanes that differ in bit 3
+        c[m] = (h3 ? b[m + 4] : b[m]) + llg_dpp<0x128>(h3 ? b[m] : b[m + 4]);
+#pragma unroll
+    for (int m = 0; m < 2; m++)  // row_half_mirror pairs lane i with i ^ 7: bit 2 differs,
+                                 // bits 3-5 (the element so far) agree
+        d[m] = (h2 ? c[m + 2] : c[m]) + llg_dpp<0x141>(h2 ? c[m] : c[m + 2]);
+    const float e = (h1 ? d[1] : d[0]) + llg_dpp<0x4E>(h1 ? d[0] : d[1]);  // bit 1
+    return e + llg_dpp<0xB1>(e);                                           // bit 0
+}
+
+// A. predictor-fused tile kernel.  Tile t writes its active mask (bit i:
+// neuron 64 t + i) to mask[t] and the (row, u) pair of its k-th active
+// neuron (ascending) to pairs[t*64 + k].
 template <int T>
 __global__ __launch_bounds__(TILE_THREADS, 2) void k_tile_up(
     const uint8_t *__restrict__ wout, long long wstride, int ff, int rank,
     const float *__restrict__ partial, const float *__restrict__ bias, float thr,
     const uint8_t *__restrict__ base, long long bstride, RowFmt f, const float *__restrict__ x,
-    int act, unsigned long long *__restrict__ mask, int2 *__restrict__ pairs,
-    int32_t *__restrict__ tile_cnt) {
+    int act, unsigned long long *__restrict__ mask, int2 *__restrict__ pairs) {
     extern __shared__ float sh[];
     float *xs = sh;                                     // nb * XS_STRIDE
     float *hid = xs + f.nb * XS_STRIDE;                 // rank (16-byte aligned)
     float *lg = hid + ((rank + 3) & ~3);                // 64
-    int *tl = reinterpret_cast<int *>(lg + 64);         // 64 tile-local indices, count, nnz
+    int *tl = reinterpret_cast<int *>(lg + 64);         // 64 tile-local indices, count
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int tile0 = blockIdx.x * 64;
@@ -321,8 +347,7 @@ __global__ __launch_bounds__(TILE_THREADS, 2) void k_tile_up(
         if (on) tl[before] = lane;
         if (lane == 0) {
             tl[64] = __popcll(m);
-            tl[65] = 0;
-            if (mask) mask[blockIdx.x] = m;
+            mask[blockIdx.x] = m;
         }
     }
     __syncthreads();
@@ -334,134 +359,172 @@ __global__ __launch_bounds__(TILE_THREADS, 2) void k_tile_up(
     int2 *tpairs = pairs + (size_t)blockIdx.x * 64;
     if (cnt <= nw || UPMAX == 1) {
         for (int k0 = 0; k0 < cnt; k0 += nw)
-            tile_up_round<T, 1>(base, bstride, f, xs, tl, &tl[65], cnt, k0, tile0, act, tpairs);
+            tile_up_round<T, 1>(base, bstride, f, xs, tl, cnt, k0, tile0, act, tpairs);
     } else {
         if constexpr (UPMAX == 2)
             for (int k0 = 0; k0 < cnt; k0 += 2 * nw)
-                tile_up_round<T, 2>(base, bstride, f, xs, tl, &tl[65], cnt, k0, tile0, act, tpairs);
+                tile_up_round<T, 2>(base, bstride, f, xs, tl, cnt, k0, tile0, act, tpairs);
     }
-    __syncthreads();
-    if (threadIdx.x == 0) tile_cnt[blockIdx.x] = tl[65];
 }
 
-// Pairs come either as a plain list pairs[0..*count) (TILED = false; the
-// count is clamped to the capacity n_tiles) or in
-// per-tile slots pairs[t*64 + k], k < tile_cnt[t] (TILED = true); for the
-// latter, group g owns tiles [g*tg, (g+1)*tg) and its workgroups enumerate
-// them through a prefix sum of the counts.  With TILED, workgroup 0 also
-// writes the number of active neurons (popcounts of the tile masks).
-template <int T, bool TILED>
-__global__ __launch_bounds__(256) void k_sparse_down(
-    const uint8_t *__restrict__ base, long long bstride, RowFmt f, const int2 *__restrict__ pairs,
-    const int32_t *__restrict__ count_p, const int32_t *__restrict__ tile_cnt, int n_tiles,
-    const unsigned long long *__restrict__ mask, int32_t *__restrict__ n_active_out,
-    int n_slices, int n_groups, float *__restrict__ out) {
-    __shared__ __attribute__((aligned(16))) float red[16 * DN_SLICE * DN_RED_ST];
-    __shared__ int pref[65];
-    __shared__ int2 head[64 * DN_HEAD];  // the first DN_HEAD pair slots of each tile
-    const int id = blockIdx.x;
-    const int xcd = id & 7;
-    const int k = id >> 3;
-    const int g = xcd + 8 * (k / n_slices);
-    const int s = k % n_slices;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    int j0, j1, tg = 0, t0 = 0;
-    if (TILED) {
-        tg = (n_tiles + n_groups - 1) / n_groups;  // <= 64 (checked on the host)
-        t0 = g * tg;
-        // the counts and the first DN_HEAD slots of every tile, in one round
-        for (int i = threadIdx.x; i < tg * DN_HEAD; i += blockDim.x) {
-            const int tt = min(t0 + i / DN_HEAD, n_tiles - 1);
-            head[i] = pairs[tt * 64 + i % DN_HEAD];
-        }
-        if (wave == 0) {
-            const int c = (lane < tg && t0 + lane < n_tiles) ? tile_cnt[t0 + lane] : 0;
-            int incl = c;
-            for (int o = 1; o < 64; o <<= 1) {
-                const int v = __shfl_up(incl, o, 64);
-                if (lane >= o) incl += v;
-            }
-            pref[lane + 1] = incl;
-            if (lane == 0) pref[0] = 0;
-        }
-        if (id == 0 && wave == 1 && n_active_out) {
-            int c = 0;
-            for (int i = lane; i < n_tiles; i += 64) c += __popcll(mask[i]);
-            for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
-            if (lane == 0) *n_active_out = c;
-        }
-        __syncthreads();
-        j0 = 0;
-        j1 = pref[64];
-    } else {
-        const int count = min(max(*count_p, 0), n_tiles);
-        const int chunk = (count + n_groups - 1) / n_groups;
-        j0 = g * chunk;
-        j1 = min(count, j0 + chunk);
+// Most pairs a k_sparse_down thread loads at once, by type (the row bytes of
+// all of them are in flight together).
+template <int T>
+constexpr int dn_np() {
+    return T == LLG_TYPE_F32 ? 2 : (T == LLG_TYPE_F16 ? 4 : (T == LLG_TYPE_Q8_0 ? 8 : 16));
+}
+
+// acc[32] += u * dequant(block b of the down row) for the first nvalid of the
+// NP entries e[] (a pair with u == 0 is skipped, ffn_flash.go:290).  An
+// entry is (row, u bits), or with UM (row, slot) and u = us[slot].y, loaded
+// together with the row bytes.  Every load is issued before any is used;
+// skipped entries read row 0 (in bounds), so no load sits under a per-lane
+// condition.
+template <int T, int NP, bool UM>
+__device__ __forceinline__ void dn_batch(const uint8_t *__restrict__ base, long long bstride,
+                                         const RowFmt &f, int b, const int2 (&e)[NP], int nvalid,
+                                         const int2 *__restrict__ us, float (&acc)[32],
+                                         float &corr) {
+    BlockRaw<T> r[NP];
+    float u[NP];
+#pragma unroll
+    for (int k = 0; k < NP; k++) {
+        if (UM) u[k] = __int_as_float(us[k < nvalid ? e[k].y : 0].y);
+        else u[k] = __int_as_float(e[k].y);
+        const bool v = k < nvalid && (UM || u[k] != 0.0f);
+        llg_block_load<T>(r[k], base + (long long)(v ? e[k].x : 0) * bstride + f.stride, f, b);
     }
-    if (j0 >= j1) return;  // uniform over the workgroup: nothing to add
-    const int bl = lane & 7;
-    const int sub = lane >> 3;
-    const int b = s * DN_SLICE + bl;
-    const int bc = min(b, f.nb - 1);  // lanes past the last block load it and drop it
+#pragma unroll
+    for (int k = 0; k < NP; k++)
+        if (k < nvalid && u[k] != 0.0f) llg_raw_axpy<T>(r[k], u[k], acc, corr);
+}
+
+// Entries j = tid + bd * (i0 + i), i < K, of a dense list of n (get(j) reads
+// entry j), through dn_batch.
+template <int T, int K, bool UM, class Get>
+__device__ __forceinline__ void dn_run(const uint8_t *__restrict__ base, long long bstride,
+                                       const RowFmt &f, int b, int n, int i0, Get &&get,
+                                       const int2 *__restrict__ us, float (&acc)[32],
+                                       float &corr) {
+    const int tid = threadIdx.x, bd = blockDim.x;
+    int2 e[K];
+#pragma unroll
+    for (int i = 0; i < K; i++) e[i] = get(min(tid + bd * (i0 + i), n - 1));
+    const int mine = (n - tid + bd - 1) / bd;  // entries of this thread in the list
+    dn_batch<T, K, UM>(base, bstride, f, b, e, min(max(mine - i0, 0), K), us, acc, corr);
+}
+
+// Every entry of a dense list of n, ceil(n / bd) per thread: the batch size
+// follows that count (wavefront-uniform), so a thread issues no loads for
+// entries it does not have.
+template <int T, bool UM, class Get>
+__device__ __forceinline__ void dn_list(const uint8_t *__restrict__ base, long long bstride,
+                                        const RowFmt &f, int b, int n, Get &&get,
+                                        const int2 *__restrict__ us, float (&acc)[32],
+                                        float &corr) {
+    constexpr int KM = dn_np<T>();
+    const int per = (n + (int)blockDim.x - 1) / (int)blockDim.x;
+    for (int i0 = 0; i0 < per; i0 += KM) {
+        const int k = min(per - i0, KM);
+        if (k == 1)
+            dn_run<T, 1, UM>(base, bstride, f, b, n, i0, get, us, acc, corr);
+        else if (k == 2)
+            dn_run<T, 2, UM>(base, bstride, f, b, n, i0, get, us, acc, corr);
+        else if (k <= 4)
+            dn_run<T, (KM < 4 ? KM : 4), UM>(base, bstride, f, b, n, i0, get, us, acc, corr);
+        else if (k <= 8)
+            dn_run<T, (KM < 8 ? KM : 8), UM>(base, bstride, f, b, n, i0, get, us, acc, corr);
+        else
+            dn_run<T, KM, UM>(base, bstride, f, b, n, i0, get, us, acc, corr);
+    }
+}
+
+
+// Down products.  Pairs come either as a plain list pairs[0..*count) (TILED
+// = false; the count is clamped to `cap`) or from the predictor tiles (TILED
+// = true): tile t's active neurons are the set bits of mask[t], and the pair
+// of its k-th (ascending) is in slot pairs[t*64 + k].  Thread t reads the
+// masks of tiles t, t + bd, ... in one round; a block scan of their
+// popcounts places every active neuron in a dense list in LDS, (row, slot)
+// in tile order within a thread and thread order across, DN_LCAP at a time,
+// and each neuron's u is then loaded with its row bytes.  Either list is
+// split evenly over the threads (dn_list).  Workgroup = output block b (32
+// outputs): out[32 b + e] (+)= sum over the pairs of u * down_row[32 b + e].
+// With ACC the sum is added to out (a residual), else stored.  With TILED,
+// workgroup 0 also writes the number of active neurons.
+#define DN_LCAP 4096   // entries of the dense LDS list per pass
+template <int T, bool TILED, bool ACC>
+__global__ __launch_bounds__(DN_THREADS) void k_sparse_down(
+    const uint8_t *__restrict__ base, long long bstride, RowFmt f, const int2 *__restrict__ pairs,
+    const int32_t *__restrict__ count_p, int cap, const unsigned long long *__restrict__ mask,
+    int n_tiles, int32_t *__restrict__ n_active_out, int per_xcd, float *__restrict__ out) {
+    __shared__ float red[DN_THREADS / 64][32];
+    __shared__ int wsum[DN_THREADS / 64];
+    __shared__ int2 lst[TILED ? DN_LCAP : 1];
+    const int b = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (b >= f.nb) return;  // uniform over the workgroup
+    const int tid = threadIdx.x, bd = blockDim.x, lane = tid & 63, wave = tid >> 6;
+    const int nw = bd >> 6;
+    const int o = b * 32 + (lane >> 1);
+    float prev = 0.0f;
+    if (ACC && wave == 0 && (lane & 1) == 0 && o < f.cols) prev = out[o];  // early, off the path
     float acc[32];
     float corr = 0.0f;
 #pragma unroll
     for (int e = 0; e < 32; e++) acc[e] = 0.0f;
-    {
-        for (int j = j0 + wave * 8 + sub; j < j1; j += 64) {
-            // two pairs per pass: both rows' bytes are requested before either is used
-            int2 p0, p1 = make_int2(0, 0);
-            if (TILED) {
-                int t = 0;
-                while (pref[t + 1] <= j) t++;
-                int k = j - pref[t];
-                p0 = k < DN_HEAD ? head[t * DN_HEAD + k] : pairs[(t0 + t) * 64 + k];
-                if (j + 32 < j1) {
-                    const int jj = j + 32;
-                    while (pref[t + 1] <= jj) t++;
-                    k = jj - pref[t];
-                    p1 = k < DN_HEAD ? head[t * DN_HEAD + k] : pairs[(t0 + t) * 64 + k];
-                }
-            } else {
-                p0 = pairs[j];
-                if (j + 32 < j1) p1 = pairs[j + 32];
-            }
-            float u0 = __int_as_float(p0.y), u1 = __int_as_float(p1.y);
-            if (b >= f.nb) u0 = u1 = 0.0f;
-            // Unconditional loads (a row index of a zero activation may be -1 or
-            // stale: such lanes read row 0); only the use is skipped, as
-            // ffn_flash.go:290 skips u == 0.
-            BlockRaw<T> r0, r1;
-            llg_block_load<T>(r0, base + (long long)(u0 != 0.0f ? p0.x : 0) * bstride + f.stride, f, bc);
-            llg_block_load<T>(r1, base + (long long)(u1 != 0.0f ? p1.x : 0) * bstride + f.stride, f, bc);
-            if (u0 != 0.0f) llg_raw_axpy<T>(r0, u0, acc, corr);
-            if (u1 != 0.0f) llg_raw_axpy<T>(r1, u1, acc, corr);
+    if (TILED) {
+        const unsigned long long m0 = tid < n_tiles ? mask[tid] : 0ull;
+        int mine = __popcll(m0);
+        for (int t = tid + bd; t < n_tiles; t += bd) mine += __popcll(mask[t]);
+        // exclusive block scan of the per-thread counts
+        int incl = mine;
+        for (int d = 1; d < 64; d <<= 1) {
+            const int v = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += v;
         }
+        if (lane == 63) wsum[wave] = incl;
+        __syncthreads();
+        int before = 0, total = 0;
+        for (int w = 0; w < nw; w++) {
+            before += w < wave ? wsum[w] : 0;
+            total += wsum[w];
+        }
+        const int off0 = before + incl - mine;
+        if (n_active_out && blockIdx.x == 0 && tid == 0) *n_active_out = total;
+        for (int cb = 0; cb < total; cb += DN_LCAP) {
+            if (cb > 0) __syncthreads();  // the previous pass has read lst
+            int off = off0;
+            for (int t = tid; t < n_tiles; t += bd) {
+                unsigned long long m = t == tid ? m0 : mask[t];
+                const int c = __popcll(m);
+                if (off + c > cb && off < cb + DN_LCAP) {
+                    for (int k = 0; m; k++, m &= m - 1) {
+                        const int g = off + k - cb;
+                        if (g >= 0 && g < DN_LCAP)
+                            lst[g] = make_int2(t * 64 + __ffsll((long long)m) - 1, t * 64 + k);
+                    }
+                }
+                off += c;
+            }
+            __syncthreads();
+            dn_list<T, true>(base, bstride, f, b, min(total - cb, DN_LCAP),
+                             [&](int j) { return lst[j]; }, pairs, acc, corr);
+        }
+    } else {
+        const int n = min(max(*count_p, 0), cap);
+        dn_list<T, false>(base, bstride, f, b, n, [&](int j) { return pairs[j]; }, pairs, acc,
+                          corr);
     }
-    // Sum over the 8 pair sub-lanes and 4 wavefronts sharing block bl: one DPP
-    // step folds sub-lanes 2r+1 into 2r (row_ror:8 within each 16-lane row),
-    // then the 16 partial sums per output meet in LDS (row stride 36 floats).
 #pragma unroll
-    for (int e = 0; e < 32; e++) {
-        const float v = acc[e] - corr;
-        acc[e] = v + llg_dpp<0x128>(v);
-    }
-    if ((lane & 8) == 0) {
-        float *dst = &red[((wave * 4 + (lane >> 4)) * DN_SLICE + bl) * DN_RED_ST];
-#pragma unroll
-        for (int q = 0; q < 8; q++)
-            *reinterpret_cast<float4 *>(dst + 4 * q) =
-                make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
-    }
+    for (int e = 0; e < 32; e++) acc[e] -= corr;
+    const float ws = dn_wave_transpose_sum(acc);
+    if ((lane & 1) == 0) red[wave][lane >> 1] = ws;
     __syncthreads();
-    const int t = threadIdx.x;
-    const int o = s * DN_SLICE * 32 + t;
-    float sum = 0.0f;
-#pragma unroll
-    for (int r = 0; r < 16; r++) sum += red[(r * DN_SLICE + (t >> 5)) * DN_RED_ST + (t & 31)];
-    if (o < f.cols) unsafeAtomicAdd(out + o, sum);
+    if (wave == 0 && (lane & 1) == 0) {
+        float sum = 0.0f;
+        for (int w = 0; w < nw; w++) sum += red[w][lane >> 1];
+        if (o < f.cols) out[o] = ACC ? prev + sum : sum;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -473,19 +536,22 @@ size_t llg_sparse_ws_bytes(int max_active) {
 
 static size_t xs_bytes(const RowFmt &f) { return (size_t)f.nb * XS_STRIDE * 4; }
 
-// 8 or 16 pair groups (a multiple of the 8 XCDs): enough workgroups to spread
-// the rows, few enough that the atomics per output stay small.
-static int down_groups(int max_pairs) { return max_pairs > 256 ? 16 : 8; }
+// k_sparse_down's grid: 8 * ceil(nb / 8) workgroups (one per output block,
+// the block order spread evenly over the 8 XCDs); a list launch uses one
+// thread per entry, 64 to DN_THREADS, a tiled launch DN_THREADS.
+static int down_per_xcd(const RowFmt &f) { return (f.nb + 7) / 8; }
+static int down_threads(int items) {
+    const int t = (items + 63) / 64 * 64;
+    return t < 64 ? 64 : (t > DN_THREADS ? DN_THREADS : t);
+}
 
 template <int T>
 static void launch_down(hipStream_t st, const uint8_t *base, long long bstride, const RowFmt &f,
                         const int2 *pairs, const int32_t *count, int max_pairs, float *out) {
-    const int n_slices = (f.nb + DN_SLICE - 1) / DN_SLICE;
-    const int n_groups = down_groups(max_pairs);
-    hipLaunchKernelGGL((k_sparse_down<T, false>), dim3(n_slices * n_groups), dim3(256), 0, st,
-                       base, bstride, f, pairs, count, (const int32_t *)nullptr, max_pairs,
-                       (const unsigned long long *)nullptr, (int32_t *)nullptr, n_slices,
-                       n_groups, out);
+    const int px = down_per_xcd(f);
+    hipLaunchKernelGGL((k_sparse_down<T, false, false>), dim3(8 * px), dim3(down_threads(max_pairs)),
+                       0, st, base, bstride, f, pairs, count, max_pairs,
+                       (const unsigned long long *)nullptr, 0, (int32_t *)nullptr, px, out);
 }
 
 template <int T>
@@ -499,11 +565,11 @@ static void launch_list(hipStream_t st, const uint8_t *base, long long bstride, 
     if (fr.src)
         hipLaunchKernelGGL((k_list_up<T, true>), dim3(grid), dim3(256), xs_bytes(f), st, base,
                            bstride, f, slot_of, x, active, n_active, max_active, n_rows, act,
-                           pairs, out, fr);
+                           pairs, fr);
     else
         hipLaunchKernelGGL((k_list_up<T, false>), dim3(grid), dim3(256), xs_bytes(f), st, base,
                            bstride, f, slot_of, x, active, n_active, max_active, n_rows, act,
-                           pairs, out, fr);
+                           pairs, fr);
     launch_down<T>(st, base, bstride, f, pairs, n_active, max_active, out);
 }
 
@@ -543,34 +609,39 @@ int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, con
     return 0;
 }
 
+// Workspace of the fused path: the predictor's partials and masks, then the
+// tiles' pair slots (64 per tile).
 size_t llg_fused_ws_bytes(int rank, int ff) {
     const long long n_tiles = (ff + 63) / 64;
-    return (size_t)llg_predict_ws_bytes(rank, ff) + (size_t)llg_align(n_tiles * 64 * 8, 256) +
-           (size_t)llg_align(n_tiles * 4, 256);
+    return (size_t)llg_predict_ws_bytes(rank, ff) + (size_t)llg_align(n_tiles * 64 * 8, 256);
 }
 
 template <int T>
 static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial, const float *bias,
                          float thr, LlgObject *b, const float *x, int act,
-                         unsigned long long *mask, int2 *pairs, int32_t *tile_cnt,
-                         int32_t *n_active, float *out) {
+                         unsigned long long *mask, int2 *pairs, int32_t *n_active, float *out,
+                         bool accumulate) {
     const int ff = wout->rows, rank = wout->fmt.cols;
     const int n_tiles = (ff + 63) / 64;
     const RowFmt &f = b->fmt;
-    const size_t lds = xs_bytes(f) + (size_t)(((rank + 3) & ~3) + 64 + 66) * 4;
-    hipLaunchKernelGGL(k_tile_up<T>, dim3(n_tiles), dim3(TILE_THREADS), lds, st, wout->d, wout->stride, ff,
-                       rank, partial, bias, thr, b->d, b->stride, f, x, act, mask, pairs,
-                       tile_cnt);
-    const int n_slices = (f.nb + DN_SLICE - 1) / DN_SLICE;
-    const int n_groups = down_groups(ff);
-    hipLaunchKernelGGL((k_sparse_down<T, true>), dim3(n_slices * n_groups), dim3(256), 0, st,
-                       b->d, b->stride, f, pairs, (const int32_t *)nullptr, tile_cnt, n_tiles,
-                       mask, n_active, n_slices, n_groups, out);
+    const size_t lds = xs_bytes(f) + (size_t)(((rank + 3) & ~3) + 64 + 65) * 4;
+    hipLaunchKernelGGL(k_tile_up<T>, dim3(n_tiles), dim3(TILE_THREADS), lds, st, wout->d,
+                       wout->stride, ff, rank, partial, bias, thr, b->d, b->stride, f, x, act,
+                       mask, pairs);
+    const int px = down_per_xcd(f);
+    if (accumulate)
+        hipLaunchKernelGGL((k_sparse_down<T, true, true>), dim3(8 * px), dim3(DN_THREADS), 0, st,
+                           b->d, b->stride, f, (const int2 *)pairs, (const int32_t *)nullptr, 0,
+                           (const unsigned long long *)mask, n_tiles, n_active, px, out);
+    else
+        hipLaunchKernelGGL((k_sparse_down<T, true, false>), dim3(8 * px), dim3(DN_THREADS), 0, st,
+                           b->d, b->stride, f, (const int2 *)pairs, (const int32_t *)nullptr, 0,
+                           (const unsigned long long *)mask, n_tiles, n_active, px, out);
 }
 
-// ffnFlash path 2 on the device: K1 + K2 + K3, plus the ascending active list
-// through k_compact when d_active is given.  d_n_active (optional) receives
-// the number of active neurons.
+// ffnFlash path 2 on the device: k_pred_hidden, k_tile_up, k_sparse_down,
+// plus the ascending active list through k_compact when d_active is given.
+// d_n_active (optional) receives the number of active neurons.
 int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
                       LlgObject *b, const float *d_a, const float *d_x, float thr, int act,
                       float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws,
@@ -581,40 +652,40 @@ int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *
     const int n_tiles = (ff + 63) / 64;
     if (xs_bytes(f) + (size_t)(rank + 136) * 4 > 64 * 1024)
         return llg_set_error(d, LLG_E_ARG, "predict_sparse: hidden size %d too large", f.cols);
-    if ((n_tiles + down_groups(ff) - 1) / down_groups(ff) > 64)
-        return llg_set_error(d, LLG_E_ARG, "predict_sparse: d_ff %d too large", ff);
-    hipStream_t st = llg_dev_stream(d);
     int2 *pairs = reinterpret_cast<int2 *>(ws + llg_predict_ws_bytes(rank, ff));
-    int32_t *tile_cnt = reinterpret_cast<int32_t *>(ws + llg_predict_ws_bytes(rank, ff) +
-                                                    llg_align((long long)n_tiles * 64 * 8, 256));
     float *partial;
     unsigned long long *mask;
     int psplit;
-    // K1 also clears out, the atomic target of K3 (or, with d_out_add, adds
-    // d_out_add to it: out then ends as out + d_out_add + the FFN output)
-    int rc = llg_pred_hidden_enqueue(d, wup, d_a, ws, &partial, &mask, &psplit, d_out, f.cols,
-                                     nullptr, 0, nullptr, d_out_add);
+    // k_sparse_down stores out; with d_out_add, k_pred_hidden first adds
+    // d_out_add to out and k_sparse_down adds the FFN output to that (out ends
+    // as (out + d_out_add) + the FFN output, the residual order of
+    // ffn_flash.go:161-166)
+    int rc = llg_pred_hidden_enqueue(d, wup, d_a, ws, &partial, &mask, &psplit,
+                                     d_out_add ? d_out : nullptr, f.cols, nullptr, 0, nullptr,
+                                     d_out_add);
     if (rc) return rc;
     if (psplit != PRED_SPLIT_N)
         return llg_set_error(d, LLG_E_ARG, "predict_sparse: hidden split %d != %d", psplit,
                              PRED_SPLIT_N);
     const float *d_bias = bias ? reinterpret_cast<const float *>(bias->d) : nullptr;
+    hipStream_t st = llg_dev_stream(d);
+    const bool accum = d_out_add != nullptr;
     switch (f.type) {
     case LLG_TYPE_Q4_0:
         launch_fused<LLG_TYPE_Q4_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, pairs,
-                                    tile_cnt, d_n_active, d_out);
+                                    d_n_active, d_out, accum);
         break;
     case LLG_TYPE_Q8_0:
         launch_fused<LLG_TYPE_Q8_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, pairs,
-                                    tile_cnt, d_n_active, d_out);
+                                    d_n_active, d_out, accum);
         break;
     case LLG_TYPE_F16:
         launch_fused<LLG_TYPE_F16>(st, wout, partial, d_bias, thr, b, d_x, act, mask, pairs,
-                                   tile_cnt, d_n_active, d_out);
+                                   d_n_active, d_out, accum);
         break;
     case LLG_TYPE_F32:
         launch_fused<LLG_TYPE_F32>(st, wout, partial, d_bias, thr, b, d_x, act, mask, pairs,
-                                   tile_cnt, d_n_active, d_out);
+                                   d_n_active, d_out, accum);
         break;
     default:
         return llg_set_error(d, LLG_E_TYPE, "predict_sparse: unsupported type %d", f.type);

@@ -17,7 +17,7 @@ import torch
 import llg
 import llg.gguf as gg
 from oracle import refcpu as R
-from tests.helpers import make_sparse_layer, max_rel_err, normal, threshold_for
+from tests.helpers import make_sparse_layer, max_rel_err, normal, threshold_for  # noqa: F401
 
 pytestmark = pytest.mark.gpu
 
@@ -83,15 +83,20 @@ def test_noalloc_matches_allocating_entry(dev):
 
 
 def test_noalloc_rejects_workload_above_scratch(dev):
-    """d_ff 65536 at rank 16 needs more pair slots than the fixed scratch
-    holds: the allocation-free entry point refuses it, the other runs it."""
+    """d_ff 65536 needs 1024 tiles x 64 pair slots, more than the fixed
+    scratch holds: the allocation-free entry point refuses the layer, the
+    allocating one runs it."""
+    h, ff, rank = 2048, 65536, 16
+    g = torch.Generator(device="cuda")
+    g.manual_seed(20261)
+    up = gg.quantize(torch.randn((ff, h), generator=g, device="cuda") * 0.02, gg.Q4_0)
+    dn = gg.quantize(torch.randn((ff, h), generator=g, device="cuda") * 0.02, gg.Q4_0)
     rng = np.random.default_rng(20261)
-    h, ff, rank = 64, 65536, 16
-    up, dn = make_sparse_layer(rng, h, ff, gg.Q4_0)
     wup = normal(rng, (rank, h), 0.05)
     wout = normal(rng, (ff, rank), 0.05)
     x = normal(rng, h, 1.0)
     _, lg = R.predict(wup, wout, None, x, 0.0)
+    torch.cuda.synchronize()
     L = dict(h=h, ff=ff, x=x, thr=threshold_for(lg, 3000),
              pred=llg.Predictor(dev, wup, wout, None, 0.0),
              bundle=dev.upload_bundle(up, dn, gg.Q4_0, h, ff))
@@ -102,7 +107,7 @@ def test_noalloc_rejects_workload_above_scratch(dev):
     dev.check(rc, "predict_sparse")
     ref_act, _ = R.predict(wup, wout, None, x, L["thr"])
     assert np.array_equal(act, ref_act)
-    ref = R.ffn_sparse_load(up, dn, gg.Q4_0, h, ff, x, ref_act)
+    ref = R.ffn_sparse_load(up.cpu().numpy(), dn.cpu().numpy(), gg.Q4_0, h, ff, x, ref_act)
     assert max_rel_err(out, ref) <= TOL
     L["pred"].w_up.release()
     L["pred"].w_out.release()
