@@ -39,7 +39,12 @@
 #define XS_STRIDE 36      // floats per staged 32-float x block (bank-conflict-free)
 #define BATCH 4           // blocks whose loads a lane issues together
 #define PRED_SPLIT_N 8    // partials per hidden unit written by k_pred_hidden
-#define TILE_THREADS 512  // k_tile_up workgroup: 8 wavefronts for the up rows
+// Neurons per k_tile_up workgroup.  64: 128-neuron tiles (one 16-wavefront
+// workgroup per CU for the Falcon-7B layer) took 9.3 against 8.6 us.
+template <int T>
+constexpr int fused_tn() {
+    return 64;
+}
 #define DN_THREADS 512    // k_sparse_down workgroup: one tile (or list stride) per thread
 
 __device__ __forceinline__ void stage_x(float *xs, const float *__restrict__ x, int nb) {
@@ -185,13 +190,15 @@ __device__ __forceinline__ void row_dotn(const uint8_t *__restrict__ base, long 
 }
 
 // One round of the tile's up rows: active neuron k = k0 + wave + nw*i (i <
-// NR) of the tile on this wavefront; its pair (row, u) goes to the tile's
-// slot k (a zero activation is kept, and k_sparse_down skips it).
+// NR) of the tile on this wavefront.  Its pair (row, u) goes to slot k' of
+// its 64-neuron subtile, k' = k less the list index sb[] at which that
+// subtile's neurons start (a zero activation is kept, and k_sparse_down
+// skips it).
 template <int T, int NR>
 __device__ __forceinline__ void tile_up_round(const uint8_t *__restrict__ base, long long bstride,
                                               const RowFmt &f, const float *xs, const int *tl,
-                                              int cnt, int k0, int tile0, int act,
-                                              int2 *__restrict__ tpairs) {
+                                              const int *sb, int cnt, int k0, int tile0, int act,
+                                              int2 *__restrict__ pairs) {
     const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     int rows[NR];
 #pragma unroll
@@ -206,7 +213,9 @@ __device__ __forceinline__ void tile_up_round(const uint8_t *__restrict__ base, 
 #pragma unroll
         for (int i = 0; i < NR; i++) {
             if (rows[i] < 0) break;
-            tpairs[k0 + wave + nw * i] = make_int2(rows[i], __float_as_int(llg_act(act, s[i])));
+            const int k = k0 + wave + nw * i;
+            const int slot = (rows[i] >> 6) * 64 + k - sb[(rows[i] - tile0) >> 6];
+            pairs[slot] = make_int2(rows[i], __float_as_int(llg_act(act, s[i])));
         }
     }
 }
@@ -310,60 +319,74 @@ __device__ __forceinline__ float dn_wave_transpose_sum(const float (&v)[32]) {
     return e + llg_dpp<0xB1>(e);                                           // bit 0
 }
 
-// A. predictor-fused tile kernel.  Tile t writes its active mask (bit i:
-// neuron 64 t + i) to mask[t] and the (row, u) pair of its k-th active
-// neuron (ascending) to pairs[t*64 + k].
-template <int T>
-__global__ __launch_bounds__(TILE_THREADS, 2) void k_tile_up(
+// A. predictor-fused tile kernel over TN = 64 or 128 neurons (TN / 16
+// wavefronts compute the logits, TN / 64 ballots select).  Each 64-neuron
+// subtile s writes its active mask (bit i: neuron 64 s + i) to mask[s] and
+// the (row, u) pair of its k-th active neuron (ascending) to pairs[s*64 + k].
+// The up rows take one wavefront each for up to TN / 8 active neurons (two
+// per wavefront for up to TN / 4), so that most tiles need one round.
+template <int TN>
+constexpr int tile_threads() {
+    return TN == 128 ? 1024 : 512;
+}
+template <int T, int TN>
+__global__ __launch_bounds__(tile_threads<TN>(), TN == 128 ? 1 : 2) void k_tile_up(
     const uint8_t *__restrict__ wout, long long wstride, int ff, int rank,
     const float *__restrict__ partial, const float *__restrict__ bias, float thr,
     const uint8_t *__restrict__ base, long long bstride, RowFmt f, const float *__restrict__ x,
     int act, unsigned long long *__restrict__ mask, int2 *__restrict__ pairs) {
+    constexpr int SUB = TN / 64;
     extern __shared__ float sh[];
     float *xs = sh;                                     // nb * XS_STRIDE
     float *hid = xs + f.nb * XS_STRIDE;                 // rank (16-byte aligned)
-    float *lg = hid + ((rank + 3) & ~3);                // 64
-    int *tl = reinterpret_cast<int *>(lg + 64);         // 64 tile-local indices, count
+    float *lg = hid + ((rank + 3) & ~3);                // TN
+    int *tl = reinterpret_cast<int *>(lg + TN);         // TN tile-local indices, count
+    int *sb = tl + TN + 1;                              // SUB list starts
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int tile0 = blockIdx.x * 64;
-    WoutTile t;  // logits: wavefronts 0-3 (16 neurons each)
-    if (wave < 4) load_wout_tile(t, wout, wstride, ff, rank, tile0);  // used after the barrier
+    const int tile0 = blockIdx.x * TN;
+    WoutTile t;  // logits: wavefronts 0 .. TN/16 - 1 (16 neurons each)
+    if (wave < TN / 16) load_wout_tile(t, wout, wstride, ff, rank, tile0);  // used after the barrier
     stage_x(xs, x, f.nb);
     load_hidden<PRED_SPLIT_N>(hid, partial, rank);
     __syncthreads();
-    if (wave < 4) finish_logits(t, wout, wstride, ff, rank, tile0, hid, lg);
+    if (wave < TN / 16) finish_logits(t, wout, wstride, ff, rank, tile0, hid, lg);
     __syncthreads();
     if (wave == 0) {
-        const int i = tile0 + lane;
-        bool on = false;
-        if (i < ff) {
-            float v = lg[lane];
-            if (bias) v += bias[i];  // predictor.go:69-73
-            on = v > thr;            // predictor.go:78
+        int k = 0;
+#pragma unroll
+        for (int s = 0; s < SUB; s++) {
+            const int i = tile0 + 64 * s + lane;
+            bool on = false;
+            if (i < ff) {
+                float v = lg[64 * s + lane];
+                if (bias) v += bias[i];  // predictor.go:69-73
+                on = v > thr;            // predictor.go:78
+            }
+            const unsigned long long m = __ballot(on);
+            const int before = __popcll(m & ((1ull << lane) - 1ull));
+            if (on) tl[k + before] = 64 * s + lane;
+            if (lane == 0) {
+                sb[s] = k;
+                if (tile0 + 64 * s < ff) mask[blockIdx.x * SUB + s] = m;
+            }
+            k += __popcll(m);
         }
-        const unsigned long long m = __ballot(on);
-        const int before = __popcll(m & ((1ull << lane) - 1ull));
-        if (on) tl[before] = lane;
-        if (lane == 0) {
-            tl[64] = __popcll(m);
-            mask[blockIdx.x] = m;
-        }
+        if (lane == 0) tl[TN] = k;
     }
     __syncthreads();
-    const int cnt = tl[64];
-    // up rows of the active neurons on all TILE_THREADS/64 wavefronts, one
-    // round of loads for up to 16 (1 or 2 rows per wavefront by count)
+    const int cnt = tl[TN];
+    // up rows of the active neurons, one round of loads for up to 2 * nw
+    // (1 or 2 rows per wavefront by count)
     constexpr int UPMAX = T == LLG_TYPE_F32 ? 1 : 2;
-    const int nw = TILE_THREADS / 64;
-    int2 *tpairs = pairs + (size_t)blockIdx.x * 64;
+    constexpr int nw = tile_threads<TN>() / 64;
     if (cnt <= nw || UPMAX == 1) {
         for (int k0 = 0; k0 < cnt; k0 += nw)
-            tile_up_round<T, 1>(base, bstride, f, xs, tl, cnt, k0, tile0, act, tpairs);
+            tile_up_round<T, 1>(base, bstride, f, xs, tl, sb, cnt, k0, tile0, act, pairs);
     } else {
         if constexpr (UPMAX == 2)
             for (int k0 = 0; k0 < cnt; k0 += 2 * nw)
-                tile_up_round<T, 2>(base, bstride, f, xs, tl, cnt, k0, tile0, act, tpairs);
+                tile_up_round<T, 2>(base, bstride, f, xs, tl, sb, cnt, k0, tile0, act, pairs);
     }
 }
 
@@ -400,13 +423,12 @@ __device__ __forceinline__ void dn_batch(const uint8_t *__restrict__ base, long 
 }
 
 // Entries j = tid + bd * (i0 + i), i < K, of a dense list of n (get(j) reads
-// entry j), through dn_batch.
+// entry j) shared by bd threads, through dn_batch.
 template <int T, int K, bool UM, class Get>
 __device__ __forceinline__ void dn_run(const uint8_t *__restrict__ base, long long bstride,
                                        const RowFmt &f, int b, int n, int i0, Get &&get,
                                        const int2 *__restrict__ us, float (&acc)[32],
-                                       float &corr) {
-    const int tid = threadIdx.x, bd = blockDim.x;
+                                       float &corr, int tid, int bd) {
     int2 e[K];
 #pragma unroll
     for (int i = 0; i < K; i++) e[i] = get(min(tid + bd * (i0 + i), n - 1));
@@ -414,53 +436,67 @@ __device__ __forceinline__ void dn_run(const uint8_t *__restrict__ base, long lo
     dn_batch<T, K, UM>(base, bstride, f, b, e, min(max(mine - i0, 0), K), us, acc, corr);
 }
 
-// Every entry of a dense list of n, ceil(n / bd) per thread: the batch size
-// follows that count (wavefront-uniform), so a thread issues no loads for
-// entries it does not have.
+// Every entry of a dense list of n shared by bd threads (this one is tid),
+// ceil(n / bd) per thread: the batch size follows that count (uniform over
+// the wavefront), so a thread issues no loads for entries it does not have.
 template <int T, bool UM, class Get>
 __device__ __forceinline__ void dn_list(const uint8_t *__restrict__ base, long long bstride,
                                         const RowFmt &f, int b, int n, Get &&get,
                                         const int2 *__restrict__ us, float (&acc)[32],
-                                        float &corr) {
+                                        float &corr, int tid, int bd) {
     constexpr int KM = dn_np<T>();
-    const int per = (n + (int)blockDim.x - 1) / (int)blockDim.x;
+    const int per = (n + bd - 1) / bd;
     for (int i0 = 0; i0 < per; i0 += KM) {
         const int k = min(per - i0, KM);
         if (k == 1)
-            dn_run<T, 1, UM>(base, bstride, f, b, n, i0, get, us, acc, corr);
+            dn_run<T, 1, UM>(base, bstride, f, b, n, i0, get, us, acc, corr, tid, bd);
         else if (k == 2)
-            dn_run<T, 2, UM>(base, bstride, f, b, n, i0, get, us, acc, corr);
+            dn_run<T, 2, UM>(base, bstride, f, b, n, i0, get, us, acc, corr, tid, bd);
         else if (k <= 4)
-            dn_run<T, (KM < 4 ? KM : 4), UM>(base, bstride, f, b, n, i0, get, us, acc, corr);
+            dn_run<T, (KM < 4 ? KM : 4), UM>(base, bstride, f, b, n, i0, get, us, acc, corr, tid,
+                                             bd);
         else if (k <= 8)
-            dn_run<T, (KM < 8 ? KM : 8), UM>(base, bstride, f, b, n, i0, get, us, acc, corr);
+            dn_run<T, (KM < 8 ? KM : 8), UM>(base, bstride, f, b, n, i0, get, us, acc, corr, tid,
+                                             bd);
         else
-            dn_run<T, KM, UM>(base, bstride, f, b, n, i0, get, us, acc, corr);
+            dn_run<T, KM, UM>(base, bstride, f, b, n, i0, get, us, acc, corr, tid, bd);
     }
 }
 
+// Inclusive prefix sum over the wavefront: row shifts within each 16-lane
+// row, then the row totals broadcast to the rows after them.
+__device__ __forceinline__ int dn_wave_scan(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
+    return v;
+}
 
 // Down products.  Pairs come either as a plain list pairs[0..*count) (TILED
-// = false; the count is clamped to `cap`) or from the predictor tiles (TILED
-// = true): tile t's active neurons are the set bits of mask[t], and the pair
-// of its k-th (ascending) is in slot pairs[t*64 + k].  Thread t reads the
-// masks of tiles t, t + bd, ... in one round; a block scan of their
-// popcounts places every active neuron in a dense list in LDS, (row, slot)
-// in tile order within a thread and thread order across, DN_LCAP at a time,
-// and each neuron's u is then loaded with its row bytes.  Either list is
-// split evenly over the threads (dn_list).  Workgroup = output block b (32
-// outputs): out[32 b + e] (+)= sum over the pairs of u * down_row[32 b + e].
-// With ACC the sum is added to out (a residual), else stored.  With TILED,
-// workgroup 0 also writes the number of active neurons.
-#define DN_LCAP 4096   // entries of the dense LDS list per pass
+// = false; the count is clamped to `cap`), split evenly over the threads, or
+// from the predictor tiles (TILED = true): tile t's active neurons are the
+// set bits of mask[t], and the pair of its k-th (ascending) is in slot
+// pairs[t*64 + k].  Wavefront w takes tiles 64 w + l (lane l), 64 (w + nw) +
+// l, ...: a wavefront scan of the lanes' popcounts places its tiles' active
+// neurons, as (row, slot), in its own dense list in LDS (DN_WCAP at a time),
+// which its lanes then share; each neuron's u is loaded with its row bytes.
+// No barrier stands between the masks and the row loads.  Workgroup =
+// output block b (32 outputs): out[32 b + e] (+)= sum over the pairs of u *
+// down_row[32 b + e], the wavefronts' sums added in order.  With ACC the sum
+// is added to out (a residual), else stored.  With TILED, workgroup 0 also
+// writes the number of active neurons.
+#define DN_WCAP 512   // entries of a wavefront's LDS list per pass
 template <int T, bool TILED, bool ACC>
 __global__ __launch_bounds__(DN_THREADS) void k_sparse_down(
     const uint8_t *__restrict__ base, long long bstride, RowFmt f, const int2 *__restrict__ pairs,
     const int32_t *__restrict__ count_p, int cap, const unsigned long long *__restrict__ mask,
     int n_tiles, int32_t *__restrict__ n_active_out, int per_xcd, float *__restrict__ out) {
     __shared__ float red[DN_THREADS / 64][32];
-    __shared__ int wsum[DN_THREADS / 64];
-    __shared__ int2 lst[TILED ? DN_LCAP : 1];
+    __shared__ int ired[DN_THREADS / 64];
+    __shared__ int2 lst[TILED ? DN_THREADS / 64 : 1][TILED ? DN_WCAP : 1];
     const int b = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     if (b >= f.nb) return;  // uniform over the workgroup
     const int tid = threadIdx.x, bd = blockDim.x, lane = tid & 63, wave = tid >> 6;
@@ -472,58 +508,57 @@ __global__ __launch_bounds__(DN_THREADS) void k_sparse_down(
     float corr = 0.0f;
 #pragma unroll
     for (int e = 0; e < 32; e++) acc[e] = 0.0f;
+    int n_act = 0;
     if (TILED) {
-        const unsigned long long m0 = tid < n_tiles ? mask[tid] : 0ull;
-        int mine = __popcll(m0);
-        for (int t = tid + bd; t < n_tiles; t += bd) mine += __popcll(mask[t]);
-        // exclusive block scan of the per-thread counts
-        int incl = mine;
-        for (int d = 1; d < 64; d <<= 1) {
-            const int v = __shfl_up(incl, d, 64);
-            if (lane >= d) incl += v;
-        }
-        if (lane == 63) wsum[wave] = incl;
-        __syncthreads();
-        int before = 0, total = 0;
-        for (int w = 0; w < nw; w++) {
-            before += w < wave ? wsum[w] : 0;
-            total += wsum[w];
-        }
-        const int off0 = before + incl - mine;
-        if (n_active_out && blockIdx.x == 0 && tid == 0) *n_active_out = total;
-        for (int cb = 0; cb < total; cb += DN_LCAP) {
-            if (cb > 0) __syncthreads();  // the previous pass has read lst
-            int off = off0;
-            for (int t = tid; t < n_tiles; t += bd) {
-                unsigned long long m = t == tid ? m0 : mask[t];
-                const int c = __popcll(m);
-                if (off + c > cb && off < cb + DN_LCAP) {
+        int2 *wl = lst[TILED ? wave : 0];
+        for (int t0 = wave * 64; t0 < n_tiles; t0 += nw * 64) {  // uniform per wavefront
+            const int t = t0 + lane;
+            const unsigned long long m0 = t < n_tiles ? mask[t] : 0ull;
+            const int c = __popcll(m0);
+            const int incl = dn_wave_scan(c);
+            const int total = __builtin_amdgcn_readlane(incl, 63);
+            const int off = incl - c;
+            n_act += c;
+            for (int cb = 0; cb < total; cb += DN_WCAP) {
+                if (off + c > cb && off < cb + DN_WCAP) {
+                    unsigned long long m = m0;
                     for (int k = 0; m; k++, m &= m - 1) {
                         const int g = off + k - cb;
-                        if (g >= 0 && g < DN_LCAP)
-                            lst[g] = make_int2(t * 64 + __ffsll((long long)m) - 1, t * 64 + k);
+                        if (g >= 0 && g < DN_WCAP)
+                            wl[g] = make_int2(t * 64 + __ffsll((long long)m) - 1, t * 64 + k);
                     }
                 }
-                off += c;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                dn_list<T, true>(base, bstride, f, b, min(total - cb, DN_WCAP),
+                                 [&](int j) { return wl[j]; }, pairs, acc, corr, lane, 64);
+                __builtin_amdgcn_wave_barrier();  // the list is read before the next pass writes
             }
-            __syncthreads();
-            dn_list<T, true>(base, bstride, f, b, min(total - cb, DN_LCAP),
-                             [&](int j) { return lst[j]; }, pairs, acc, corr);
         }
     } else {
         const int n = min(max(*count_p, 0), cap);
         dn_list<T, false>(base, bstride, f, b, n, [&](int j) { return pairs[j]; }, pairs, acc,
-                          corr);
+                          corr, tid, bd);
     }
 #pragma unroll
     for (int e = 0; e < 32; e++) acc[e] -= corr;
     const float ws = dn_wave_transpose_sum(acc);
     if ((lane & 1) == 0) red[wave][lane >> 1] = ws;
+    if (TILED && n_active_out && blockIdx.x == 0) {
+        for (int d = 32; d > 0; d >>= 1) n_act += __shfl_xor(n_act, d, 64);
+        if (lane == 0) ired[wave] = n_act;
+    }
     __syncthreads();
     if (wave == 0 && (lane & 1) == 0) {
         float sum = 0.0f;
         for (int w = 0; w < nw; w++) sum += red[w][lane >> 1];
         if (o < f.cols) out[o] = ACC ? prev + sum : sum;
+    }
+    if (TILED && n_active_out && blockIdx.x == 0 && tid == 0) {
+        int c = 0;
+        for (int w = 0; w < nw; w++) c += ired[w];
+        *n_active_out = c;
     }
 }
 
@@ -624,10 +659,11 @@ static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial, 
     const int ff = wout->rows, rank = wout->fmt.cols;
     const int n_tiles = (ff + 63) / 64;
     const RowFmt &f = b->fmt;
-    const size_t lds = xs_bytes(f) + (size_t)(((rank + 3) & ~3) + 64 + 65) * 4;
-    hipLaunchKernelGGL(k_tile_up<T>, dim3(n_tiles), dim3(TILE_THREADS), lds, st, wout->d,
-                       wout->stride, ff, rank, partial, bias, thr, b->d, b->stride, f, x, act,
-                       mask, pairs);
+    constexpr int TN = fused_tn<T>();
+    const size_t lds = xs_bytes(f) + (size_t)(((rank + 3) & ~3) + TN + TN + 1 + TN / 64) * 4;
+    hipLaunchKernelGGL((k_tile_up<T, TN>), dim3((ff + TN - 1) / TN), dim3(tile_threads<TN>()), lds,
+                       st, wout->d, wout->stride, ff, rank, partial, bias, thr, b->d, b->stride, f,
+                       x, act, mask, pairs);
     const int px = down_per_xcd(f);
     if (accumulate)
         hipLaunchKernelGGL((k_sparse_down<T, true, true>), dim3(8 * px), dim3(DN_THREADS), 0, st,
@@ -650,7 +686,7 @@ int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *
     const RowFmt &f = b->fmt;
     const int ff = wout->rows, rank = wup->rows;
     const int n_tiles = (ff + 63) / 64;
-    if (xs_bytes(f) + (size_t)(rank + 136) * 4 > 64 * 1024)
+    if (xs_bytes(f) + (size_t)(rank + 2 * 128 + 8) * 4 > 64 * 1024)
         return llg_set_error(d, LLG_E_ARG, "predict_sparse: hidden size %d too large", f.cols);
     int2 *pairs = reinterpret_cast<int2 *>(ws + llg_predict_ws_bytes(rank, ff));
     float *partial;
