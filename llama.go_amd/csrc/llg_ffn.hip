@@ -10,7 +10,9 @@
 // MV_ROWS rows at a time and issues the loads of all their blocks before
 // using any (two layouts of the blocks over the lanes, below).  With
 // one chunk the row sum is final and the activation is applied; with several
-// chunks each workgroup adds its partial with an fp32 atomic into a zeroed y.
+// chunks each workgroup stores its partial sums, part[chunk][row], and
+// k_chunk_sum adds the chunks in order (a fixed order: results are the same
+// on every run).
 //
 // Gated (G): y[r] = silu(gate_r . x) * (up_r . x) (ffnSwiGLU, forward.go:
 // 368-389) with gate = w and up = w2; a wavefront's two row slots hold gate
@@ -34,8 +36,8 @@ __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w,
                                                   RowFmt f, int rows, int tile_rows,
                                                   int chunk_blocks,
                                                   const float *__restrict__ x, int act,
-                                                  float *__restrict__ y, float *__restrict__ zero,
-                                                  int zero_n, LlgLnArgs ln,
+                                                  float *__restrict__ y, float *__restrict__ part,
+                                                  LlgLnArgs ln,
                                                   const uint8_t *__restrict__ w2 = nullptr) {
     static_assert(!G || (LNP == 0 && MV_ROWS == 2), "gated rows pair gate and up");
     constexpr int RW = G ? 1 : MV_ROWS;  // output rows per wavefront pass
@@ -46,10 +48,6 @@ __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w,
     const int ch = blockIdx.x % n_chunks;
     const int cb0 = ch * chunk_blocks;
     const int cnb = min(chunk_blocks, f.nb - cb0);
-    if (zero) {
-        const int gtid = blockIdx.x * blockDim.x + threadIdx.x;
-        for (int i = gtid; i < zero_n; i += gridDim.x * blockDim.x) zero[i] = 0.0f;
-    }
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform per wavefront
     const int r_end = min(rows, (tile + 1) * tile_rows);
@@ -146,11 +144,24 @@ __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w,
                 if (n_chunks == 1)
                     y[r0 + q] = act >= 0 ? llg_act(act, v) : v;
                 else
-                    unsafeAtomicAdd(y + r0 + q, v);
+                    part[(size_t)ch * rows + r0 + q] = v;
             }
         }
     }
 }
+
+// y[r] = act(sum over the chunks c of part[c][r]), chunks in order.
+__global__ void k_chunk_sum(const float *__restrict__ part, int n_chunks, int rows, int act,
+                            float *__restrict__ y) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    float v = part[r];
+    for (int c = 1; c < n_chunks; c++) v += part[(size_t)c * rows + r];
+    y[r] = act >= 0 ? llg_act(act, v) : v;
+}
+
+// Floats of partial sums a matvec over w needs (0 when its rows fit one chunk).
+static size_t mv_part_floats(const RowFmt &f, int rows, int act);
 
 static int mv_chunk_blocks(const RowFmt &f, int act) {
     // An activation needs the whole row in one workgroup.
@@ -159,11 +170,17 @@ static int mv_chunk_blocks(const RowFmt &f, int act) {
     return (f.nb + n_chunks - 1) / n_chunks;
 }
 
-// zero/zero_n: a buffer the launch also clears (the next kernel's atomic target).
+static size_t mv_part_floats(const RowFmt &f, int rows, int act) {
+    const int cb = mv_chunk_blocks(f, act);
+    const int n_chunks = (f.nb + cb - 1) / cb;
+    return n_chunks > 1 ? (size_t)n_chunks * rows : 0;
+}
+
+// part: room for mv_part_floats (the partial sums of a chunked matvec).
 // ln (optional): the staged x is the LayerNorm of a residual sum (llg_stage_ln).
 // up (optional): gated rows, y = silu(w . x) * (up . x) (act is ignored).
 static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y,
-                         float *zero, int zero_n, const LlgLnArgs *ln = nullptr,
+                         float *part, const LlgLnArgs *ln = nullptr,
                          const LlgObject *up = nullptr) {
     hipStream_t st = llg_dev_stream(d);
     const RowFmt &f = w->fmt;
@@ -173,9 +190,8 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
     const size_t lds = (size_t)cb * MV_XS * 4;
     if (lds > 160 * 1024)
         return llg_set_error(d, LLG_E_ARG, "matvec: row of %d elements too long", f.cols);
-    if (n_chunks > 1 && zero != d_y) {
-        LLG_HIP_TRY(d, hipMemsetAsync(d_y, 0, (size_t)w->rows * 4, st));
-    }
+    if (n_chunks > 1 && !part)
+        return llg_set_error(d, LLG_E_ARG, "matvec: chunked rows need a partial buffer");
     const int tile_rows = (w->rows < MV_SMALL_ROWS ? MV_TILE_SMALL : MV_TILE) / (up ? 2 : 1);
     const int grid = (w->rows + tile_rows - 1) / tile_rows * n_chunks;
     const LlgLnArgs none{};
@@ -183,14 +199,13 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
     const int lnp = ln ? (ln->n / 4 + 255) / 256 : 0;
 #define MV_GO(TY, NP)                                                                              \
     hipLaunchKernelGGL((k_matvec_q<TY, NP>), dim3(grid), dim3(256), lds, st, w->d, w->stride, f,   \
-                       w->rows, tile_rows, cb, d_x, act, d_y, zero, zero_n, la,              \
-                       (const uint8_t *)nullptr)
+                       w->rows, tile_rows, cb, d_x, act, d_y, part, la, (const uint8_t *)nullptr)
 #define MV_LAUNCH(TY)                                                                              \
     do {                                                                                           \
         if (up)                                                                                    \
             hipLaunchKernelGGL((k_matvec_q<TY, 0, true>), dim3(grid), dim3(256), lds, st, w->d,    \
-                               w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, zero, zero_n, \
-                               la, up->d);                                                         \
+                               w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, part, la,     \
+                               up->d);                                                             \
         else if (!ln) MV_GO(TY, 0);                                                                \
         else if (lnp <= 2) MV_GO(TY, 2);                                                           \
         else if (lnp <= 4) MV_GO(TY, 4);                                                           \
@@ -217,6 +232,11 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
 #undef MV_LAUNCH
 #undef MV_GO
     LLG_LAUNCH_CHECK(d, "matvec_q");
+    if (n_chunks > 1) {
+        hipLaunchKernelGGL(k_chunk_sum, dim3((w->rows + 255) / 256), dim3(256), 0, st,
+                           (const float *)part, n_chunks, w->rows, act, d_y);
+        LLG_LAUNCH_CHECK(d, "matvec chunk sum");
+    }
     return 0;
 }
 
@@ -225,36 +245,44 @@ int llg_matvec_ln_enqueue(LlgDevice *d, const LlgObject *w, const LlgLnArgs &ln,
         return llg_set_error(d, LLG_E_ARG, "matvec: LayerNorm length %d != %d", ln.n, w->fmt.cols);
     if (ln.n > 256 * 16 * 4)
         return llg_set_error(d, LLG_E_ARG, "matvec: LayerNorm length %d above 16384", ln.n);
-    return matvec_launch(d, w, nullptr, -1, d_y, nullptr, 0, &ln);
+    return matvec_launch(d, w, nullptr, -1, d_y, nullptr, &ln);
 }
 
-int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y) {
-    return matvec_launch(d, w, d_x, act, d_y, nullptr, 0);
+int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y,
+                       float *part) {
+    return matvec_launch(d, w, d_x, act, d_y, part);
 }
 
-// Dense FFN: hid = act(up . x) (whole rows), then out = down . hid; the up
-// launch clears `out` when the down matvec accumulates over column chunks.
+size_t llg_matvec_part_bytes(const LlgObject *w, int act) {
+    return mv_part_floats(w->fmt, w->rows, act) * 4;
+}
+
+// Workspace of the dense FFN: the hidden row (ff floats), then the down
+// matvec's partial sums.
+static size_t dense_ws_bytes(const LlgObject *up, const LlgObject *down) {
+    return (size_t)llg_align((long long)up->rows * 4, 256) + llg_matvec_part_bytes(down, -1);
+}
+
+// Dense FFN: hid = act(up . x) (whole rows), then out = down . hid.
 static int dense_enqueue(LlgDevice *d, const LlgObject *up, const LlgObject *down,
-                         const float *d_x, int act, float *hid, float *d_out) {
+                         const float *d_x, int act, uint8_t *ws, float *d_out) {
     if (int rc = llg_check_act(d, act)) return rc;
-    const int down_chunks = (down->fmt.nb + mv_chunk_blocks(down->fmt, -1) - 1) /
-                            mv_chunk_blocks(down->fmt, -1);
-    int rc = matvec_launch(d, up, d_x, act, hid, down_chunks > 1 ? d_out : nullptr,
-                           down->rows);
+    float *hid = reinterpret_cast<float *>(ws);
+    float *part = reinterpret_cast<float *>(ws + llg_align((long long)up->rows * 4, 256));
+    int rc = matvec_launch(d, up, d_x, act, hid, nullptr);
     if (rc) return rc;
-    return matvec_launch(d, down, hid, -1, d_out, d_out, 0);
+    return matvec_launch(d, down, hid, -1, d_out, part);
 }
 
 // SwiGLU dense FFN (forward.go:368-389): hid = silu(gate . x) * (up . x),
 // then out = down . hid.
 static int swiglu_enqueue(LlgDevice *d, const LlgObject *gate, const LlgObject *up,
-                          const LlgObject *down, const float *d_x, float *hid, float *d_out) {
-    const int down_chunks = (down->fmt.nb + mv_chunk_blocks(down->fmt, -1) - 1) /
-                            mv_chunk_blocks(down->fmt, -1);
-    int rc = matvec_launch(d, gate, d_x, LLG_ACT_SILU, hid, down_chunks > 1 ? d_out : nullptr,
-                           down->rows, nullptr, up);
+                          const LlgObject *down, const float *d_x, uint8_t *ws, float *d_out) {
+    float *hid = reinterpret_cast<float *>(ws);
+    float *part = reinterpret_cast<float *>(ws + llg_align((long long)up->rows * 4, 256));
+    int rc = matvec_launch(d, gate, d_x, LLG_ACT_SILU, hid, nullptr, nullptr, up);
     if (rc) return rc;
-    return matvec_launch(d, down, hid, -1, d_out, d_out, 0);
+    return matvec_launch(d, down, hid, -1, d_out, part);
 }
 
 // ---------------------------------------------------------------------------
@@ -412,7 +440,13 @@ int llg_hipd_matvec_q(LlgHipDevice h, int64_t hm, const float *d_x, float *d_y) 
     int rc = check_matvec(d, w);
     if (rc) return rc;
     if (!d_x || !d_y) return llg_set_error(d, LLG_E_ARG, "matvec_q: null pointer");
-    return llg_matvec_enqueue(d, w, d_x, -1, d_y);
+    int rc2;
+    float *part = nullptr;
+    if (const size_t pb = llg_matvec_part_bytes(w, -1)) {
+        part = (float *)llg_ws(d, pb, &rc2);
+        if (rc2) return rc2;
+    }
+    return llg_matvec_enqueue(d, w, d_x, -1, d_y, part);
 }
 
 int llg_hip_matvec_q(LlgHipDevice h, int64_t hm, const float *x, float *y) {
@@ -424,10 +458,13 @@ int llg_hip_matvec_q(LlgHipDevice h, int64_t hm, const float *x, float *y) {
     if (rc) return rc;
     if (!x || !y) return llg_set_error(d, LLG_E_ARG, "matvec_q: null pointer");
     const long long o_y = llg_align((long long)w->fmt.cols * 4, 256);
-    uint8_t *ws = (uint8_t *)llg_ws(d, o_y + (size_t)w->rows * 4, &rc);
+    const long long o_p = o_y + llg_align((long long)w->rows * 4, 256);
+    uint8_t *ws = (uint8_t *)llg_ws(d, o_p + llg_matvec_part_bytes(w, -1), &rc);
     if (rc) return rc;
     if ((rc = llg_h2d(d, ws, x, (size_t)w->fmt.cols * 4))) return rc;
-    if ((rc = llg_matvec_enqueue(d, w, (const float *)ws, -1, (float *)(ws + o_y)))) return rc;
+    if ((rc = llg_matvec_enqueue(d, w, (const float *)ws, -1, (float *)(ws + o_y),
+                                 (float *)(ws + o_p))))
+        return rc;
     if ((rc = llg_d2h(d, y, ws + o_y, (size_t)w->rows * 4))) return rc;
     return llg_sync_dev(d);
 }
@@ -452,9 +489,9 @@ int llg_hipd_ffn_dense(LlgHipDevice h, int64_t hu, int64_t hdn, const float *d_x
     int rc = check_dense(d, hu, hdn, &up, &down);
     if (rc) return rc;
     if (!d_x || !d_out) return llg_set_error(d, LLG_E_ARG, "ffn_dense: null pointer");
-    float *hid = (float *)llg_ws(d, (size_t)up->rows * 4, &rc);
+    uint8_t *ws = (uint8_t *)llg_ws(d, dense_ws_bytes(up, down), &rc);
     if (rc) return rc;
-    return dense_enqueue(d, up, down, d_x, act, hid, d_out);
+    return dense_enqueue(d, up, down, d_x, act, ws, d_out);
 }
 
 int llg_hip_ffn_dense(LlgHipDevice h, int64_t hu, int64_t hdn, const float *x, int act,
@@ -468,10 +505,10 @@ int llg_hip_ffn_dense(LlgHipDevice h, int64_t hu, int64_t hdn, const float *x, i
     const int hd = up->fmt.cols, ff = up->rows;
     const long long o_out = llg_align((long long)hd * 4, 256);
     const long long o_h = o_out + llg_align((long long)hd * 4, 256);
-    uint8_t *ws = (uint8_t *)llg_ws(d, o_h + (size_t)ff * 4, &rc);
+    uint8_t *ws = (uint8_t *)llg_ws(d, o_h + dense_ws_bytes(up, down), &rc);
     if (rc) return rc;
     if ((rc = llg_h2d(d, ws, x, (size_t)hd * 4))) return rc;
-    if ((rc = dense_enqueue(d, up, down, (const float *)ws, act, (float *)(ws + o_h),
+    if ((rc = dense_enqueue(d, up, down, (const float *)ws, act, ws + o_h,
                             (float *)(ws + o_out))))
         return rc;
     if ((rc = llg_d2h(d, out, ws + o_out, (size_t)hd * 4))) return rc;
@@ -499,9 +536,9 @@ int llg_hipd_ffn_swiglu(LlgHipDevice h, int64_t hg, int64_t hu, int64_t hdn, con
     int rc = check_swiglu(d, hg, hu, hdn, &gate, &up, &down);
     if (rc) return rc;
     if (!d_x || !d_out) return llg_set_error(d, LLG_E_ARG, "ffn_swiglu: null pointer");
-    float *hid = (float *)llg_ws(d, (size_t)up->rows * 4, &rc);
+    uint8_t *ws = (uint8_t *)llg_ws(d, dense_ws_bytes(up, down), &rc);
     if (rc) return rc;
-    return swiglu_enqueue(d, gate, up, down, d_x, hid, d_out);
+    return swiglu_enqueue(d, gate, up, down, d_x, ws, d_out);
 }
 
 int llg_hip_ffn_swiglu(LlgHipDevice h, int64_t hg, int64_t hu, int64_t hdn, const float *x,
@@ -515,10 +552,10 @@ int llg_hip_ffn_swiglu(LlgHipDevice h, int64_t hg, int64_t hu, int64_t hdn, cons
     const int hd = up->fmt.cols, ff = up->rows;
     const long long o_out = llg_align((long long)hd * 4, 256);
     const long long o_h = o_out + llg_align((long long)hd * 4, 256);
-    uint8_t *ws = (uint8_t *)llg_ws(d, o_h + (size_t)ff * 4, &rc);
+    uint8_t *ws = (uint8_t *)llg_ws(d, o_h + dense_ws_bytes(up, down), &rc);
     if (rc) return rc;
     if ((rc = llg_h2d(d, ws, x, (size_t)hd * 4))) return rc;
-    if ((rc = swiglu_enqueue(d, gate, up, down, (const float *)ws, (float *)(ws + o_h),
+    if ((rc = swiglu_enqueue(d, gate, up, down, (const float *)ws, ws + o_h,
                              (float *)(ws + o_out))))
         return rc;
     if ((rc = llg_d2h(d, out, ws + o_out, (size_t)hd * 4))) return rc;

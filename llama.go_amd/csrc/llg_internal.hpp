@@ -55,7 +55,11 @@ int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, con
                        float *d_out, uint8_t *ws, const LlgFreshRows *fresh = nullptr);
 
 // Dense quantized matvec y[rows] = act(W . x) (llg_ffn.hip); act < 0 = none.
-int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y);
+// part: room for llg_matvec_part_bytes(w, act) (column-chunked rows keep
+// their partial sums there, added in chunk order); may be null when that is 0.
+int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y,
+                       float *part);
+size_t llg_matvec_part_bytes(const LlgObject *w, int act);
 // y = W . LayerNorm((x_in + a1) + a2), the residual sum and the normed row
 // also written to ln.x_out / ln.normed_out (llg_stage_ln).
 int llg_matvec_ln_enqueue(LlgDevice *d, const LlgObject *w, const LlgLnArgs &ln, float *d_y);

@@ -45,6 +45,7 @@ struct LlgModel {
     std::vector<LlgModelLayer> layers;
     // device buffers, carved out of the object's allocation
     float *x, *normed, *qkv, *attn, *attn_out, *logits, *kv, *pred_logits;  // x: the residual
+    float *mvpart;  // partial sums of a column-chunked Wo or LM-head matvec
     float2 *rope;  // [max_seq x head_dim/2] (cos, sin)
     int32_t *token, *n_active, *act_scratch;
     uint8_t *ws;
@@ -375,7 +376,7 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
             hipLaunchKernelGGL(k_attn<128>, dim3(m.n_heads), dim3(ATTN_THREADS), attn_lds, st, m.qkv,
                                m.n_heads, m.n_kv, pos, m.rope, m.max_seq, kvl, m.attn);
         LLG_LAUNCH_CHECK(d, "model attention");
-        if ((rc = llg_matvec_enqueue(d, L.wo, m.attn, -1, m.attn_out))) return rc;
+        if ((rc = llg_matvec_enqueue(d, L.wo, m.attn, -1, m.attn_out, m.mvpart))) return rc;
         if (pred_logits &&
             (rc = llg_predict_enqueue(d, L.pwup, L.pwout, nullptr, m.attn_out, L.thr, m.act_scratch,
                                       m.act_scratch + m.ff, pred_logits + (size_t)l * m.ff, m.ws)))
@@ -400,7 +401,7 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
     else if (np <= 8) RN(8);
     else RN(16);
 #undef RN
-    int rc = llg_matvec_enqueue(d, m.lm_head, m.normed, -1, m.logits);
+    int rc = llg_matvec_enqueue(d, m.lm_head, m.normed, -1, m.logits, m.mvpart);
     if (rc) return rc;
     hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, m.logits, m.vocab, token_out);
     LLG_LAUNCH_CHECK(d, "model step");
@@ -495,7 +496,11 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     const size_t v_pl = llg_align((long long)m->n_layers * m->ff * 4, 256);
     const size_t v_rope = llg_align((long long)m->max_seq * m->head_dim / 2 * 8, 256);
     const size_t wsb = model_ws_bytes(*m);
-    const size_t total = 3 * v_h + v_qkv + v_att + v_log + v_kv + v_i + v_ff + v_pl + v_rope + wsb;
+    size_t v_mp = llg_matvec_part_bytes(m->lm_head, -1);
+    for (const LlgModelLayer &L : m->layers) v_mp = std::max(v_mp, llg_matvec_part_bytes(L.wo, -1));
+    v_mp = llg_align((long long)v_mp, 256);
+    const size_t total =
+        3 * v_h + v_qkv + v_att + v_log + v_kv + v_i + v_ff + v_pl + v_rope + v_mp + wsb;
     uint8_t *buf = nullptr;
     if (hipMalloc(&buf, total) != hipSuccess) return fail(LLG_E_NOMEM, "buffer allocation failed");
     uint8_t *p = buf;
@@ -515,6 +520,8 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     p += v_pl;
     m->rope = reinterpret_cast<float2 *>(p);
     p += v_rope;
+    m->mvpart = v_mp ? reinterpret_cast<float *>(p) : nullptr;
+    p += v_mp;
     m->ws = p;
     hipStream_t st = llg_dev_stream(d);
     hipError_t e = hipMemsetAsync(buf, 0, total, st);

@@ -8,8 +8,12 @@
 //                  top-k, wsum guard and p/wsum (moe_forward.go:42-68)
 //   k_moe_gateup   h[s][j] = silu(gate_e[j] . x) * (up_e[j] . x) for the k
 //                  chosen experts (moe_forward.go:101-132)
-//   k_moe_down     out[d] = sum_s w_s * (down_e[d] . h[s]) accumulated in the
-//                  chosen order, starting from 0 (moe_forward.go:71-77, 141-148)
+//   k_moe_down     part[s][c][d] = down_e[d] . h[s] over column chunk c of h
+//   k_moe_dec_combine
+//                  out[d] = sum_s w_s * (sum_c part[s][c][d]), slots in the
+//                  chosen order and chunks in order, starting from 0
+//                  (moe_forward.go:71-77, 141-148): every sum has a fixed
+//                  order, so results are the same on every run
 // Expert e's rows are e*eff + j of gate/up and e*hidden + d of down, the
 // addressing of ReadContiguousRows (flash/storage.go:72-94).
 // Batches of 16 or more tokens over Q4_0 experts go to the grouped MFMA GEMM
@@ -154,8 +158,7 @@ __device__ __forceinline__ void moe_rows_dot(const uint8_t *const (&rp)[NR], con
 // h[ts][j] = silu(gate_e[j] . x_t) * (up_e[j] . x_t), ts = token*k + slot,
 // e = ids[ts] (moe_forward.go:101-132).  Workgroup: one ts, MOE_GU_TILE
 // consecutive j; each wavefront owns MOE_GU_J j (2*MOE_GU_J rows: gate, up)
-// whose loads are issued before x_t is staged.  `zero` (the down kernel's
-// atomic target) is cleared here.
+// whose loads are issued before x_t is staged.
 #define MOE_GU_J 4
 #define MOE_GU_TILE (4 * MOE_GU_J)
 template <int T, int NB>
@@ -164,16 +167,13 @@ __global__ __launch_bounds__(256) void k_moe_gateup(const uint8_t *__restrict__ 
                                                     long long stride, RowFmt f, int eff, int k,
                                                     const int32_t *__restrict__ ids,
                                                     const float *__restrict__ x,
-                                                    float *__restrict__ hbuf,
-                                                    float *__restrict__ zero, int zero_n) {
+                                                    float *__restrict__ hbuf) {
     extern __shared__ float xs[];
     const int n_tiles = (eff + MOE_GU_TILE - 1) / MOE_GU_TILE;
     const int ts = blockIdx.x / n_tiles;
     const int j0 = (blockIdx.x % n_tiles) * MOE_GU_TILE +
                    MOE_GU_J * __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < zero_n; i += gridDim.x * blockDim.x)
-        zero[i] = 0.0f;
     const int e = ids[ts];
     const int t = ts / k;
     const uint8_t *rp[2 * MOE_GU_J];
@@ -205,10 +205,10 @@ __global__ __launch_bounds__(256) void k_moe_gateup(const uint8_t *__restrict__ 
     }
 }
 
-// out[t][d] += w_s * (down_e[d] . h[ts]) over one column chunk of h
-// (moe_forward.go:71-77, 141-148; chunks and slots meet in fp32 atomics on a
-// zeroed out).  Workgroup: one ts, MOE_DN_TILE consecutive d, one chunk of at
-// most MOE_DN_CHUNK blocks of h staged in LDS; wavefront: MOE_DN_R rows.
+// part[ts][ch][d] = down_e[d] . h[ts] over column chunk ch of h
+// (moe_forward.go:141-148); k_moe_dec_combine adds the chunks and slots.
+// Workgroup: one ts, MOE_DN_TILE consecutive d, one chunk of at most
+// MOE_DN_CHUNK blocks of h staged in LDS; wavefront: MOE_DN_R rows.
 #define MOE_DN_R 4
 #define MOE_DN_TILE (4 * MOE_DN_R)
 #define MOE_DN_CHUNK 160
@@ -217,9 +217,8 @@ __global__ __launch_bounds__(256) void k_moe_down(const uint8_t *__restrict__ do
                                                   long long stride, RowFmt f, int hidden, int k,
                                                   int chunk_blocks,
                                                   const int32_t *__restrict__ ids,
-                                                  const float *__restrict__ wts,
                                                   const float *__restrict__ hbuf,
-                                                  float *__restrict__ out) {
+                                                  float *__restrict__ part) {
     extern __shared__ float xs[];
     const int n_chunks = (f.nb + chunk_blocks - 1) / chunk_blocks;
     const int n_tiles = (hidden + MOE_DN_TILE - 1) / MOE_DN_TILE;
@@ -231,7 +230,6 @@ __global__ __launch_bounds__(256) void k_moe_down(const uint8_t *__restrict__ do
     const int cb0 = ch * chunk_blocks;
     const int cnb = min(chunk_blocks, f.nb - cb0);
     const int e = ids[ts];
-    const int t = ts / k;
     const uint8_t *rp[MOE_DN_R];
 #pragma unroll
     for (int q = 0; q < MOE_DN_R; q++)  // rows past hidden reload the last row, dropped
@@ -249,13 +247,13 @@ __global__ __launch_bounds__(256) void k_moe_down(const uint8_t *__restrict__ do
         m.issue(rp, f, cb0 + b0, cnb - b0);
         m.use(xs, b0, min(cnb - b0, 64 * NB), s);
     }
-    const float ws = wts[ts];
 #pragma unroll
     for (int q = 0; q < MOE_DN_R; q++) s[q] = llg_wave_sum(s[q]);
     if (lane == 0) {
+        float *pr = part + ((size_t)ts * n_chunks + ch) * hidden;
 #pragma unroll
         for (int q = 0; q < MOE_DN_R; q++)
-            if (d0 + q < hidden) unsafeAtomicAdd(out + (size_t)t * hidden + d0 + q, ws * s[q]);
+            if (d0 + q < hidden) pr[d0 + q] = s[q];
     }
 }
 
@@ -343,9 +341,7 @@ template <int T>
 __global__ __launch_bounds__(256, MOE_P_BLOCKS) void k_moe_gateup_p(
     const uint8_t *__restrict__ gate, const uint8_t *__restrict__ up, long long stride, RowFmt f,
     int eff, int k, int n_items, const int32_t *__restrict__ ids,
-    const float *__restrict__ x, float *__restrict__ hbuf, float *__restrict__ zero, int zero_n) {
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < zero_n; i += gridDim.x * blockDim.x)
-        zero[i] = 0.0f;
+    const float *__restrict__ x, float *__restrict__ hbuf) {
     const int lane = threadIdx.x & 63;
     const long long W = (long long)gridDim.x * 4;
     const long long w = (long long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -385,8 +381,8 @@ __global__ __launch_bounds__(256, MOE_P_BLOCKS) void k_moe_gateup_p(
 
 // down item = MOE_DN_P consecutive d of one (ts, chunk of 64 blocks of h):
 // item index = (ts * n_chunks + chunk) * (hidden / MOE_DN_P) + d / MOE_DN_P,
-// so a wavefront's range mostly shares one h slice.  out[t][d] += w_ts *
-// partial (fp32 atomics on the zeroed out).
+// so a wavefront's range mostly shares one h slice.  The item's dot products
+// go to part[ts][chunk][d]; k_moe_dec_combine adds chunks and slots.
 #define MOE_DN_P 8
 template <int T>
 __device__ __forceinline__ void dn_issue(BlockRaw<T> (&r)[MOE_DN_P],
@@ -398,7 +394,7 @@ __device__ __forceinline__ void dn_issue(BlockRaw<T> (&r)[MOE_DN_P],
 
 template <int T>
 __device__ __forceinline__ void dn_finish(const BlockRaw<T> (&r)[MOE_DN_P], const XSlice<1> &hs,
-                                          bool ok, float ws, float *__restrict__ o) {
+                                          bool ok, float *__restrict__ o) {
     float s[MOE_DN_P];
 #pragma unroll
     for (int q = 0; q < MOE_DN_P; q++) {
@@ -409,15 +405,14 @@ __device__ __forceinline__ void dn_finish(const BlockRaw<T> (&r)[MOE_DN_P], cons
     for (int q = 0; q < MOE_DN_P; q++) s[q] = llg_wave_sum(s[q]);
     if ((threadIdx.x & 63) == 0) {
 #pragma unroll
-        for (int q = 0; q < MOE_DN_P; q++) unsafeAtomicAdd(o + q, ws * s[q]);
+        for (int q = 0; q < MOE_DN_P; q++) o[q] = s[q];
     }
 }
 
 template <int T>
 __global__ __launch_bounds__(256, MOE_P_BLOCKS) void k_moe_down_p(
     const uint8_t *__restrict__ down, long long stride, RowFmt f, int hidden, int k, int n_items,
-    const int32_t *__restrict__ ids, const float *__restrict__ wts, const float *__restrict__ hbuf,
-    float *__restrict__ out) {
+    const int32_t *__restrict__ ids, const float *__restrict__ hbuf, float *__restrict__ part) {
     const int lane = threadIdx.x & 63;
     const long long W = (long long)gridDim.x * 4;
     const long long w = (long long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -434,7 +429,6 @@ __global__ __launch_bounds__(256, MOE_P_BLOCKS) void k_moe_down_p(
     int sc_h = sc_a, ts_h = ts_e;
     XSlice<1> hs;
     xslice_load<1>(hs, hbuf + (size_t)ts_h * f.cols, (sc_h - ts_h * n_chunks) * 64, f.nb);
-    float ws = wts[ts_h];
     for (int i = i0;;) {
         if (i + 1 < i1) {
             sc_b = (i + 1) / per_chunk;
@@ -448,10 +442,9 @@ __global__ __launch_bounds__(256, MOE_P_BLOCKS) void k_moe_down_p(
             sc_h = sc_a;
             ts_h = sc_a / n_chunks;
             xslice_load<1>(hs, hbuf + (size_t)ts_h * f.cols, (sc_h - ts_h * n_chunks) * 64, f.nb);
-            ws = wts[ts_h];
         }
-        dn_finish<T>(ra, hs, (sc_h - ts_h * n_chunks) * 64 + lane < f.nb, ws,
-                     out + (size_t)(ts_h / k) * hidden + MOE_DN_P * (i - sc_a * per_chunk));
+        dn_finish<T>(ra, hs, (sc_h - ts_h * n_chunks) * 64 + lane < f.nb,
+                     part + (size_t)sc_h * hidden + MOE_DN_P * (i - sc_a * per_chunk));
         if (++i >= i1) break;
         if (i + 1 < i1) {
             sc_a = (i + 1) / per_chunk;
@@ -465,12 +458,41 @@ __global__ __launch_bounds__(256, MOE_P_BLOCKS) void k_moe_down_p(
             sc_h = sc_b;
             ts_h = sc_b / n_chunks;
             xslice_load<1>(hs, hbuf + (size_t)ts_h * f.cols, (sc_h - ts_h * n_chunks) * 64, f.nb);
-            ws = wts[ts_h];
         }
-        dn_finish<T>(rb, hs, (sc_h - ts_h * n_chunks) * 64 + lane < f.nb, ws,
-                     out + (size_t)(ts_h / k) * hidden + MOE_DN_P * (i - sc_b * per_chunk));
+        dn_finish<T>(rb, hs, (sc_h - ts_h * n_chunks) * 64 + lane < f.nb,
+                     part + (size_t)sc_h * hidden + MOE_DN_P * (i - sc_b * per_chunk));
         if (++i >= i1) break;
     }
+}
+
+// out[t][d] = sum over the slots s of w[t][s] * (sum over the chunks c of
+// part[t*k + s][c][d]), slots in order from 0 and chunks in order
+// (moe_forward.go:71-77): one thread per 4 outputs.
+__global__ void k_moe_dec_combine(const float *__restrict__ part, const float *__restrict__ w,
+                                  int k, int n_tok, int hidden, int n_chunks,
+                                  float *__restrict__ out) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;  // float4 index
+    const int h4 = hidden / 4;
+    if (i >= (long long)n_tok * h4) return;
+    const int t = (int)(i / h4), d4 = (int)(i % h4);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int sl = 0; sl < k; sl++) {
+        const float ws = w[t * k + sl];
+        const float4 *pr = reinterpret_cast<const float4 *>(part + (size_t)(t * k + sl) * n_chunks * hidden);
+        float4 y = pr[d4];
+        for (int c = 1; c < n_chunks; c++) {
+            const float4 q = pr[(size_t)c * h4 + d4];
+            y.x += q.x;
+            y.y += q.y;
+            y.z += q.z;
+            y.w += q.w;
+        }
+        acc.x += ws * y.x;
+        acc.y += ws * y.y;
+        acc.z += ws * y.z;
+        acc.w += ws * y.w;
+    }
+    reinterpret_cast<float4 *>(out)[i] = acc;
 }
 
 struct MoeArgs {
@@ -518,28 +540,51 @@ static bool use_gemm(const MoeArgs &a, int n_tok) {
     return llg_moe_gemm_supported(a.gate->fmt.type, a.hidden, a.eff, n_tok);
 }
 
+// Column chunks of h the decode down kernels split a row into (64 blocks for
+// the persistent form, up to MOE_DN_CHUNK for the tile form).
+static int moe_dec_chunks(const MoeArgs &a, bool persistent) {
+    const int nb = a.down->fmt.nb;
+    if (persistent) return (nb + 63) / 64;
+    return (nb + MOE_DN_CHUNK - 1) / MOE_DN_CHUNK;
+}
+
+static size_t moe_hbuf_bytes(const MoeArgs &a, int n_tok) {
+    return (size_t)llg_align((long long)n_tok * a.k * a.eff * 4, 256);
+}
+
 static size_t moe_ws_bytes(const MoeArgs &a, int n_tok) {
     const size_t head = (size_t)llg_align((long long)n_tok * a.k * 4, 256) * 2;
     if (use_gemm(a, n_tok))
         return head + llg_moe_gemm_ws_bytes(n_tok, a.k, a.n_exp, a.hidden, a.eff);
-    return head + (size_t)n_tok * a.k * a.eff * 4;
+    // h, then the down partials (the larger chunk count of the two forms)
+    return head + moe_hbuf_bytes(a, n_tok) +
+           (size_t)n_tok * a.k * moe_dec_chunks(a, true) * a.hidden * 4;
+}
+
+static void moe_launch_combine(hipStream_t st, const MoeArgs &a, int n_tok, const float *w,
+                               const float *part, int n_chunks, float *out) {
+    const long long n4 = (long long)n_tok * a.hidden / 4;
+    hipLaunchKernelGGL(k_moe_dec_combine, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st,
+                       part, w, a.k, n_tok, a.hidden, n_chunks, out);
 }
 
 template <int T, int NB>
 static void moe_launch_experts_nb(hipStream_t st, const MoeArgs &a, int n_tok, const int32_t *ids,
-                                  const float *w, const float *x, float *hbuf, float *out) {
+                                  const float *w, const float *x, float *hbuf, float *part,
+                                  float *out) {
     const long long nts = (long long)n_tok * a.k;
     const long long g1 = nts * ((a.eff + MOE_GU_TILE - 1) / MOE_GU_TILE);
     hipLaunchKernelGGL((k_moe_gateup<T, NB>), dim3((unsigned)g1), dim3(256),
                        (size_t)a.gate->fmt.nb * MOE_XS * 4, st, a.gate->d, a.up->d, a.gate->stride,
-                       a.gate->fmt, a.eff, a.k, ids, x, hbuf, out, n_tok * a.hidden);
+                       a.gate->fmt, a.eff, a.k, ids, x, hbuf);
     const int nb = a.down->fmt.nb;
-    const int n_chunks = (nb + MOE_DN_CHUNK - 1) / MOE_DN_CHUNK;
+    const int n_chunks = moe_dec_chunks(a, false);
     const int cb = (nb + n_chunks - 1) / n_chunks;
     const long long g2 = nts * ((a.hidden + MOE_DN_TILE - 1) / MOE_DN_TILE) * n_chunks;
     hipLaunchKernelGGL((k_moe_down<T, 3>), dim3((unsigned)g2), dim3(256), (size_t)cb * MOE_XS * 4,
-                       st, a.down->d, a.down->stride, a.down->fmt, a.hidden, a.k, cb, ids, w, hbuf,
-                       out);
+                       st, a.down->d, a.down->stride, a.down->fmt, a.hidden, a.k, cb, ids, hbuf,
+                       part);
+    moe_launch_combine(st, a, n_tok, w, part, n_chunks, out);
 }
 
 // Q4_0/Q8_0 with hidden <= 4096 take the persistent kernels; other shapes and
@@ -547,7 +592,7 @@ static void moe_launch_experts_nb(hipStream_t st, const MoeArgs &a, int n_tok, c
 template <int T>
 static void moe_launch_experts(hipStream_t st, int cus, const MoeArgs &a, int n_tok,
                                const int32_t *ids, const float *w, const float *x, float *hbuf,
-                               float *out) {
+                               float *part, float *out) {
     if constexpr (T == LLG_TYPE_Q4_0 || T == LLG_TYPE_Q8_0) {
         const long long n_dn = (long long)n_tok * a.k * ((a.down->fmt.nb + 63) / 64) * a.hidden / MOE_DN_P;
         if (a.gate->fmt.nb <= 128 && a.hidden % MOE_DN_P == 0 && n_dn < (1LL << 31) &&
@@ -560,17 +605,19 @@ static void moe_launch_experts(hipStream_t st, int cus, const MoeArgs &a, int n_
             const long long g1 = std::min(full, (gu_items + 3) / 4);
             const long long g2 = std::min(full, (dn_items + 3) / 4);
             hipLaunchKernelGGL(k_moe_gateup_p<T>, dim3((unsigned)g1), dim3(256), 0, st, a.gate->d,
-                               a.up->d, a.gate->stride, a.gate->fmt, a.eff, a.k, (int)gu_items, ids, x, hbuf,
-                               out, n_tok * a.hidden);
+                               a.up->d, a.gate->stride, a.gate->fmt, a.eff, a.k, (int)gu_items, ids, x,
+                               hbuf);
             hipLaunchKernelGGL(k_moe_down_p<T>, dim3((unsigned)g2), dim3(256), 0, st, a.down->d,
-                               a.down->stride, a.down->fmt, a.hidden, a.k, (int)dn_items, ids, w, hbuf, out);
+                               a.down->stride, a.down->fmt, a.hidden, a.k, (int)dn_items, ids, hbuf,
+                               part);
+            moe_launch_combine(st, a, n_tok, w, part, n_chunks, out);
             return;
         }
     }
     if (a.gate->fmt.nb <= 64)
-        moe_launch_experts_nb<T, 1>(st, a, n_tok, ids, w, x, hbuf, out);
+        moe_launch_experts_nb<T, 1>(st, a, n_tok, ids, w, x, hbuf, part, out);
     else
-        moe_launch_experts_nb<T, 2>(st, a, n_tok, ids, w, x, hbuf, out);
+        moe_launch_experts_nb<T, 2>(st, a, n_tok, ids, w, x, hbuf, part, out);
 }
 
 static int moe_enqueue(LlgDevice *d, const MoeArgs &a, const float *d_x, int n_tok, float *d_out,
@@ -580,6 +627,7 @@ static int moe_enqueue(LlgDevice *d, const MoeArgs &a, const float *d_x, int n_t
     int32_t *ids = d_ids ? d_ids : reinterpret_cast<int32_t *>(ws);
     float *w = d_w ? d_w : reinterpret_cast<float *>(ws + kb);
     float *hbuf = reinterpret_cast<float *>(ws + 2 * kb);
+    float *part = reinterpret_cast<float *>(ws + 2 * kb + moe_hbuf_bytes(a, n_tok));
     hipLaunchKernelGGL(k_moe_router, dim3(n_tok), dim3(512), 0, st, a.router->d, a.router->stride,
                        a.hidden, a.n_exp, a.k, d_x, (const float *)nullptr, ids, w);
     LLG_LAUNCH_CHECK(d, "moe_router");
@@ -588,16 +636,16 @@ static int moe_enqueue(LlgDevice *d, const MoeArgs &a, const float *d_x, int n_t
                                     n_tok, ids, w, d_out, ws + 2 * kb);
     switch (a.gate->fmt.type) {
     case LLG_TYPE_Q4_0:
-        moe_launch_experts<LLG_TYPE_Q4_0>(st, llg_cu_count(d), a, n_tok, ids, w, d_x, hbuf, d_out);
+        moe_launch_experts<LLG_TYPE_Q4_0>(st, llg_cu_count(d), a, n_tok, ids, w, d_x, hbuf, part, d_out);
         break;
     case LLG_TYPE_Q8_0:
-        moe_launch_experts<LLG_TYPE_Q8_0>(st, llg_cu_count(d), a, n_tok, ids, w, d_x, hbuf, d_out);
+        moe_launch_experts<LLG_TYPE_Q8_0>(st, llg_cu_count(d), a, n_tok, ids, w, d_x, hbuf, part, d_out);
         break;
     case LLG_TYPE_F16:
-        moe_launch_experts<LLG_TYPE_F16>(st, llg_cu_count(d), a, n_tok, ids, w, d_x, hbuf, d_out);
+        moe_launch_experts<LLG_TYPE_F16>(st, llg_cu_count(d), a, n_tok, ids, w, d_x, hbuf, part, d_out);
         break;
     case LLG_TYPE_F32:
-        moe_launch_experts<LLG_TYPE_F32>(st, llg_cu_count(d), a, n_tok, ids, w, d_x, hbuf, d_out);
+        moe_launch_experts<LLG_TYPE_F32>(st, llg_cu_count(d), a, n_tok, ids, w, d_x, hbuf, part, d_out);
         break;
     default:
         return llg_set_error(d, LLG_E_TYPE, "moe: unsupported type");

@@ -111,3 +111,49 @@ def test_falcon_decode_bit_identical(dev, rng):
     for l0, l1 in zip(runs[0][0], runs[1][0]):
         assert np.array_equal(_bits(l0), _bits(l1))
     assert np.array_equal(runs[0][1], runs[1][1])
+
+
+def _gpu_quant(shape, std, seed, t):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return gg.quantize(torch.randn(shape, generator=g, device="cuda") * std, t).cpu().numpy()
+
+
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0])
+def test_dense_ffn_repeats_bit_identical(dev, rng, t):
+    """The dense FFN at the Falcon-7B layer's shape: its down matvec splits the
+    18176-wide rows into column chunks whose partial sums are added in chunk
+    order, so repeated calls agree to the bit."""
+    h, ff = 4544, 18176
+    up, down = _gpu_quant((ff, h), 0.02, 41, t), _gpu_quant((h, ff), 0.02, 42, t)
+    u, d = dev.upload_matrix(up, t, ff, h), dev.upload_matrix(down, t, h, ff)
+    x = normal(rng, h, 1.0)
+    outs = [llg.ffn_dense(dev, u, d, x, gg.ACT_RELU) for _ in range(REPEATS)]
+    _same_bits(outs)
+    assert max_rel_err(outs[0], R.ffn_dense(up, down, t, h, ff, x)) <= 1e-3
+    gate = _gpu_quant((ff, h), 0.02, 43, t)
+    gt = dev.upload_matrix(gate, t, ff, h)
+    _same_bits([llg.ffn_swiglu(dev, gt, u, d, x) for _ in range(REPEATS)])
+    for m in (u, d, gt):
+        m.release()
+
+
+@pytest.mark.parametrize("n_tok", [1, 3, 77])
+def test_moe_repeats_bit_identical(dev, rng, n_tok):
+    """moeFFN at the Mixtral layer's shape: decode batches (per-token expert
+    kernels, partial dot products added in chunk then slot order) and a
+    grouped-GEMM batch give bit-identical outputs, ids and weights."""
+    d, eff, E, k = 4096, 14336, 8, 2
+    router = normal(rng, (E, d), 0.02)
+    gate = _gpu_quant((E * eff, d), 0.02, 51, gg.Q4_0)
+    up = _gpu_quant((E * eff, d), 0.02, 52, gg.Q4_0)
+    down = _gpu_quant((E * d, eff), 0.02, 53, gg.Q4_0)
+    hs = [dev.upload_f32(router), dev.upload_matrix(gate, gg.Q4_0, E * eff, d),
+          dev.upload_matrix(up, gg.Q4_0, E * eff, d), dev.upload_matrix(down, gg.Q4_0, E * d, eff)]
+    x = normal(rng, (n_tok, d), 1.0)
+    res = [llg.moe_ffn(dev, *hs, E, k, x) for _ in range(REPEATS)]
+    _same_bits([r[0] for r in res])
+    for r in res[1:]:
+        assert np.array_equal(r[1], res[0][1]) and np.array_equal(_bits(r[2]), _bits(res[0][2]))
+    for hnd in hs:
+        hnd.release()

@@ -240,7 +240,7 @@ def test_ffn_dense_config1(dev, rng, t, act):
 def test_ffn_swiglu_llama7b_shape(dev, rng, t):
     """ffnSwiGLU (forward.go:368-389) at a LLaMA-7B layer's shape (d = 4096,
     F = 11008): the down rows are 11008 long, so the down matvec splits
-    columns into chunks and accumulates with atomics."""
+    columns into chunks and adds their partial sums in chunk order."""
     h, ff = 4096, 11008
     gate = gpu_quant((ff, h), 0.02, 41, t)
     up = gpu_quant((ff, h), 0.02, 42, t)
@@ -760,6 +760,24 @@ def test_falcon_forward(dev, rng, n_kv, t):
     with pytest.raises(llg.LlgError) as e:
         m.forward(d["vocab"], 0)
     assert e.value.code == llg.LLG_E_RANGE
+    m.release()
+
+
+def test_falcon_wide_heads_chunked_wo(dev, rng):
+    """48 query heads of 128 over 4 KV heads: Wo's rows are 6144 wide, so its
+    matvec runs in column chunks whose partial sums the model adds in order;
+    against the oracle at every position."""
+    d = dict(FALCON_GPU, hidden=512, n_heads=48, n_kv=4, head_dim=128, ff=1024, max_seq=16)
+    w = make_falcon(rng, d, std=0.02)
+    toks = rng.integers(0, d["vocab"], 8)
+    _, nact, thr = ref_falcon_f64(w, d, toks)
+    ref = R.Falcon(d, w, thr)
+    m = llg.FalconModel(dev, d, w, thr)
+    for s, tk in enumerate(toks):
+        lg, _, na = m.forward(int(tk), s)
+        rl, rn = ref.forward(int(tk), s)
+        assert np.array_equal(na, rn), (s, na, rn)
+        assert max_rel_err(lg, rl) <= TOL, s
     m.release()
 
 
