@@ -24,15 +24,17 @@
 #define MV_TILE 32        // rows per workgroup (4 wavefronts x 4 passes x MV_ROWS)
 #define MV_TILE_SMALL 8   // rows per workgroup below MV_SMALL_ROWS rows (one pass)
 #define MV_SMALL_ROWS 8192
+#define MV_BAL_MIN 2048   // balanced launch from this many rows (at least 4 wavefronts per CU)
 #define MV_CHUNK 160      // max blocks of x staged per workgroup
 #define MV_XS 36          // staged floats per 32-float block
 #define MV_BATCH 3        // pair layout: blocks per lane per row and step
 #define MV_NI 5           // flat layout: slots per lane per step (MV_ROWS x MV_CHUNK / 64, rounded up)
 
 // LNP > 0: x is the LayerNorm of a residual sum, staged with LNP float4 groups
-// per thread (llg_stage_ln); LNP = 0: x is read from memory.
-template <int T, int LNP, bool G = false>
-__global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w, long long stride,
+// per thread (llg_stage_ln); LNP = 0: x is read from memory.  NT: the largest
+// workgroup the instance is launched with.
+template <int T, int LNP, bool G = false, int NT = 256>
+__global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, long long stride,
                                                   RowFmt f, int rows, int tile_rows,
                                                   int chunk_blocks,
                                                   const float *__restrict__ x, int act,
@@ -42,7 +44,7 @@ __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w,
     static_assert(!G || (LNP == 0 && MV_ROWS == 2), "gated rows pair gate and up");
     constexpr int RW = G ? 1 : MV_ROWS;  // output rows per wavefront pass
     extern __shared__ float xs[];
-    __shared__ float red[4];
+    __shared__ float red[NT / 64];
     const int n_chunks = (f.nb + chunk_blocks - 1) / chunk_blocks;
     const int tile = blockIdx.x / n_chunks;
     const int ch = blockIdx.x % n_chunks;
@@ -100,7 +102,8 @@ __global__ __launch_bounds__(256) void k_matvec_q(const uint8_t *__restrict__ w,
     else
         llg_stage_x_sum<MV_XS>(xs, x + (size_t)cb0 * 32, cnb, issue_first);
     __syncthreads();
-    for (int r0 = r_first; r0 < r_end; r0 += 4 * RW) {
+    const int n_waves = blockDim.x >> 6;
+    for (int r0 = r_first; r0 < r_end; r0 += n_waves * RW) {
         float s[MV_ROWS] = {0.0f, 0.0f};
         for (int kb = 0; kb < n_slots; kb += 64 * (FLAT ? MV_NI : MV_BATCH)) {
             if (r0 != r_first || kb != 0) issue(r0, kb);
@@ -192,14 +195,40 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
         return llg_set_error(d, LLG_E_ARG, "matvec: row of %d elements too long", f.cols);
     if (n_chunks > 1 && !part)
         return llg_set_error(d, LLG_E_ARG, "matvec: chunked rows need a partial buffer");
-    const int tile_rows = (w->rows < MV_SMALL_ROWS ? MV_TILE_SMALL : MV_TILE) / (up ? 2 : 1);
-    const int grid = (w->rows + tile_rows - 1) / tile_rows * n_chunks;
+    int tile_rows = (w->rows < MV_SMALL_ROWS ? MV_TILE_SMALL : MV_TILE) / (up ? 2 : 1);
+    int threads = 256;
     const LlgLnArgs none{};
     const LlgLnArgs &la = ln ? *ln : none;
-    const int lnp = ln ? (ln->n / 4 + 255) / 256 : 0;
+    int lnp = ln ? (ln->n / 4 + 255) / 256 : 0;
+    // Balanced: a matrix of MV_BAL_MIN..MV_SMALL_ROWS whole rows goes to at
+    // most one workgroup per CU, each a single pass of MV_ROWS rows per
+    // wavefront, so x (or the LayerNorm inputs) is staged once per CU rather
+    // than by two or three workgroups of 8 rows.
+    bool bal = false;
+    if (!up && n_chunks == 1 && w->rows >= MV_BAL_MIN && w->rows < MV_SMALL_ROWS) {
+        const int cus = llg_cu_count(d);
+        const int rpw = MV_ROWS * ((w->rows + MV_ROWS * cus - 1) / (MV_ROWS * cus));
+        const int th = 64 * (rpw / MV_ROWS);
+        const int lnp_b = ln ? (ln->n / 4 + th - 1) / th : 0;
+        if (th >= 256 && th <= 1024 && lnp_b <= 4) {
+            bal = true;
+            tile_rows = rpw;
+            threads = th;
+            lnp = lnp_b;
+        }
+    }
+    const int grid = (w->rows + tile_rows - 1) / tile_rows * n_chunks;
 #define MV_GO(TY, NP)                                                                              \
-    hipLaunchKernelGGL((k_matvec_q<TY, NP>), dim3(grid), dim3(256), lds, st, w->d, w->stride, f,   \
-                       w->rows, tile_rows, cb, d_x, act, d_y, part, la, (const uint8_t *)nullptr)
+    do {                                                                                           \
+        if (bal)                                                                                   \
+            hipLaunchKernelGGL((k_matvec_q<TY, (NP <= 4 ? NP : 4), false, 1024>), dim3(grid),      \
+                               dim3(threads), lds, st, w->d, w->stride, f, w->rows, tile_rows, cb, \
+                               d_x, act, d_y, part, la, (const uint8_t *)nullptr);                 \
+        else                                                                                       \
+            hipLaunchKernelGGL((k_matvec_q<TY, NP>), dim3(grid), dim3(256), lds, st, w->d,         \
+                               w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, part, la,     \
+                               (const uint8_t *)nullptr);                                         \
+    } while (0)
 #define MV_LAUNCH(TY)                                                                              \
     do {                                                                                           \
         if (up)                                                                                    \
@@ -502,7 +531,7 @@ int llg_hip_ffn_dense(LlgHipDevice h, int64_t hu, int64_t hdn, const float *x, i
     int rc = check_dense(d, hu, hdn, &up, &down);
     if (rc) return rc;
     if (!x || !out) return llg_set_error(d, LLG_E_ARG, "ffn_dense: null pointer");
-    const int hd = up->fmt.cols, ff = up->rows;
+    const int hd = up->fmt.cols;
     const long long o_out = llg_align((long long)hd * 4, 256);
     const long long o_h = o_out + llg_align((long long)hd * 4, 256);
     uint8_t *ws = (uint8_t *)llg_ws(d, o_h + dense_ws_bytes(up, down), &rc);
@@ -549,7 +578,7 @@ int llg_hip_ffn_swiglu(LlgHipDevice h, int64_t hg, int64_t hu, int64_t hdn, cons
     int rc = check_swiglu(d, hg, hu, hdn, &gate, &up, &down);
     if (rc) return rc;
     if (!x || !out) return llg_set_error(d, LLG_E_ARG, "ffn_swiglu: null pointer");
-    const int hd = up->fmt.cols, ff = up->rows;
+    const int hd = up->fmt.cols;
     const long long o_out = llg_align((long long)hd * 4, 256);
     const long long o_h = o_out + llg_align((long long)hd * 4, 256);
     uint8_t *ws = (uint8_t *)llg_ws(d, o_h + dense_ws_bytes(up, down), &rc);

@@ -159,174 +159,259 @@ __global__ void k_rope_table(float2 *__restrict__ tab, int max_seq, int half, fl
     tab[j] = make_float2((float)cos(fr), (float)sin(fr));
 }
 
-// One workgroup per query head; HD = head_dim (64 or 128).  HD/4 lanes hold
-// one key row (a float4 each), so a wavefront scores 256/HD positions per
-// load; each lane requests ATT_U rows before reducing any.  Rows 0..pos-1 come
-// from the layer's cache; row pos is this token's rotated key / value, taken
-// from registers and LDS (the cache row is written by the group's first query
-// head for later tokens, so no workgroup waits on another).  Scores live in
-// LDS (pos + 1 floats).
-#define ATT_U 8     // key rows per lane requested together
-#define ATT_VU 8    // value rows per thread requested together
+// One workgroup per query head; HD = head_dim (64 or 128).  LP = HD/4 lanes
+// hold one cached row (a float4 each), so a wavefront covers PW = 64/LP
+// positions per load and U loads: a round of the workgroup covers
+// PR = 16 * PW * U positions, wavefront w taking the PW*U consecutive rows
+// from w*PW*U.  Every key and value row of a round is requested before
+// anything waits: the first round's loads go out before q, k and v of this
+// token are read and rotated, so the cache and the QKV output arrive
+// together.  Row pos is this token's rotated key and its value, taken from
+// LDS (the cache row is written by the group's first query head for later
+// tokens, so no workgroup waits on another).
+//
+// Softmax (forward.go:463-479) in one pass: each position group keeps the
+// running max m, the sum l of exp(score - m) and acc = sum exp(score - m) v
+// over its rows; groups merge by rescaling to the larger max (exp(-inf) = 0
+// for empty groups), wavefronts in LDS in wavefront order, so the result is
+// the same on every run.  out = acc / l.  The exponentials are fp32 expf of
+// the fp32 difference; the reference rounds a double exp to float, which
+// differs by about an ulp.
 template <int HD>
+struct AttnShape {
+    static constexpr int LP = HD / 4;                    // lanes per position
+    static constexpr int PW = 64 / LP;                   // positions per wavefront load
+    static constexpr int NW = ATTN_THREADS / 64;         // wavefronts
+    static constexpr int per_round(int u) { return NW * PW * u; }
+};
+
+// Value of lane u of each LP-lane position group (LP = 16: 16-lane rows;
+// LP = 32: 32-lane halves), by ds_swizzle in bit mode.
+template <int LP, int U>
+__device__ __forceinline__ float group_lane(float v) {
+    constexpr int pattern = LP == 16 ? (0x10 | (U << 5)) : (U << 5);
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), pattern));
+}
+
+template <int LP, int U, int K = 0>
+__device__ __forceinline__ void group_bcast(float v, float (&p)[U]) {
+    if constexpr (K < U) {
+        p[K] = group_lane<LP, K>(v);
+        group_bcast<LP, U, K + 1>(v, p);
+    }
+}
+
+// (m, l, acc) <- merge of (m, l, acc) and (mo, lo, ao): rescaled to the larger max.
+__device__ __forceinline__ void attn_merge(float &m, float &l, float4 &acc, float mo, float lo,
+                                           float4 ao) {
+    const float M = fmaxf(m, mo);
+    const float a = m == -INFINITY ? 0.0f : expf(m - M);
+    const float b = mo == -INFINITY ? 0.0f : expf(mo - M);
+    l = l * a + lo * b;
+    acc.x = acc.x * a + ao.x * b;
+    acc.y = acc.y * a + ao.y * b;
+    acc.z = acc.z * a + ao.z * b;
+    acc.w = acc.w * a + ao.w * b;
+    m = M;
+}
+
+template <int HD, int U>
 __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__ qkv, int n_heads,
                                                        int n_kv, int pos,
                                                        const float2 *__restrict__ rope,
                                                        int max_seq, float *__restrict__ kv,
                                                        float *__restrict__ out) {
-    constexpr int LP = HD / 4;       // lanes per position
-    constexpr int PW = 64 / LP;      // positions per wavefront per load
-    extern __shared__ float sc[];    // pos + 1 scores, then probabilities
-    __shared__ __attribute__((aligned(16))) float qh[HD], kh[HD];
-    __shared__ float red[ATTN_THREADS / 64];
-    __shared__ __attribute__((aligned(16))) float part[ATTN_THREADS / (HD / 4)][HD];
+    using S = AttnShape<HD>;
+    constexpr int LP = S::LP, PW = S::PW, NW = S::NW, PR = NW * PW * U;
+    static_assert(U <= LP, "lane u of a group computes the exponential of load u");
+    __shared__ __attribute__((aligned(16))) float qh[HD], kh[HD], vh[HD];
+    __shared__ __attribute__((aligned(16))) float wacc[NW][HD];
+    __shared__ float wm[NW], wl[NW];
     const int h = blockIdx.x;
     const int kvh = h * n_kv / n_heads;  // forward.go:266
-    const int kv_dim = n_kv * HD;
+    const int kv_dim = n_kv * HD, row4 = kv_dim / 4;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int sub = lane % LP, slot = lane / LP;
+    const float4 *kc4 = reinterpret_cast<const float4 *>(kv + (size_t)kvh * HD) + sub;
+    const float4 *vc4 =
+        reinterpret_cast<const float4 *>(kv + (size_t)max_seq * kv_dim + (size_t)kvh * HD) + sub;
+    const int t0 = wave * PW * U + slot;  // + round * PR + u * PW
+    float4 kk[U], vv[U];
+    auto issue = [&](int r) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int t = max(0, min(r * PR + t0 + u * PW, pos - 1));  // row pos comes from LDS
+            kk[u] = kc4[(size_t)t * row4];
+            vv[u] = vc4[(size_t)t * row4];
+        }
+    };
+    issue(0);
     const float *q = qkv + (size_t)h * HD;
-    const float *kc = qkv + (size_t)n_heads * HD + (size_t)kvh * HD;
-    const float *vc = qkv + (size_t)n_heads * HD + kv_dim + (size_t)kvh * HD;
+    const float *kcur = qkv + (size_t)n_heads * HD + (size_t)kvh * HD;
+    const float *vcur = kcur + kv_dim;
+    const bool first = h == kvh * (n_heads / n_kv);  // appends row pos (kvcache.go:42-52)
     if (tid < HD / 2) {  // RoPE, pairs (i, i + HD/2) (forward.go:483-497)
         const int i = tid;
         const float2 cs = rope[(size_t)pos * (HD / 2) + i];
         const float c = cs.x, s = cs.y;
-        const float q0 = q[i], q1 = q[i + HD / 2], k0 = kc[i], k1 = kc[i + HD / 2];
+        const float q0 = q[i], q1 = q[i + HD / 2], k0 = kcur[i], k1 = kcur[i + HD / 2];
+        const float r0 = k0 * c - k1 * s, r1 = k0 * s + k1 * c;
         qh[i] = q0 * c - q1 * s;
         qh[i + HD / 2] = q0 * s + q1 * c;
-        kh[i] = k0 * c - k1 * s;
-        kh[i + HD / 2] = k0 * s + k1 * c;
+        kh[i] = r0;
+        kh[i + HD / 2] = r1;
+        if (first) {
+            kv[(size_t)pos * kv_dim + (size_t)kvh * HD + i] = r0;
+            kv[(size_t)pos * kv_dim + (size_t)kvh * HD + i + HD / 2] = r1;
+        }
+    } else if (tid >= 64 && tid < 64 + HD) {
+        const int i = tid - 64;
+        const float v = vcur[i];
+        vh[i] = v;
+        if (first) kv[(size_t)max_seq * kv_dim + (size_t)pos * kv_dim + (size_t)kvh * HD + i] = v;
     }
     __syncthreads();
-    const float *kcache = kv;
-    const float *vcache = kv + (size_t)max_seq * kv_dim;
-    if (h == kvh * (n_heads / n_kv) && tid < HD) {  // append row pos (kvcache.go:42-52)
-        kv[(size_t)pos * kv_dim + kvh * HD + tid] = kh[tid];
-        kv[(size_t)max_seq * kv_dim + (size_t)pos * kv_dim + kvh * HD + tid] = vc[tid];
-    }
     const float scale = (float)(1.0 / sqrt((double)HD));  // forward.go:255
-    const int sub = lane % LP, slot = lane / LP;
     const float4 qv = reinterpret_cast<const float4 *>(qh)[sub];
-    for (int t0 = wave * PW * ATT_U; t0 < pos; t0 += (ATTN_THREADS / 64) * PW * ATT_U) {
-        float4 kk[ATT_U];
+    const float4 kn = reinterpret_cast<const float4 *>(kh)[sub];
+    const float4 vn = reinterpret_cast<const float4 *>(vh)[sub];
+    float m = -INFINITY, l = 0.0f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int n_rounds = (pos + PR) / PR;  // rows 0..pos
+    for (int r = 0; r < n_rounds; r++) {
+        if (r > 0) issue(r);
+        float sc[U];
+        float mr = -INFINITY;
 #pragma unroll
-        for (int u = 0; u < ATT_U; u++) {
-            const int t = min(t0 + u * PW + slot, pos - 1);
-            kk[u] = reinterpret_cast<const float4 *>(kcache + (size_t)t * kv_dim + kvh * HD)[sub];
-        }
-#pragma unroll
-        for (int u = 0; u < ATT_U; u++) {
-            float dot = qv.x * kk[u].x + qv.y * kk[u].y + qv.z * kk[u].z + qv.w * kk[u].w;
+        for (int u = 0; u < U; u++) {
+            const int t = r * PR + t0 + u * PW;
+            const float4 k4 = t == pos ? kn : kk[u];
+            float dot = qv.x * k4.x + qv.y * k4.y + qv.z * k4.z + qv.w * k4.w;
             dot = row16_sum(dot);
             if (LP == 32) dot += __shfl_xor(dot, 16, 64);
-            const int t = t0 + u * PW + slot;
-            if (sub == 0 && t < pos) sc[t] = dot * scale;
+            sc[u] = dot * scale;
+            if (t <= pos) mr = fmaxf(mr, sc[u]);
         }
-    }
-    if (wave == 0) {  // row pos
-        const float4 k4 = reinterpret_cast<const float4 *>(kh)[sub];
-        float dot = qv.x * k4.x + qv.y * k4.y + qv.z * k4.z + qv.w * k4.w;
-        dot = row16_sum(dot);
-        if (LP == 32) dot += __shfl_xor(dot, 16, 64);
-        if (lane == 0) sc[pos] = dot * scale;
-    }
-    __syncthreads();
-    // softmax (forward.go:463-479): max, exp in double rounded to float, sum, divide
-    const int T = pos + 1;
-    float m = -INFINITY;
-    for (int t = tid; t < T; t += blockDim.x) m = fmaxf(m, sc[t]);
-    m = wave_max(m);
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    for (int i = 0; i < ATTN_THREADS / 64; i++) m = fmaxf(m, red[i]);
-    float s = 0.0f;
-    for (int t = tid; t < T; t += blockDim.x) {
-        const float e = (float)exp((double)(sc[t] - m));
-        sc[t] = e;
-        s += e;
-    }
-    const float sum = llg_block_sum(s, red);  // its barriers also publish sc
-    // out[d] = sum_t p_t * v_t[d]: thread (c, g) holds float4 column c of the
-    // head and takes t = g, g + VG, ... < pos, ATT_VU rows per step; the groups
-    // meet in LDS and row pos is added last
-    constexpr int VC = HD / 4;               // float4 columns
-    constexpr int VG = ATTN_THREADS / VC;    // position groups
-    const int c4 = tid % VC, g = tid / VC;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int t0 = g; t0 < pos; t0 += VG * ATT_VU) {
-        float4 vv[ATT_VU];
+        // lane `sub` of the group takes the exponential of load u = sub
+        float mine = sc[0];
 #pragma unroll
-        for (int u = 0; u < ATT_VU; u++) {
-            const int t = min(t0 + u * VG, pos - 1);
-            vv[u] = reinterpret_cast<const float4 *>(vcache + (size_t)t * kv_dim + kvh * HD)[c4];
-        }
+        for (int u = 1; u < U; u++)
+            if (sub == u) mine = sc[u];
+        const bool valid = sub < U && r * PR + t0 + sub * PW <= pos;
+        const float pm = valid ? expf(mine - mr) : 0.0f;
+        float p[U];
+        group_bcast<LP, U>(pm, p);
+        float lr = 0.0f;
+        float4 ar = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int u = 0; u < ATT_VU; u++) {
-            const int t = t0 + u * VG;
-            if (t < pos) {
-                const float p = sc[t] / sum;
-                acc.x += p * vv[u].x;
-                acc.y += p * vv[u].y;
-                acc.z += p * vv[u].z;
-                acc.w += p * vv[u].w;
-            }
+        for (int u = 0; u < U; u++) {
+            const int t = r * PR + t0 + u * PW;
+            const float4 v4 = t == pos ? vn : vv[u];
+            lr += p[u];
+            ar.x += p[u] * v4.x;
+            ar.y += p[u] * v4.y;
+            ar.z += p[u] * v4.z;
+            ar.w += p[u] * v4.w;
+        }
+        if (r == 0) {
+            m = mr;
+            l = lr;
+            acc = ar;
+        } else if (mr != -INFINITY) {
+            attn_merge(m, l, acc, mr, lr, ar);
         }
     }
-    reinterpret_cast<float4 *>(&part[g][0])[c4] = acc;
+    // the PW groups of a wavefront, then the wavefronts in order
+#pragma unroll
+    for (int o = LP; o < 64; o <<= 1) {
+        const float mo = __shfl_xor(m, o, 64), lo = __shfl_xor(l, o, 64);
+        const float4 ao = make_float4(__shfl_xor(acc.x, o, 64), __shfl_xor(acc.y, o, 64),
+                                      __shfl_xor(acc.z, o, 64), __shfl_xor(acc.w, o, 64));
+        attn_merge(m, l, acc, mo, lo, ao);
+    }
+    if (lane < LP) reinterpret_cast<float4 *>(&wacc[wave][0])[lane] = acc;
+    if (lane == 0) {
+        wm[wave] = m;
+        wl[wave] = l;
+    }
     __syncthreads();
     if (tid < HD) {
-        float r = part[0][tid];
+        float M = wm[0];
 #pragma unroll
-        for (int i = 1; i < VG; i++) r += part[i][tid];
-        r += (sc[pos] / sum) * vc[tid];
-        out[(size_t)h * HD + tid] = r;
+        for (int w = 1; w < NW; w++) M = fmaxf(M, wm[w]);
+        float L = 0.0f, R = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float e = wm[w] == -INFINITY ? 0.0f : expf(wm[w] - M);
+            L += wl[w] * e;
+            R += wacc[w][tid] * e;
+        }
+        out[(size_t)h * HD + tid] = R / L;
     }
 }
 
 // First index of the maximum (generate.go:197-205: strict '>' from index 0,
-// so a NaN at index 0 wins and later NaNs never do).
-__global__ __launch_bounds__(1024) void k_argmax(const float *__restrict__ v, int n,
-                                                 int32_t *__restrict__ out) {
-    __shared__ float bv_s[16];
-    __shared__ int bi_s[16];
-    float bv = -INFINITY;
-    int bi = n;
-    for (int i0 = threadIdx.x; i0 < n; i0 += 16 * blockDim.x) {
-        float xs[16];
+// so a NaN at index 0 wins and later NaNs never do).  One workgroup; each
+// thread requests all of its float4 groups (up to AM_U per pass) before
+// using any, so a 65024-entry vocabulary takes one memory round.  Two
+// branch-free passes over the registers: the maximum M (fmaxf skips NaN),
+// then the smallest index holding M.
+#define AM_U 16
+#define AM_THREADS 1024
+__global__ __launch_bounds__(AM_THREADS) void k_argmax(const float *__restrict__ v, int n,
+                                                       int32_t *__restrict__ out) {
+    __shared__ float mv_s[AM_THREADS / 64];
+    __shared__ int mi_s[AM_THREADS / 64];
+    const int n4 = n >> 2;
+    const float4 *v4 = reinterpret_cast<const float4 *>(v);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // pass 1: the maximum.  Up to AM_U * AM_THREADS float4 groups stay in
+    // registers for pass 2; a longer row is read again there.
+    constexpr int CH = AM_U * AM_THREADS;
+    float4 xs[AM_U];
+    auto load = [&](int c0) {
 #pragma unroll
-        for (int k = 0; k < 16; k++) xs[k] = v[min(i0 + k * (int)blockDim.x, n - 1)];
+        for (int k = 0; k < AM_U; k++) xs[k] = v4[max(0, min(c0 + tid + k * AM_THREADS, n4 - 1))];
+    };
+    const float tail = tid < (n & 3) ? v[4 * n4 + tid] : -INFINITY;
+    float m = tail;
+    for (int c0 = 0; c0 < n4; c0 += CH) {
+        load(c0);
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const int i = i0 + k * blockDim.x;
-            const float x = xs[k];
-            if (i < n && x == x && (x > bv || (x == bv && i < bi))) {
-                bv = x;
-                bi = i;
-            }
-        }
+        for (int k = 0; k < AM_U; k++)
+            if (c0 + tid + k * AM_THREADS < n4)
+                m = fmaxf(m, fmaxf(fmaxf(xs[k].x, xs[k].y), fmaxf(xs[k].z, xs[k].w)));
     }
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (ov > bv || (ov == bv && oi < bi)) {
-            bv = ov;
-            bi = oi;
-        }
-    }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) {
-        bv_s[wave] = bv;
-        bi_s[wave] = bi;
-    }
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if (lane == 0) mv_s[wave] = m;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < (int)(blockDim.x >> 6); w++)
-            if (bv_s[w] > bv_s[0] || (bv_s[w] == bv_s[0] && bi_s[w] < bi_s[0])) {
-                bv_s[0] = bv_s[w];
-                bi_s[0] = bi_s[w];
+    float M = mv_s[0];
+#pragma unroll
+    for (int w = 1; w < AM_THREADS / 64; w++) M = fmaxf(M, mv_s[w]);
+    // pass 2: first index holding M (chunks from the last, so the first wins)
+    int bi = n;
+    for (int c0 = (n4 - 1) / CH * CH; c0 >= 0; c0 -= CH) {
+        if (n4 > CH) load(c0);
+#pragma unroll
+        for (int k = AM_U - 1; k >= 0; k--) {
+            const int j = c0 + tid + k * AM_THREADS;
+            if (j < n4) {
+                bi = xs[k].w == M ? 4 * j + 3 : bi;
+                bi = xs[k].z == M ? 4 * j + 2 : bi;
+                bi = xs[k].y == M ? 4 * j + 1 : bi;
+                bi = xs[k].x == M ? 4 * j : bi;
             }
+        }
+    }
+    if (tid < (n & 3) && tail == M) bi = min(bi, 4 * n4 + tid);
+    for (int o = 32; o > 0; o >>= 1) bi = min(bi, __shfl_xor(bi, o, 64));
+    if (lane == 0) mi_s[wave] = bi;
+    __syncthreads();
+    if (tid == 0) {
+        int b = mi_s[0];
+        for (int w = 1; w < AM_THREADS / 64; w++) b = min(b, mi_s[w]);
         const float v0 = v[0];
-        *out = (v0 != v0 || bi_s[0] >= n) ? 0 : bi_s[0];
+        *out = (v0 != v0 || b >= n) ? 0 : b;
     }
 }
 
@@ -338,6 +423,24 @@ static LlgModel *get_model(LlgDevice *d, int64_t h) {
 
 static size_t model_ws_bytes(const LlgModel &m) {
     return std::max(llg_fused_ws_bytes(m.rank, m.ff), (size_t)llg_predict_ws_bytes(m.rank, m.ff));
+}
+
+// The attention launch for rows 0..pos: the fewest loads per lane U whose
+// round covers them all, else rounds of the largest.
+template <int HD>
+static void launch_attn(hipStream_t st, const LlgModel &m, int pos, float *kvl) {
+    using S = AttnShape<HD>;
+    const int n = pos + 1;
+#define ATT(U)                                                                                     \
+    hipLaunchKernelGGL((k_attn<HD, U>), dim3(m.n_heads), dim3(ATTN_THREADS), 0, st, m.qkv,        \
+                       m.n_heads, m.n_kv, pos, m.rope, m.max_seq, kvl, m.attn)
+    if (n <= S::per_round(1)) ATT(1);
+    else if (n <= S::per_round(2)) ATT(2);
+    else if (n <= S::per_round(4)) ATT(4);
+    else if (n <= S::per_round(6)) ATT(6);
+    else if (n <= S::per_round(8)) ATT(8);
+    else ATT(10);
+#undef ATT
 }
 
 // One token: embed -> layers -> norm -> LM head -> argmax, on the stream.
@@ -353,7 +456,6 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
     float *r = m.x;  // the residual stream
     hipLaunchKernelGGL(k_embed, dim3((m.hidden + 255) / 256), dim3(256), 0, st, m.embed->d,
                        m.embed->stride, m.embed->fmt, token_in, m.vocab, r);
-    const size_t attn_lds = (size_t)(pos + 1) * 4;
     for (int l = 0; l < m.n_layers; l++) {
         const LlgModelLayer &L = m.layers[l];
         LlgLnArgs ln;
@@ -370,11 +472,9 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
         if (rc) return rc;
         float *kvl = m.kv + (size_t)l * 2 * m.max_seq * m.n_kv * m.head_dim;
         if (m.head_dim == 64)
-            hipLaunchKernelGGL(k_attn<64>, dim3(m.n_heads), dim3(ATTN_THREADS), attn_lds, st, m.qkv,
-                               m.n_heads, m.n_kv, pos, m.rope, m.max_seq, kvl, m.attn);
+            launch_attn<64>(st, m, pos, kvl);
         else
-            hipLaunchKernelGGL(k_attn<128>, dim3(m.n_heads), dim3(ATTN_THREADS), attn_lds, st, m.qkv,
-                               m.n_heads, m.n_kv, pos, m.rope, m.max_seq, kvl, m.attn);
+            launch_attn<128>(st, m, pos, kvl);
         LLG_LAUNCH_CHECK(d, "model attention");
         if ((rc = llg_matvec_enqueue(d, L.wo, m.attn, -1, m.attn_out, m.mvpart))) return rc;
         if (pred_logits &&
@@ -403,7 +503,7 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
 #undef RN
     int rc = llg_matvec_enqueue(d, m.lm_head, m.normed, -1, m.logits, m.mvpart);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, st, m.logits, m.vocab, token_out);
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(AM_THREADS), 0, st, m.logits, m.vocab, token_out);
     LLG_LAUNCH_CHECK(d, "model step");
     return 0;
 }
@@ -533,7 +633,7 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     }
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (e != hipSuccess) {
-        hipFree(buf);
+        (void)hipFree(buf);
         delete m;
         return llg_hip_error(d, e, "falcon_create");
     }

@@ -2,14 +2,14 @@
 (inference/ffn_flash.go:115-185 ForwardFlash, attention over all cached
 positions forward.go:258-301, kvcache/kvcache.go:43-78).
 
-The attention kernel splits a head's cached rows over its wavefronts and over
-passes (head_dim 64: 32 key rows per wavefront, a second pass from row 512;
-value rows in steps of 512.  head_dim 128: 16 key rows per wavefront, passes
-from rows 256 and 512; value steps of 256), so these tests decode far enough
-that every wavefront and the later passes run under the check:
+The attention kernel splits a head's cached rows over its 16 wavefronts in
+rounds whose size grows with the position (head_dim 64: 64, 128, 256, 384,
+512 or 640 rows, then further rounds of 640 merged by online softmax;
+head_dim 128: half those), so these tests decode far enough that every round
+size and the merge of later rounds run under the check:
   - the full-model config's widths (hidden 4544, 71 query heads of 64 with
     one shared KV head, d_ff 18176, predictor rank 128, a 2048-row KV cache)
-    with one layer and a reduced vocabulary, 600 positions;
+    with one layer and a reduced vocabulary, 700 positions;
   - head_dim 128 with grouped KV heads (8 query heads over 2 KV heads), two
     layers, 600 positions.
 Every position is compared: logits within the FFN bar (1e-3 of the max-abs),
@@ -131,10 +131,10 @@ def _decode_vs_oracle(dev, d, w, n_pos, seed):
     assert np.all((frac > 0.03) & (frac < 0.07)), frac  # about 5% active per layer
 
 
-def test_falcon_config4_widths_600_positions(dev):
+def test_falcon_config4_widths_700_positions(dev):
     d = dict(CONFIG4_WIDTHS)
     w = make_falcon(np.random.default_rng(404), d, gg.Q4_0, std=0.02)
-    _decode_vs_oracle(dev, d, w, 600, 4041)
+    _decode_vs_oracle(dev, d, w, 700, 4041)
 
 
 def test_falcon_head_dim128_gqa_600_positions(dev):
