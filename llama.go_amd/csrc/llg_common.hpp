@@ -638,6 +638,18 @@ struct LlgLnArgs {
     int n;
 };
 
+// A matvec over attn with the predictor's first matrix folded in: p is
+// WUp . Wo ([rank x cols] f32), and wavefront task (j, s) stores
+// part[s * rank + j] = p[j, chunk s] . x[chunk s] (n_split chunks of
+// split_blocks 32-float blocks, the last shorter); the matvec's row sums are
+// added into resid (resid[r] += y[r]).
+struct LlgPredFold {
+    const float *p;
+    float *part;
+    float *resid;
+    int rank, n_split, split_blocks;
+};
+
 // NP = float4 groups per thread (n <= 4 * NP * blockDim.x): every load of the
 // residual terms and of w and b is issued before the first use, so the
 // prologue costs one memory round trip plus the two block reductions.

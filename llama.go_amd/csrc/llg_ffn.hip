@@ -33,15 +33,23 @@
 // LNP > 0: x is the LayerNorm of a residual sum, staged with LNP float4 groups
 // per thread (llg_stage_ln); LNP = 0: x is read from memory.  NT: the largest
 // workgroup the instance is launched with.
-template <int T, int LNP, bool G = false, int NT = 256>
+//
+// PF: the predictor fold (LlgPredFold, one chunk only): wavefront w of
+// workgroup b takes fold tasks t = w * gridDim.x + b, b + grid * waves, ...
+// (spread over the workgroups), the first one's loads requested with the
+// first rows'; the row sums go to pf.resid (+=) and, if y is set, to y.
+#define MV_PFL 3  // float4 loads per lane of a fold task (split_blocks <= 24)
+template <int T, int LNP, bool G = false, int NT = 256, bool PF = false>
 __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, long long stride,
                                                   RowFmt f, int rows, int tile_rows,
                                                   int chunk_blocks,
                                                   const float *__restrict__ x, int act,
                                                   float *__restrict__ y, float *__restrict__ part,
                                                   LlgLnArgs ln,
-                                                  const uint8_t *__restrict__ w2 = nullptr) {
+                                                  const uint8_t *__restrict__ w2 = nullptr,
+                                                  LlgPredFold pf = LlgPredFold{}) {
     static_assert(!G || (LNP == 0 && MV_ROWS == 2), "gated rows pair gate and up");
+    static_assert(!PF || (LNP == 0 && !G), "the fold rides on a plain matvec");
     constexpr int RW = G ? 1 : MV_ROWS;  // output rows per wavefront pass
     extern __shared__ float xs[];
     __shared__ float red[NT / 64];
@@ -96,12 +104,54 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
                                       cb0 + min(kb + lane + 64 * i, cnb - 1));
         }
     };
-    auto issue_first = [&]() { issue(min(r_first, r_end - 1), 0); };
+    // fold tasks of this wavefront: t0, t0 + fstep, ... < n_tasks
+    const int n_tasks = PF ? pf.rank * pf.n_split : 0;
+    const int fstep = gridDim.x * (int)(blockDim.x >> 6);
+    const int ft0 = wave * gridDim.x + blockIdx.x;
+    float4 pr[PF ? MV_PFL : 1];
+    // float4 groups of chunk sp (0 for a chunk past the row's end)
+    auto fold_nq = [&](int sp) { return max(0, min(pf.split_blocks, f.nb - sp * pf.split_blocks)) * 8; };
+    auto fold_issue = [&](int t) {
+        const int j = t / pf.n_split, sp = t % pf.n_split;
+        const int nq = fold_nq(sp);
+        const float4 *row = reinterpret_cast<const float4 *>(pf.p + (size_t)j * f.cols) +
+                            (nq > 0 ? (size_t)sp * pf.split_blocks * 8 : 0);
+#pragma unroll
+        for (int k = 0; k < MV_PFL; k++) pr[k] = row[min(lane + 64 * k, max(nq, 1) - 1)];
+    };
+    auto issue_first = [&]() {
+        issue(min(r_first, r_end - 1), 0);
+        if constexpr (PF)
+            if (ft0 < n_tasks) fold_issue(ft0);
+    };
     if constexpr (LNP > 0)  // x is the LayerNorm of the residual sum (one chunk: cb0 = 0)
         llg_stage_ln<MV_XS, LNP>(xs, ln, red, issue_first);
     else
         llg_stage_x_sum<MV_XS>(xs, x + (size_t)cb0 * 32, cnb, issue_first);
     __syncthreads();
+    if constexpr (PF) {
+        for (int t = ft0; t < n_tasks; t += fstep) {
+            if (t != ft0) fold_issue(t);
+            const int j = t / pf.n_split, sp = t % pf.n_split;
+            const int nq = fold_nq(sp);
+            const float *xb = xs + (size_t)sp * pf.split_blocks * MV_XS;
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < MV_PFL; k++) {
+                const int q = lane + 64 * k;
+                if (q < nq) {
+                    const float4 xv =
+                        *reinterpret_cast<const float4 *>(xb + (q >> 3) * MV_XS + (q & 7) * 4);
+                    acc += pr[k].x * xv.x;
+                    acc += pr[k].y * xv.y;
+                    acc += pr[k].z * xv.z;
+                    acc += pr[k].w * xv.w;
+                }
+            }
+            acc = llg_wave_sum(acc);
+            if (lane == 0) pf.part[sp * pf.rank + j] = acc;
+        }
+    }
     const int n_waves = blockDim.x >> 6;
     for (int r0 = r_first; r0 < r_end; r0 += n_waves * RW) {
         float s[MV_ROWS] = {0.0f, 0.0f};
@@ -144,10 +194,13 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
         for (int q = 0; q < MV_ROWS; q++) {
             const float v = llg_wave_sum(s[q]);
             if (lane == 0 && r0 + q < r_end) {
-                if (n_chunks == 1)
-                    y[r0 + q] = act >= 0 ? llg_act(act, v) : v;
-                else
+                if (n_chunks == 1) {
+                    const float o = act >= 0 ? llg_act(act, v) : v;
+                    if constexpr (PF) pf.resid[r0 + q] = pf.resid[r0 + q] + o;  // x += attnOut
+                    if (!PF || y) y[r0 + q] = o;
+                } else {
                     part[(size_t)ch * rows + r0 + q] = v;
+                }
             }
         }
     }
@@ -182,9 +235,10 @@ static size_t mv_part_floats(const RowFmt &f, int rows, int act) {
 // part: room for mv_part_floats (the partial sums of a chunked matvec).
 // ln (optional): the staged x is the LayerNorm of a residual sum (llg_stage_ln).
 // up (optional): gated rows, y = silu(w . x) * (up . x) (act is ignored).
+// pf (optional): the predictor fold (whole rows in one workgroup, no LayerNorm).
 static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y,
                          float *part, const LlgLnArgs *ln = nullptr,
-                         const LlgObject *up = nullptr) {
+                         const LlgObject *up = nullptr, const LlgPredFold *pf = nullptr) {
     hipStream_t st = llg_dev_stream(d);
     const RowFmt &f = w->fmt;
     if (up) act = LLG_ACT_SILU;  // whole rows in one workgroup
@@ -195,6 +249,10 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
         return llg_set_error(d, LLG_E_ARG, "matvec: row of %d elements too long", f.cols);
     if (n_chunks > 1 && !part)
         return llg_set_error(d, LLG_E_ARG, "matvec: chunked rows need a partial buffer");
+    if (pf && (n_chunks > 1 || ln || up || act >= 0 || pf->n_split < 1 ||
+               pf->split_blocks * 8 > 64 * MV_PFL ||
+               (long long)pf->split_blocks * pf->n_split < f.nb))
+        return llg_set_error(d, LLG_E_ARG, "matvec: predictor fold needs whole plain rows");
     int tile_rows = (w->rows < MV_SMALL_ROWS ? MV_TILE_SMALL : MV_TILE) / (up ? 2 : 1);
     int threads = 256;
     const LlgLnArgs none{};
@@ -220,7 +278,15 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
     const int grid = (w->rows + tile_rows - 1) / tile_rows * n_chunks;
 #define MV_GO(TY, NP)                                                                              \
     do {                                                                                           \
-        if (bal)                                                                                   \
+        if (pf && bal)                                                                             \
+            hipLaunchKernelGGL((k_matvec_q<TY, 0, false, 1024, true>), dim3(grid), dim3(threads),  \
+                               lds, st, w->d, w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, \
+                               part, la, (const uint8_t *)nullptr, *pf);                           \
+        else if (pf)                                                                               \
+            hipLaunchKernelGGL((k_matvec_q<TY, 0, false, 256, true>), dim3(grid), dim3(256), lds,  \
+                               st, w->d, w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y,      \
+                               part, la, (const uint8_t *)nullptr, *pf);                           \
+        else if (bal)                                                                              \
             hipLaunchKernelGGL((k_matvec_q<TY, (NP <= 4 ? NP : 4), false, 1024>), dim3(grid),      \
                                dim3(threads), lds, st, w->d, w->stride, f, w->rows, tile_rows, cb, \
                                d_x, act, d_y, part, la, (const uint8_t *)nullptr);                 \
@@ -280,6 +346,13 @@ int llg_matvec_ln_enqueue(LlgDevice *d, const LlgObject *w, const LlgLnArgs &ln,
 int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y,
                        float *part) {
     return matvec_launch(d, w, d_x, act, d_y, part);
+}
+
+bool llg_matvec_fold_ok(const LlgObject *w) { return mv_chunk_blocks(w->fmt, -1) == w->fmt.nb; }
+
+int llg_matvec_fold_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, float *d_y,
+                            const LlgPredFold &pf) {
+    return matvec_launch(d, w, d_x, -1, d_y, nullptr, nullptr, nullptr, &pf);
 }
 
 size_t llg_matvec_part_bytes(const LlgObject *w, int act) {

@@ -21,6 +21,14 @@ int llg_pred_masks_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObj
                            const float *d_a, float thr, uint8_t *ws,
                            unsigned long long **mask_out, float *zero_out, int zero_n,
                            int32_t *zero_extra);
+// Where the hidden partials ([split][rank] floats) and the tile masks sit in
+// a predictor workspace; the number of partials per hidden unit.
+void llg_pred_ws_layout(uint8_t *ws, int rank, float **partial, unsigned long long **mask);
+int llg_pred_split();
+// Logits, masks and the active list from hidden partials already in ws.
+int llg_pred_logits_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, float thr,
+                            uint8_t *ws, int32_t *d_active, int32_t *d_n_active,
+                            float *d_logits);
 // Ascending active list from 64-bit tile masks (one workgroup).
 int llg_compact_enqueue(LlgDevice *d, const unsigned long long *mask, int n_tiles,
                         int32_t *d_active, int32_t *d_n_active);
@@ -60,6 +68,12 @@ int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, con
 int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y,
                        float *part);
 size_t llg_matvec_part_bytes(const LlgObject *w, int act);
+// The attention-output matvec with the predictor fold (LlgPredFold): y (may
+// be null) = W . x, pf.resid += W . x, and the fold tasks' partial sums.
+// llg_matvec_fold_ok: W's rows fit one workgroup's staged x.
+bool llg_matvec_fold_ok(const LlgObject *w);
+int llg_matvec_fold_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, float *d_y,
+                            const LlgPredFold &pf);
 // y = W . LayerNorm((x_in + a1) + a2), the residual sum and the normed row
 // also written to ln.x_out / ln.normed_out (llg_stage_ln).
 int llg_matvec_ln_enqueue(LlgDevice *d, const LlgObject *w, const LlgLnArgs &ln, float *d_y);
@@ -70,6 +84,11 @@ int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *
                       LlgObject *b, const float *d_a, const float *d_x, float thr, int act,
                       float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws,
                       const float *d_out_add = nullptr);
+// The same after the hidden partials are in ws (llg_pred_ws_layout): the
+// tile kernel and the down kernel; accumulate: d_out += the FFN output.
+int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgObject *b,
+                           const float *d_x, float thr, int act, float *d_out,
+                           int32_t *d_active, int32_t *d_n_active, uint8_t *ws, bool accumulate);
 
 // MoE prefill as grouped MFMA GEMMs (llg_moe_gemm.hip).
 bool llg_moe_gemm_supported(int type, int hidden, int eff, int n_tok);

@@ -13,12 +13,24 @@
 //                     row pos of the layer's cache (kvcache.go:42-52), softmax
 //                     attention of every query head over rows 0..pos of its KV
 //                     head (forward.go:258-301)
-//     k_matvec_q      attn_out = Wo . attn                      (forward.go:305)
-//     sparse step     ffnFlash path 2 with the predictor on attn_out and the FFN
-//                     on normed (ffn_flash.go:157-163, 225-231); its first
-//                     kernel adds attn_out to r (x += attnOut, ffn_flash.go:161),
-//                     and its down sums are added into r (x += ffnOut, :164-166),
+//     k_matvec_q      attn_out = Wo . attn (forward.go:305), added into r
+//                     (x += attnOut, ffn_flash.go:161); the same launch
+//                     computes the predictor's hidden partials P . attn, where
+//                     P = WUp . Wo was formed once at load (below)
+//     sparse step     ffnFlash path 2 (ffn_flash.go:157-163, 225-231): logits
+//                     from the hidden partials, the active up rows on normed,
+//                     and the down sums added into r (x += ffnOut, :164-166),
 //                     so r ends as the next layer's residual
+//
+// The predictor fold.  The reference's predictor input is attn_out = Wo .
+// attn, and its first product WUp . attn_out (predictor.go:57) is linear in
+// attn, so it equals P . attn with P = WUp . Wo ([rank x n_heads head_dim]).
+// k_fold_pred forms P once per layer at load, in fp64 sums rounded once to
+// f32, and the Wo launch computes P . attn beside Wo . attn, which removes
+// a launch and a dependent read of attn_out per layer.  The hidden values
+// differ from WUp . attn_out by fp32 rounding only (a few ulps).  Models
+// whose Wo rows are too long for one workgroup's staged x keep the separate
+// hidden kernel on attn_out.
 //   k_resid_norm      output LayerNorm of r                    (ffn_flash.go:126-129)
 //   k_matvec_q        logits = LMHead . normed                 (ffn_flash.go:130)
 //   k_argmax          next token = first index of the maximum  (generate.go:197-205)
@@ -36,6 +48,7 @@
 struct LlgModelLayer {
     LlgObject *norm_w, *norm_b, *wqkv, *wo, *pwup, *pwout, *bundle;
     float thr;
+    float *pfold;  // P = WUp . Wo [rank x n_heads head_dim], or null (no fold)
 };
 
 struct LlgModel {
@@ -157,6 +170,50 @@ __global__ void k_rope_table(float2 *__restrict__ tab, int max_seq, int half, fl
     const int pos = j / half, i = j % half;
     const double fr = (double)pos / pow((double)base, (double)(2 * i) / (double)(2 * half));
     tab[j] = make_float2((float)cos(fr), (float)sin(fr));
+}
+
+// P = WUp . dequant(Wo) of one layer: [rank x hidden] . [hidden x cols], fp64
+// sums rounded once to f32.  32 x 32 output tiles through LDS, 256 threads of
+// 2 x 2 outputs each.  Runs once per layer at load.
+#define FOLD_T 32
+__global__ __launch_bounds__(256) void k_fold_pred(const uint8_t *__restrict__ wup,
+                                                   long long wup_stride, int rank, int hidden,
+                                                   const uint8_t *__restrict__ wo,
+                                                   long long wo_stride, RowFmt wf,
+                                                   float *__restrict__ pf) {
+    __shared__ double a[FOLD_T][FOLD_T + 1], b[FOLD_T][FOLD_T + 1];
+    const int cols = wf.cols;
+    const int j0 = blockIdx.y * FOLD_T, c0 = blockIdx.x * FOLD_T;
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    double acc[2][2] = {{0.0, 0.0}, {0.0, 0.0}};
+    for (int k0 = 0; k0 < hidden; k0 += FOLD_T) {
+        for (int i = threadIdx.x; i < FOLD_T * FOLD_T; i += 256) {
+            const int r = i / FOLD_T, q = i % FOLD_T;
+            const int j = j0 + r, k = k0 + q;
+            a[r][q] = j < rank && k < hidden
+                          ? (double)reinterpret_cast<const float *>(wup + (long long)j * wup_stride)[k]
+                          : 0.0;
+            const int kk = k0 + r, c = c0 + q;
+            b[r][q] = kk < hidden && c < cols
+                          ? (double)llg_dequant_elem(wo + (long long)kk * wo_stride, wf, c)
+                          : 0.0;
+        }
+        __syncthreads();
+        for (int k = 0; k < FOLD_T; k++) {
+            const double a0 = a[2 * ty][k], a1 = a[2 * ty + 1][k];
+            const double b0 = b[k][2 * tx], b1 = b[k][2 * tx + 1];
+            acc[0][0] += a0 * b0;
+            acc[0][1] += a0 * b1;
+            acc[1][0] += a1 * b0;
+            acc[1][1] += a1 * b1;
+        }
+        __syncthreads();
+    }
+    for (int u = 0; u < 2; u++)
+        for (int v = 0; v < 2; v++) {
+            const int j = j0 + 2 * ty + u, c = c0 + 2 * tx + v;
+            if (j < rank && c < cols) pf[(size_t)j * cols + c] = (float)acc[u][v];
+        }
 }
 
 // One workgroup per query head; HD = head_dim (64 or 128).  LP = HD/4 lanes
@@ -476,6 +533,27 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
         else
             launch_attn<128>(st, m, pos, kvl);
         LLG_LAUNCH_CHECK(d, "model attention");
+        if (L.pfold) {  // Wo with the predictor fold: r += attn_out, hidden partials in ws
+            LlgPredFold pf;
+            unsigned long long *mask;
+            llg_pred_ws_layout(m.ws, m.rank, &pf.part, &mask);
+            pf.p = L.pfold;
+            pf.resid = r;
+            pf.rank = m.rank;
+            pf.n_split = llg_pred_split();
+            pf.split_blocks = (L.wo->fmt.nb + pf.n_split - 1) / pf.n_split;
+            if ((rc = llg_matvec_fold_enqueue(d, L.wo, m.attn, nullptr, pf))) return rc;
+            if (pred_logits &&
+                (rc = llg_pred_logits_enqueue(d, L.pwout, nullptr, L.thr, m.ws, m.act_scratch,
+                                              m.act_scratch + m.ff,
+                                              pred_logits + (size_t)l * m.ff)))
+                return rc;
+            rc = llg_fused_tail_enqueue(d, L.pwout, nullptr, L.bundle, m.normed, L.thr, m.act, r,
+                                        nullptr, n_active_out ? n_active_out + l : nullptr, m.ws,
+                                        true);
+            if (rc) return rc;
+            continue;
+        }
         if ((rc = llg_matvec_enqueue(d, L.wo, m.attn, -1, m.attn_out, m.mvpart))) return rc;
         if (pred_logits &&
             (rc = llg_predict_enqueue(d, L.pwup, L.pwout, nullptr, m.attn_out, L.thr, m.act_scratch,
@@ -569,6 +647,7 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
         L.pwout = llg_get(d, lh[5], LLG_KIND_MATRIX);
         L.bundle = llg_get(d, lh[6], LLG_KIND_BUNDLE);
         L.thr = thresholds[l];
+        L.pfold = nullptr;
         if (!L.norm_w || !L.norm_b) return fail(LLG_E_ARG, "layer norm must be F32 [1 x hidden]");
         if (!L.wqkv || L.wqkv->rows != qkv_rows || L.wqkv->fmt.cols != m->hidden)
             return fail(LLG_E_ARG, "wqkv must be [(n_heads + 2 n_kv) head_dim x hidden]");
@@ -596,11 +675,16 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     const size_t v_pl = llg_align((long long)m->n_layers * m->ff * 4, 256);
     const size_t v_rope = llg_align((long long)m->max_seq * m->head_dim / 2 * 8, 256);
     const size_t wsb = model_ws_bytes(*m);
+    const int attn_dim = m->n_heads * m->head_dim;
+    bool fold = true;
+    for (const LlgModelLayer &L : m->layers) fold = fold && llg_matvec_fold_ok(L.wo);
+    const size_t v_pf1 = llg_align((long long)m->rank * attn_dim * 4, 256);
+    const size_t v_pf = fold ? (size_t)m->n_layers * v_pf1 : 0;
     size_t v_mp = llg_matvec_part_bytes(m->lm_head, -1);
     for (const LlgModelLayer &L : m->layers) v_mp = std::max(v_mp, llg_matvec_part_bytes(L.wo, -1));
     v_mp = llg_align((long long)v_mp, 256);
     const size_t total =
-        3 * v_h + v_qkv + v_att + v_log + v_kv + v_i + v_ff + v_pl + v_rope + v_mp + wsb;
+        3 * v_h + v_qkv + v_att + v_log + v_kv + v_i + v_ff + v_pl + v_rope + v_mp + v_pf + wsb;
     uint8_t *buf = nullptr;
     if (hipMalloc(&buf, total) != hipSuccess) return fail(LLG_E_NOMEM, "buffer allocation failed");
     uint8_t *p = buf;
@@ -622,6 +706,10 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     p += v_rope;
     m->mvpart = v_mp ? reinterpret_cast<float *>(p) : nullptr;
     p += v_mp;
+    for (LlgModelLayer &L : m->layers) {
+        L.pfold = fold ? reinterpret_cast<float *>(p) : nullptr;
+        p += fold ? v_pf1 : 0;
+    }
     m->ws = p;
     hipStream_t st = llg_dev_stream(d);
     hipError_t e = hipMemsetAsync(buf, 0, total, st);
@@ -629,6 +717,13 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     if (e == hipSuccess) {
         hipLaunchKernelGGL(k_rope_table, dim3((n_rope + 255) / 256), dim3(256), 0, st, m->rope,
                            m->max_seq, m->head_dim / 2, m->rope_base);
+        e = hipGetLastError();
+    }
+    for (const LlgModelLayer &L : m->layers) {
+        if (e != hipSuccess || !L.pfold) break;
+        const dim3 grid((attn_dim + FOLD_T - 1) / FOLD_T, (m->rank + FOLD_T - 1) / FOLD_T);
+        hipLaunchKernelGGL(k_fold_pred, grid, dim3(256), 0, st, L.pwup->d, L.pwup->stride, m->rank,
+                           m->hidden, L.wo->d, L.wo->stride, L.wo->fmt, L.pfold);
         e = hipGetLastError();
     }
     if (e == hipSuccess) e = hipStreamSynchronize(st);

@@ -160,14 +160,20 @@ int llg_predict_ws_bytes(int rank, int ff) {
                  llg_align((long long)((ff + 63) / 64) * 8, 256));
 }
 
+void llg_pred_ws_layout(uint8_t *ws, int rank, float **partial, unsigned long long **mask) {
+    *partial = reinterpret_cast<float *>(ws);
+    *mask = reinterpret_cast<unsigned long long *>(
+        ws + llg_align((long long)PRED_SPLIT * rank * 4, 256));
+}
+
+int llg_pred_split() { return PRED_SPLIT; }
+
 int llg_pred_hidden_enqueue(LlgDevice *d, LlgObject *wup, const float *d_a, uint8_t *ws,
                             float **partial, unsigned long long **mask, int *psplit,
                             float *zero_out, int zero_n, int32_t *zero_ctr, int n_ctr,
                             int32_t *zero_extra, const float *add_to) {
     const int h = wup->fmt.cols, rank = wup->rows;
-    *partial = reinterpret_cast<float *>(ws);
-    *mask = reinterpret_cast<unsigned long long *>(
-        ws + llg_align((long long)PRED_SPLIT * rank * 4, 256));
+    llg_pred_ws_layout(ws, rank, partial, mask);
     *psplit = PRED_SPLIT;
     const int grid = (rank * PRED_SPLIT + 3) / 4;
     hipLaunchKernelGGL(k_pred_hidden, dim3(grid), dim3(256), 0, llg_dev_stream(d), wup->d,
@@ -209,13 +215,22 @@ int llg_pred_masks_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObj
 int llg_predict_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
                         const float *d_a, float thr, int32_t *d_active, int32_t *d_n_active,
                         float *d_logits, uint8_t *ws) {
-    const int ff = wout->rows, rank = wup->rows;
     float *partial;
     unsigned long long *mask;
     int psplit;
     int rc = llg_pred_hidden_enqueue(d, wup, d_a, ws, &partial, &mask, &psplit, nullptr, 0,
                                      nullptr, 0, nullptr);
     if (rc) return rc;
+    return llg_pred_logits_enqueue(d, wout, bias, thr, ws, d_active, d_n_active, d_logits);
+}
+
+int llg_pred_logits_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, float thr,
+                            uint8_t *ws, int32_t *d_active, int32_t *d_n_active,
+                            float *d_logits) {
+    const int ff = wout->rows, rank = wout->fmt.cols;
+    float *partial;
+    unsigned long long *mask;
+    llg_pred_ws_layout(ws, rank, &partial, &mask);
     const int n_tiles = (ff + 63) / 64;
     const float *d_bias = bias ? reinterpret_cast<const float *>(bias->d) : nullptr;
     const size_t lds = (size_t)(((rank + 3) & ~3) + 64) * sizeof(float);

@@ -683,12 +683,6 @@ int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *
                       float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws,
                       const float *d_out_add) {
     if (int rc = llg_check_act(d, act)) return rc;
-    const RowFmt &f = b->fmt;
-    const int ff = wout->rows, rank = wup->rows;
-    const int n_tiles = (ff + 63) / 64;
-    if (xs_bytes(f) + (size_t)(rank + 2 * 128 + 8) * 4 > 64 * 1024)
-        return llg_set_error(d, LLG_E_ARG, "predict_sparse: hidden size %d too large", f.cols);
-    int2 *pairs = reinterpret_cast<int2 *>(ws + llg_predict_ws_bytes(rank, ff));
     float *partial;
     unsigned long long *mask;
     int psplit;
@@ -697,15 +691,31 @@ int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *
     // as (out + d_out_add) + the FFN output, the residual order of
     // ffn_flash.go:161-166)
     int rc = llg_pred_hidden_enqueue(d, wup, d_a, ws, &partial, &mask, &psplit,
-                                     d_out_add ? d_out : nullptr, f.cols, nullptr, 0, nullptr,
-                                     d_out_add);
+                                     d_out_add ? d_out : nullptr, b->fmt.cols, nullptr, 0,
+                                     nullptr, d_out_add);
     if (rc) return rc;
-    if (psplit != PRED_SPLIT_N)
-        return llg_set_error(d, LLG_E_ARG, "predict_sparse: hidden split %d != %d", psplit,
-                             PRED_SPLIT_N);
+    return llg_fused_tail_enqueue(d, wout, bias, b, d_x, thr, act, d_out, d_active, d_n_active,
+                                  ws, d_out_add != nullptr);
+}
+
+int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgObject *b,
+                           const float *d_x, float thr, int act, float *d_out,
+                           int32_t *d_active, int32_t *d_n_active, uint8_t *ws, bool accum) {
+    if (int rc = llg_check_act(d, act)) return rc;
+    const RowFmt &f = b->fmt;
+    const int ff = wout->rows, rank = wout->fmt.cols;
+    const int n_tiles = (ff + 63) / 64;
+    if (xs_bytes(f) + (size_t)(rank + 2 * 128 + 8) * 4 > 64 * 1024)
+        return llg_set_error(d, LLG_E_ARG, "predict_sparse: hidden size %d too large", f.cols);
+    if (llg_pred_split() != PRED_SPLIT_N)
+        return llg_set_error(d, LLG_E_ARG, "predict_sparse: hidden split %d != %d",
+                             llg_pred_split(), PRED_SPLIT_N);
+    int2 *pairs = reinterpret_cast<int2 *>(ws + llg_predict_ws_bytes(rank, ff));
+    float *partial;
+    unsigned long long *mask;
+    llg_pred_ws_layout(ws, rank, &partial, &mask);
     const float *d_bias = bias ? reinterpret_cast<const float *>(bias->d) : nullptr;
     hipStream_t st = llg_dev_stream(d);
-    const bool accum = d_out_add != nullptr;
     switch (f.type) {
     case LLG_TYPE_Q4_0:
         launch_fused<LLG_TYPE_Q4_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, pairs,
