@@ -611,6 +611,78 @@ __device__ __forceinline__ void llg_stage_x_sum(float *xs, const float *__restri
     }
 }
 
+// Attention output in split form: the positions of each head are divided
+// over n_split workgroups, each leaving acc = sum_t exp(s_t - m) v_t and
+// (m, l = sum_t exp(s_t - m)) over its rows (m = -inf, l = 0 for none).
+struct LlgAttnParts {
+    const float *acc;  // [n_split][n_heads * head_dim]
+    const float *ml;   // [n_split][n_heads][2]
+    int n_split, n_heads, head_dim;
+};
+#define LLG_ATTN_SPLIT_MAX 4
+
+// Stage the merged attention output, x[c] = sum_s acc_s[c] e_s / sum_s l_s e_s
+// with e_s = exp(m_s - max_s m_s) for the head of column c (0 for an empty
+// split), like llg_stage_x_sum (the nb blocks from block cb0).  Each thread
+// requests its columns of every split (two float4 groups at a time) before
+// merging them; issue() runs after the first requests.
+template <int XS, class Issue = LlgNoIssue>
+__device__ __forceinline__ void llg_stage_attn(float *xs, const LlgAttnParts &ap, int cb0, int nb,
+                                               Issue &&issue = Issue()) {
+    static_assert(XS >= 33, "room for the block sum");
+    constexpr int KB = 2;
+    const int n4 = nb * 8, cols = ap.n_heads * ap.head_dim;
+    const int lane = threadIdx.x & 63, base0 = threadIdx.x - lane, bd = blockDim.x;
+    const float4 *acc4 = reinterpret_cast<const float4 *>(ap.acc);
+    const float2 *ml2 = reinterpret_cast<const float2 *>(ap.ml);
+    for (int k0 = 0; base0 + k0 * bd < n4; k0 += KB) {
+        float4 a[KB][LLG_ATTN_SPLIT_MAX];
+        float2 ml[KB][LLG_ATTN_SPLIT_MAX];
+#pragma unroll
+        for (int k = 0; k < KB; k++) {
+            const int i = min(base0 + (k0 + k) * bd + lane, n4 - 1);
+            const int c = cb0 * 32 + 4 * i;
+            const int h = c / ap.head_dim;
+#pragma unroll
+            for (int s = 0; s < LLG_ATTN_SPLIT_MAX; s++)
+                if (s < ap.n_split) {
+                    a[k][s] = acc4[((size_t)s * cols + c) >> 2];
+                    ml[k][s] = ml2[s * ap.n_heads + h];
+                }
+        }
+        if (k0 == 0) {
+            __builtin_amdgcn_sched_barrier(0);  // keep the caller's loads behind these
+            issue();
+        }
+#pragma unroll
+        for (int k = 0; k < KB; k++) {
+            float M = ml[k][0].x;
+#pragma unroll
+            for (int s = 1; s < LLG_ATTN_SPLIT_MAX; s++)
+                if (s < ap.n_split) M = fmaxf(M, ml[k][s].x);
+            float L = 0.0f;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int s = 0; s < LLG_ATTN_SPLIT_MAX; s++)
+                if (s < ap.n_split) {
+                    const float e = ml[k][s].x == -INFINITY ? 0.0f : expf(ml[k][s].x - M);
+                    L += ml[k][s].y * e;
+                    v.x += a[k][s].x * e;
+                    v.y += a[k][s].y * e;
+                    v.z += a[k][s].z * e;
+                    v.w += a[k][s].w * e;
+                }
+            const float rl = 1.0f / L;
+            v.x *= rl;
+            v.y *= rl;
+            v.z *= rl;
+            v.w *= rl;
+            llg_x_sum_store<XS>(xs, v, base0 + (k0 + k) * bd + lane, n4);
+        }
+    }
+    if (base0 >= n4) issue();  // a wavefront with no columns still issues its loads
+}
+
 // Sum over the workgroup (every thread gets it); red: LDS, one float per
 // wavefront.  Contains two barriers.
 __device__ __forceinline__ float llg_block_sum(float v, float *red) {

@@ -39,7 +39,10 @@
 // (spread over the workgroups), the first one's loads requested with the
 // first rows'; the row sums go to pf.resid (+=) and, if y is set, to y.
 #define MV_PFL 3  // float4 loads per lane of a fold task (split_blocks <= 24)
-template <int T, int LNP, bool G = false, int NT = 256, bool PF = false>
+//
+// AC: x is the attention output in split form (LlgAttnParts), merged while
+// it is staged (llg_stage_attn).
+template <int T, int LNP, bool G = false, int NT = 256, bool PF = false, bool AC = false>
 __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, long long stride,
                                                   RowFmt f, int rows, int tile_rows,
                                                   int chunk_blocks,
@@ -47,9 +50,11 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
                                                   float *__restrict__ y, float *__restrict__ part,
                                                   LlgLnArgs ln,
                                                   const uint8_t *__restrict__ w2 = nullptr,
-                                                  LlgPredFold pf = LlgPredFold{}) {
+                                                  LlgPredFold pf = LlgPredFold{},
+                                                  LlgAttnParts ap = LlgAttnParts{}) {
     static_assert(!G || (LNP == 0 && MV_ROWS == 2), "gated rows pair gate and up");
     static_assert(!PF || (LNP == 0 && !G), "the fold rides on a plain matvec");
+    static_assert(!AC || (LNP == 0 && !G), "the attention merge replaces the plain x");
     constexpr int RW = G ? 1 : MV_ROWS;  // output rows per wavefront pass
     extern __shared__ float xs[];
     __shared__ float red[NT / 64];
@@ -126,6 +131,8 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
     };
     if constexpr (LNP > 0)  // x is the LayerNorm of the residual sum (one chunk: cb0 = 0)
         llg_stage_ln<MV_XS, LNP>(xs, ln, red, issue_first);
+    else if constexpr (AC)
+        llg_stage_attn<MV_XS>(xs, ap, cb0, cnb, issue_first);
     else
         llg_stage_x_sum<MV_XS>(xs, x + (size_t)cb0 * 32, cnb, issue_first);
     __syncthreads();
@@ -235,11 +242,83 @@ static size_t mv_part_floats(const RowFmt &f, int rows, int act) {
 // part: room for mv_part_floats (the partial sums of a chunked matvec).
 // ln (optional): the staged x is the LayerNorm of a residual sum (llg_stage_ln).
 // up (optional): gated rows, y = silu(w . x) * (up . x) (act is ignored).
+// Launch parameters of one k_matvec_q call.
+struct MvArgs {
+    dim3 grid;
+    int threads;
+    size_t lds;
+    hipStream_t st;
+    const LlgObject *w;
+    int tile_rows, cb;
+    const float *x;
+    int act;
+    float *y, *part;
+    LlgLnArgs ln;
+    const uint8_t *w2;
+    LlgPredFold pf;
+    LlgAttnParts ap;
+};
+
+template <int T, int LNP, bool G, int NT, bool PF, bool AC>
+static void mv_go(const MvArgs &a) {
+    hipLaunchKernelGGL((k_matvec_q<T, LNP, G, NT, PF, AC>), a.grid, dim3(a.threads), a.lds, a.st,
+                       a.w->d, a.w->stride, a.w->fmt, a.w->rows, a.tile_rows, a.cb, a.x, a.act,
+                       a.y, a.part, a.ln, a.w2, a.pf, a.ap);
+}
+
+// Instances with NT = 1024 workgroups (the balanced launch) exist for the
+// types whose blocks fit the 128 registers of a 16-wavefront workgroup:
+// Q4_0 with up to 4 LayerNorm groups per thread, Q8_0 with up to 2.
+template <int T>
+constexpr int mv_bal_lnp() {
+    return T == LLG_TYPE_Q4_0 ? 4 : T == LLG_TYPE_Q8_0 ? 2 : -1;
+}
+
+template <int T, int NT, int LNP>
+static void mv_plain(const MvArgs &a, bool pf, bool ac) {
+    if constexpr (LNP > 0) {
+        mv_go<T, LNP, false, NT, false, false>(a);
+    } else {
+        if (pf && ac) mv_go<T, 0, false, NT, true, true>(a);
+        else if (pf) mv_go<T, 0, false, NT, true, false>(a);
+        else if (ac) mv_go<T, 0, false, NT, false, true>(a);
+        else mv_go<T, 0, false, NT, false, false>(a);
+    }
+}
+
+template <int T>
+static void mv_dispatch(const MvArgs &a, bool bal, bool gated, bool pf, bool ac, int lnp) {
+    if (gated) return mv_go<T, 0, true, 256, false, false>(a);
+    if constexpr (mv_bal_lnp<T>() >= 0) {
+        if (bal) {
+            if (lnp == 0) mv_plain<T, 1024, 0>(a, pf, ac);
+            else if (lnp <= 2) mv_plain<T, 1024, 2>(a, pf, ac);
+            else if constexpr (mv_bal_lnp<T>() >= 4) mv_plain<T, 1024, 4>(a, pf, ac);
+            return;
+        }
+    }
+    if (lnp == 0) mv_plain<T, 256, 0>(a, pf, ac);
+    else if (lnp <= 2) mv_plain<T, 256, 2>(a, pf, ac);
+    else if (lnp <= 4) mv_plain<T, 256, 4>(a, pf, ac);
+    else if (lnp <= 5) mv_plain<T, 256, 5>(a, pf, ac);
+    else if (lnp <= 8) mv_plain<T, 256, 8>(a, pf, ac);
+    else mv_plain<T, 256, 16>(a, pf, ac);
+}
+
+static int mv_bal_lnp_rt(int type) {
+    switch (type) {
+    case LLG_TYPE_Q4_0: return mv_bal_lnp<LLG_TYPE_Q4_0>();
+    case LLG_TYPE_Q8_0: return mv_bal_lnp<LLG_TYPE_Q8_0>();
+    default: return -1;
+    }
+}
+
 // pf (optional): the predictor fold (whole rows in one workgroup, no LayerNorm).
+// ap (optional): x is the attention output in split form (d_x unused).
 static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y,
                          float *part, const LlgLnArgs *ln = nullptr,
-                         const LlgObject *up = nullptr, const LlgPredFold *pf = nullptr) {
-    hipStream_t st = llg_dev_stream(d);
+                         const LlgObject *up = nullptr, const LlgPredFold *pf = nullptr,
+                         const LlgAttnParts *ap = nullptr) {
     const RowFmt &f = w->fmt;
     if (up) act = LLG_ACT_SILU;  // whole rows in one workgroup
     const int cb = ln ? f.nb : mv_chunk_blocks(f, act);
@@ -253,10 +332,24 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
                pf->split_blocks * 8 > 64 * MV_PFL ||
                (long long)pf->split_blocks * pf->n_split < f.nb))
         return llg_set_error(d, LLG_E_ARG, "matvec: predictor fold needs whole plain rows");
-    int tile_rows = (w->rows < MV_SMALL_ROWS ? MV_TILE_SMALL : MV_TILE) / (up ? 2 : 1);
-    int threads = 256;
-    const LlgLnArgs none{};
-    const LlgLnArgs &la = ln ? *ln : none;
+    if (ap && (ln || up || ap->n_split < 1 || ap->n_split > LLG_ATTN_SPLIT_MAX ||
+               ap->n_heads * ap->head_dim != f.cols || ap->head_dim % 4))
+        return llg_set_error(d, LLG_E_ARG, "matvec: attention parts do not match the rows");
+    MvArgs a;
+    a.st = llg_dev_stream(d);
+    a.w = w;
+    a.cb = cb;
+    a.lds = lds;
+    a.x = d_x;
+    a.act = act;
+    a.y = d_y;
+    a.part = part;
+    a.ln = ln ? *ln : LlgLnArgs{};
+    a.w2 = up ? up->d : nullptr;
+    a.pf = pf ? *pf : LlgPredFold{};
+    a.ap = ap ? *ap : LlgAttnParts{};
+    a.tile_rows = (w->rows < MV_SMALL_ROWS ? MV_TILE_SMALL : MV_TILE) / (up ? 2 : 1);
+    a.threads = 256;
     int lnp = ln ? (ln->n / 4 + 255) / 256 : 0;
     // Balanced: a matrix of MV_BAL_MIN..MV_SMALL_ROWS whole rows goes to at
     // most one workgroup per CU, each a single pass of MV_ROWS rows per
@@ -268,67 +361,33 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
         const int rpw = MV_ROWS * ((w->rows + MV_ROWS * cus - 1) / (MV_ROWS * cus));
         const int th = 64 * (rpw / MV_ROWS);
         const int lnp_b = ln ? (ln->n / 4 + th - 1) / th : 0;
-        if (th >= 256 && th <= 1024 && lnp_b <= 4) {
+        if (th >= 256 && th <= 1024 && lnp_b <= mv_bal_lnp_rt(f.type)) {
             bal = true;
-            tile_rows = rpw;
-            threads = th;
+            a.tile_rows = rpw;
+            a.threads = th;
             lnp = lnp_b;
         }
     }
-    const int grid = (w->rows + tile_rows - 1) / tile_rows * n_chunks;
-#define MV_GO(TY, NP)                                                                              \
-    do {                                                                                           \
-        if (pf && bal)                                                                             \
-            hipLaunchKernelGGL((k_matvec_q<TY, 0, false, 1024, true>), dim3(grid), dim3(threads),  \
-                               lds, st, w->d, w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, \
-                               part, la, (const uint8_t *)nullptr, *pf);                           \
-        else if (pf)                                                                               \
-            hipLaunchKernelGGL((k_matvec_q<TY, 0, false, 256, true>), dim3(grid), dim3(256), lds,  \
-                               st, w->d, w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y,      \
-                               part, la, (const uint8_t *)nullptr, *pf);                           \
-        else if (bal)                                                                              \
-            hipLaunchKernelGGL((k_matvec_q<TY, (NP <= 4 ? NP : 4), false, 1024>), dim3(grid),      \
-                               dim3(threads), lds, st, w->d, w->stride, f, w->rows, tile_rows, cb, \
-                               d_x, act, d_y, part, la, (const uint8_t *)nullptr);                 \
-        else                                                                                       \
-            hipLaunchKernelGGL((k_matvec_q<TY, NP>), dim3(grid), dim3(256), lds, st, w->d,         \
-                               w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, part, la,     \
-                               (const uint8_t *)nullptr);                                         \
-    } while (0)
-#define MV_LAUNCH(TY)                                                                              \
-    do {                                                                                           \
-        if (up)                                                                                    \
-            hipLaunchKernelGGL((k_matvec_q<TY, 0, true>), dim3(grid), dim3(256), lds, st, w->d,    \
-                               w->stride, f, w->rows, tile_rows, cb, d_x, act, d_y, part, la,     \
-                               up->d);                                                             \
-        else if (!ln) MV_GO(TY, 0);                                                                \
-        else if (lnp <= 2) MV_GO(TY, 2);                                                           \
-        else if (lnp <= 4) MV_GO(TY, 4);                                                           \
-        else if (lnp <= 5) MV_GO(TY, 5);                                                           \
-        else if (lnp <= 8) MV_GO(TY, 8);                                                           \
-        else MV_GO(TY, 16);                                                                        \
-    } while (0)
+    a.grid = dim3((w->rows + a.tile_rows - 1) / a.tile_rows * n_chunks);
     switch (f.type) {
     case LLG_TYPE_Q4_0:
-        MV_LAUNCH(LLG_TYPE_Q4_0);
+        mv_dispatch<LLG_TYPE_Q4_0>(a, bal, up != nullptr, pf != nullptr, ap != nullptr, lnp);
         break;
     case LLG_TYPE_Q8_0:
-        MV_LAUNCH(LLG_TYPE_Q8_0);
+        mv_dispatch<LLG_TYPE_Q8_0>(a, bal, up != nullptr, pf != nullptr, ap != nullptr, lnp);
         break;
     case LLG_TYPE_F16:
-        MV_LAUNCH(LLG_TYPE_F16);
+        mv_dispatch<LLG_TYPE_F16>(a, bal, up != nullptr, pf != nullptr, ap != nullptr, lnp);
         break;
     case LLG_TYPE_F32:
-        MV_LAUNCH(LLG_TYPE_F32);
+        mv_dispatch<LLG_TYPE_F32>(a, bal, up != nullptr, pf != nullptr, ap != nullptr, lnp);
         break;
     default:
         return llg_set_error(d, LLG_E_TYPE, "matvec: unsupported type %d", f.type);
     }
-#undef MV_LAUNCH
-#undef MV_GO
     LLG_LAUNCH_CHECK(d, "matvec_q");
     if (n_chunks > 1) {
-        hipLaunchKernelGGL(k_chunk_sum, dim3((w->rows + 255) / 256), dim3(256), 0, st,
+        hipLaunchKernelGGL(k_chunk_sum, dim3((w->rows + 255) / 256), dim3(256), 0, a.st,
                            (const float *)part, n_chunks, w->rows, act, d_y);
         LLG_LAUNCH_CHECK(d, "matvec chunk sum");
     }
@@ -350,9 +409,9 @@ int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int a
 
 bool llg_matvec_fold_ok(const LlgObject *w) { return mv_chunk_blocks(w->fmt, -1) == w->fmt.nb; }
 
-int llg_matvec_fold_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, float *d_y,
-                            const LlgPredFold &pf) {
-    return matvec_launch(d, w, d_x, -1, d_y, nullptr, nullptr, nullptr, &pf);
+int llg_matvec_attn_enqueue(LlgDevice *d, const LlgObject *w, const LlgAttnParts &ap, float *d_y,
+                            float *part, const LlgPredFold *pf) {
+    return matvec_launch(d, w, nullptr, -1, d_y, part, nullptr, nullptr, pf, &ap);
 }
 
 size_t llg_matvec_part_bytes(const LlgObject *w, int act) {

@@ -68,12 +68,13 @@ int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, con
 int llg_matvec_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, int act, float *d_y,
                        float *part);
 size_t llg_matvec_part_bytes(const LlgObject *w, int act);
-// The attention-output matvec with the predictor fold (LlgPredFold): y (may
-// be null) = W . x, pf.resid += W . x, and the fold tasks' partial sums.
-// llg_matvec_fold_ok: W's rows fit one workgroup's staged x.
+// The attention-output matvec y = W . x, x the merge of the split attention
+// output (LlgAttnParts).  With pf (LlgPredFold; W's rows must fit one
+// workgroup's staged x, llg_matvec_fold_ok): y may be null, pf.resid += W . x,
+// and the fold tasks' partial sums.  part: as for llg_matvec_enqueue.
 bool llg_matvec_fold_ok(const LlgObject *w);
-int llg_matvec_fold_enqueue(LlgDevice *d, const LlgObject *w, const float *d_x, float *d_y,
-                            const LlgPredFold &pf);
+int llg_matvec_attn_enqueue(LlgDevice *d, const LlgObject *w, const LlgAttnParts &ap, float *d_y,
+                            float *part, const LlgPredFold *pf);
 // y = W . LayerNorm((x_in + a1) + a2), the residual sum and the normed row
 // also written to ln.x_out / ln.normed_out (llg_stage_ln).
 int llg_matvec_ln_enqueue(LlgDevice *d, const LlgObject *w, const LlgLnArgs &ln, float *d_y);

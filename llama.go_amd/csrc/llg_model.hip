@@ -53,12 +53,14 @@ struct LlgModelLayer {
 
 struct LlgModel {
     int n_layers, hidden, n_heads, n_kv, head_dim, ff, vocab, max_seq, rank, act;
+    int cus;  // compute units of the device
     float rope_base, eps;
     LlgObject *embed, *out_w, *out_b, *lm_head;
     std::vector<LlgModelLayer> layers;
     // device buffers, carved out of the object's allocation
     float *x, *normed, *qkv, *attn, *attn_out, *logits, *kv, *pred_logits;  // x: the residual
     float *mvpart;  // partial sums of a column-chunked Wo or LM-head matvec
+    float *attn_ml;  // attention splits' (max, sum); attn holds their acc rows
     float2 *rope;  // [max_seq x head_dim/2] (cos, sin)
     int32_t *token, *n_active, *act_scratch;
     uint8_t *ws;
@@ -231,9 +233,14 @@ __global__ __launch_bounds__(256) void k_fold_pred(const uint8_t *__restrict__ w
 // running max m, the sum l of exp(score - m) and acc = sum exp(score - m) v
 // over its rows; groups merge by rescaling to the larger max (exp(-inf) = 0
 // for empty groups), wavefronts in LDS in wavefront order, so the result is
-// the same on every run.  out = acc / l.  The exponentials are fp32 expf of
-// the fp32 difference; the reference rounds a double exp to float, which
-// differs by about an ulp.
+// the same on every run.  The exponentials are fp32 expf of the fp32
+// difference; the reference rounds a double exp to float, which differs by
+// about an ulp.
+//
+// The rows 0..pos of a head are split over n_split workgroups (blockIdx =
+// head * n_split + split), so long caches spread over more CUs; each leaves
+// its (acc, m, l) (LlgAttnParts) and the Wo matvec merges the splits while
+// it stages its x (out = sum acc e / sum l e, e = exp(m - max m)).
 template <int HD>
 struct AttnShape {
     static constexpr int LP = HD / 4;                    // lanes per position
@@ -277,14 +284,17 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
                                                        int n_kv, int pos,
                                                        const float2 *__restrict__ rope,
                                                        int max_seq, float *__restrict__ kv,
-                                                       float *__restrict__ out) {
+                                                       int n_split, float *__restrict__ acc_out,
+                                                       float *__restrict__ ml_out) {
     using S = AttnShape<HD>;
     constexpr int LP = S::LP, PW = S::PW, NW = S::NW, PR = NW * PW * U;
     static_assert(U <= LP, "lane u of a group computes the exponential of load u");
     __shared__ __attribute__((aligned(16))) float qh[HD], kh[HD], vh[HD];
     __shared__ __attribute__((aligned(16))) float wacc[NW][HD];
     __shared__ float wm[NW], wl[NW];
-    const int h = blockIdx.x;
+    const int h = blockIdx.x / n_split, sp = blockIdx.x % n_split;
+    const int chunk = (pos + n_split) / n_split;  // rows 0..pos over n_split workgroups
+    const int row0 = sp * chunk, row1 = min(pos + 1, row0 + chunk);  // this one's rows [row0, row1)
     const int kvh = h * n_kv / n_heads;  // forward.go:266
     const int kv_dim = n_kv * HD, row4 = kv_dim / 4;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -292,7 +302,7 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
     const float4 *kc4 = reinterpret_cast<const float4 *>(kv + (size_t)kvh * HD) + sub;
     const float4 *vc4 =
         reinterpret_cast<const float4 *>(kv + (size_t)max_seq * kv_dim + (size_t)kvh * HD) + sub;
-    const int t0 = wave * PW * U + slot;  // + round * PR + u * PW
+    const int t0 = row0 + wave * PW * U + slot;  // + round * PR + u * PW
     float4 kk[U], vv[U];
     auto issue = [&](int r) {
 #pragma unroll
@@ -306,7 +316,8 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
     const float *q = qkv + (size_t)h * HD;
     const float *kcur = qkv + (size_t)n_heads * HD + (size_t)kvh * HD;
     const float *vcur = kcur + kv_dim;
-    const bool first = h == kvh * (n_heads / n_kv);  // appends row pos (kvcache.go:42-52)
+    // the group's first query head appends row pos (kvcache.go:42-52)
+    const bool first = h == kvh * (n_heads / n_kv) && sp == 0;
     if (tid < HD / 2) {  // RoPE, pairs (i, i + HD/2) (forward.go:483-497)
         const int i = tid;
         const float2 cs = rope[(size_t)pos * (HD / 2) + i];
@@ -334,7 +345,7 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
     const float4 vn = reinterpret_cast<const float4 *>(vh)[sub];
     float m = -INFINITY, l = 0.0f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int n_rounds = (pos + PR) / PR;  // rows 0..pos
+    const int n_rounds = (max(row1 - row0, 0) + PR - 1) / PR;
     for (int r = 0; r < n_rounds; r++) {
         if (r > 0) issue(r);
         float sc[U];
@@ -347,14 +358,14 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
             dot = row16_sum(dot);
             if (LP == 32) dot += __shfl_xor(dot, 16, 64);
             sc[u] = dot * scale;
-            if (t <= pos) mr = fmaxf(mr, sc[u]);
+            if (t < row1) mr = fmaxf(mr, sc[u]);
         }
         // lane `sub` of the group takes the exponential of load u = sub
         float mine = sc[0];
 #pragma unroll
         for (int u = 1; u < U; u++)
             if (sub == u) mine = sc[u];
-        const bool valid = sub < U && r * PR + t0 + sub * PW <= pos;
+        const bool valid = sub < U && r * PR + t0 + sub * PW < row1;
         const float pm = valid ? expf(mine - mr) : 0.0f;
         float p[U];
         group_bcast<LP, U>(pm, p);
@@ -392,7 +403,7 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
         wl[wave] = l;
     }
     __syncthreads();
-    if (tid < HD) {
+    if (tid < HD) {  // this workgroup's (acc, m, l), merged with the other splits by the reader
         float M = wm[0];
 #pragma unroll
         for (int w = 1; w < NW; w++) M = fmaxf(M, wm[w]);
@@ -403,7 +414,11 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
             L += wl[w] * e;
             R += wacc[w][tid] * e;
         }
-        out[(size_t)h * HD + tid] = R / L;
+        acc_out[((size_t)sp * n_heads + h) * HD + tid] = R;
+        if (tid == 0) {
+            ml_out[((size_t)sp * n_heads + h) * 2] = M;
+            ml_out[((size_t)sp * n_heads + h) * 2 + 1] = L;
+        }
     }
 }
 
@@ -482,15 +497,28 @@ static size_t model_ws_bytes(const LlgModel &m) {
     return std::max(llg_fused_ws_bytes(m.rank, m.ff), (size_t)llg_predict_ws_bytes(m.rank, m.ff));
 }
 
-// The attention launch for rows 0..pos: the fewest loads per lane U whose
-// round covers them all, else rounds of the largest.
+// Rows per attention workgroup above which a head's rows are split further:
+// up to LLG_ATTN_SPLIT_MAX workgroups per head, and no more workgroups than
+// CUs (a CU given two would take twice as long as the rest).
+#define ATTN_SPLIT_ROWS 160
+static int attn_splits(const LlgModel &m, int pos) {
+    const int by_rows = (pos + ATTN_SPLIT_ROWS) / ATTN_SPLIT_ROWS;
+    const int by_cus = std::max(1, m.cus / m.n_heads);
+    return std::min(std::min(LLG_ATTN_SPLIT_MAX, by_cus), by_rows);
+}
+
+// The attention launch for rows 0..pos: attn_splits workgroups per head, and
+// the fewest loads per lane U whose round covers a workgroup's rows, else
+// rounds of the largest.
 template <int HD>
 static void launch_attn(hipStream_t st, const LlgModel &m, int pos, float *kvl) {
     using S = AttnShape<HD>;
-    const int n = pos + 1;
+    const int ns = attn_splits(m, pos);
+    const int n = (pos + ns) / ns;
+    const dim3 grid(m.n_heads * ns);
 #define ATT(U)                                                                                     \
-    hipLaunchKernelGGL((k_attn<HD, U>), dim3(m.n_heads), dim3(ATTN_THREADS), 0, st, m.qkv,        \
-                       m.n_heads, m.n_kv, pos, m.rope, m.max_seq, kvl, m.attn)
+    hipLaunchKernelGGL((k_attn<HD, U>), grid, dim3(ATTN_THREADS), 0, st, m.qkv, m.n_heads,        \
+                       m.n_kv, pos, m.rope, m.max_seq, kvl, ns, m.attn, m.attn_ml)
     if (n <= S::per_round(1)) ATT(1);
     else if (n <= S::per_round(2)) ATT(2);
     else if (n <= S::per_round(4)) ATT(4);
@@ -498,6 +526,16 @@ static void launch_attn(hipStream_t st, const LlgModel &m, int pos, float *kvl) 
     else if (n <= S::per_round(8)) ATT(8);
     else ATT(10);
 #undef ATT
+}
+
+static LlgAttnParts attn_parts(const LlgModel &m, int pos) {
+    LlgAttnParts ap;
+    ap.acc = m.attn;
+    ap.ml = m.attn_ml;
+    ap.n_split = attn_splits(m, pos);
+    ap.n_heads = m.n_heads;
+    ap.head_dim = m.head_dim;
+    return ap;
 }
 
 // One token: embed -> layers -> norm -> LM head -> argmax, on the stream.
@@ -542,7 +580,9 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
             pf.rank = m.rank;
             pf.n_split = llg_pred_split();
             pf.split_blocks = (L.wo->fmt.nb + pf.n_split - 1) / pf.n_split;
-            if ((rc = llg_matvec_fold_enqueue(d, L.wo, m.attn, nullptr, pf))) return rc;
+            if ((rc = llg_matvec_attn_enqueue(d, L.wo, attn_parts(m, pos), nullptr, m.mvpart,
+                                              &pf)))
+                return rc;
             if (pred_logits &&
                 (rc = llg_pred_logits_enqueue(d, L.pwout, nullptr, L.thr, m.ws, m.act_scratch,
                                               m.act_scratch + m.ff,
@@ -554,7 +594,9 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
             if (rc) return rc;
             continue;
         }
-        if ((rc = llg_matvec_enqueue(d, L.wo, m.attn, -1, m.attn_out, m.mvpart))) return rc;
+        if ((rc = llg_matvec_attn_enqueue(d, L.wo, attn_parts(m, pos), m.attn_out, m.mvpart,
+                                          nullptr)))
+            return rc;
         if (pred_logits &&
             (rc = llg_predict_enqueue(d, L.pwup, L.pwout, nullptr, m.attn_out, L.thr, m.act_scratch,
                                       m.act_scratch + m.ff, pred_logits + (size_t)l * m.ff, m.ws)))
@@ -613,6 +655,7 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     m->max_seq = dims[7];
     m->rope_base = rope_base;
     m->eps = norm_eps;
+    m->cus = llg_cu_count(d);
     m->act = act;
     auto fail = [&](int code, const char *msg) {
         delete m;
@@ -667,7 +710,8 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     const size_t kv_dim = (size_t)m->n_kv * m->head_dim;
     const size_t v_h = llg_align((long long)m->hidden * 4, 256);
     const size_t v_qkv = llg_align((long long)qkv_rows * 4, 256);
-    const size_t v_att = llg_align((long long)m->n_heads * m->head_dim * 4, 256);
+    const size_t v_att = llg_align((long long)LLG_ATTN_SPLIT_MAX * m->n_heads * m->head_dim * 4, 256);
+    const size_t v_aml = llg_align((long long)LLG_ATTN_SPLIT_MAX * m->n_heads * 2 * 4, 256);
     const size_t v_log = llg_align((long long)m->vocab * 4, 256);
     const size_t v_kv = llg_align((long long)m->n_layers * 2 * m->max_seq * kv_dim * 4, 256);
     const size_t v_i = llg_align((long long)(m->n_layers + 4) * 4, 256);
@@ -684,7 +728,8 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     for (const LlgModelLayer &L : m->layers) v_mp = std::max(v_mp, llg_matvec_part_bytes(L.wo, -1));
     v_mp = llg_align((long long)v_mp, 256);
     const size_t total =
-        3 * v_h + v_qkv + v_att + v_log + v_kv + v_i + v_ff + v_pl + v_rope + v_mp + v_pf + wsb;
+        3 * v_h + v_qkv + v_att + v_aml + v_log + v_kv + v_i + v_ff + v_pl + v_rope + v_mp + v_pf +
+        wsb;
     uint8_t *buf = nullptr;
     if (hipMalloc(&buf, total) != hipSuccess) return fail(LLG_E_NOMEM, "buffer allocation failed");
     uint8_t *p = buf;
@@ -693,6 +738,7 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     m->attn_out = reinterpret_cast<float *>(p); p += v_h;
     m->qkv = reinterpret_cast<float *>(p); p += v_qkv;
     m->attn = reinterpret_cast<float *>(p); p += v_att;
+    m->attn_ml = reinterpret_cast<float *>(p); p += v_aml;
     m->logits = reinterpret_cast<float *>(p); p += v_log;
     m->kv = reinterpret_cast<float *>(p); p += v_kv;
     m->token = reinterpret_cast<int32_t *>(p);
