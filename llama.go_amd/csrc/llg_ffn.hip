@@ -3,16 +3,17 @@
 // llg_sparse.hip).
 //
 // k_matvec_q: y[r] = act(sum_b block_dot(row r, b, x)).  A workgroup owns a
-// tile of `tile_rows` rows (32, or 8 for matrices under 8192 rows so that the
-// grid still covers the CUs) and one column chunk of at most MV_CHUNK blocks; it
+// tile of `tile_rows` rows and one column chunk of at most MV_CHUNK blocks; it
 // stages that chunk of x in LDS (36-float stride per 32-float block, so 16
 // lanes reading one block each hit distinct banks).  Each wavefront takes
 // MV_ROWS rows at a time and issues the loads of all their blocks before
-// using any (two layouts of the blocks over the lanes, below).  With
-// one chunk the row sum is final and the activation is applied; with several
-// chunks each workgroup stores its partial sums, part[chunk][row], and
-// k_chunk_sum adds the chunks in order (a fixed order: results are the same
-// on every run).
+// using any (two layouts of the blocks over the lanes, below).  Tiles are 8
+// rows (one pass of 4 wavefronts), 16 or 32 for very tall matrices; a matrix
+// of 2048-8191 whole rows instead gets one workgroup per CU (the balanced
+// launch, below).  With one chunk the row sum is final and the activation is
+// applied; with several chunks each workgroup stores its partial sums,
+// part[chunk][row], and k_chunk_sum adds the chunks in order (a fixed order:
+// results are the same on every run).
 //
 // Gated (G): y[r] = silu(gate_r . x) * (up_r . x) (ffnSwiGLU, forward.go:
 // 368-389) with gate = w and up = w2; a wavefront's two row slots hold gate
@@ -21,8 +22,8 @@
 #include "llg_internal.hpp"
 
 #define MV_ROWS 2
-#define MV_TILE 32        // rows per workgroup (4 wavefronts x 4 passes x MV_ROWS)
-#define MV_TILE_SMALL 8   // rows per workgroup below MV_SMALL_ROWS rows (one pass)
+#define MV_TILE_SMALL 8   // rows per workgroup: one pass of 4 wavefronts x MV_ROWS ...
+#define MV_MAX_WG 4096    // ... doubled (up to 32) while the grid has more workgroups than this
 #define MV_SMALL_ROWS 8192
 #define MV_BAL_MIN 2048   // balanced launch from this many rows (at least 4 wavefronts per CU)
 #define MV_CHUNK 160      // max blocks of x staged per workgroup
@@ -39,9 +40,6 @@
 // (spread over the workgroups), the first one's loads requested with the
 // first rows'; the row sums go to pf.resid (+=) and, if y is set, to y.
 #define MV_PFL 3  // float4 loads per lane of a fold task (split_blocks <= 24)
-//
-// AC: x is the attention output in split form (LlgAttnParts), merged while
-// it is staged (llg_stage_attn).
 template <int T, int LNP, bool G = false, int NT = 256, bool PF = false, bool AC = false>
 __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, long long stride,
                                                   RowFmt f, int rows, int tile_rows,
@@ -91,24 +89,25 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
         else return w + (long long)min(r0_ + q, r_end - 1) * stride;
     };
     const int n_slots = FLAT ? MV_ROWS * cnb : cnb;  // what the kb steps run over
-    auto issue = [&](int r0_, int kb) {
+    auto issue_to = [&](BlockRaw<T>(&dst)[NR], int r0_, int kb) {
         if constexpr (FLAT) {
             const uint8_t *p0 = row_ptr(r0_, 0), *p1 = row_ptr(r0_, 1);
 #pragma unroll
             for (int i = 0; i < MV_NI; i++) {
                 const int k = kb + lane + 64 * i;
                 const bool q = k >= cnb;
-                llg_block_load<T>(r[i], q ? p1 : p0, f, cb0 + min(k - (q ? cnb : 0), cnb - 1));
+                llg_block_load<T>(dst[i], q ? p1 : p0, f, cb0 + min(k - (q ? cnb : 0), cnb - 1));
             }
         } else {
 #pragma unroll
             for (int i = 0; i < MV_BATCH; i++)
 #pragma unroll
                 for (int q = 0; q < MV_ROWS; q++)
-                    llg_block_load<T>(r[i * MV_ROWS + q], row_ptr(r0_, q), f,
+                    llg_block_load<T>(dst[i * MV_ROWS + q], row_ptr(r0_, q), f,
                                       cb0 + min(kb + lane + 64 * i, cnb - 1));
         }
     };
+    auto issue = [&](int r0_, int kb) { issue_to(r, r0_, kb); };
     // fold tasks of this wavefront: t0, t0 + fstep, ... < n_tasks
     const int n_tasks = PF ? pf.rank * pf.n_split : 0;
     const int fstep = gridDim.x * (int)(blockDim.x >> 6);
@@ -159,47 +158,45 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
             if (lane == 0) pf.part[sp * pf.rank + j] = acc;
         }
     }
-    const int n_waves = blockDim.x >> 6;
-    for (int r0 = r_first; r0 < r_end; r0 += n_waves * RW) {
-        float s[MV_ROWS] = {0.0f, 0.0f};
-        for (int kb = 0; kb < n_slots; kb += 64 * (FLAT ? MV_NI : MV_BATCH)) {
-            if (r0 != r_first || kb != 0) issue(r0, kb);
-            if constexpr (FLAT) {
+    // the dots of one kb step of the pass at r0 from the blocks in src
+    auto dots = [&](const BlockRaw<T>(&src)[NR], int kb, int r0, float(&sv)[MV_ROWS]) {
+        if constexpr (FLAT) {
 #pragma unroll
-                for (int i = 0; i < MV_NI; i++) {
-                    const int k = kb + lane + 64 * i;
-                    if (k >= n_slots) continue;
-                    const bool q = k >= cnb;
-                    const float *xb = xs + (k - (q ? cnb : 0)) * MV_XS;
-                    const float d =
-                        llg_raw_dot<T>(r[i], reinterpret_cast<const float4 *>(xb), xb[32]);
-                    if (q)
-                        s[1] += d;
-                    else
-                        s[0] += d;
-                }
-            } else {
+            for (int i = 0; i < MV_NI; i++) {
+                const int k = kb + lane + 64 * i;
+                if (k >= n_slots) continue;
+                const bool q = k >= cnb;
+                const float *xb = xs + (k - (q ? cnb : 0)) * MV_XS;
+                const float d = llg_raw_dot<T>(src[i], reinterpret_cast<const float4 *>(xb), xb[32]);
+                if (q)
+                    sv[1] += d;
+                else
+                    sv[0] += d;
+            }
+        } else {
 #pragma unroll
-                for (int i = 0; i < MV_BATCH; i++) {
-                    const int bl = kb + lane + 64 * i;
-                    if (bl >= cnb) continue;
-                    const float *xb = xs + bl * MV_XS;
-                    const float4 *x4 = reinterpret_cast<const float4 *>(xb);
+            for (int i = 0; i < MV_BATCH; i++) {
+                const int bl = kb + lane + 64 * i;
+                if (bl >= cnb) continue;
+                const float *xb = xs + bl * MV_XS;
+                const float4 *x4 = reinterpret_cast<const float4 *>(xb);
 #pragma unroll
-                    for (int q = 0; q < MV_ROWS; q++)
-                        if (r0 + (G ? 0 : q) < r_end)
-                            s[q] += llg_raw_dot<T>(r[i * MV_ROWS + q], x4, xb[32]);
-                }
+                for (int q = 0; q < MV_ROWS; q++)
+                    if (r0 + (G ? 0 : q) < r_end)
+                        sv[q] += llg_raw_dot<T>(src[i * MV_ROWS + q], x4, xb[32]);
             }
         }
+    };
+    // the row sums of the pass at r0: activation and store, or the chunk's partials
+    auto finish = [&](float(&sv)[MV_ROWS], int r0) {
         if constexpr (G) {  // silu(gate) * up in fp32 (forward.go:370-383)
-            const float g = llg_wave_sum(s[0]), u = llg_wave_sum(s[1]);
+            const float g = llg_wave_sum(sv[0]), u = llg_wave_sum(sv[1]);
             if (lane == 0 && r0 < r_end) y[r0] = llg_act(LLG_ACT_SILU, g) * u;
-            continue;
+            return;
         }
 #pragma unroll
         for (int q = 0; q < MV_ROWS; q++) {
-            const float v = llg_wave_sum(s[q]);
+            const float v = llg_wave_sum(sv[q]);
             if (lane == 0 && r0 + q < r_end) {
                 if (n_chunks == 1) {
                     const float o = act >= 0 ? llg_act(act, v) : v;
@@ -210,6 +207,16 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
                 }
             }
         }
+    };
+    const int step = (int)(blockDim.x >> 6) * RW;
+    constexpr int KSTEP = 64 * (FLAT ? MV_NI : MV_BATCH);
+    for (int r0 = r_first; r0 < r_end; r0 += step) {
+        float sv[MV_ROWS] = {0.0f, 0.0f};
+        for (int kb = 0; kb < n_slots; kb += KSTEP) {
+            if (r0 != r_first || kb != 0) issue(r0, kb);
+            dots(r, kb, r0, sv);
+        }
+        finish(sv, r0);
     }
 }
 
@@ -348,9 +355,15 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
     a.w2 = up ? up->d : nullptr;
     a.pf = pf ? *pf : LlgPredFold{};
     a.ap = ap ? *ap : LlgAttnParts{};
-    a.tile_rows = (w->rows < MV_SMALL_ROWS ? MV_TILE_SMALL : MV_TILE) / (up ? 2 : 1);
+    // Rows per workgroup: one pass per wavefront (8 rows) gives the most
+    // loads in flight; very tall matrices take 16 or 32 rows so that the grid
+    // stays within MV_MAX_WG workgroups (an 18176-row Q4_0 matvec: 13.6 us at
+    // 8 rows, 15.2 at 16, 16.8 at 32; 65024 rows: 41.0, 38.7, 39.3).
+    int tr = MV_TILE_SMALL;
+    while (tr < 32 && (long long)(w->rows + tr - 1) / tr * n_chunks > MV_MAX_WG) tr *= 2;
+    a.tile_rows = tr / (up ? 2 : 1);
     a.threads = 256;
-    int lnp = ln ? (ln->n / 4 + 255) / 256 : 0;
+    int lnp = ln ? (ln->n / 4 + a.threads - 1) / a.threads : 0;
     // Balanced: a matrix of MV_BAL_MIN..MV_SMALL_ROWS whole rows goes to at
     // most one workgroup per CU, each a single pass of MV_ROWS rows per
     // wavefront, so x (or the LayerNorm inputs) is staged once per CU rather
