@@ -44,9 +44,11 @@ BUNDLE_ALG = 2 * Q4_ROW              # 5112 B per neuron (unpadded)
 PRED_BYTES = (RANK * H + FF * RANK) * 4
 # HBM bytes per sparse step from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE over
 # k_pred_hidden + k_tile_up + k_sparse_down, each counter scaled by its reading
-# for a 1 GiB streaming copy (FETCH x2.0, WRITE x1.0); the summary with the
-# commands is profiles/sparse_step_falcon7b_q4_0_hbm_traffic.md.
-SPARSE_STEP_TRAFFIC = 16.50e6
+# for a 1 GiB streaming copy (FETCH x2.0, WRITE x1.0), measured on this bench
+# line (exactly 909 active neurons per step); the summary with the commands is
+# profiles/sparse_step_falcon7b_q4_0_hbm_traffic.md.
+SPARSE_STEP_TRAFFIC = 18.23e6
+SPARSE_STEP_TRAFFIC_ACTIVE = 909
 
 
 def log(msg: str):
@@ -172,6 +174,7 @@ def bench_sparse(args, torch, llg, dev):
                      "kernel": "k_pred_hidden + k_tile_up + k_sparse_down (one decode step)",
                      "achieved": step_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": step_gbs / HBM_PEAK_GBS, "traffic": SPARSE_STEP_TRAFFIC,
+                     "traffic_active_neurons": SPARSE_STEP_TRAFFIC_ACTIVE,
                      "alg_bytes_per_launch": step_alg, "avg_launch_us": ms_step * 1e3},
         "breakdown": {
             "ffn_list_path_us": ffn_ms * 1e3,

@@ -232,7 +232,7 @@ int llg_hipd_ffn_predict_sparse(LlgHipDevice dev, int64_t wup, int64_t wout, int
  * GPU, held until the process ends) instead of the handle's growable
  * workspace, and it calls no hipMalloc, hipFree or hipMemset.  A predictor and
  * bundle whose workspace exceeds the array give LLG_E_SCRATCH (the Falcon-7B
- * layer, rank 128 x d_ff 18176, needs 150 KiB).  Every call on one GPU shares
+ * layer, rank 128 x d_ff 18176, needs 148 KiB).  Every call on one GPU shares
  * the array: calls that overlap on one GPU (from several handles or streams)
  * race; calls ordered on one stream do not. */
 int llg_hipd_ffn_predict_sparse_noalloc(LlgHipDevice dev, int64_t wup, int64_t wout,

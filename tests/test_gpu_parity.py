@@ -550,6 +550,13 @@ def test_window_rejects_duplicates(dev, rng):
 
 # ---------------------------------------------------------------- MoE
 def test_moe_route_bit_exact(dev, rng):
+    """Router ids and weights equal the oracle's to the bit on identical logits
+    (moe_forward.go:43-68, forward.go:463-479), ties and NaN rows included.
+    With 8 experts the tie order (index order) is the reference's: Go's
+    sort.Slice sorts up to 12 elements by stable insertion sort.  The 64-expert
+    case checks the same index-order rule, which is the oracle's; Go's pdqsort
+    order among equal scores for more than 12 experts is not restated, so there
+    the tie order is parity-unpinned."""
     lg = normal(rng, (200, 8), 1.5)
     lg[0] = 0.0                          # all tied
     lg[1] = [0, 1, 1, 1, 0, 0, 0, 0]     # three-way tie for first
@@ -565,7 +572,7 @@ def test_moe_route_bit_exact(dev, rng):
         else:
             assert np.array_equal(w[t].view(np.uint32), rw.view(np.uint32)), t
     lg64 = normal(rng, (50, 64), 2.0)
-    lg64[:, 10] = lg64[:, 40]            # ties across a wide expert set
+    lg64[:, 10] = lg64[:, 40]            # ties across a wide expert set (oracle's rule)
     ids, w = dev.moe_route(lg64, 8)
     for t in range(lg64.shape[0]):
         rid, rw = R.moe_route(lg64[t], 8)
