@@ -21,8 +21,6 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep the compiler from emitting packed fp32 VALU ops.
-# -munsafe-fp-atomics: hardware fp32 atomic add (the accumulation targets are
-# ordinary device memory).
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
@@ -30,7 +28,6 @@ HIP_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-result",
-    "-munsafe-fp-atomics",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE}",
 ]
