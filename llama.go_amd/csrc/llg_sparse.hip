@@ -39,12 +39,6 @@
 #define XS_STRIDE 36      // floats per staged 32-float x block (bank-conflict-free)
 #define BATCH 4           // blocks whose loads a lane issues together
 #define PRED_SPLIT_N 8    // partials per hidden unit written by k_pred_hidden
-// Neurons per k_tile_up workgroup.  64: 128-neuron tiles (one 16-wavefront
-// workgroup per CU for the Falcon-7B layer) took 9.3 against 8.6 us.
-template <int T>
-constexpr int fused_tn() {
-    return 64;
-}
 #define DN_THREADS 512    // k_sparse_down workgroup: one tile (or list stride) per thread
 
 __device__ __forceinline__ void stage_x(float *xs, const float *__restrict__ x, int nb) {
@@ -190,14 +184,13 @@ __device__ __forceinline__ void row_dotn(const uint8_t *__restrict__ base, long 
 }
 
 // One round of the tile's up rows: active neuron k = k0 + wave + nw*i (i <
-// NR) of the tile on this wavefront.  Its pair (row, u) goes to slot k' of
-// its 64-neuron subtile, k' = k less the list index sb[] at which that
-// subtile's neurons start (a zero activation is kept, and k_sparse_down
-// skips it).
+// NR) of the tile on this wavefront.  Its pair (row, u) goes to slot `row`
+// (the pair array is indexed by neuron, so no workgroup needs another's
+// counts; a zero activation is kept, and k_sparse_down skips it).
 template <int T, int NR>
 __device__ __forceinline__ void tile_up_round(const uint8_t *__restrict__ base, long long bstride,
                                               const RowFmt &f, const float *xs, const int *tl,
-                                              const int *sb, int cnt, int k0, int tile0, int act,
+                                              int cnt, int k0, int tile0, int act,
                                               int2 *__restrict__ pairs) {
     const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     int rows[NR];
@@ -213,9 +206,7 @@ __device__ __forceinline__ void tile_up_round(const uint8_t *__restrict__ base, 
 #pragma unroll
         for (int i = 0; i < NR; i++) {
             if (rows[i] < 0) break;
-            const int k = k0 + wave + nw * i;
-            const int slot = (rows[i] >> 6) * 64 + k - sb[(rows[i] - tile0) >> 6];
-            pairs[slot] = make_int2(rows[i], __float_as_int(llg_act(act, s[i])));
+            pairs[rows[i]] = make_int2(rows[i], __float_as_int(llg_act(act, s[i])));
         }
     }
 }
@@ -319,74 +310,70 @@ __device__ __forceinline__ float dn_wave_transpose_sum(const float (&v)[32]) {
     return e + llg_dpp<0xB1>(e);                                           // bit 0
 }
 
-// A. predictor-fused tile kernel over TN = 64 or 128 neurons (TN / 16
-// wavefronts compute the logits, TN / 64 ballots select).  Each 64-neuron
-// subtile s writes its active mask (bit i: neuron 64 s + i) to mask[s] and
-// the (row, u) pair of its k-th active neuron (ascending) to pairs[s*64 + k].
-// The up rows take one wavefront each for up to TN / 8 active neurons (two
-// per wavefront for up to TN / 4), so that most tiles need one round.
-template <int TN>
-constexpr int tile_threads() {
-    return TN == 128 ? 1024 : 512;
-}
-template <int T, int TN>
-__global__ __launch_bounds__(tile_threads<TN>(), TN == 128 ? 1 : 2) void k_tile_up(
+// A. predictor-fused kernel over a tile of TU neurons per workgroup,
+// [TU b, TU (b + 1)).  Wavefront w computes the logits of neurons 16 w ..
+// 16 w + 15 of the tile; wavefront 0 ballots them into the tile's 64-bit mask
+// (mask[b]) and keeps the tile's ascending active list in LDS.  The up rows
+// take one wavefront each for up to 8 active neurons (two per wavefront for
+// up to 16), so that most tiles need one round; the pair (row, u) of neuron n
+// goes to pairs[n].  (Ranges of 71 neurons, one workgroup per CU for d_ff
+// 18176 instead of 284 tiles on 256 CUs, took 8.75 us against 8.73 with the
+// shared mask words stored plainly, and 9.03 us with the atomic OR they need:
+// the cold WOut stream, not the grid's balance, bounds this kernel.)
+#define TU 64           // neurons per tile (one mask word)
+#define TU_MAX TU
+#define TU_THREADS 512
+template <int T>
+__global__ __launch_bounds__(TU_THREADS, 2) void k_tile_up(
     const uint8_t *__restrict__ wout, long long wstride, int ff, int rank,
     const float *__restrict__ partial, const float *__restrict__ bias, float thr,
     const uint8_t *__restrict__ base, long long bstride, RowFmt f, const float *__restrict__ x,
     int act, unsigned long long *__restrict__ mask, int2 *__restrict__ pairs) {
-    constexpr int SUB = TN / 64;
     extern __shared__ float sh[];
     float *xs = sh;                                     // nb * XS_STRIDE
     float *hid = xs + f.nb * XS_STRIDE;                 // rank (16-byte aligned)
-    float *lg = hid + ((rank + 3) & ~3);                // TN
-    int *tl = reinterpret_cast<int *>(lg + TN);         // TN tile-local indices, count
-    int *sb = tl + TN + 1;                              // SUB list starts
+    float *lg = hid + ((rank + 3) & ~3);                // TU_MAX
+    int *tl = reinterpret_cast<int *>(lg + TU_MAX);     // TU_MAX tile-local indices, count
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int tile0 = blockIdx.x * TN;
-    WoutTile t;  // logits: wavefronts 0 .. TN/16 - 1 (16 neurons each)
-    if (wave < TN / 16) load_wout_tile(t, wout, wstride, ff, rank, tile0);  // used after the barrier
+    const int n0 = blockIdx.x * TU, n1 = min(ff, n0 + TU);
+    WoutTile t;  // logits: wavefronts with neurons in the tile
+    const bool lw = wave * 16 < n1 - n0;
+    if (lw) load_wout_tile(t, wout, wstride, n1, rank, n0);  // used after the barrier
     stage_x(xs, x, f.nb);
     load_hidden<PRED_SPLIT_N>(hid, partial, rank);
     __syncthreads();
-    if (wave < TN / 16) finish_logits(t, wout, wstride, ff, rank, tile0, hid, lg);
+    if (lw) finish_logits(t, wout, wstride, n1, rank, n0, hid, lg);
     __syncthreads();
     if (wave == 0) {
-        int k = 0;
-#pragma unroll
-        for (int s = 0; s < SUB; s++) {
-            const int i = tile0 + 64 * s + lane;
-            bool on = false;
-            if (i < ff) {
-                float v = lg[64 * s + lane];
-                if (bias) v += bias[i];  // predictor.go:69-73
-                on = v > thr;            // predictor.go:78
-            }
-            const unsigned long long m = __ballot(on);
-            const int before = __popcll(m & ((1ull << lane) - 1ull));
-            if (on) tl[k + before] = 64 * s + lane;
-            if (lane == 0) {
-                sb[s] = k;
-                if (tile0 + 64 * s < ff) mask[blockIdx.x * SUB + s] = m;
-            }
-            k += __popcll(m);
+        const int i = n0 + lane;
+        bool on = false;
+        if (i < n1) {
+            float v = lg[lane];
+            if (bias) v += bias[i];  // predictor.go:69-73
+            on = v > thr;            // predictor.go:78
         }
-        if (lane == 0) tl[TN] = k;
+        const unsigned long long m = __ballot(on);
+        const int before = __popcll(m & ((1ull << lane) - 1ull));
+        if (on) tl[before] = lane;
+        if (lane == 0) {
+            mask[blockIdx.x] = m;
+            tl[TU_MAX] = __popcll(m);
+        }
     }
     __syncthreads();
-    const int cnt = tl[TN];
+    const int cnt = tl[TU_MAX];
     // up rows of the active neurons, one round of loads for up to 2 * nw
     // (1 or 2 rows per wavefront by count)
     constexpr int UPMAX = T == LLG_TYPE_F32 ? 1 : 2;
-    constexpr int nw = tile_threads<TN>() / 64;
+    constexpr int nw = TU_THREADS / 64;
     if (cnt <= nw || UPMAX == 1) {
         for (int k0 = 0; k0 < cnt; k0 += nw)
-            tile_up_round<T, 1>(base, bstride, f, xs, tl, sb, cnt, k0, tile0, act, pairs);
+            tile_up_round<T, 1>(base, bstride, f, xs, tl, cnt, k0, n0, act, pairs);
     } else {
         if constexpr (UPMAX == 2)
             for (int k0 = 0; k0 < cnt; k0 += 2 * nw)
-                tile_up_round<T, 2>(base, bstride, f, xs, tl, sb, cnt, k0, tile0, act, pairs);
+                tile_up_round<T, 2>(base, bstride, f, xs, tl, cnt, k0, n0, act, pairs);
     }
 }
 
@@ -478,10 +465,11 @@ __device__ __forceinline__ int dn_wave_scan(int v) {
 // Down products.  Pairs come either as a plain list pairs[0..*count) (TILED
 // = false; the count is clamped to `cap`), split evenly over the threads, or
 // from the predictor tiles (TILED = true): tile t's active neurons are the
-// set bits of mask[t], and the pair of its k-th (ascending) is in slot
-// pairs[t*64 + k].  Wavefront w takes tiles 64 w + l (lane l), 64 (w + nw) +
-// l, ...: a wavefront scan of the lanes' popcounts places its tiles' active
-// neurons, as (row, slot), in its own dense list in LDS (DN_WCAP at a time),
+// set bits of mask[t], and the pair of neuron n is pairs[n].  Wavefront w
+// takes tiles w, w + nw, w + 2 nw, ... (lane l: tile l nw + w), so every
+// wavefront gets a share of the pairs: a wavefront scan of the lanes'
+// popcounts places its tiles' active neurons in its own dense list in LDS
+// (DN_WCAP at a time),
 // which its lanes then share; each neuron's u is loaded with its row bytes.
 // No barrier stands between the masks and the row loads.  Workgroup =
 // output block b (32 outputs): out[32 b + e] (+)= sum over the pairs of u *
@@ -511,8 +499,10 @@ __global__ __launch_bounds__(DN_THREADS) void k_sparse_down(
     int n_act = 0;
     if (TILED) {
         int2 *wl = lst[TILED ? wave : 0];
-        for (int t0 = wave * 64; t0 < n_tiles; t0 += nw * 64) {  // uniform per wavefront
-            const int t = t0 + lane;
+        // wavefront w takes tiles w, w + nw, ... (lane l: (p0 + l) * nw + w), so
+        // every wavefront gets a share of the pairs
+        for (int p0 = 0; p0 * nw + wave < n_tiles; p0 += 64) {  // uniform per wavefront
+            const int t = (p0 + lane) * nw + wave;
             const unsigned long long m0 = t < n_tiles ? mask[t] : 0ull;
             const int c = __popcll(m0);
             const int incl = dn_wave_scan(c);
@@ -524,8 +514,10 @@ __global__ __launch_bounds__(DN_THREADS) void k_sparse_down(
                     unsigned long long m = m0;
                     for (int k = 0; m; k++, m &= m - 1) {
                         const int g = off + k - cb;
-                        if (g >= 0 && g < DN_WCAP)
-                            wl[g] = make_int2(t * 64 + __ffsll((long long)m) - 1, t * 64 + k);
+                        if (g >= 0 && g < DN_WCAP) {
+                            const int row = t * 64 + __ffsll((long long)m) - 1;
+                            wl[g] = make_int2(row, row);  // the pair of neuron n is pairs[n]
+                        }
                     }
                 }
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -652,18 +644,17 @@ size_t llg_fused_ws_bytes(int rank, int ff) {
 }
 
 template <int T>
-static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial, const float *bias,
-                         float thr, LlgObject *b, const float *x, int act,
+static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial,
+                         const float *bias, float thr, LlgObject *b, const float *x, int act,
                          unsigned long long *mask, int2 *pairs, int32_t *n_active, float *out,
                          bool accumulate) {
     const int ff = wout->rows, rank = wout->fmt.cols;
     const int n_tiles = (ff + 63) / 64;
     const RowFmt &f = b->fmt;
-    constexpr int TN = fused_tn<T>();
-    const size_t lds = xs_bytes(f) + (size_t)(((rank + 3) & ~3) + TN + TN + 1 + TN / 64) * 4;
-    hipLaunchKernelGGL((k_tile_up<T, TN>), dim3((ff + TN - 1) / TN), dim3(tile_threads<TN>()), lds,
-                       st, wout->d, wout->stride, ff, rank, partial, bias, thr, b->d, b->stride, f,
-                       x, act, mask, pairs);
+    const size_t lds = xs_bytes(f) + (size_t)(((rank + 3) & ~3) + TU_MAX + TU_MAX + 1) * 4;
+    hipLaunchKernelGGL((k_tile_up<T>), dim3(n_tiles), dim3(TU_THREADS), lds, st, wout->d,
+                       wout->stride, ff, rank, partial, bias, thr, b->d, b->stride, f, x, act,
+                       mask, pairs);
     const int px = down_per_xcd(f);
     if (accumulate)
         hipLaunchKernelGGL((k_sparse_down<T, true, true>), dim3(8 * px), dim3(DN_THREADS), 0, st,
