@@ -25,6 +25,8 @@
 // fragment feeds 4 MFMAs.  A in K chunks of 128 staged in LDS (double
 // buffered; the next chunk is loaded into registers while the current one is
 // multiplied); B straight into registers, one chunk ahead.
+#include <type_traits>
+
 #include "llg_common.hpp"
 #include "llg_internal.hpp"
 
@@ -187,11 +189,18 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
 
-    // A: 64 rows x 16 uint4 per chunk -> 4 per thread (rows past the tile
-    // reload the tile's last row; their results are dropped).
+    // The tile's rows take NMS = ceil(nrows / 16) of the four 16-row MFMA
+    // groups; the body is instantiated per NMS and chosen once per workgroup,
+    // so a ragged tile issues no MFMAs, A loads or stores for its empty groups
+    // and each instance stays straight-line code.
+    auto body = [&](auto nms_c) __attribute__((always_inline)) {
+    constexpr int NMS = decltype(nms_c)::value;
+    // A: 64 rows x 16 uint4 per chunk -> thread load q covers rows 16 q ..
+    // 16 q + 15, so only q < NMS are needed (rows past the tile reload the
+    // tile's last row; their results are dropped).
     long long a_off[4];
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
+    for (int q = 0; q < NMS; q++) {
         const int idx = tid + 256 * q;
         const int r = idx >> 4, part = idx & 15;
         const int rr = min(r, nrows - 1);
@@ -215,7 +224,7 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
     u32x4_t bq[NB][NF];
     uint32_t bd[NB][NF];
 #define GM_LOAD_A(c)                                                                             \
-    _Pragma("unroll") for (int q = 0; q < 4; q++) ra[q] =                                       \
+    _Pragma("unroll") for (int q = 0; q < NMS; q++) ra[q] =                                     \
         *reinterpret_cast<const u32x4_t *>(A + a_off[q] + (long long)(c) * GM_KC)
 #define GM_LOAD_B(c, slot)                                                                       \
     _Pragma("unroll") for (int f = 0; f < NF; f++) {                                             \
@@ -224,16 +233,16 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
         bd[slot][f] = *reinterpret_cast<const unsigned short *>(brow[f] + d_off + blk * 2);      \
     }
 #define GM_STORE_A(buf)                                                                          \
-    _Pragma("unroll") for (int q = 0; q < 4; q++) {                                             \
+    _Pragma("unroll") for (int q = 0; q < NMS; q++) {                                           \
         const int idx = tid + 256 * q;                                                           \
         *reinterpret_cast<u32x4_t *>(&As[buf][(idx >> 4) * GM_AST + (idx & 15) * 8]) = ra[q];    \
     }
 
-    floatx4_t acc[NF][4];  // [fragment][16-row group]
+    floatx4_t acc[NF][NMS];  // [fragment][16-row group]
 #pragma unroll
     for (int f = 0; f < NF; f++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[f][i] = {0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < NMS; i++) acc[f][i] = {0.f, 0.f, 0.f, 0.f};
 
     const int ncs = K / GM_KC / ksplit;  // chunks of this slice: c0 .. ce - 1
     const int c0 = ks * ncs, ce = c0 + ncs;
@@ -250,9 +259,9 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
         GM_LOAD_B(min(c + GM_BD, ce - 1), (slot + GM_BD) % NB);
 #pragma unroll
         for (int s = 0; s < 4; s++) {
-            half8_t a[4];
+            half8_t a[NMS];
 #pragma unroll
-            for (int ms = 0; ms < 4; ms++)
+            for (int ms = 0; ms < NMS; ms++)
                 a[ms] = *reinterpret_cast<const half8_t *>(
                     &As[buf][(ms * 16 + li) * GM_AST + s * 32 + lg * 8]);
 #pragma unroll
@@ -261,7 +270,7 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
                 const half8_t b =
                     q4_frag(w, __builtin_bit_cast(_Float16, (unsigned short)bd[slot][f]));
 #pragma unroll
-                for (int ms = 0; ms < 4; ms++)
+                for (int ms = 0; ms < NMS; ms++)
                     acc[f][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ms], b, acc[f][ms], 0, 0, 0);
             }
         }
@@ -280,7 +289,7 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
     // epilogue: gate/up pairs fragment ns (gate) with ns + 2 (up)
     constexpr int NS = MODE == 0 ? 2 : 4;  // 16-column groups per wavefront
 #pragma unroll
-    for (int ms = 0; ms < 4; ms++)
+    for (int ms = 0; ms < NMS; ms++)
 #pragma unroll
         for (int ns = 0; ns < NS; ns++) {
             const int n = n0 + wave * WC + ns * 16 + li;
@@ -298,6 +307,13 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
                 }
             }
         }
+    };
+    switch ((nrows + 15) / 16) {
+    case 1: body(std::integral_constant<int, 1>{}); break;
+    case 2: body(std::integral_constant<int, 2>{}); break;
+    case 3: body(std::integral_constant<int, 3>{}); break;
+    default: body(std::integral_constant<int, 4>{}); break;
+    }
 }
 
 // out[t][d] = sum_s w[t][s] * Y[pair_row[t*k+s]][d], summed from 0 in slot order;

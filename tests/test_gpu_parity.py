@@ -788,6 +788,28 @@ def test_falcon_wide_heads_chunked_wo(dev, rng):
     m.release()
 
 
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0])
+def test_falcon_balanced_matvecs_and_fold(dev, rng, t):
+    """Hidden 2048 with 32 heads of 64: QKV (2176 rows) and Wo (2048 rows) take
+    the one-workgroup-per-CU matvec, the LayerNorm prologue with two float4
+    groups per thread, and Wo the predictor fold (P = WUp . Wo at load, the
+    hidden partials computed beside Wo . attn); against the oracle's
+    WUp . (Wo . attn) at every position, Q4_0 and Q8_0."""
+    d = dict(FALCON_GPU, hidden=2048, n_heads=32, n_kv=2, head_dim=64, ff=4096, rank=32,
+             max_seq=16)
+    w = make_falcon(rng, d, t, std=0.02)
+    toks = rng.integers(0, d["vocab"], 12)
+    _, nact, thr = ref_falcon_f64(w, d, toks, t=t)
+    ref = R.Falcon(d, w, thr, t)
+    m = llg.FalconModel(dev, d, w, thr, t=t)
+    for s, tk in enumerate(toks):
+        lg, _, na = m.forward(int(tk), s)
+        rl, rn = ref.forward(int(tk), s)
+        assert np.array_equal(na, rn) and np.array_equal(na, nact[s]), (s, na, rn)
+        assert max_rel_err(lg, rl) <= TOL, s
+    m.release()
+
+
 def test_released_weights_stay_alive_for_their_model(dev, rng):
     """Every weight handle released before the model: the model still reads
     them (the handles are retired, the memory is kept until the model goes)."""
