@@ -836,7 +836,7 @@ void *llg_ws(LlgDevice *d, size_t bytes, int *rc);
 // The device address of this GPU's fixed scratch array (allocation-free entry
 // points), or null with *rc set when `bytes` exceeds LLG_SCRATCH_BYTES
 // (LLG_E_SCRATCH) or the address lookup at init failed.
-#define LLG_SCRATCH_BYTES (512 * 1024)
+#define LLG_SCRATCH_BYTES (8 * 1024 * 1024)
 uint8_t *llg_dev_scratch(LlgDevice *d, size_t bytes, int *rc);
 // Copy host -> device workspace slot / device -> host, on the stream.
 int llg_h2d(LlgDevice *d, void *dst, const void *src, size_t bytes);

@@ -547,7 +547,7 @@ int llg_hipd_ffn_predict_sparse(LlgHipDevice h, int64_t hwup, int64_t hwout, int
     int rc = check_fused(d, hwup, hwout, hbias, hb, &wup, &wout, &bias, &b);
     if (rc) return rc;
     if (!d_a || !d_x || !d_out) return llg_set_error(d, LLG_E_ARG, "predict_sparse: null pointer");
-    uint8_t *ws = (uint8_t *)llg_ws(d, llg_fused_ws_bytes(wup->rows, wout->rows), &rc);
+    uint8_t *ws = (uint8_t *)llg_ws(d, llg_fused_ws_bytes(wup->rows, wout->rows, b->fmt.nb), &rc);
     if (rc) return rc;
     return llg_fused_enqueue(d, wup, wout, bias, b, d_a, d_x, thr, act, d_out, d_active,
                              d_n_active, ws);
@@ -566,7 +566,7 @@ int llg_hipd_ffn_predict_sparse_noalloc(LlgHipDevice h, int64_t hwup, int64_t hw
     int rc = check_fused(d, hwup, hwout, hbias, hb, &wup, &wout, &bias, &b);
     if (rc) return rc;
     if (!d_a || !d_x || !d_out) return llg_set_error(d, LLG_E_ARG, "predict_sparse: null pointer");
-    uint8_t *ws = llg_dev_scratch(d, llg_fused_ws_bytes(wup->rows, wout->rows), &rc);
+    uint8_t *ws = llg_dev_scratch(d, llg_fused_ws_bytes(wup->rows, wout->rows, b->fmt.nb), &rc);
     if (!ws) return rc;
     return llg_fused_enqueue(d, wup, wout, bias, b, d_a, d_x, thr, act, d_out, d_active,
                              d_n_active, ws);
@@ -588,7 +588,7 @@ int llg_hip_ffn_predict_sparse(LlgHipDevice h, int64_t hwup, int64_t hwout, int6
     const long long o_act = o_out + llg_align((long long)hd * 4, 256);
     const long long o_n = o_act + llg_align((long long)ff * 4, 256);
     const long long o_ws = o_n + 256;
-    uint8_t *ws = (uint8_t *)llg_ws(d, o_ws + llg_fused_ws_bytes(wup->rows, ff), &rc);
+    uint8_t *ws = (uint8_t *)llg_ws(d, o_ws + llg_fused_ws_bytes(wup->rows, ff, b->fmt.nb), &rc);
     if (rc) return rc;
     if ((rc = llg_h2d(d, ws + o_a, a, (size_t)hd * 4))) return rc;
     if ((rc = llg_h2d(d, ws + o_x, x, (size_t)hd * 4))) return rc;

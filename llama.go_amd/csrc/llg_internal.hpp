@@ -80,13 +80,14 @@ int llg_matvec_attn_enqueue(LlgDevice *d, const LlgObject *w, const LlgAttnParts
 int llg_matvec_ln_enqueue(LlgDevice *d, const LlgObject *w, const LlgLnArgs &ln, float *d_y);
 
 // Predictor-fused sparse FFN (ffnFlash path 2) (llg_sparse.hip).
-size_t llg_fused_ws_bytes(int rank, int ff);
+// nb: 32-element blocks of the bundle rows (the tiles' partial outputs).
+size_t llg_fused_ws_bytes(int rank, int ff, int nb);
 int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
                       LlgObject *b, const float *d_a, const float *d_x, float thr, int act,
                       float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws,
                       const float *d_out_add = nullptr);
 // The same after the hidden partials are in ws (llg_pred_ws_layout): the
-// tile kernel and the down kernel; accumulate: d_out += the FFN output.
+// tile kernel and the partial-sum kernel; accumulate: d_out += the FFN output.
 int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgObject *b,
                            const float *d_x, float thr, int act, float *d_out,
                            int32_t *d_active, int32_t *d_n_active, uint8_t *ws, bool accumulate);

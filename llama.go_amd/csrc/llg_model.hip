@@ -494,7 +494,8 @@ static LlgModel *get_model(LlgDevice *d, int64_t h) {
 }
 
 static size_t model_ws_bytes(const LlgModel &m) {
-    return std::max(llg_fused_ws_bytes(m.rank, m.ff), (size_t)llg_predict_ws_bytes(m.rank, m.ff));
+    return std::max(llg_fused_ws_bytes(m.rank, m.ff, (m.hidden + 31) / 32),
+                    (size_t)llg_predict_ws_bytes(m.rank, m.ff));
 }
 
 // Rows per attention workgroup above which a head's rows are split further:

@@ -6,32 +6,33 @@
 //  A. predictor-fused step (ffnFlash path 2, ffn_flash.go:225-231), 3 launches:
 //     K1 k_pred_hidden (llg_predictor.hip): hidden partials (and x += attn_out
 //        for a caller that accumulates into a residual)
-//     K2 k_tile_up: one workgroup per 64-neuron tile: logits from WOut rows,
-//        strict '>' against the threshold via a wavefront ballot, then the up
-//        dot product of each of the tile's active neurons, u = act(up . x),
-//        one neuron per wavefront of 8 (two when more than 8 are active);
-//        active neuron k of the tile (ascending) goes to the tile's pair
-//        slot k, so no two workgroups touch one address and the slot order
-//        is fixed
-//     K3 k_sparse_down over the tiles' pairs
+//     K2 k_tile_ffn: one workgroup per two 64-neuron tiles (Q4_0/Q8_0; one
+//        tile for F16/F32): logits from WOut rows, strict '>' against the
+//        threshold via a wavefront ballot (one mask word per tile), then each
+//        active neuron's up row (u = act(up . x)) and, in the same round of
+//        loads, its down row (the two rows are one contiguous bundle); the
+//        workgroup's partial output, sum of u * down over its active neurons
+//        in ascending order, goes to its own row of `part`
+//     K3 k_tile_reduce: out = sum of the partial rows in row order
 //  B. explicit active list (ffnSparseLoad, NeuronCache.FFNForward), 2 launches:
 //     k_list_up: one wavefront per listed neuron, pair j = (row, u_j)
-//     K3 k_sparse_down
+//     k_sparse_down: one workgroup per output block of 32 outputs reads every
+//        pair (each thread a stride of the list)
+//
+// No output is summed with atomics, and every sum has a fixed order, so the
+// results are bit-identical from run to run.  u == 0 rows are skipped as at
+// ffn_flash.go:290.
 //
 // x is staged once per workgroup in LDS with a 36-float stride per 32-float
 // block, so the 16-byte reads of 16 consecutive lanes (one block each) hit
 // 64 distinct banks.  Every lane issues the loads of all its blocks before it
 // uses any of them.
 //
-// k_sparse_down: one workgroup per output block of 32 outputs reads every
-// pair (thread = tile, or a stride of the list), so no output is summed
-// across workgroups: no atomics, and the summation order is fixed (each
-// thread adds its pairs in slot order, then a fixed shuffle/DPP transpose
-// reduction per wavefront and an ordered sum over the wavefronts).  Results
-// are bit-identical from run to run.  u == 0 rows are skipped as at
-// ffn_flash.go:290.  blockIdx -> block keeps neighbouring blocks (which
-// share the rows' cache lines) on one XCD (workgroups go round-robin over
-// the 8 XCDs).
+// k_sparse_down: each thread adds its pairs in list order, then a fixed
+// shuffle/DPP transpose reduction per wavefront and an ordered sum over the
+// wavefronts finish the block.  blockIdx -> block keeps neighbouring blocks
+// (which share the rows' cache lines) on one XCD (workgroups go round-robin
+// over the 8 XCDs).
 #include "llg_common.hpp"
 #include "llg_internal.hpp"
 #include "llg_pred_tile.hpp"
@@ -183,34 +184,6 @@ __device__ __forceinline__ void row_dotn(const uint8_t *__restrict__ base, long 
     for (int q = 0; q < NR; q++) s[q] = llg_wave_sum(s[q]);
 }
 
-// One round of the tile's up rows: active neuron k = k0 + wave + nw*i (i <
-// NR) of the tile on this wavefront.  Its pair (row, u) goes to slot `row`
-// (the pair array is indexed by neuron, so no workgroup needs another's
-// counts; a zero activation is kept, and k_sparse_down skips it).
-template <int T, int NR>
-__device__ __forceinline__ void tile_up_round(const uint8_t *__restrict__ base, long long bstride,
-                                              const RowFmt &f, const float *xs, const int *tl,
-                                              int cnt, int k0, int tile0, int act,
-                                              int2 *__restrict__ pairs) {
-    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    int rows[NR];
-#pragma unroll
-    for (int i = 0; i < NR; i++) {
-        const int k = k0 + wave + nw * i;
-        rows[i] = k < cnt ? tile0 + tl[k] : -1;
-    }
-    if (rows[0] < 0) return;  // wavefront-uniform: nothing in this round
-    float s[NR];
-    row_dotn<T, NR, NR == 1 ? 4 : 3>(base, bstride, rows, f, xs, s);
-    if ((threadIdx.x & 63) == 0) {
-#pragma unroll
-        for (int i = 0; i < NR; i++) {
-            if (rows[i] < 0) break;
-            pairs[rows[i]] = make_int2(rows[i], __float_as_int(llg_act(act, s[i])));
-        }
-    }
-}
-
 // B. explicit list: pair j = (row of active[j], act(up . x)).
 // With src (windowed rows): a neuron n with fresh[n] == epoch (loaded by this
 // token's update) is read from row n of src, and its whole bundle is copied
@@ -310,33 +283,186 @@ __device__ __forceinline__ float dn_wave_transpose_sum(const float (&v)[32]) {
     return e + llg_dpp<0xB1>(e);                                           // bit 0
 }
 
-// A. predictor-fused kernel over a tile of TU neurons per workgroup,
-// [TU b, TU (b + 1)).  Wavefront w computes the logits of neurons 16 w ..
-// 16 w + 15 of the tile; wavefront 0 ballots them into the tile's 64-bit mask
-// (mask[b]) and keeps the tile's ascending active list in LDS.  The up rows
-// take one wavefront each for up to 8 active neurons (two per wavefront for
-// up to 16), so that most tiles need one round; the pair (row, u) of neuron n
-// goes to pairs[n].  (Ranges of 71 neurons, one workgroup per CU for d_ff
-// 18176 instead of 284 tiles on 256 CUs, took 8.75 us against 8.73 with the
-// shared mask words stored plainly, and 9.03 us with the atomic OR they need:
-// the cold WOut stream, not the grid's balance, bounds this kernel.)
-#define TU 64           // neurons per tile (one mask word)
-#define TU_MAX TU
-#define TU_THREADS 512
+#define TU 64  // neurons per predictor tile (one mask word)
+
+// One round of the tile's up rows with the activations kept in LDS, over the
+// first nw wavefronts: active neuron k = k0 + wave + nw*i (i < NR) of the
+// tile on this wavefront, ul[k] = act(up . x).
+template <int T, int NR>
+__device__ __forceinline__ void tile_u_round(const uint8_t *__restrict__ base, long long bstride,
+                                             const RowFmt &f, const float *xs, const int *tl,
+                                             int cnt, int k0, int tile0, int act, float *ul,
+                                             int nw) {
+    const int wave = threadIdx.x >> 6;
+    int rows[NR];
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+        const int k = k0 + wave + nw * i;
+        rows[i] = k < cnt ? tile0 + tl[k] : -1;
+    }
+    if (rows[0] < 0) return;  // wavefront-uniform: nothing in this round
+    float s[NR];
+    row_dotn<T, NR, NR == 1 ? 4 : 3>(base, bstride, rows, f, xs, s);
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int i = 0; i < NR; i++)
+            if (rows[i] >= 0) ul[k0 + wave + nw * i] = llg_act(act, s[i]);
+    }
+}
+
+// Half of a 32-element block of a row in the row format: the bytes of
+// elements [16 h, 16 h + 16) of block b, and the block scale (Q4_0: words
+// 2h, 2h + 1 of the block's nibbles; Q8_0: bytes 16h..16h+15; F16/F32: 16
+// values).
 template <int T>
-__global__ __launch_bounds__(TU_THREADS, 2) void k_tile_up(
+struct HalfRaw;
+template <>
+struct HalfRaw<LLG_TYPE_Q4_0> {
+    uint2 q;
+    unsigned short d;
+};
+template <>
+struct HalfRaw<LLG_TYPE_Q8_0> {
+    uint4 q;
+    unsigned short d;
+};
+template <>
+struct HalfRaw<LLG_TYPE_F16> {
+    uint4 q[2];
+};
+template <>
+struct HalfRaw<LLG_TYPE_F32> {
+    float4 q[4];
+};
+
+template <int T>
+__device__ __forceinline__ void half_load(HalfRaw<T> &r, const uint8_t *__restrict__ row,
+                                          const RowFmt &f, int b, int h) {
+    if constexpr (T == LLG_TYPE_Q4_0) {
+        r.q = *reinterpret_cast<const uint2 *>(row + (size_t)b * 16 + h * 8);
+        r.d = *reinterpret_cast<const unsigned short *>(row + f.d_off + b * 2);
+    } else if constexpr (T == LLG_TYPE_Q8_0) {
+        r.q = *reinterpret_cast<const uint4 *>(row + (size_t)b * 32 + h * 16);
+        r.d = *reinterpret_cast<const unsigned short *>(row + f.d_off + b * 2);
+    } else if constexpr (T == LLG_TYPE_F16) {
+        const uint4 *p = reinterpret_cast<const uint4 *>(row + (size_t)b * 64 + h * 32);
+        r.q[0] = p[0];
+        r.q[1] = p[1];
+    } else {
+        const float4 *p = reinterpret_cast<const float4 *>(row + (size_t)b * 128 + h * 64);
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.q[i] = p[i];
+    }
+}
+
+// acc[0..15] += u * dequant(half block), with the quantized types' offset
+// folded into *corr (the caller subtracts corr from every element once):
+// Q4_0 adds u d (64 + q) (a nibble under the f16 exponent bits 0x5400 is
+// exactly 64 + q, multiplied into fp32 by v_fma_mix) and corr 72 u d; Q8_0
+// adds u d (q + 128) and corr 128 u d.
+template <int T>
+__device__ __forceinline__ void half_axpy(const HalfRaw<T> &r, float u, float (&acc)[16],
+                                          float &corr) {
+    if constexpr (T == LLG_TYPE_Q4_0) {
+        const float s = u * llg_f16(r.d);
+        corr += 72.0f * s;
+        const uint32_t w[2] = {r.q.x, r.q.y};
+        const uint32_t m = 0x00F000F0u, e = 0x54005400u;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {  // nibble p of word i is element 8 i + p
+            const half2_llg p0 = __builtin_bit_cast(half2_llg, llg_and_or(w[i] << 4, m, e));
+            const half2_llg p1 = __builtin_bit_cast(half2_llg, llg_and_or(w[i], m, e));
+            const half2_llg p2 = __builtin_bit_cast(half2_llg, llg_and_or(w[i] >> 4, m, e));
+            const half2_llg p3 = __builtin_bit_cast(half2_llg, llg_and_or(w[i] >> 8, m, e));
+            acc[8 * i + 0] = __builtin_fmaf((float)p0[0], s, acc[8 * i + 0]);
+            acc[8 * i + 1] = __builtin_fmaf((float)p1[0], s, acc[8 * i + 1]);
+            acc[8 * i + 2] = __builtin_fmaf((float)p2[0], s, acc[8 * i + 2]);
+            acc[8 * i + 3] = __builtin_fmaf((float)p3[0], s, acc[8 * i + 3]);
+            acc[8 * i + 4] = __builtin_fmaf((float)p0[1], s, acc[8 * i + 4]);
+            acc[8 * i + 5] = __builtin_fmaf((float)p1[1], s, acc[8 * i + 5]);
+            acc[8 * i + 6] = __builtin_fmaf((float)p2[1], s, acc[8 * i + 6]);
+            acc[8 * i + 7] = __builtin_fmaf((float)p3[1], s, acc[8 * i + 7]);
+        }
+    } else if constexpr (T == LLG_TYPE_Q8_0) {
+        const float s = u * llg_f16(r.d);
+        corr += 128.0f * s;
+        const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t v = w[i] ^ 0x80808080u;
+#pragma unroll
+            for (int k = 0; k < 4; k++) acc[4 * i + k] += s * (float)((v >> (8 * k)) & 0xFF);
+        }
+    } else if constexpr (T == LLG_TYPE_F16) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t w[4] = {r.q[i].x, r.q[i].y, r.q[i].z, r.q[i].w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                acc[8 * i + 2 * k] += u * llg_f16(w[k] & 0xFFFF);
+                acc[8 * i + 2 * k + 1] += u * llg_f16(w[k] >> 16);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            acc[4 * i + 0] += u * r.q[i].x;
+            acc[4 * i + 1] += u * r.q[i].y;
+            acc[4 * i + 2] += u * r.q[i].z;
+            acc[4 * i + 3] += u * r.q[i].w;
+        }
+    }
+}
+
+// 64-neuron tiles per k_tile_ffn workgroup, and its threads: the quantized
+// types take two tiles on 1024 threads (one workgroup per CU, 128 registers),
+// F16/F32 rows need more registers and take one tile on 512 threads.
+template <int T>
+constexpr int tf_tiles() {
+    return T == LLG_TYPE_Q4_0 || T == LLG_TYPE_Q8_0 ? 2 : 1;
+}
+template <int T>
+constexpr int tf_threads() {
+    return 512 * tf_tiles<T>();
+}
+// Down rows a k_tile_ffn thread holds at once (half blocks), by type.
+template <int T>
+constexpr int tf_dk() {
+    return T == LLG_TYPE_Q4_0 ? 16 : (T == LLG_TYPE_Q8_0 ? 8 : (T == LLG_TYPE_F16 ? 4 : 2));
+}
+
+// A'. The predictor-fused tiles with their down products (the form the step
+// uses): a workgroup owns tf_tiles 64-neuron tiles (WOut rows: 16 per
+// wavefront; the ballot writes one mask word per tile and the workgroup's
+// ascending active list), then
+//   - the top ceil(2 nb / 64) wavefronts (at most half of them) own the
+//     output half blocks (16 outputs) of the tile's partial; right after the
+//     ballot each of their threads requests its first half block of the down
+//     row of each active neuron (up to tf_dk at once), so the down bytes
+//     arrive in the round of the up rows (a neuron's up and down rows are one
+//     contiguous bundle);
+//   - the other wavefronts take the up rows: ul[k] = act(up . x) in LDS;
+//   - part[w][o] = sum over the workgroup's active neurons, ascending, of
+//     u * down[o] (a zero u is skipped, ffn_flash.go:290).
+// Every tile writes its partial (zeros when nothing is active), and
+// k_tile_reduce adds the tiles' partials in tile order, so the result is the
+// same on every run.
+template <int T>
+__global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile_ffn(
     const uint8_t *__restrict__ wout, long long wstride, int ff, int rank,
     const float *__restrict__ partial, const float *__restrict__ bias, float thr,
     const uint8_t *__restrict__ base, long long bstride, RowFmt f, const float *__restrict__ x,
-    int act, unsigned long long *__restrict__ mask, int2 *__restrict__ pairs) {
+    int act, unsigned long long *__restrict__ mask, float *__restrict__ part, int pstride) {
     extern __shared__ float sh[];
     float *xs = sh;                                     // nb * XS_STRIDE
     float *hid = xs + f.nb * XS_STRIDE;                 // rank (16-byte aligned)
-    float *lg = hid + ((rank + 3) & ~3);                // TU_MAX
-    int *tl = reinterpret_cast<int *>(lg + TU_MAX);     // TU_MAX tile-local indices, count
+    constexpr int TW = tf_tiles<T>(), NT = TW * TU, NTH = tf_threads<T>();
+    float *lg = hid + ((rank + 3) & ~3);                // NT
+    int *tl = reinterpret_cast<int *>(lg + NT);         // NT workgroup-local indices, count
+    float *ul = reinterpret_cast<float *>(tl + NT + 1);  // NT activations
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n0 = blockIdx.x * TU, n1 = min(ff, n0 + TU);
+    const int n0 = blockIdx.x * NT, n1 = min(ff, n0 + NT);
     WoutTile t;  // logits: wavefronts with neurons in the tile
     const bool lw = wave * 16 < n1 - n0;
     if (lw) load_wout_tile(t, wout, wstride, n1, rank, n0);  // used after the barrier
@@ -346,35 +472,175 @@ __global__ __launch_bounds__(TU_THREADS, 2) void k_tile_up(
     if (lw) finish_logits(t, wout, wstride, n1, rank, n0, hid, lg);
     __syncthreads();
     if (wave == 0) {
-        const int i = n0 + lane;
-        bool on = false;
-        if (i < n1) {
-            float v = lg[lane];
-            if (bias) v += bias[i];  // predictor.go:69-73
-            on = v > thr;            // predictor.go:78
+        int c = 0;
+#pragma unroll
+        for (int w = 0; w < TW; w++) {
+            const int i = n0 + TU * w + lane;
+            bool on = false;
+            if (i < n1) {
+                float v = lg[TU * w + lane];
+                if (bias) v += bias[i];  // predictor.go:69-73
+                on = v > thr;            // predictor.go:78
+            }
+            const unsigned long long m = __ballot(on);
+            const int before = __popcll(m & ((1ull << lane) - 1ull));
+            if (on) tl[c + before] = TU * w + lane;
+            if (lane == 0 && n0 + TU * w < n1) mask[blockIdx.x * TW + w] = m;
+            c += __popcll(m);
         }
-        const unsigned long long m = __ballot(on);
-        const int before = __popcll(m & ((1ull << lane) - 1ull));
-        if (on) tl[before] = lane;
-        if (lane == 0) {
-            mask[blockIdx.x] = m;
-            tl[TU_MAX] = __popcll(m);
+        if (lane == 0) tl[NT] = c;
+    }
+    __syncthreads();
+    const int cnt = tl[NT];
+    // The top n_dw wavefronts own the down half blocks: thread j of them (j =
+    // tid - 64 n_uw) takes half blocks i = j, j + 64 n_dw, ... (block i / 2,
+    // half i % 2); the other n_uw wavefronts take the up rows.  The two roles
+    // are branches of one if, so their registers are not live at the same
+    // time.
+    constexpr int DK = tf_dk<T>();
+    const int n_half = 2 * f.nb;
+    const int n_dw = min((n_half + 63) / 64, NTH / 128);
+    const int n_uw = NTH / 64 - n_dw;
+    const int j = (int)threadIdx.x - 64 * n_uw;
+    const int dstep = 64 * n_dw;
+    const uint8_t *dbase = base + f.stride;  // down row of neuron n: dbase + n * bstride
+    HalfRaw<T> dr[DK];
+    // lane q of a down wavefront holds active neuron k0 + q's workgroup-local
+    // index (one LDS read per round; each row index is then a readlane)
+    int trow = lane < cnt ? tl[lane] : 0;
+    if (wave >= n_uw) {
+        // the first half block's down bytes of the first DK active neurons, so
+        // that they arrive in the round of the up rows (address clamped for
+        // the lanes past the last half block)
+        const int ic = min(j, n_half - 1);
+#pragma unroll
+        for (int k = 0; k < DK; k++) {
+            if (k < cnt) {
+                const int n = n0 + __builtin_amdgcn_readlane(trow, k);
+                half_load<T>(dr[k], dbase + (long long)n * bstride, f, ic >> 1, ic & 1);
+            }
+        }
+    } else {
+        constexpr int UPMAX = T == LLG_TYPE_F32 ? 1 : 2;
+        if (cnt <= n_uw || UPMAX == 1) {
+            for (int k0 = 0; k0 < cnt; k0 += n_uw)
+                tile_u_round<T, 1>(base, bstride, f, xs, tl, cnt, k0, n0, act, ul, n_uw);
+        } else {
+            if constexpr (UPMAX == 2)
+                for (int k0 = 0; k0 < cnt; k0 += 2 * n_uw)
+                    tile_u_round<T, 2>(base, bstride, f, xs, tl, cnt, k0, n0, act, ul, n_uw);
         }
     }
     __syncthreads();
-    const int cnt = tl[TU_MAX];
-    // up rows of the active neurons, one round of loads for up to 2 * nw
-    // (1 or 2 rows per wavefront by count)
-    constexpr int UPMAX = T == LLG_TYPE_F32 ? 1 : 2;
-    constexpr int nw = TU_THREADS / 64;
-    if (cnt <= nw || UPMAX == 1) {
-        for (int k0 = 0; k0 < cnt; k0 += nw)
-            tile_up_round<T, 1>(base, bstride, f, xs, tl, cnt, k0, n0, act, pairs);
-    } else {
-        if constexpr (UPMAX == 2)
-            for (int k0 = 0; k0 < cnt; k0 += 2 * nw)
-                tile_up_round<T, 2>(base, bstride, f, xs, tl, cnt, k0, n0, act, pairs);
+    if (wave < n_uw) return;  // uniform per wavefront (no barrier follows)
+    for (int i = j; i - j < n_half; i += dstep) {  // uniform bound: every lane runs each pass
+        const int ic = min(i, n_half - 1);
+        float acc[16];
+        float corr = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[e] = 0.0f;
+        for (int k0 = 0; k0 < cnt; k0 += DK) {
+            // activations of this round's neurons, one LDS read (lane q: k0 + q)
+            const float uq = k0 + lane < cnt ? ul[k0 + lane] : 0.0f;
+            if (k0 > 0 || i != j) {  // later rounds (the first is in flight already)
+                trow = k0 + lane < cnt ? tl[k0 + lane] : 0;
+#pragma unroll
+                for (int k = 0; k < DK; k++) {
+                    if (k0 + k < cnt) {
+                        const int n = n0 + __builtin_amdgcn_readlane(trow, k);
+                        half_load<T>(dr[k], dbase + (long long)n * bstride, f, ic >> 1, ic & 1);
+                    }
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < DK; k++) {
+                if (k0 + k < cnt) {
+                    const float u = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(uq), k));
+                    if (u != 0.0f) half_axpy<T>(dr[k], u, acc, corr);
+                }
+            }
+        }
+        if (i < n_half) {
+            float4 *o4 = reinterpret_cast<float4 *>(part + (long long)blockIdx.x * pstride + i * 16);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                o4[e] = make_float4(acc[4 * e] - corr, acc[4 * e + 1] - corr,
+                                    acc[4 * e + 2] - corr, acc[4 * e + 3] - corr);
+        }
     }
+}
+
+// out[32 b + e] (+)= sum over the partial rows t < n_parts of part[t][32 b +
+// e].  Workgroup b (256 threads): thread (g, c) sums the float4 column c of
+// the block over rows g, g + 32, g + 64, ... in that order (all loads of a
+// batch issued together), then the 32 group sums are added pairwise in a
+// fixed tree, so the order is the same on every run.  With ACC the sum is
+// added to out (a residual), else stored.  Workgroup 0 also writes the number
+// of active neurons (the popcounts of the tile masks).
+#define TR_GROUPS 32
+#define TR_BATCH 5
+template <bool ACC>
+__global__ __launch_bounds__(256) void k_tile_reduce(const float *__restrict__ part, int pstride,
+                                                     int n_parts, int n_tiles, int cols,
+                                                     const unsigned long long *__restrict__ mask,
+                                                     int32_t *__restrict__ n_active_out,
+                                                     float *__restrict__ out) {
+    __shared__ float4 red[TR_GROUPS][8];
+    __shared__ int cnt[4];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const int c = tid & 7, g = tid >> 3;
+    const int o = b * 32 + 4 * c;
+    float4 prev = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (ACC && g == 0) {  // early, off the path
+        if (o + 0 < cols) prev.x = out[o + 0];
+        if (o + 1 < cols) prev.y = out[o + 1];
+        if (o + 2 < cols) prev.z = out[o + 2];
+        if (o + 3 < cols) prev.w = out[o + 3];
+    }
+    int na = 0;
+    if (n_active_out && b == 0)
+        for (int i = tid; i < n_tiles; i += 256) na += __popcll(mask[i]);
+    const float4 *p = reinterpret_cast<const float4 *>(part + b * 32) + c;
+    const int ps4 = pstride / 4;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int t0 = g; t0 < n_parts; t0 += TR_GROUPS * TR_BATCH) {  // uniform over the workgroup
+        float4 v[TR_BATCH];
+#pragma unroll
+        for (int i = 0; i < TR_BATCH; i++)
+            v[i] = p[(long long)min(t0 + TR_GROUPS * i, n_parts - 1) * ps4];
+#pragma unroll
+        for (int i = 0; i < TR_BATCH; i++) {
+            if (t0 + TR_GROUPS * i < n_parts) {
+                s.x += v[i].x;
+                s.y += v[i].y;
+                s.z += v[i].z;
+                s.w += v[i].w;
+            }
+        }
+    }
+    red[g][c] = s;
+    if (n_active_out && b == 0) {
+        for (int d = 32; d > 0; d >>= 1) na += __shfl_xor(na, d, 64);
+        if ((tid & 63) == 0) cnt[tid >> 6] = na;
+    }
+    __syncthreads();
+    // the group sums pairwise in a fixed tree (the same order on every run)
+#pragma unroll
+    for (int hg = TR_GROUPS / 2; hg > 0; hg >>= 1) {
+        if (g < hg) {
+            const float4 a = red[g][c], v = red[g + hg][c];
+            red[g][c] = make_float4(a.x + v.x, a.y + v.y, a.z + v.z, a.w + v.w);
+        }
+        __syncthreads();
+    }
+    if (g == 0) {
+        const float4 sum = red[0][c];
+        if (o + 0 < cols) out[o + 0] = ACC ? prev.x + sum.x : sum.x;
+        if (o + 1 < cols) out[o + 1] = ACC ? prev.y + sum.y : sum.y;
+        if (o + 2 < cols) out[o + 2] = ACC ? prev.z + sum.z : sum.z;
+        if (o + 3 < cols) out[o + 3] = ACC ? prev.w + sum.w : sum.w;
+    }
+    if (n_active_out && b == 0 && tid == 0) *n_active_out = cnt[0] + cnt[1] + cnt[2] + cnt[3];
 }
 
 // Most pairs a k_sparse_down thread loads at once, by type (the row bytes of
@@ -385,23 +651,19 @@ constexpr int dn_np() {
 }
 
 // acc[32] += u * dequant(block b of the down row) for the first nvalid of the
-// NP entries e[] (a pair with u == 0 is skipped, ffn_flash.go:290).  An
-// entry is (row, u bits), or with UM (row, slot) and u = us[slot].y, loaded
-// together with the row bytes.  Every load is issued before any is used;
-// skipped entries read row 0 (in bounds), so no load sits under a per-lane
-// condition.
-template <int T, int NP, bool UM>
+// NP entries e[] = (row, u bits) (a pair with u == 0 is skipped,
+// ffn_flash.go:290).  Every load is issued before any is used; skipped
+// entries read row 0 (in bounds), so no load sits under a per-lane condition.
+template <int T, int NP>
 __device__ __forceinline__ void dn_batch(const uint8_t *__restrict__ base, long long bstride,
                                          const RowFmt &f, int b, const int2 (&e)[NP], int nvalid,
-                                         const int2 *__restrict__ us, float (&acc)[32],
-                                         float &corr) {
+                                         float (&acc)[32], float &corr) {
     BlockRaw<T> r[NP];
     float u[NP];
 #pragma unroll
     for (int k = 0; k < NP; k++) {
-        if (UM) u[k] = __int_as_float(us[k < nvalid ? e[k].y : 0].y);
-        else u[k] = __int_as_float(e[k].y);
-        const bool v = k < nvalid && (UM || u[k] != 0.0f);
+        u[k] = __int_as_float(e[k].y);
+        const bool v = k < nvalid && u[k] != 0.0f;
         llg_block_load<T>(r[k], base + (long long)(v ? e[k].x : 0) * bstride + f.stride, f, b);
     }
 #pragma unroll
@@ -411,146 +673,70 @@ __device__ __forceinline__ void dn_batch(const uint8_t *__restrict__ base, long 
 
 // Entries j = tid + bd * (i0 + i), i < K, of a dense list of n (get(j) reads
 // entry j) shared by bd threads, through dn_batch.
-template <int T, int K, bool UM, class Get>
+template <int T, int K, class Get>
 __device__ __forceinline__ void dn_run(const uint8_t *__restrict__ base, long long bstride,
                                        const RowFmt &f, int b, int n, int i0, Get &&get,
-                                       const int2 *__restrict__ us, float (&acc)[32],
-                                       float &corr, int tid, int bd) {
+                                       float (&acc)[32], float &corr, int tid, int bd) {
     int2 e[K];
 #pragma unroll
     for (int i = 0; i < K; i++) e[i] = get(min(tid + bd * (i0 + i), n - 1));
     const int mine = (n - tid + bd - 1) / bd;  // entries of this thread in the list
-    dn_batch<T, K, UM>(base, bstride, f, b, e, min(max(mine - i0, 0), K), us, acc, corr);
+    dn_batch<T, K>(base, bstride, f, b, e, min(max(mine - i0, 0), K), acc, corr);
 }
 
 // Every entry of a dense list of n shared by bd threads (this one is tid),
 // ceil(n / bd) per thread: the batch size follows that count (uniform over
 // the wavefront), so a thread issues no loads for entries it does not have.
-template <int T, bool UM, class Get>
+template <int T, class Get>
 __device__ __forceinline__ void dn_list(const uint8_t *__restrict__ base, long long bstride,
                                         const RowFmt &f, int b, int n, Get &&get,
-                                        const int2 *__restrict__ us, float (&acc)[32],
-                                        float &corr, int tid, int bd) {
+                                        float (&acc)[32], float &corr, int tid, int bd) {
     constexpr int KM = dn_np<T>();
     const int per = (n + bd - 1) / bd;
     for (int i0 = 0; i0 < per; i0 += KM) {
         const int k = min(per - i0, KM);
         if (k == 1)
-            dn_run<T, 1, UM>(base, bstride, f, b, n, i0, get, us, acc, corr, tid, bd);
+            dn_run<T, 1>(base, bstride, f, b, n, i0, get, acc, corr, tid, bd);
         else if (k == 2)
-            dn_run<T, 2, UM>(base, bstride, f, b, n, i0, get, us, acc, corr, tid, bd);
+            dn_run<T, 2>(base, bstride, f, b, n, i0, get, acc, corr, tid, bd);
         else if (k <= 4)
-            dn_run<T, (KM < 4 ? KM : 4), UM>(base, bstride, f, b, n, i0, get, us, acc, corr, tid,
-                                             bd);
+            dn_run<T, (KM < 4 ? KM : 4)>(base, bstride, f, b, n, i0, get, acc, corr, tid, bd);
         else if (k <= 8)
-            dn_run<T, (KM < 8 ? KM : 8), UM>(base, bstride, f, b, n, i0, get, us, acc, corr, tid,
-                                             bd);
+            dn_run<T, (KM < 8 ? KM : 8)>(base, bstride, f, b, n, i0, get, acc, corr, tid, bd);
         else
-            dn_run<T, KM, UM>(base, bstride, f, b, n, i0, get, us, acc, corr, tid, bd);
+            dn_run<T, KM>(base, bstride, f, b, n, i0, get, acc, corr, tid, bd);
     }
 }
 
-// Inclusive prefix sum over the wavefront: row shifts within each 16-lane
-// row, then the row totals broadcast to the rows after them.
-__device__ __forceinline__ int dn_wave_scan(int v) {
-    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
-    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
-    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
-    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
-    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
-    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
-    return v;
-}
-
-// Down products.  Pairs come either as a plain list pairs[0..*count) (TILED
-// = false; the count is clamped to `cap`), split evenly over the threads, or
-// from the predictor tiles (TILED = true): tile t's active neurons are the
-// set bits of mask[t], and the pair of neuron n is pairs[n].  Wavefront w
-// takes tiles w, w + nw, w + 2 nw, ... (lane l: tile l nw + w), so every
-// wavefront gets a share of the pairs: a wavefront scan of the lanes'
-// popcounts places its tiles' active neurons in its own dense list in LDS
-// (DN_WCAP at a time),
-// which its lanes then share; each neuron's u is loaded with its row bytes.
-// No barrier stands between the masks and the row loads.  Workgroup =
-// output block b (32 outputs): out[32 b + e] (+)= sum over the pairs of u *
-// down_row[32 b + e], the wavefronts' sums added in order.  With ACC the sum
-// is added to out (a residual), else stored.  With TILED, workgroup 0 also
-// writes the number of active neurons.
-#define DN_WCAP 512   // entries of a wavefront's LDS list per pass
-template <int T, bool TILED, bool ACC>
+// Down products over a plain pair list pairs[0..*count) (the count is
+// clamped to `cap`), split evenly over the threads.  Workgroup = output block
+// b (32 outputs): out[32 b + e] = sum over the pairs of u * down_row[32 b +
+// e], the wavefronts' sums added in order.
+template <int T>
 __global__ __launch_bounds__(DN_THREADS) void k_sparse_down(
     const uint8_t *__restrict__ base, long long bstride, RowFmt f, const int2 *__restrict__ pairs,
-    const int32_t *__restrict__ count_p, int cap, const unsigned long long *__restrict__ mask,
-    int n_tiles, int32_t *__restrict__ n_active_out, int per_xcd, float *__restrict__ out) {
+    const int32_t *__restrict__ count_p, int cap, int per_xcd, float *__restrict__ out) {
     __shared__ float red[DN_THREADS / 64][32];
-    __shared__ int ired[DN_THREADS / 64];
-    __shared__ int2 lst[TILED ? DN_THREADS / 64 : 1][TILED ? DN_WCAP : 1];
     const int b = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     if (b >= f.nb) return;  // uniform over the workgroup
     const int tid = threadIdx.x, bd = blockDim.x, lane = tid & 63, wave = tid >> 6;
     const int nw = bd >> 6;
     const int o = b * 32 + (lane >> 1);
-    float prev = 0.0f;
-    if (ACC && wave == 0 && (lane & 1) == 0 && o < f.cols) prev = out[o];  // early, off the path
     float acc[32];
     float corr = 0.0f;
 #pragma unroll
     for (int e = 0; e < 32; e++) acc[e] = 0.0f;
-    int n_act = 0;
-    if (TILED) {
-        int2 *wl = lst[TILED ? wave : 0];
-        // wavefront w takes tiles w, w + nw, ... (lane l: (p0 + l) * nw + w), so
-        // every wavefront gets a share of the pairs
-        for (int p0 = 0; p0 * nw + wave < n_tiles; p0 += 64) {  // uniform per wavefront
-            const int t = (p0 + lane) * nw + wave;
-            const unsigned long long m0 = t < n_tiles ? mask[t] : 0ull;
-            const int c = __popcll(m0);
-            const int incl = dn_wave_scan(c);
-            const int total = __builtin_amdgcn_readlane(incl, 63);
-            const int off = incl - c;
-            n_act += c;
-            for (int cb = 0; cb < total; cb += DN_WCAP) {
-                if (off + c > cb && off < cb + DN_WCAP) {
-                    unsigned long long m = m0;
-                    for (int k = 0; m; k++, m &= m - 1) {
-                        const int g = off + k - cb;
-                        if (g >= 0 && g < DN_WCAP) {
-                            const int row = t * 64 + __ffsll((long long)m) - 1;
-                            wl[g] = make_int2(row, row);  // the pair of neuron n is pairs[n]
-                        }
-                    }
-                }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                dn_list<T, true>(base, bstride, f, b, min(total - cb, DN_WCAP),
-                                 [&](int j) { return wl[j]; }, pairs, acc, corr, lane, 64);
-                __builtin_amdgcn_wave_barrier();  // the list is read before the next pass writes
-            }
-        }
-    } else {
-        const int n = min(max(*count_p, 0), cap);
-        dn_list<T, false>(base, bstride, f, b, n, [&](int j) { return pairs[j]; }, pairs, acc,
-                          corr, tid, bd);
-    }
+    const int n = min(max(*count_p, 0), cap);
+    dn_list<T>(base, bstride, f, b, n, [&](int j) { return pairs[j]; }, acc, corr, tid, bd);
 #pragma unroll
     for (int e = 0; e < 32; e++) acc[e] -= corr;
     const float ws = dn_wave_transpose_sum(acc);
     if ((lane & 1) == 0) red[wave][lane >> 1] = ws;
-    if (TILED && n_active_out && blockIdx.x == 0) {
-        for (int d = 32; d > 0; d >>= 1) n_act += __shfl_xor(n_act, d, 64);
-        if (lane == 0) ired[wave] = n_act;
-    }
     __syncthreads();
     if (wave == 0 && (lane & 1) == 0) {
         float sum = 0.0f;
         for (int w = 0; w < nw; w++) sum += red[w][lane >> 1];
-        if (o < f.cols) out[o] = ACC ? prev + sum : sum;
-    }
-    if (TILED && n_active_out && blockIdx.x == 0 && tid == 0) {
-        int c = 0;
-        for (int w = 0; w < nw; w++) c += ired[w];
-        *n_active_out = c;
+        if (o < f.cols) out[o] = sum;
     }
 }
 
@@ -576,9 +762,8 @@ template <int T>
 static void launch_down(hipStream_t st, const uint8_t *base, long long bstride, const RowFmt &f,
                         const int2 *pairs, const int32_t *count, int max_pairs, float *out) {
     const int px = down_per_xcd(f);
-    hipLaunchKernelGGL((k_sparse_down<T, false, false>), dim3(8 * px), dim3(down_threads(max_pairs)),
-                       0, st, base, bstride, f, pairs, count, max_pairs,
-                       (const unsigned long long *)nullptr, 0, (int32_t *)nullptr, px, out);
+    hipLaunchKernelGGL((k_sparse_down<T>), dim3(8 * px), dim3(down_threads(max_pairs)), 0, st, base,
+                       bstride, f, pairs, count, max_pairs, px, out);
 }
 
 template <int T>
@@ -637,36 +822,38 @@ int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, con
 }
 
 // Workspace of the fused path: the predictor's partials and masks, then the
-// tiles' pair slots (64 per tile).
-size_t llg_fused_ws_bytes(int rank, int ff) {
-    const long long n_tiles = (ff + 63) / 64;
-    return (size_t)llg_predict_ws_bytes(rank, ff) + (size_t)llg_align(n_tiles * 64 * 8, 256);
+// tiles' partial outputs (one row of nb * 32 floats per tile).
+size_t llg_fused_ws_bytes(int rank, int ff, int nb) {
+    const long long n_tiles = (ff + 63) / 64;  // an upper bound on the partial rows
+    return (size_t)llg_predict_ws_bytes(rank, ff) + (size_t)llg_align(n_tiles * nb * 32 * 4, 256);
 }
 
 template <int T>
 static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial,
                          const float *bias, float thr, LlgObject *b, const float *x, int act,
-                         unsigned long long *mask, int2 *pairs, int32_t *n_active, float *out,
+                         unsigned long long *mask, float *part, int32_t *n_active, float *out,
                          bool accumulate) {
     const int ff = wout->rows, rank = wout->fmt.cols;
     const int n_tiles = (ff + 63) / 64;
     const RowFmt &f = b->fmt;
-    const size_t lds = xs_bytes(f) + (size_t)(((rank + 3) & ~3) + TU_MAX + TU_MAX + 1) * 4;
-    hipLaunchKernelGGL((k_tile_up<T>), dim3(n_tiles), dim3(TU_THREADS), lds, st, wout->d,
+    const int pstride = f.nb * 32;
+    constexpr int NT = tf_tiles<T>() * TU;
+    const int n_parts = (ff + NT - 1) / NT;  // workgroups, one partial row each
+    const size_t lds = xs_bytes(f) + (size_t)(((rank + 3) & ~3) + 3 * NT + 1) * 4;
+    hipLaunchKernelGGL((k_tile_ffn<T>), dim3(n_parts), dim3(tf_threads<T>()), lds, st, wout->d,
                        wout->stride, ff, rank, partial, bias, thr, b->d, b->stride, f, x, act,
-                       mask, pairs);
-    const int px = down_per_xcd(f);
+                       mask, part, pstride);
     if (accumulate)
-        hipLaunchKernelGGL((k_sparse_down<T, true, true>), dim3(8 * px), dim3(DN_THREADS), 0, st,
-                           b->d, b->stride, f, (const int2 *)pairs, (const int32_t *)nullptr, 0,
-                           (const unsigned long long *)mask, n_tiles, n_active, px, out);
+        hipLaunchKernelGGL((k_tile_reduce<true>), dim3(f.nb), dim3(256), 0, st,
+                           (const float *)part, pstride, n_parts, n_tiles, f.cols,
+                           (const unsigned long long *)mask, n_active, out);
     else
-        hipLaunchKernelGGL((k_sparse_down<T, true, false>), dim3(8 * px), dim3(DN_THREADS), 0, st,
-                           b->d, b->stride, f, (const int2 *)pairs, (const int32_t *)nullptr, 0,
-                           (const unsigned long long *)mask, n_tiles, n_active, px, out);
+        hipLaunchKernelGGL((k_tile_reduce<false>), dim3(f.nb), dim3(256), 0, st,
+                           (const float *)part, pstride, n_parts, n_tiles, f.cols,
+                           (const unsigned long long *)mask, n_active, out);
 }
 
-// ffnFlash path 2 on the device: k_pred_hidden, k_tile_up, k_sparse_down,
+// ffnFlash path 2 on the device: k_pred_hidden, k_tile_ffn, k_tile_reduce,
 // plus the ascending active list through k_compact when d_active is given.
 // d_n_active (optional) receives the number of active neurons.
 int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
@@ -696,12 +883,12 @@ int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgOb
     const RowFmt &f = b->fmt;
     const int ff = wout->rows, rank = wout->fmt.cols;
     const int n_tiles = (ff + 63) / 64;
-    if (xs_bytes(f) + (size_t)(rank + 2 * 128 + 8) * 4 > 64 * 1024)
+    if (xs_bytes(f) + (size_t)(rank + 6 * TU + 8) * 4 > 64 * 1024)
         return llg_set_error(d, LLG_E_ARG, "predict_sparse: hidden size %d too large", f.cols);
     if (llg_pred_split() != PRED_SPLIT_N)
         return llg_set_error(d, LLG_E_ARG, "predict_sparse: hidden split %d != %d",
                              llg_pred_split(), PRED_SPLIT_N);
-    int2 *pairs = reinterpret_cast<int2 *>(ws + llg_predict_ws_bytes(rank, ff));
+    float *part = reinterpret_cast<float *>(ws + llg_predict_ws_bytes(rank, ff));
     float *partial;
     unsigned long long *mask;
     llg_pred_ws_layout(ws, rank, &partial, &mask);
@@ -709,19 +896,19 @@ int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgOb
     hipStream_t st = llg_dev_stream(d);
     switch (f.type) {
     case LLG_TYPE_Q4_0:
-        launch_fused<LLG_TYPE_Q4_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, pairs,
+        launch_fused<LLG_TYPE_Q4_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
                                     d_n_active, d_out, accum);
         break;
     case LLG_TYPE_Q8_0:
-        launch_fused<LLG_TYPE_Q8_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, pairs,
+        launch_fused<LLG_TYPE_Q8_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
                                     d_n_active, d_out, accum);
         break;
     case LLG_TYPE_F16:
-        launch_fused<LLG_TYPE_F16>(st, wout, partial, d_bias, thr, b, d_x, act, mask, pairs,
+        launch_fused<LLG_TYPE_F16>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
                                    d_n_active, d_out, accum);
         break;
     case LLG_TYPE_F32:
-        launch_fused<LLG_TYPE_F32>(st, wout, partial, d_bias, thr, b, d_x, act, mask, pairs,
+        launch_fused<LLG_TYPE_F32>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
                                    d_n_active, d_out, accum);
         break;
     default:
