@@ -144,11 +144,12 @@ constexpr int bc_first() {
 
 // Up-row dot products of NR rows (wavefront-uniform indices, < 0: none) by
 // one wavefront, NBATCH blocks per lane per pass, all loads of a pass issued
-// before any is used; same conventions as row_dot2.
-template <int T, int NR, int NBATCH>
+// before any is used; same conventions as row_dot2.  issued(): called once,
+// when the first pass's loads are issued (before any is used).
+template <int T, int NR, int NBATCH, typename Issued = LlgNoIssue>
 __device__ __forceinline__ void row_dotn(const uint8_t *__restrict__ base, long long bstride,
                                          const int (&row)[NR], const RowFmt &f, const float *xs,
-                                         float (&s)[NR]) {
+                                         float (&s)[NR], Issued &&issued = Issued()) {
     const int lane = threadIdx.x & 63;
     const uint8_t *p[NR];
     bool v[NR];
@@ -166,6 +167,10 @@ __device__ __forceinline__ void row_dotn(const uint8_t *__restrict__ base, long 
 #pragma unroll
             for (int q = 0; q < NR; q++)
                 llg_block_load<T>(r[i][q], p[q], f, min(b0 + lane + 64 * i, f.nb - 1));
+        if (b0 == 0) {
+            __builtin_amdgcn_sched_barrier(0);  // issued() stays behind these loads
+            issued();
+        }
 #pragma unroll
         for (int i = 0; i < NBATCH; i++) {
             const int b = b0 + lane + 64 * i;
@@ -287,12 +292,13 @@ __device__ __forceinline__ float dn_wave_transpose_sum(const float (&v)[32]) {
 
 // One round of the tile's up rows with the activations kept in LDS, over the
 // first nw wavefronts: active neuron k = k0 + wave + nw*i (i < NR) of the
-// tile on this wavefront, ul[k] = act(up . x).
-template <int T, int NR>
+// tile on this wavefront, ul[k] = act(up . x).  issued(): called once this
+// wavefront's loads of the round are issued (at once when it has no row).
+template <int T, int NR, typename Issued = LlgNoIssue>
 __device__ __forceinline__ void tile_u_round(const uint8_t *__restrict__ base, long long bstride,
                                              const RowFmt &f, const float *xs, const int *tl,
                                              int cnt, int k0, int tile0, int act, float *ul,
-                                             int nw) {
+                                             int nw, Issued &&issued = Issued()) {
     const int wave = threadIdx.x >> 6;
     int rows[NR];
 #pragma unroll
@@ -300,9 +306,12 @@ __device__ __forceinline__ void tile_u_round(const uint8_t *__restrict__ base, l
         const int k = k0 + wave + nw * i;
         rows[i] = k < cnt ? tile0 + tl[k] : -1;
     }
-    if (rows[0] < 0) return;  // wavefront-uniform: nothing in this round
+    if (rows[0] < 0) {  // wavefront-uniform: nothing in this round
+        issued();
+        return;
+    }
     float s[NR];
-    row_dotn<T, NR, NR == 1 ? 4 : 3>(base, bstride, rows, f, xs, s);
+    row_dotn<T, NR, 3>(base, bstride, rows, f, xs, s, issued);
     if ((threadIdx.x & 63) == 0) {
 #pragma unroll
         for (int i = 0; i < NR; i++)
@@ -310,102 +319,93 @@ __device__ __forceinline__ void tile_u_round(const uint8_t *__restrict__ base, l
     }
 }
 
-// Half of a 32-element block of a row in the row format: the bytes of
-// elements [16 h, 16 h + 16) of block b, and the block scale (Q4_0: words
-// 2h, 2h + 1 of the block's nibbles; Q8_0: bytes 16h..16h+15; F16/F32: 16
-// values).
+// A quarter of a 32-element block of a row in the row format: the bytes of
+// elements [8 q, 8 q + 8) of block b, and the block scale (Q4_0: word q of the
+// block's nibbles; Q8_0: bytes 8q..8q+7; F16/F32: 8 values).
 template <int T>
-struct HalfRaw;
+struct QuarterRaw;
 template <>
-struct HalfRaw<LLG_TYPE_Q4_0> {
+struct QuarterRaw<LLG_TYPE_Q4_0> {
+    uint32_t q;
+    unsigned short d;
+};
+template <>
+struct QuarterRaw<LLG_TYPE_Q8_0> {
     uint2 q;
     unsigned short d;
 };
 template <>
-struct HalfRaw<LLG_TYPE_Q8_0> {
+struct QuarterRaw<LLG_TYPE_F16> {
     uint4 q;
-    unsigned short d;
 };
 template <>
-struct HalfRaw<LLG_TYPE_F16> {
-    uint4 q[2];
-};
-template <>
-struct HalfRaw<LLG_TYPE_F32> {
-    float4 q[4];
+struct QuarterRaw<LLG_TYPE_F32> {
+    float4 q[2];
 };
 
 template <int T>
-__device__ __forceinline__ void half_load(HalfRaw<T> &r, const uint8_t *__restrict__ row,
-                                          const RowFmt &f, int b, int h) {
+__device__ __forceinline__ void quarter_load(QuarterRaw<T> &r, const uint8_t *__restrict__ row,
+                                             const RowFmt &f, int b, int q) {
     if constexpr (T == LLG_TYPE_Q4_0) {
-        r.q = *reinterpret_cast<const uint2 *>(row + (size_t)b * 16 + h * 8);
+        r.q = *reinterpret_cast<const uint32_t *>(row + (size_t)b * 16 + q * 4);
         r.d = *reinterpret_cast<const unsigned short *>(row + f.d_off + b * 2);
     } else if constexpr (T == LLG_TYPE_Q8_0) {
-        r.q = *reinterpret_cast<const uint4 *>(row + (size_t)b * 32 + h * 16);
+        r.q = *reinterpret_cast<const uint2 *>(row + (size_t)b * 32 + q * 8);
         r.d = *reinterpret_cast<const unsigned short *>(row + f.d_off + b * 2);
     } else if constexpr (T == LLG_TYPE_F16) {
-        const uint4 *p = reinterpret_cast<const uint4 *>(row + (size_t)b * 64 + h * 32);
+        r.q = *reinterpret_cast<const uint4 *>(row + (size_t)b * 64 + q * 16);
+    } else {
+        const float4 *p = reinterpret_cast<const float4 *>(row + (size_t)b * 128 + q * 32);
         r.q[0] = p[0];
         r.q[1] = p[1];
-    } else {
-        const float4 *p = reinterpret_cast<const float4 *>(row + (size_t)b * 128 + h * 64);
-#pragma unroll
-        for (int i = 0; i < 4; i++) r.q[i] = p[i];
     }
 }
 
-// acc[0..15] += u * dequant(half block), with the quantized types' offset
+// acc[0..7] += u * dequant(quarter block), with the quantized types' offset
 // folded into *corr (the caller subtracts corr from every element once):
 // Q4_0 adds u d (64 + q) (a nibble under the f16 exponent bits 0x5400 is
 // exactly 64 + q, multiplied into fp32 by v_fma_mix) and corr 72 u d; Q8_0
 // adds u d (q + 128) and corr 128 u d.
 template <int T>
-__device__ __forceinline__ void half_axpy(const HalfRaw<T> &r, float u, float (&acc)[16],
-                                          float &corr) {
+__device__ __forceinline__ void quarter_axpy(const QuarterRaw<T> &r, float u, float (&acc)[8],
+                                             float &corr) {
     if constexpr (T == LLG_TYPE_Q4_0) {
         const float s = u * llg_f16(r.d);
         corr += 72.0f * s;
-        const uint32_t w[2] = {r.q.x, r.q.y};
-        const uint32_t m = 0x00F000F0u, e = 0x54005400u;
-#pragma unroll
-        for (int i = 0; i < 2; i++) {  // nibble p of word i is element 8 i + p
-            const half2_llg p0 = __builtin_bit_cast(half2_llg, llg_and_or(w[i] << 4, m, e));
-            const half2_llg p1 = __builtin_bit_cast(half2_llg, llg_and_or(w[i], m, e));
-            const half2_llg p2 = __builtin_bit_cast(half2_llg, llg_and_or(w[i] >> 4, m, e));
-            const half2_llg p3 = __builtin_bit_cast(half2_llg, llg_and_or(w[i] >> 8, m, e));
-            acc[8 * i + 0] = __builtin_fmaf((float)p0[0], s, acc[8 * i + 0]);
-            acc[8 * i + 1] = __builtin_fmaf((float)p1[0], s, acc[8 * i + 1]);
-            acc[8 * i + 2] = __builtin_fmaf((float)p2[0], s, acc[8 * i + 2]);
-            acc[8 * i + 3] = __builtin_fmaf((float)p3[0], s, acc[8 * i + 3]);
-            acc[8 * i + 4] = __builtin_fmaf((float)p0[1], s, acc[8 * i + 4]);
-            acc[8 * i + 5] = __builtin_fmaf((float)p1[1], s, acc[8 * i + 5]);
-            acc[8 * i + 6] = __builtin_fmaf((float)p2[1], s, acc[8 * i + 6]);
-            acc[8 * i + 7] = __builtin_fmaf((float)p3[1], s, acc[8 * i + 7]);
-        }
+        const uint32_t w = r.q, m = 0x00F000F0u, e = 0x54005400u;
+        // nibble p of the word is element p
+        const half2_llg p0 = __builtin_bit_cast(half2_llg, llg_and_or(w << 4, m, e));
+        const half2_llg p1 = __builtin_bit_cast(half2_llg, llg_and_or(w, m, e));
+        const half2_llg p2 = __builtin_bit_cast(half2_llg, llg_and_or(w >> 4, m, e));
+        const half2_llg p3 = __builtin_bit_cast(half2_llg, llg_and_or(w >> 8, m, e));
+        acc[0] = __builtin_fmaf((float)p0[0], s, acc[0]);
+        acc[1] = __builtin_fmaf((float)p1[0], s, acc[1]);
+        acc[2] = __builtin_fmaf((float)p2[0], s, acc[2]);
+        acc[3] = __builtin_fmaf((float)p3[0], s, acc[3]);
+        acc[4] = __builtin_fmaf((float)p0[1], s, acc[4]);
+        acc[5] = __builtin_fmaf((float)p1[1], s, acc[5]);
+        acc[6] = __builtin_fmaf((float)p2[1], s, acc[6]);
+        acc[7] = __builtin_fmaf((float)p3[1], s, acc[7]);
     } else if constexpr (T == LLG_TYPE_Q8_0) {
         const float s = u * llg_f16(r.d);
         corr += 128.0f * s;
-        const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+        const uint32_t w[2] = {r.q.x, r.q.y};
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < 2; i++) {
             const uint32_t v = w[i] ^ 0x80808080u;
 #pragma unroll
             for (int k = 0; k < 4; k++) acc[4 * i + k] += s * (float)((v >> (8 * k)) & 0xFF);
         }
     } else if constexpr (T == LLG_TYPE_F16) {
+        const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const uint32_t w[4] = {r.q[i].x, r.q[i].y, r.q[i].z, r.q[i].w};
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                acc[8 * i + 2 * k] += u * llg_f16(w[k] & 0xFFFF);
-                acc[8 * i + 2 * k + 1] += u * llg_f16(w[k] >> 16);
-            }
+        for (int k = 0; k < 4; k++) {
+            acc[2 * k] += u * llg_f16(w[k] & 0xFFFF);
+            acc[2 * k + 1] += u * llg_f16(w[k] >> 16);
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < 2; i++) {
             acc[4 * i + 0] += u * r.q[i].x;
             acc[4 * i + 1] += u * r.q[i].y;
             acc[4 * i + 2] += u * r.q[i].z;
@@ -414,38 +414,40 @@ __device__ __forceinline__ void half_axpy(const HalfRaw<T> &r, float u, float (&
     }
 }
 
-// 64-neuron tiles per k_tile_ffn workgroup, and its threads: the quantized
-// types take two tiles on 1024 threads (one workgroup per CU, 128 registers),
-// F16/F32 rows need more registers and take one tile on 512 threads.
+// 64-neuron tiles per k_tile_ffn workgroup, and its threads: Q4_0 takes two
+// tiles on 1024 threads (one workgroup per CU, 128 registers); the wider
+// rows of the other types need more registers and take one tile on 512
+// threads.
 template <int T>
 constexpr int tf_tiles() {
-    return T == LLG_TYPE_Q4_0 || T == LLG_TYPE_Q8_0 ? 2 : 1;
+    return T == LLG_TYPE_Q4_0 ? 2 : 1;
 }
 template <int T>
 constexpr int tf_threads() {
     return 512 * tf_tiles<T>();
 }
-// Down rows a k_tile_ffn thread holds at once (half blocks), by type.
+// Down rows a k_tile_ffn thread holds at once (quarter blocks), by type.
 template <int T>
 constexpr int tf_dk() {
-    return T == LLG_TYPE_Q4_0 ? 16 : (T == LLG_TYPE_Q8_0 ? 8 : (T == LLG_TYPE_F16 ? 4 : 2));
+    return T == LLG_TYPE_Q4_0 || T == LLG_TYPE_Q8_0 ? 16 : (T == LLG_TYPE_F16 ? 8 : 4);
 }
 
 // A'. The predictor-fused tiles with their down products (the form the step
 // uses): a workgroup owns tf_tiles 64-neuron tiles (WOut rows: 16 per
 // wavefront; the ballot writes one mask word per tile and the workgroup's
 // ascending active list), then
-//   - the top ceil(2 nb / 64) wavefronts (at most half of them) own the
-//     output half blocks (16 outputs) of the tile's partial; right after the
-//     ballot each of their threads requests its first half block of the down
-//     row of each active neuron (up to tf_dk at once), so the down bytes
-//     arrive in the round of the up rows (a neuron's up and down rows are one
+//   - every wavefront takes up rows (active neuron k on wavefront k mod the
+//     wavefront count): ul[k] = act(up . x) in LDS;
+//   - the top ceil(4 nb / 64) wavefronts also own the output quarter blocks
+//     (8 outputs) of the workgroup's partial: right after their up-row loads
+//     each of their threads requests its first quarter block of the down row
+//     of each active neuron (up to tf_dk at once), so the down bytes arrive
+//     in the round of the up rows (a neuron's up and down rows are one
 //     contiguous bundle);
-//   - the other wavefronts take the up rows: ul[k] = act(up . x) in LDS;
 //   - part[w][o] = sum over the workgroup's active neurons, ascending, of
 //     u * down[o] (a zero u is skipped, ffn_flash.go:290).
-// Every tile writes its partial (zeros when nothing is active), and
-// k_tile_reduce adds the tiles' partials in tile order, so the result is the
+// Every workgroup writes its partial (zeros when nothing is active), and
+// k_tile_reduce adds the partials in a fixed order, so the result is the
 // same on every run.
 template <int T>
 __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile_ffn(
@@ -492,53 +494,50 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
     }
     __syncthreads();
     const int cnt = tl[NT];
-    // The top n_dw wavefronts own the down half blocks: thread j of them (j =
-    // tid - 64 n_uw) takes half blocks i = j, j + 64 n_dw, ... (block i / 2,
-    // half i % 2); the other n_uw wavefronts take the up rows.  The two roles
-    // are branches of one if, so their registers are not live at the same
-    // time.
+    // The top n_dw wavefronts own the down quarter blocks: thread j of them
+    // (j = tid - 64 n_uw) takes quarter blocks i = j, j + 64 n_dw, ... (block
+    // i / 4, quarter i % 4).  Every wavefront takes up rows.
     constexpr int DK = tf_dk<T>();
-    const int n_half = 2 * f.nb;
-    const int n_dw = min((n_half + 63) / 64, NTH / 128);
+    const int n_qb = 4 * f.nb;  // quarter blocks
+    const int n_dw = min((n_qb + 63) / 64, NTH / 64);
     const int n_uw = NTH / 64 - n_dw;
     const int j = (int)threadIdx.x - 64 * n_uw;
     const int dstep = 64 * n_dw;
     const uint8_t *dbase = base + f.stride;  // down row of neuron n: dbase + n * bstride
-    HalfRaw<T> dr[DK];
+    QuarterRaw<T> dr[DK];
     // lane q of a down wavefront holds active neuron k0 + q's workgroup-local
     // index (one LDS read per round; each row index is then a readlane)
     int trow = lane < cnt ? tl[lane] : 0;
-    if (wave >= n_uw) {
-        // the first half block's down bytes of the first DK active neurons, so
-        // that they arrive in the round of the up rows (address clamped for
-        // the lanes past the last half block)
-        const int ic = min(j, n_half - 1);
+    // the first quarter block's down bytes of the first DK active neurons,
+    // requested right after this wavefront's up-row loads, so that they
+    // arrive in the round of the up rows (address clamped for the lanes past
+    // the last quarter block)
+    auto issue_down = [&]() {
+        if (wave >= n_uw) {
+            const int ic = min(j, n_qb - 1);
 #pragma unroll
-        for (int k = 0; k < DK; k++) {
-            if (k < cnt) {
-                const int n = n0 + __builtin_amdgcn_readlane(trow, k);
-                half_load<T>(dr[k], dbase + (long long)n * bstride, f, ic >> 1, ic & 1);
+            for (int k = 0; k < DK; k++) {
+                if (k < cnt) {
+                    const int n = n0 + __builtin_amdgcn_readlane(trow, k);
+                    quarter_load<T>(dr[k], dbase + (long long)n * bstride, f, ic >> 2, ic & 3);
+                }
             }
         }
-    } else {
-        constexpr int UPMAX = T == LLG_TYPE_F32 ? 1 : 2;
-        if (cnt <= n_uw || UPMAX == 1) {
-            for (int k0 = 0; k0 < cnt; k0 += n_uw)
-                tile_u_round<T, 1>(base, bstride, f, xs, tl, cnt, k0, n0, act, ul, n_uw);
-        } else {
-            if constexpr (UPMAX == 2)
-                for (int k0 = 0; k0 < cnt; k0 += 2 * n_uw)
-                    tile_u_round<T, 2>(base, bstride, f, xs, tl, cnt, k0, n0, act, ul, n_uw);
-        }
-    }
+    };
+    // up rows: every wavefront takes active neuron k = wave (+ 16 per further
+    // round, which a workgroup needs for more than 16 active neurons)
+    constexpr int NW = NTH / 64;
+    tile_u_round<T, 1>(base, bstride, f, xs, tl, cnt, 0, n0, act, ul, NW, issue_down);
+    for (int k0 = NW; k0 < cnt; k0 += NW)
+        tile_u_round<T, 1>(base, bstride, f, xs, tl, cnt, k0, n0, act, ul, NW);
     __syncthreads();
     if (wave < n_uw) return;  // uniform per wavefront (no barrier follows)
-    for (int i = j; i - j < n_half; i += dstep) {  // uniform bound: every lane runs each pass
-        const int ic = min(i, n_half - 1);
-        float acc[16];
+    for (int i = j; i - j < n_qb; i += dstep) {  // uniform bound: every lane runs each pass
+        const int ic = min(i, n_qb - 1);
+        float acc[8];
         float corr = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 16; e++) acc[e] = 0.0f;
+        for (int e = 0; e < 8; e++) acc[e] = 0.0f;
         for (int k0 = 0; k0 < cnt; k0 += DK) {
             // activations of this round's neurons, one LDS read (lane q: k0 + q)
             const float uq = k0 + lane < cnt ? ul[k0 + lane] : 0.0f;
@@ -548,7 +547,7 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
                 for (int k = 0; k < DK; k++) {
                     if (k0 + k < cnt) {
                         const int n = n0 + __builtin_amdgcn_readlane(trow, k);
-                        half_load<T>(dr[k], dbase + (long long)n * bstride, f, ic >> 1, ic & 1);
+                        quarter_load<T>(dr[k], dbase + (long long)n * bstride, f, ic >> 2, ic & 3);
                     }
                 }
             }
@@ -556,14 +555,14 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
             for (int k = 0; k < DK; k++) {
                 if (k0 + k < cnt) {
                     const float u = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(uq), k));
-                    if (u != 0.0f) half_axpy<T>(dr[k], u, acc, corr);
+                    if (u != 0.0f) quarter_axpy<T>(dr[k], u, acc, corr);
                 }
             }
         }
-        if (i < n_half) {
-            float4 *o4 = reinterpret_cast<float4 *>(part + (long long)blockIdx.x * pstride + i * 16);
+        if (i < n_qb) {
+            float4 *o4 = reinterpret_cast<float4 *>(part + (long long)blockIdx.x * pstride + i * 8);
 #pragma unroll
-            for (int e = 0; e < 4; e++)
+            for (int e = 0; e < 2; e++)
                 o4[e] = make_float4(acc[4 * e] - corr, acc[4 * e + 1] - corr,
                                     acc[4 * e + 2] - corr, acc[4 * e + 3] - corr);
         }
