@@ -432,6 +432,52 @@ constexpr int tf_dk() {
     return T == LLG_TYPE_Q4_0 || T == LLG_TYPE_Q8_0 ? 16 : (T == LLG_TYPE_F16 ? 8 : 4);
 }
 
+// The logit of row 16 w + l / 4 of the tile in every lane l of wavefront w
+// (the quad layout of load_wout_tile; the scalar layout for other ranks),
+// the same sums as finish_logits.
+__device__ __forceinline__ float tile_logit(const WoutTile &t, const uint8_t *__restrict__ wout,
+                                            long long stride, int ff, int rank, int tile0,
+                                            const float *hid) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (t.v) {
+        const float4 *h4 = reinterpret_cast<const float4 *>(hid);
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < PRED_MAXV; k++) {
+            if (k < t.v) {
+                const float4 hv = h4[4 * k + t.q];
+                acc += t.w[k].x * hv.x;
+                acc += t.w[k].y * hv.y;
+                acc += t.w[k].z * hv.z;
+                acc += t.w[k].w * hv.w;
+            }
+        }
+        return llg_quad_sum(acc);
+    }
+    float mine = 0.0f;
+    for (int r = 0; r < 16; r++) {
+        const int i = tile0 + wave * 16 + r;
+        float acc = 0.0f;
+        if (i < ff) {
+            const float *w = reinterpret_cast<const float *>(wout + (long long)i * stride);
+            for (int c = lane; c < rank; c += 64) acc += w[c] * hid[c];
+        }
+        acc = llg_wave_sum(acc);
+        if ((lane >> 2) == r) mine = acc;
+    }
+    return mine;
+}
+
+// Bits 0, 4, 8, ..., 60 of m as a 16-bit word (bit r = bit 4 r).
+__device__ __forceinline__ uint32_t quad_bits(unsigned long long m) {
+    m &= 0x1111111111111111ull;
+    m = (m | (m >> 3)) & 0x0303030303030303ull;
+    m = (m | (m >> 6)) & 0x000F000F000F000Full;
+    m = (m | (m >> 12)) & 0x000000FF000000FFull;
+    m = (m | (m >> 24)) & 0xFFFFull;
+    return (uint32_t)m;
+}
+
 // A'. The predictor-fused tiles with their down products (the form the step
 // uses): a workgroup owns tf_tiles 64-neuron tiles (WOut rows: 16 per
 // wavefront; the ballot writes one mask word per tile and the workgroup's
@@ -456,14 +502,14 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
     const uint8_t *__restrict__ base, long long bstride, RowFmt f, const float *__restrict__ x,
     int act, unsigned long long *__restrict__ mask, float *__restrict__ part, int pstride) {
     extern __shared__ float sh[];
+    constexpr int TW = tf_tiles<T>(), NT = TW * TU, NTH = tf_threads<T>(), NW = NTH / 64;
     float *xs = sh;                                     // nb * XS_STRIDE
     float *hid = xs + f.nb * XS_STRIDE;                 // rank (16-byte aligned)
-    constexpr int TW = tf_tiles<T>(), NT = TW * TU, NTH = tf_threads<T>();
-    float *lg = hid + ((rank + 3) & ~3);                // NT
-    int *tl = reinterpret_cast<int *>(lg + NT);         // NT workgroup-local indices, count
-    float *ul = reinterpret_cast<float *>(tl + NT + 1);  // NT activations
+    float *ul = hid + ((rank + 3) & ~3);                // NT activations
+    uint32_t *wm = reinterpret_cast<uint32_t *>(ul + NT);  // NW 16-row masks
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int *tl = reinterpret_cast<int *>(wm + NW) + wave * NT;  // this wavefront's active list
     const int n0 = blockIdx.x * NT, n1 = min(ff, n0 + NT);
     WoutTile t;  // logits: wavefronts with neurons in the tile
     const bool lw = wave * 16 < n1 - n0;
@@ -471,29 +517,39 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
     stage_x(xs, x, f.nb);
     load_hidden<PRED_SPLIT_N>(hid, partial, rank);
     __syncthreads();
-    if (lw) finish_logits(t, wout, wstride, n1, rank, n0, hid, lg);
-    __syncthreads();
-    if (wave == 0) {
-        int c = 0;
-#pragma unroll
-        for (int w = 0; w < TW; w++) {
-            const int i = n0 + TU * w + lane;
-            bool on = false;
+    if (wave < NT / 16) {
+        // the strict '>' of the logits of this wavefront's 16 rows (the four
+        // lanes of a row agree), as a 16-bit mask
+        bool on = false;
+        if (lw) {
+            float v = tile_logit(t, wout, wstride, n1, rank, n0, hid);
+            const int i = n0 + wave * 16 + (lane >> 2);
             if (i < n1) {
-                float v = lg[TU * w + lane];
                 if (bias) v += bias[i];  // predictor.go:69-73
                 on = v > thr;            // predictor.go:78
             }
-            const unsigned long long m = __ballot(on);
-            const int before = __popcll(m & ((1ull << lane) - 1ull));
-            if (on) tl[c + before] = TU * w + lane;
-            if (lane == 0 && n0 + TU * w < n1) mask[blockIdx.x * TW + w] = m;
-            c += __popcll(m);
         }
-        if (lane == 0) tl[NT] = c;
+        const uint32_t m16 = quad_bits(__ballot(on));
+        if (lane == 0) wm[wave] = m16;
     }
     __syncthreads();
-    const int cnt = tl[NT];
+    // every wavefront forms the tile masks and its own copy of the ascending
+    // active list (no further barrier)
+    unsigned long long mw[TW];
+    int cnt = 0;
+#pragma unroll
+    for (int w = 0; w < TW; w++) {
+        mw[w] = (unsigned long long)wm[4 * w] | ((unsigned long long)wm[4 * w + 1] << 16) |
+                ((unsigned long long)wm[4 * w + 2] << 32) |
+                ((unsigned long long)wm[4 * w + 3] << 48);
+        const unsigned long long lt = (1ull << lane) - 1ull;
+        if ((mw[w] >> lane) & 1ull) tl[cnt + __popcll(mw[w] & lt)] = TU * w + lane;
+        cnt += __popcll(mw[w]);
+        if (wave == 0 && lane == 0 && n0 + TU * w < n1) mask[blockIdx.x * TW + w] = mw[w];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // The top n_dw wavefronts own the down quarter blocks: thread j of them
     // (j = tid - 64 n_uw) takes quarter blocks i = j, j + 64 n_dw, ... (block
     // i / 4, quarter i % 4).  Every wavefront takes up rows.
@@ -526,7 +582,6 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
     };
     // up rows: every wavefront takes active neuron k = wave (+ 16 per further
     // round, which a workgroup needs for more than 16 active neurons)
-    constexpr int NW = NTH / 64;
     tile_u_round<T, 1>(base, bstride, f, xs, tl, cnt, 0, n0, act, ul, NW, issue_down);
     for (int k0 = NW; k0 < cnt; k0 += NW)
         tile_u_round<T, 1>(base, bstride, f, xs, tl, cnt, k0, n0, act, ul, NW);
@@ -827,6 +882,14 @@ size_t llg_fused_ws_bytes(int rank, int ff, int nb) {
     return (size_t)llg_predict_ws_bytes(rank, ff) + (size_t)llg_align(n_tiles * nb * 32 * 4, 256);
 }
 
+// LDS of k_tile_ffn: staged x, hidden, activations, the logit masks and a
+// per-wavefront active list.
+template <int T>
+static size_t tile_lds_bytes(const RowFmt &f, int rank) {
+    constexpr int NT = tf_tiles<T>() * TU, NW = tf_threads<T>() / 64;
+    return xs_bytes(f) + (size_t)(((rank + 3) & ~3) + NT + NW + NW * NT) * 4;
+}
+
 template <int T>
 static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial,
                          const float *bias, float thr, LlgObject *b, const float *x, int act,
@@ -838,7 +901,7 @@ static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial,
     const int pstride = f.nb * 32;
     constexpr int NT = tf_tiles<T>() * TU;
     const int n_parts = (ff + NT - 1) / NT;  // workgroups, one partial row each
-    const size_t lds = xs_bytes(f) + (size_t)(((rank + 3) & ~3) + 3 * NT + 1) * 4;
+    const size_t lds = tile_lds_bytes<T>(f, rank);
     hipLaunchKernelGGL((k_tile_ffn<T>), dim3(n_parts), dim3(tf_threads<T>()), lds, st, wout->d,
                        wout->stride, ff, rank, partial, bias, thr, b->d, b->stride, f, x, act,
                        mask, part, pstride);
@@ -882,7 +945,9 @@ int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgOb
     const RowFmt &f = b->fmt;
     const int ff = wout->rows, rank = wout->fmt.cols;
     const int n_tiles = (ff + 63) / 64;
-    if (xs_bytes(f) + (size_t)(rank + 6 * TU + 8) * 4 > 64 * 1024)
+    const size_t lds = f.type == LLG_TYPE_Q4_0 ? tile_lds_bytes<LLG_TYPE_Q4_0>(f, rank)
+                                               : tile_lds_bytes<LLG_TYPE_F32>(f, rank);
+    if (lds > 64 * 1024)
         return llg_set_error(d, LLG_E_ARG, "predict_sparse: hidden size %d too large", f.cols);
     if (llg_pred_split() != PRED_SPLIT_N)
         return llg_set_error(d, LLG_E_ARG, "predict_sparse: hidden split %d != %d",
