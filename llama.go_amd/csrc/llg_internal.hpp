@@ -45,14 +45,23 @@ inline int llg_check_act(LlgDevice *d, int act) {
     return llg_act_ok(act) ? 0 : llg_set_error(d, LLG_E_ARG, "activation %d is not ReLU, GELU or SiLU", act);
 }
 
-// Windowed rows loaded by the current update: a listed neuron n with
-// fresh[n] == epoch is read from row n of src, and its whole bundle is copied
-// into its resident row slot_of[n] of dst (the writable base) on the way.
-struct LlgFreshRows {
+// The window update folded into the two launches of the window's update + FFN
+// step (llg_window.hip, window.go:71-117).  Neuron n is resident in row n of
+// dst (slot_of[n] == n) or not (slot_of[n] == -1).  The list launch records
+// the set in ring_new, marks each listed neuron (cur_ep = epoch) and counts it
+// in cnt, subtracts the expiring set ring_exp from cnt, and reads a listed
+// neuron that is not resident from row n of src, copying its bundle to row n
+// of dst (fresh = epoch; the loads are counted in cntr[epoch & 1]).  The down
+// launch then evicts the expiring neurons whose count reached 0 and that the
+// set does not hold, marks the loaded ones resident, and leaves the counts in
+// state ([2] resident neurons, [3] loads of this update).
+struct LlgWinUpd {
     const uint8_t *src;
-    const int32_t *fresh;
-    int epoch;
     uint8_t *dst;
+    int32_t *slot_of, *cnt, *cur_ep, *fresh, *state, *cntr;
+    int32_t *ring_new, *ring_len_new, *ring_set_new;
+    const int32_t *ring_exp, *ring_len_exp, *ring_set_exp;
+    int epoch;
 };
 // max_active: capacity of the list and of the pair workspace (the count read
 // on the device is clamped to it); n_rows: the neurons of the bundle or window
@@ -60,7 +69,7 @@ struct LlgFreshRows {
 int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, const RowFmt &f,
                        const int32_t *slot_of, const float *d_x, const int32_t *d_active,
                        const int32_t *d_n_active, int max_active, int n_rows, int act,
-                       float *d_out, uint8_t *ws, const LlgFreshRows *fresh = nullptr);
+                       float *d_out, uint8_t *ws, const LlgWinUpd *win = nullptr);
 
 // Dense quantized matvec y[rows] = act(W . x) (llg_ffn.hip); act < 0 = none.
 // part: room for llg_matvec_part_bytes(w, act) (column-chunked rows keep

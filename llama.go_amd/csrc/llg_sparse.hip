@@ -36,11 +36,13 @@
 #include "llg_common.hpp"
 #include "llg_internal.hpp"
 #include "llg_pred_tile.hpp"
+#include "llg_window_upd.hpp"
 
 #define XS_STRIDE 36      // floats per staged 32-float x block (bank-conflict-free)
 #define BATCH 4           // blocks whose loads a lane issues together
 #define PRED_SPLIT_N 8    // partials per hidden unit written by k_pred_hidden
 #define DN_THREADS 512    // k_sparse_down workgroup: one tile (or list stride) per thread
+#define WIN_XWG 8         // workgroups that take the folded window update's side work
 
 __device__ __forceinline__ void stage_x(float *xs, const float *__restrict__ x, int nb) {
     llg_stage_x_sum<XS_STRIDE>(xs, x, nb);
@@ -190,29 +192,39 @@ __device__ __forceinline__ void row_dotn(const uint8_t *__restrict__ base, long 
 }
 
 // B. explicit list: pair j = (row of active[j], act(up . x)).
-// With src (windowed rows): a neuron n with fresh[n] == epoch (loaded by this
-// token's update) is read from row n of src, and its whole bundle is copied
-// to its resident row on the way (the gather of loadRows, window.go:207-245,
-// done by the first reader).
-// (base and dst are the same buffer then: base is not __restrict__.)  FR
-// selects that form (fr.src set), which holds the copies in registers.
 // The count read on the device is clamped to the pair capacity `cap`, and a
 // neuron outside [0, n_rows) counts as absent (activation 0), so no list
 // makes the kernel read or write out of bounds.
-template <int T, bool FR>
+// WIN (the window's update + FFN step): the first half of the folded update
+// (llg_window_upd.hpp): lane 0 of each entry's wavefront records, marks and
+// counts it, and a listed neuron that is not resident is read from row n of
+// u.src and its whole bundle copied to row n of the resident buffer (base) on
+// the way (the gather of loadRows, window.go:207-245); the last WIN_XWG
+// workgroups take the expiring set.  The pair's row is then n (the down
+// launch reads every listed neuron from its resident row).
+template <int T, bool WIN>
 __global__ __launch_bounds__(256) void k_list_up(
     const uint8_t *base, long long bstride, RowFmt f, const int32_t *__restrict__ slot_of,
     const float *__restrict__ x, const int32_t *__restrict__ active,
     const int32_t *__restrict__ n_active_p, int cap, int n_rows, int act,
-    int2 *__restrict__ pairs, LlgFreshRows fr) {
+    int2 *__restrict__ pairs, LlgWinUpd u) {
     extern __shared__ float xs[];
     const int n_active = min(max(*n_active_p, 0), cap);
+    if constexpr (WIN) {
+        // the last WIN_XWG workgroups take the expiring set, beside the list
+        const int gl = (int)gridDim.x - WIN_XWG;
+        if ((int)blockIdx.x >= gl) {
+            win_expire_all(u, n_active, n_rows, (blockIdx.x - gl) * blockDim.x + threadIdx.x,
+                           WIN_XWG * blockDim.x);
+            return;
+        }
+    }
     const int first = blockIdx.x * 4;
     if (first >= n_active) return;  // whole workgroup idle: skip the x staging
     stage_x(xs, x, f.nb);
     __syncthreads();
     const int lane = threadIdx.x & 63;
-    const int stride = gridDim.x * 4;
+    const int stride = ((int)gridDim.x - (WIN ? WIN_XWG : 0)) * 4;
     for (int j = first + (threadIdx.x >> 6); j < n_active; j += 2 * stride) {
         const int j1 = j + stride;
         auto neuron = [&](int jj) {
@@ -221,35 +233,43 @@ __global__ __launch_bounds__(256) void k_list_up(
         };
         const int n0 = neuron(j);
         const int n1 = j1 < n_active ? neuron(j1) : -1;
-        const int row0 = n0 < 0 ? -1 : (slot_of ? slot_of[n0] : n0);
-        const int row1 = n1 < 0 ? -1 : (slot_of ? slot_of[n1] : n1);
+        int row0, row1;
         float s0, s1;
-        if constexpr (FR) {
-            const int r0 = __builtin_amdgcn_readfirstlane(row0);
-            const int r1 = __builtin_amdgcn_readfirstlane(row1);
-            const bool f0 = __builtin_amdgcn_readfirstlane(r0 >= 0 && fr.fresh[n0] == fr.epoch);
-            const bool f1 = __builtin_amdgcn_readfirstlane(r1 >= 0 && fr.fresh[n1] == fr.epoch);
-            const uint8_t *p0 = f0 ? fr.src + (long long)n0 * bstride
-                                   : base + (long long)(r0 >= 0 ? r0 : 0) * bstride;
-            const uint8_t *p1 = f1 ? fr.src + (long long)n1 * bstride
-                                   : base + (long long)(r1 >= 0 ? r1 : 0) * bstride;
+        if constexpr (WIN) {
+            row0 = __builtin_amdgcn_readfirstlane(n0);
+            row1 = __builtin_amdgcn_readfirstlane(n1);
+            int ld0 = 0, ld1 = 0;
+            if (lane == 0) {
+                ld0 = win_note_active(u, j, n0);
+                if (j1 < n_active) ld1 = win_note_active(u, j1, n1);
+            }
+            const bool f0 = __builtin_amdgcn_readfirstlane(ld0);
+            const bool f1 = __builtin_amdgcn_readfirstlane(ld1);
+            const uint8_t *p0 = (f0 ? u.src : base) + (long long)(row0 >= 0 ? row0 : 0) * bstride;
+            const uint8_t *p1 = (f1 ? u.src : base) + (long long)(row1 >= 0 ? row1 : 0) * bstride;
             const int n16 = (int)(bstride >> 4);
             constexpr int NC = bc_first<T>();
             const bc_u4 *sp0 = reinterpret_cast<const bc_u4 *>(p0);
             const bc_u4 *sp1 = reinterpret_cast<const bc_u4 *>(p1);
-            bc_u4 *dp0 = reinterpret_cast<bc_u4 *>(fr.dst + (long long)(f0 ? r0 : 0) * bstride);
-            bc_u4 *dp1 = reinterpret_cast<bc_u4 *>(fr.dst + (long long)(f1 ? r1 : 0) * bstride);
+            bc_u4 *dp0 = reinterpret_cast<bc_u4 *>(u.dst + (long long)(f0 ? row0 : 0) * bstride);
+            bc_u4 *dp1 = reinterpret_cast<bc_u4 *>(u.dst + (long long)(f1 ? row1 : 0) * bstride);
             BundleCopy<NC> c0, c1;
             if (f0) bc_issue(c0, sp0, n16);
             if (f1) bc_issue(c1, sp1, n16);
             // the copies are stored once the dot's loads are in flight
-            row_dot2p<T>(p0, p1, r0 >= 0, r1 >= 0, f, xs, s0, s1, [&]() {
+            row_dot2p<T>(p0, p1, row0 >= 0, row1 >= 0, f, xs, s0, s1, [&]() {
                 if (f0) bc_store(c0, dp0, n16);
                 if (f1) bc_store(c1, dp1, n16);
             });
             if (f0) bc_rest<NC>(sp0, dp0, n16);
             if (f1) bc_rest<NC>(sp1, dp1, n16);
+            if (lane == 0) {
+                if (f0) win_note_load(u, n0);
+                if (f1) win_note_load(u, n1);
+            }
         } else {
+            row0 = n0 < 0 ? -1 : (slot_of ? slot_of[n0] : n0);
+            row1 = n1 < 0 ? -1 : (slot_of ? slot_of[n1] : n1);
             row_dot2<T>(base, bstride, row0, row1, f, xs, s0, s1);
         }
         if (lane == 0) {  // a non-resident row keeps activation 0 (window.go:150-152)
@@ -765,12 +785,24 @@ __device__ __forceinline__ void dn_list(const uint8_t *__restrict__ base, long l
 // Down products over a plain pair list pairs[0..*count) (the count is
 // clamped to `cap`), split evenly over the threads.  Workgroup = output block
 // b (32 outputs): out[32 b + e] = sum over the pairs of u * down_row[32 b +
-// e], the wavefronts' sums added in order.
-template <int T>
+// e], the wavefronts' sums added in order.  WIN: the last WIN_XWG workgroups
+// take the second half of the folded window update (llg_window_upd.hpp).
+template <int T, bool WIN>
 __global__ __launch_bounds__(DN_THREADS) void k_sparse_down(
     const uint8_t *__restrict__ base, long long bstride, RowFmt f, const int2 *__restrict__ pairs,
-    const int32_t *__restrict__ count_p, int cap, int per_xcd, float *__restrict__ out) {
+    const int32_t *__restrict__ count_p, int cap, int n_rows, int per_xcd, float *__restrict__ out,
+    LlgWinUpd u) {
     __shared__ float red[DN_THREADS / 64][32];
+    if constexpr (WIN) {
+        // the last WIN_XWG workgroups finish the window update, beside the
+        // down products
+        const int gd = (int)gridDim.x - WIN_XWG;
+        if ((int)blockIdx.x >= gd) {
+            win_finish_all(u, min(max(*count_p, 0), cap), n_rows,
+                           (blockIdx.x - gd) * blockDim.x + threadIdx.x, WIN_XWG * blockDim.x);
+            return;
+        }
+    }
     const int b = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     if (b >= f.nb) return;  // uniform over the workgroup
     const int tid = threadIdx.x, bd = blockDim.x, lane = tid & 63, wave = tid >> 6;
@@ -812,41 +844,45 @@ static int down_threads(int items) {
     return t < 64 ? 64 : (t > DN_THREADS ? DN_THREADS : t);
 }
 
-template <int T>
+template <int T, bool WIN>
 static void launch_down(hipStream_t st, const uint8_t *base, long long bstride, const RowFmt &f,
-                        const int2 *pairs, const int32_t *count, int max_pairs, float *out) {
+                        const int2 *pairs, const int32_t *count, int max_pairs, int n_rows,
+                        float *out, const LlgWinUpd &u) {
     const int px = down_per_xcd(f);
-    hipLaunchKernelGGL((k_sparse_down<T>), dim3(8 * px), dim3(down_threads(max_pairs)), 0, st, base,
-                       bstride, f, pairs, count, max_pairs, px, out);
+    hipLaunchKernelGGL((k_sparse_down<T, WIN>), dim3(8 * px + (WIN ? WIN_XWG : 0)),
+                       dim3(down_threads(max_pairs)), 0, st, base, bstride, f, pairs, count,
+                       max_pairs, n_rows, px, out, u);
 }
 
 template <int T>
 static void launch_list(hipStream_t st, const uint8_t *base, long long bstride, const RowFmt &f,
                         const int32_t *slot_of, const float *x, const int32_t *active,
                         const int32_t *n_active, int max_active, int n_rows, int act,
-                        float *out, int2 *pairs, const LlgFreshRows &fr) {
+                        float *out, int2 *pairs, const LlgWinUpd *win) {
     int grid = (max_active + 3) / 4;
     if (grid < 1) grid = 1;
     if (grid > 2048) grid = 2048;
-    if (fr.src)
-        hipLaunchKernelGGL((k_list_up<T, true>), dim3(grid), dim3(256), xs_bytes(f), st, base,
+    const LlgWinUpd u = win ? *win : LlgWinUpd{};
+    if (win) {
+        hipLaunchKernelGGL((k_list_up<T, true>), dim3(grid + WIN_XWG), dim3(256), xs_bytes(f), st, base,
                            bstride, f, slot_of, x, active, n_active, max_active, n_rows, act,
-                           pairs, fr);
-    else
+                           pairs, u);
+        launch_down<T, true>(st, base, bstride, f, pairs, n_active, max_active, n_rows, out, u);
+    } else {
         hipLaunchKernelGGL((k_list_up<T, false>), dim3(grid), dim3(256), xs_bytes(f), st, base,
                            bstride, f, slot_of, x, active, n_active, max_active, n_rows, act,
-                           pairs, fr);
-    launch_down<T>(st, base, bstride, f, pairs, n_active, max_active, out);
+                           pairs, u);
+        launch_down<T, false>(st, base, bstride, f, pairs, n_active, max_active, n_rows, out, u);
+    }
 }
 
 int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, const RowFmt &f,
                        const int32_t *slot_of, const float *d_x, const int32_t *d_active,
                        const int32_t *d_n_active, int max_active, int n_rows, int act,
-                       float *d_out, uint8_t *ws, const LlgFreshRows *fresh) {
+                       float *d_out, uint8_t *ws, const LlgWinUpd *win) {
     if (int rc = llg_check_act(d, act)) return rc;
-    const LlgFreshRows fr = fresh ? *fresh : LlgFreshRows{nullptr, nullptr, 0, nullptr};
-    if (fr.src && (!slot_of || !fr.fresh || !fr.dst || (bstride & 15)))
-        return llg_set_error(d, LLG_E_ARG, "sparse ffn: windowed rows need slots and tags");
+    if (win && (!win->src || win->dst != base || (bstride & 15)))
+        return llg_set_error(d, LLG_E_ARG, "sparse ffn: the window step reads its resident rows");
     if (xs_bytes(f) > 64 * 1024)
         return llg_set_error(d, LLG_E_ARG, "sparse ffn: hidden size %d too large", f.cols);
     hipStream_t st = llg_dev_stream(d);
@@ -854,19 +890,19 @@ int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, con
     switch (f.type) {
     case LLG_TYPE_Q4_0:
         launch_list<LLG_TYPE_Q4_0>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                   max_active, n_rows, act, d_out, pairs, fr);
+                                   max_active, n_rows, act, d_out, pairs, win);
         break;
     case LLG_TYPE_Q8_0:
         launch_list<LLG_TYPE_Q8_0>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                   max_active, n_rows, act, d_out, pairs, fr);
+                                   max_active, n_rows, act, d_out, pairs, win);
         break;
     case LLG_TYPE_F16:
         launch_list<LLG_TYPE_F16>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                  max_active, n_rows, act, d_out, pairs, fr);
+                                  max_active, n_rows, act, d_out, pairs, win);
         break;
     case LLG_TYPE_F32:
         launch_list<LLG_TYPE_F32>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                  max_active, n_rows, act, d_out, pairs, fr);
+                                  max_active, n_rows, act, d_out, pairs, win);
         break;
     default:
         return llg_set_error(d, LLG_E_TYPE, "sparse ffn: unsupported type %d", f.type);
