@@ -43,11 +43,12 @@ Q4_ROW = H // 32 * 18                # 2556 B per GGUF Q4_0 row
 BUNDLE_ALG = 2 * Q4_ROW              # 5112 B per neuron (unpadded)
 PRED_BYTES = (RANK * H + FF * RANK) * 4
 # HBM bytes per sparse step from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE over
-# k_pred_hidden + k_tile_up + k_sparse_down, each counter scaled by its reading
+# k_pred_hidden + k_tile_ffn + k_tile_reduce, each counter scaled by its reading
 # for a 1 GiB streaming copy (FETCH x2.0, WRITE x1.0), measured on this bench
-# line (exactly 909 active neurons per step); the summary with the commands is
-# profiles/sparse_step_falcon7b_q4_0_hbm_traffic.md.
-SPARSE_STEP_TRAFFIC = 18.23e6
+# line (exactly 909 active neurons per step): the weights once plus the
+# workgroups' partial outputs written and read back; the summary with the
+# commands is profiles/sparse_step_falcon7b_q4_0_hbm_traffic.md.
+SPARSE_STEP_TRAFFIC = 22.15e6
 SPARSE_STEP_TRAFFIC_ACTIVE = 909
 
 
@@ -171,7 +172,7 @@ def bench_sparse(args, torch, llg, dev):
                                 "predictor logit", "batch": 1,
                    "layer_copies_rotated": L, "step": "predict+select+gathered up/down FFN"},
         "roofline": {"bound": "hbm",
-                     "kernel": "k_pred_hidden + k_tile_up + k_sparse_down (one decode step)",
+                     "kernel": "k_pred_hidden + k_tile_ffn + k_tile_reduce (one decode step)",
                      "achieved": step_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": step_gbs / HBM_PEAK_GBS, "traffic": SPARSE_STEP_TRAFFIC,
                      "traffic_active_neurons": SPARSE_STEP_TRAFFIC_ACTIVE,
@@ -634,9 +635,10 @@ def bench_falcon(args, torch, llg, dev):
                       "prompt_tokens": F4_PROMPT, "generated_tokens": n_gen,
                       "prefill_ms": prefill_ms, "prefill_tokens_per_s": F4_PROMPT / prefill_ms * 1e3,
                       "mean_active_per_layer": mean_act},
-           "roofline": {"bound": "hbm", "kernel": "one decode token: 32 x (k_resid_norm, "
-                        "k_matvec_q qkv, k_attn, k_matvec_q wo, k_pred_hidden, k_tile_up, "
-                        "k_sparse_down) + k_resid_norm, k_matvec_q lm head, k_argmax",
+           "roofline": {"bound": "hbm", "kernel": "one decode token: k_embed, 32 x (k_matvec_q "
+                        "qkv with the LayerNorm prologue, k_attn, k_matvec_q wo with the "
+                        "attention merge and the predictor fold, k_tile_ffn, k_tile_reduce) + "
+                        "k_resid_norm, k_matvec_q lm head, k_argmax",
                         "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": gbs / HBM_PEAK_GBS, "traffic": None, "alg_bytes_per_step": alg,
                         "avg_step_us": ms * 1e3}}
