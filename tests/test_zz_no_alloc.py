@@ -83,9 +83,9 @@ def test_noalloc_matches_allocating_entry(dev):
 
 
 def test_noalloc_rejects_workload_above_scratch(dev):
-    """d_ff 65536 needs 1024 tiles x 64 pair slots, more than the fixed
-    scratch holds: the allocation-free entry point refuses the layer, the
-    allocating one runs it."""
+    """d_ff 65536 at h 2048 needs 1024 partial rows of 2048 floats (8 MiB) beside
+    the predictor's partials, more than the fixed scratch holds: the
+    allocation-free entry point refuses the layer, the allocating one runs it."""
     h, ff, rank = 2048, 65536, 16
     g = torch.Generator(device="cuda")
     g.manual_seed(20261)
