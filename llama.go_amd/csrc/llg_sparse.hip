@@ -861,7 +861,7 @@ static void launch_list(hipStream_t st, const uint8_t *base, long long bstride, 
                         float *out, int2 *pairs, const LlgWinUpd *win) {
     int grid = (max_active + 3) / 4;
     if (grid < 1) grid = 1;
-    if (grid > 2048) grid = 2048;
+    if (grid > 512) grid = 512;
     const LlgWinUpd u = win ? *win : LlgWinUpd{};
     if (win) {
         hipLaunchKernelGGL((k_list_up<T, true>), dim3(grid + WIN_XWG), dim3(256), xs_bytes(f), st, base,
