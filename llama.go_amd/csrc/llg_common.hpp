@@ -624,36 +624,37 @@ struct LlgAttnParts {
 // Stage the merged attention output, x[c] = sum_s acc_s[c] e_s / sum_s l_s e_s
 // with e_s = exp(m_s - max_s m_s) for the head of column c (0 for an empty
 // split), like llg_stage_x_sum (the nb blocks from block cb0).  Each thread
-// requests its columns of every split (two float4 groups at a time) before
-// merging them; issue() runs after the first requests.
-template <int XS, class Issue = LlgNoIssue>
+// requests its columns of every split (KB float4 groups at a time) before
+// merging them; issue() runs after the first requests.  KB: float4 groups
+// per thread in a round.
+template <int XS, int KB = 2, class Issue = LlgNoIssue>
 __device__ __forceinline__ void llg_stage_attn(float *xs, const LlgAttnParts &ap, int cb0, int nb,
                                                Issue &&issue = Issue()) {
     static_assert(XS >= 33, "room for the block sum");
-    constexpr int KB = 2;
     const int n4 = nb * 8, cols = ap.n_heads * ap.head_dim;
     const int lane = threadIdx.x & 63, base0 = threadIdx.x - lane, bd = blockDim.x;
     const float4 *acc4 = reinterpret_cast<const float4 *>(ap.acc);
     const float2 *ml2 = reinterpret_cast<const float2 *>(ap.ml);
-    for (int k0 = 0; base0 + k0 * bd < n4; k0 += KB) {
-        float4 a[KB][LLG_ATTN_SPLIT_MAX];
-        float2 ml[KB][LLG_ATTN_SPLIT_MAX];
+    float4 a[KB][LLG_ATTN_SPLIT_MAX];
+    float2 ml[KB][LLG_ATTN_SPLIT_MAX];
+    // Every split slot is loaded (a slot past n_split reads split 0 again
+    // and is skipped in the merge), and the first round by every wavefront
+    // with clamped indices: straight-line loads stay ahead of the caller's.
+    auto load = [&](int k0) {
 #pragma unroll
         for (int k = 0; k < KB; k++) {
             const int i = min(base0 + (k0 + k) * bd + lane, n4 - 1);
             const int c = cb0 * 32 + 4 * i;
             const int h = c / ap.head_dim;
 #pragma unroll
-            for (int s = 0; s < LLG_ATTN_SPLIT_MAX; s++)
-                if (s < ap.n_split) {
-                    a[k][s] = acc4[((size_t)s * cols + c) >> 2];
-                    ml[k][s] = ml2[s * ap.n_heads + h];
-                }
+            for (int s = 0; s < LLG_ATTN_SPLIT_MAX; s++) {
+                const int sc = s < ap.n_split ? s : 0;
+                a[k][s] = acc4[((size_t)sc * cols + c) >> 2];
+                ml[k][s] = ml2[sc * ap.n_heads + h];
+            }
         }
-        if (k0 == 0) {
-            __builtin_amdgcn_sched_barrier(0);  // keep the caller's loads behind these
-            issue();
-        }
+    };
+    auto merge = [&](int k0) {
 #pragma unroll
         for (int k = 0; k < KB; k++) {
             float M = ml[k][0].x;
@@ -679,8 +680,15 @@ __device__ __forceinline__ void llg_stage_attn(float *xs, const LlgAttnParts &ap
             v.w *= rl;
             llg_x_sum_store<XS>(xs, v, base0 + (k0 + k) * bd + lane, n4);
         }
+    };
+    load(0);
+    __builtin_amdgcn_sched_barrier(0);  // keep the caller's loads behind these
+    issue();
+    merge(0);
+    for (int k0 = KB; base0 + k0 * bd < n4; k0 += KB) {
+        load(k0);
+        merge(k0);
     }
-    if (base0 >= n4) issue();  // a wavefront with no columns still issues its loads
 }
 
 // Sum over the workgroup (every thread gets it); red: LDS, one float per
@@ -696,6 +704,18 @@ __device__ __forceinline__ float llg_block_sum(float v, float *red) {
     return s;
 }
 
+// llg_block_sum over a slot no thread has read yet (red: one float per
+// wavefront): one barrier.
+__device__ __forceinline__ float llg_block_sum_fresh(float v, float *red) {
+    v = llg_wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = 0; i < nw; i++) s += red[i];
+    return s;
+}
+
 // Residual add + LayerNorm as the prologue of a matvec over the normed row
 // (tensor/ops.go:138-165, residual order of ffn_flash.go:161-166):
 // v = (x_in + a1) + a2 (a1, a2 may be null), normed = (v - mean) / std * w + b
@@ -703,12 +723,38 @@ __device__ __forceinline__ float llg_block_sum(float v, float *red) {
 // XS floats per 32-element block and the block sum at [32], like
 // llg_stage_x_sum; workgroup 0 also writes v to x_out and normed to
 // normed_out.  n is a multiple of 32.
+//
+// stats (optional, with a1 = a2 = null and n <= 32 * LLG_LN_STATS_PER * 64):
+// per 32-element block b of x_in, (sum, sum of squared deviations from the
+// block mean), as written by the kernel that produced x_in.  Every wavefront
+// then merges them itself (the parallel form of the two-pass variance:
+// mean = sum / n, M2 = sum_b M2_b + 32 (mean_b - mean)^2), so the prologue
+// needs no workgroup reduction.
+#define LLG_LN_STATS_PER 4
 struct LlgLnArgs {
     const float *x_in, *a1, *a2, *w, *b;
     float *x_out, *normed_out;
+    const float2 *stats;
     float eps;
     int n;
 };
+
+// (sum, M2) of the 32 values v[0..3] held by each of 8 consecutive lanes
+// (lanes 8 j .. 8 j + 7 hold one block): the lane-pair sums in a fixed
+// butterfly order, so every lane of the group gets the same result.
+__device__ __forceinline__ float2 llg_block32_stats(const float4 &v) {
+    float s = (v.x + v.y) + (v.z + v.w);
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    s += __shfl_xor(s, 4, 64);
+    const float m = s / 32.0f;
+    const float d0 = v.x - m, d1 = v.y - m, d2 = v.z - m, d3 = v.w - m;
+    float q = (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+    q += __shfl_xor(q, 1, 64);
+    q += __shfl_xor(q, 2, 64);
+    q += __shfl_xor(q, 4, 64);
+    return make_float2(s, q);
+}
 
 // A matvec over attn with the predictor's first matrix folded in: p is
 // WUp . Wo ([rank x cols] f32), and wavefront task (j, s) stores
@@ -724,7 +770,8 @@ struct LlgPredFold {
 
 // NP = float4 groups per thread (n <= 4 * NP * blockDim.x): every load of the
 // residual terms and of w and b is issued before the first use, so the
-// prologue costs one memory round trip plus the two block reductions.
+// prologue costs one memory round trip plus the two block reductions (one
+// barrier each: red holds 2 floats per wavefront, unread before the call).
 // issue() as in llg_stage_x_sum.
 template <int XS, int NP, class Issue = LlgNoIssue>
 __device__ __forceinline__ void llg_stage_ln(float *xs, const LlgLnArgs &a, float *red,
@@ -737,7 +784,9 @@ __device__ __forceinline__ void llg_stage_ln(float *xs, const LlgLnArgs &a, floa
     const float4 *w4 = reinterpret_cast<const float4 *>(a.w);
     const float4 *b4 = reinterpret_cast<const float4 *>(a.b);
     const bool w0 = blockIdx.x == 0;
+    const int lane = tid & 63, nbk = a.n >> 5;
     float4 v[NP], p[NP], q[NP], wv[NP], bv[NP];
+    float2 st[LLG_LN_STATS_PER];
 #pragma unroll
     for (int k = 0; k < NP; k++) {
         const int i = min(tid + k * bd, n4 - 1);
@@ -746,6 +795,10 @@ __device__ __forceinline__ void llg_stage_ln(float *xs, const LlgLnArgs &a, floa
         if (q4) q[k] = q4[i];
         wv[k] = w4[i];
         bv[k] = b4[i];
+    }
+    if (a.stats) {
+#pragma unroll
+        for (int k = 0; k < LLG_LN_STATS_PER; k++) st[k] = a.stats[min(lane + 64 * k, nbk - 1)];
     }
     __builtin_amdgcn_sched_barrier(0);  // keep the caller's loads behind these
     issue();
@@ -766,14 +819,33 @@ __device__ __forceinline__ void llg_stage_ln(float *xs, const LlgLnArgs &a, floa
             if (w0 && a.x_out) reinterpret_cast<float4 *>(a.x_out)[i] = v[k];
         }
     }
-    const float mean = llg_block_sum(s, red) / (float)a.n;
-    float qs = 0.0f;
+    float mean, var;
+    if (a.stats) {
+        // this wavefront merges the block statistics (same order in every one)
+        float sm = 0.0f;
 #pragma unroll
-    for (int k = 0; k < NP; k++) {
-        const float d0 = v[k].x - mean, d1 = v[k].y - mean, d2 = v[k].z - mean, d3 = v[k].w - mean;
-        if (tid + k * bd < n4) qs += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+        for (int k = 0; k < LLG_LN_STATS_PER; k++)
+            if (lane + 64 * k < nbk) sm += st[k].x;
+        mean = llg_wave_sum(sm) / (float)a.n;
+        float m2 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < LLG_LN_STATS_PER; k++)
+            if (lane + 64 * k < nbk) {
+                const float d = st[k].x / 32.0f - mean;
+                m2 += st[k].y + 32.0f * d * d;
+            }
+        var = llg_wave_sum(m2) / (float)a.n;
+    } else {
+        mean = llg_block_sum_fresh(s, red) / (float)a.n;
+        float qs = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NP; k++) {
+            const float d0 = v[k].x - mean, d1 = v[k].y - mean, d2 = v[k].z - mean,
+                        d3 = v[k].w - mean;
+            if (tid + k * bd < n4) qs += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+        }
+        var = llg_block_sum_fresh(qs, red + (blockDim.x >> 6)) / (float)a.n;
     }
-    const float var = llg_block_sum(qs, red) / (float)a.n;
     const float sd = (float)sqrt((double)var + (double)a.eps);
 #pragma unroll
     for (int k = 0; k < NP; k++) {

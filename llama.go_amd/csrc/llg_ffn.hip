@@ -55,7 +55,7 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
     static_assert(!AC || (LNP == 0 && !G), "the attention merge replaces the plain x");
     constexpr int RW = G ? 1 : MV_ROWS;  // output rows per wavefront pass
     extern __shared__ float xs[];
-    __shared__ float red[NT / 64];
+    __shared__ float red[2 * (NT / 64)];
     const int n_chunks = (f.nb + chunk_blocks - 1) / chunk_blocks;
     const int tile = blockIdx.x / n_chunks;
     const int ch = blockIdx.x % n_chunks;
@@ -124,6 +124,12 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
         for (int k = 0; k < MV_PFL; k++) pr[k] = row[min(lane + 64 * k, max(nq, 1) - 1)];
     };
     auto issue_first = [&]() {
+        // Every wavefront calls this once, right after requesting its staging
+        // loads: the barrier (no wait on memory) puts the staging loads of the
+        // whole workgroup ahead of any weight load.  A CU returns vector loads
+        // in request order, so otherwise a wavefront's x (or LayerNorm inputs)
+        // would arrive behind the weights of the wavefronts before it.
+        __builtin_amdgcn_s_barrier();
         issue(min(r_first, r_end - 1), 0);
         if constexpr (PF)
             if (ft0 < n_tasks) fold_issue(ft0);
@@ -131,7 +137,8 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
     if constexpr (LNP > 0)  // x is the LayerNorm of the residual sum (one chunk: cb0 = 0)
         llg_stage_ln<MV_XS, LNP>(xs, ln, red, issue_first);
     else if constexpr (AC)
-        llg_stage_attn<MV_XS>(xs, ap, cb0, cnb, issue_first);
+        // Q8_0's 1024-thread instance has registers for one group per round
+        llg_stage_attn<MV_XS, T == LLG_TYPE_Q8_0 ? 1 : 2>(xs, ap, cb0, cnb, issue_first);
     else
         llg_stage_x_sum<MV_XS>(xs, x + (size_t)cb0 * 32, cnb, issue_first);
     __syncthreads();
@@ -412,6 +419,8 @@ int llg_matvec_ln_enqueue(LlgDevice *d, const LlgObject *w, const LlgLnArgs &ln,
         return llg_set_error(d, LLG_E_ARG, "matvec: LayerNorm length %d != %d", ln.n, w->fmt.cols);
     if (ln.n > 256 * 16 * 4)
         return llg_set_error(d, LLG_E_ARG, "matvec: LayerNorm length %d above 16384", ln.n);
+    if (ln.stats && (ln.a1 || ln.a2 || ln.n % 32 || ln.n > 32 * 64 * LLG_LN_STATS_PER))
+        return llg_set_error(d, LLG_E_ARG, "matvec: block statistics for a LayerNorm of %d", ln.n);
     return matvec_launch(d, w, nullptr, -1, d_y, nullptr, &ln);
 }
 

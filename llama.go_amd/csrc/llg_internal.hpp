@@ -94,12 +94,14 @@ size_t llg_fused_ws_bytes(int rank, int ff, int nb);
 int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
                       LlgObject *b, const float *d_a, const float *d_x, float thr, int act,
                       float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws,
-                      const float *d_out_add = nullptr);
+                      const float *d_out_add = nullptr, float2 *d_stats = nullptr);
 // The same after the hidden partials are in ws (llg_pred_ws_layout): the
 // tile kernel and the partial-sum kernel; accumulate: d_out += the FFN output.
+// d_stats (optional): per 32 outputs, (sum, M2) of d_out as written (LlgLnArgs).
 int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgObject *b,
                            const float *d_x, float thr, int act, float *d_out,
-                           int32_t *d_active, int32_t *d_n_active, uint8_t *ws, bool accumulate);
+                           int32_t *d_active, int32_t *d_n_active, uint8_t *ws, bool accumulate,
+                           float2 *d_stats = nullptr);
 
 // MoE prefill as grouped MFMA GEMMs (llg_moe_gemm.hip).
 bool llg_moe_gemm_supported(int type, int hidden, int eff, int n_tok);

@@ -62,6 +62,11 @@ struct LlgModel {
     float *mvpart;  // partial sums of a column-chunked Wo or LM-head matvec
     float *attn_ml;  // attention splits' (max, sum); attn holds their acc rows
     float2 *rope;  // [max_seq x head_dim/2] (cos, sin)
+    // per 32 elements of x, (sum, M2) as the kernel that last wrote x left them
+    // (k_embed, then each layer's partial-sum kernel), for the next QKV
+    // LayerNorm prologue; null when hidden is not a multiple of 32 or above
+    // what the prologue merges per wavefront
+    float2 *rstats;
     int32_t *token, *n_active, *act_scratch;
     uint8_t *ws;
 };
@@ -86,15 +91,30 @@ void llg_model_destroy(LlgDevice *d, LlgObject *o) {
 }
 
 // ---------------------------------------------------------------------------
-__global__ void k_embed(const uint8_t *__restrict__ emb, long long stride, RowFmt f,
-                        const int32_t *__restrict__ token, int vocab, float *__restrict__ x) {
+// x = dequant(embedding row of the token), 4 elements per thread; with stats
+// (cols a multiple of 32) also each 32-element block's (sum, M2), from the 8
+// lanes that hold it.
+#define EMBED_THREADS 256
+__global__ __launch_bounds__(EMBED_THREADS) void k_embed(
+    const uint8_t *__restrict__ emb, long long stride, RowFmt f,
+    const int32_t *__restrict__ token, int vocab, float *__restrict__ x,
+    float2 *__restrict__ stats) {
     // a token id outside the table would be a slice-bounds panic in the
     // reference; the host entry points reject it, the device loop only feeds
     // argmax results (< vocab)
     const int t = min(max(*token, 0), vocab - 1);
     const uint8_t *row = emb + (long long)t * stride;
-    for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < f.cols; c += gridDim.x * blockDim.x)
-        x[c] = llg_dequant_elem(row, f, c);
+    const int c0 = 4 * (blockIdx.x * EMBED_THREADS + threadIdx.x);
+    float e[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        e[k] = c0 + k < f.cols ? llg_dequant_elem(row, f, c0 + k) : 0.0f;
+        if (c0 + k < f.cols) x[c0 + k] = e[k];
+    }
+    if (stats) {  // uniform: every lane takes part in the block sums
+        const float2 bs = llg_block32_stats(make_float4(e[0], e[1], e[2], e[3]));
+        if ((threadIdx.x & 7) == 0 && c0 < f.cols) stats[c0 >> 5] = bs;
+    }
 }
 
 
@@ -550,8 +570,9 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
     const int qkv_rows = (m.n_heads + 2 * m.n_kv) * m.head_dim;
     (void)qkv_rows;
     float *r = m.x;  // the residual stream
-    hipLaunchKernelGGL(k_embed, dim3((m.hidden + 255) / 256), dim3(256), 0, st, m.embed->d,
-                       m.embed->stride, m.embed->fmt, token_in, m.vocab, r);
+    hipLaunchKernelGGL(k_embed, dim3((m.hidden + 4 * EMBED_THREADS - 1) / (4 * EMBED_THREADS)),
+                       dim3(EMBED_THREADS), 0, st, m.embed->d, m.embed->stride, m.embed->fmt,
+                       token_in, m.vocab, r, m.rstats);
     for (int l = 0; l < m.n_layers; l++) {
         const LlgModelLayer &L = m.layers[l];
         LlgLnArgs ln;
@@ -562,6 +583,7 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
         ln.w = reinterpret_cast<const float *>(L.norm_w->d);
         ln.b = reinterpret_cast<const float *>(L.norm_b->d);
         ln.normed_out = m.normed;
+        ln.stats = m.rstats;
         ln.eps = m.eps;
         ln.n = m.hidden;
         int rc = llg_matvec_ln_enqueue(d, L.wqkv, ln, m.qkv);
@@ -591,7 +613,7 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
                 return rc;
             rc = llg_fused_tail_enqueue(d, L.pwout, nullptr, L.bundle, m.normed, L.thr, m.act, r,
                                         nullptr, n_active_out ? n_active_out + l : nullptr, m.ws,
-                                        true);
+                                        true, m.rstats);
             if (rc) return rc;
             continue;
         }
@@ -606,7 +628,7 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
         // r += attn_out by its first kernel, then r += the FFN output
         rc = llg_fused_enqueue(d, L.pwup, L.pwout, nullptr, L.bundle, m.attn_out, m.normed, L.thr,
                                m.act, r, nullptr, n_active_out ? n_active_out + l : nullptr, m.ws,
-                               m.attn_out);
+                               m.attn_out, m.rstats);
         if (rc) return rc;
     }
     const float *fw = reinterpret_cast<const float *>(m.out_w->d);
@@ -719,6 +741,8 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     const size_t v_ff = llg_align((long long)(m->ff + 4) * 4, 256);
     const size_t v_pl = llg_align((long long)m->n_layers * m->ff * 4, 256);
     const size_t v_rope = llg_align((long long)m->max_seq * m->head_dim / 2 * 8, 256);
+    const bool use_stats = m->hidden % 32 == 0 && m->hidden <= 32 * 64 * LLG_LN_STATS_PER;
+    const size_t v_st = use_stats ? llg_align((long long)(m->hidden / 32) * 8, 256) : 0;
     const size_t wsb = model_ws_bytes(*m);
     const int attn_dim = m->n_heads * m->head_dim;
     bool fold = true;
@@ -729,8 +753,8 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     for (const LlgModelLayer &L : m->layers) v_mp = std::max(v_mp, llg_matvec_part_bytes(L.wo, -1));
     v_mp = llg_align((long long)v_mp, 256);
     const size_t total =
-        3 * v_h + v_qkv + v_att + v_aml + v_log + v_kv + v_i + v_ff + v_pl + v_rope + v_mp + v_pf +
-        wsb;
+        3 * v_h + v_qkv + v_att + v_aml + v_log + v_kv + v_i + v_ff + v_pl + v_rope + v_st + v_mp +
+        v_pf + wsb;
     uint8_t *buf = nullptr;
     if (hipMalloc(&buf, total) != hipSuccess) return fail(LLG_E_NOMEM, "buffer allocation failed");
     uint8_t *p = buf;
@@ -751,6 +775,8 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     p += v_pl;
     m->rope = reinterpret_cast<float2 *>(p);
     p += v_rope;
+    m->rstats = use_stats ? reinterpret_cast<float2 *>(p) : nullptr;
+    p += v_st;
     m->mvpart = v_mp ? reinterpret_cast<float *>(p) : nullptr;
     p += v_mp;
     for (LlgModelLayer &L : m->layers) {

@@ -650,7 +650,9 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
 // batch issued together), then the 32 group sums are added pairwise in a
 // fixed tree, so the order is the same on every run.  With ACC the sum is
 // added to out (a residual), else stored.  Workgroup 0 also writes the number
-// of active neurons (the popcounts of the tile masks).
+// of active neurons (the popcounts of the tile masks).  stats (optional, cols
+// a multiple of 32): the block's (sum, M2) of the values written, for the
+// LayerNorm prologue of the next matvec over out (LlgLnArgs).
 #define TR_GROUPS 32
 #define TR_BATCH 5
 template <bool ACC>
@@ -658,7 +660,8 @@ __global__ __launch_bounds__(256) void k_tile_reduce(const float *__restrict__ p
                                                      int n_parts, int n_tiles, int cols,
                                                      const unsigned long long *__restrict__ mask,
                                                      int32_t *__restrict__ n_active_out,
-                                                     float *__restrict__ out) {
+                                                     float *__restrict__ out,
+                                                     float2 *__restrict__ stats) {
     __shared__ float4 red[TR_GROUPS][8];
     __shared__ int cnt[4];
     const int b = blockIdx.x, tid = threadIdx.x;
@@ -709,10 +712,17 @@ __global__ __launch_bounds__(256) void k_tile_reduce(const float *__restrict__ p
     }
     if (g == 0) {
         const float4 sum = red[0][c];
-        if (o + 0 < cols) out[o + 0] = ACC ? prev.x + sum.x : sum.x;
-        if (o + 1 < cols) out[o + 1] = ACC ? prev.y + sum.y : sum.y;
-        if (o + 2 < cols) out[o + 2] = ACC ? prev.z + sum.z : sum.z;
-        if (o + 3 < cols) out[o + 3] = ACC ? prev.w + sum.w : sum.w;
+        const float4 val = ACC ? make_float4(prev.x + sum.x, prev.y + sum.y, prev.z + sum.z,
+                                             prev.w + sum.w)
+                               : sum;
+        if (o + 0 < cols) out[o + 0] = val.x;
+        if (o + 1 < cols) out[o + 1] = val.y;
+        if (o + 2 < cols) out[o + 2] = val.z;
+        if (o + 3 < cols) out[o + 3] = val.w;
+        if (stats) {  // lanes 0-7 of wavefront 0 hold the block
+            const float2 bs = llg_block32_stats(val);
+            if (c == 0) stats[b] = bs;
+        }
     }
     if (n_active_out && b == 0 && tid == 0) *n_active_out = cnt[0] + cnt[1] + cnt[2] + cnt[3];
 }
@@ -930,7 +940,7 @@ template <int T>
 static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial,
                          const float *bias, float thr, LlgObject *b, const float *x, int act,
                          unsigned long long *mask, float *part, int32_t *n_active, float *out,
-                         bool accumulate) {
+                         bool accumulate, float2 *stats) {
     const int ff = wout->rows, rank = wout->fmt.cols;
     const int n_tiles = (ff + 63) / 64;
     const RowFmt &f = b->fmt;
@@ -944,11 +954,11 @@ static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial,
     if (accumulate)
         hipLaunchKernelGGL((k_tile_reduce<true>), dim3(f.nb), dim3(256), 0, st,
                            (const float *)part, pstride, n_parts, n_tiles, f.cols,
-                           (const unsigned long long *)mask, n_active, out);
+                           (const unsigned long long *)mask, n_active, out, stats);
     else
         hipLaunchKernelGGL((k_tile_reduce<false>), dim3(f.nb), dim3(256), 0, st,
                            (const float *)part, pstride, n_parts, n_tiles, f.cols,
-                           (const unsigned long long *)mask, n_active, out);
+                           (const unsigned long long *)mask, n_active, out, stats);
 }
 
 // ffnFlash path 2 on the device: k_pred_hidden, k_tile_ffn, k_tile_reduce,
@@ -957,7 +967,7 @@ static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial,
 int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
                       LlgObject *b, const float *d_a, const float *d_x, float thr, int act,
                       float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws,
-                      const float *d_out_add) {
+                      const float *d_out_add, float2 *d_stats) {
     if (int rc = llg_check_act(d, act)) return rc;
     float *partial;
     unsigned long long *mask;
@@ -971,14 +981,17 @@ int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *
                                      nullptr, d_out_add);
     if (rc) return rc;
     return llg_fused_tail_enqueue(d, wout, bias, b, d_x, thr, act, d_out, d_active, d_n_active,
-                                  ws, d_out_add != nullptr);
+                                  ws, d_out_add != nullptr, d_stats);
 }
 
 int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgObject *b,
                            const float *d_x, float thr, int act, float *d_out,
-                           int32_t *d_active, int32_t *d_n_active, uint8_t *ws, bool accum) {
+                           int32_t *d_active, int32_t *d_n_active, uint8_t *ws, bool accum,
+                           float2 *d_stats) {
     if (int rc = llg_check_act(d, act)) return rc;
     const RowFmt &f = b->fmt;
+    if (d_stats && f.cols % 32)
+        return llg_set_error(d, LLG_E_ARG, "predict_sparse: block statistics need 32 | %d", f.cols);
     const int ff = wout->rows, rank = wout->fmt.cols;
     const int n_tiles = (ff + 63) / 64;
     const size_t lds = f.type == LLG_TYPE_Q4_0 ? tile_lds_bytes<LLG_TYPE_Q4_0>(f, rank)
@@ -997,19 +1010,19 @@ int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgOb
     switch (f.type) {
     case LLG_TYPE_Q4_0:
         launch_fused<LLG_TYPE_Q4_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
-                                    d_n_active, d_out, accum);
+                                    d_n_active, d_out, accum, d_stats);
         break;
     case LLG_TYPE_Q8_0:
         launch_fused<LLG_TYPE_Q8_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
-                                    d_n_active, d_out, accum);
+                                    d_n_active, d_out, accum, d_stats);
         break;
     case LLG_TYPE_F16:
         launch_fused<LLG_TYPE_F16>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
-                                   d_n_active, d_out, accum);
+                                   d_n_active, d_out, accum, d_stats);
         break;
     case LLG_TYPE_F32:
         launch_fused<LLG_TYPE_F32>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
-                                   d_n_active, d_out, accum);
+                                   d_n_active, d_out, accum, d_stats);
         break;
     default:
         return llg_set_error(d, LLG_E_TYPE, "predict_sparse: unsupported type %d", f.type);
