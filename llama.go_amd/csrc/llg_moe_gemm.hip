@@ -42,6 +42,7 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 #ifndef GM_BD
 #define GM_BD 1                   // chunks of B loads in flight ahead of use
 #endif
+#define GM_STORE_STEP 2           // MFMA step of a chunk before which the next A is stored
 
 // ---------------------------------------------------------------------------
 // Grouping: pairs p = t*k + s sorted by expert (order within an expert is not
@@ -222,7 +223,7 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
     constexpr int UNR = NB % 2 == 0 ? NB : 2 * NB;  // loop unroll: static A buffer and B slot
     u32x4_t ra[4];
     u32x4_t bq[NB][NF];
-    uint32_t bd[NB][NF];
+    _Float16 bd[NB][NF];  // block scales as loaded (no conversion that would wait for them)
 #define GM_LOAD_A(c)                                                                             \
     _Pragma("unroll") for (int q = 0; q < NMS; q++) ra[q] =                                     \
         *reinterpret_cast<const u32x4_t *>(A + a_off[q] + (long long)(c) * GM_KC)
@@ -230,7 +231,7 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
     _Pragma("unroll") for (int f = 0; f < NF; f++) {                                             \
         const int blk = 4 * (c) + lg;                                                            \
         bq[slot][f] = *reinterpret_cast<const u32x4_t *>(brow[f] + blk * 16);                    \
-        bd[slot][f] = *reinterpret_cast<const unsigned short *>(brow[f] + d_off + blk * 2);      \
+        bd[slot][f] = *reinterpret_cast<const _Float16 *>(brow[f] + d_off + blk * 2);            \
     }
 #define GM_STORE_A(buf)                                                                          \
     _Pragma("unroll") for (int q = 0; q < NMS; q++) {                                           \
@@ -253,12 +254,23 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
     __syncthreads();
     // chunk c (the i-th of the slice): A in As[i & 1], B in slot i % NB.  First
     // the loads of A for chunk c + 1 and of B for chunk c + GM_BD are issued
-    // (past the end, the last chunk is reloaded and not used).
+    // (past the end, the last chunk is reloaded and not used).  A for chunk
+    // c + 1 goes to the free buffer after the chunk's second step (the buffer
+    // was last read in chunk c - 1, before the barrier that ended it): storing
+    // it at the end of the chunk, or under a condition, let the compiler move
+    // its loads down to the store and wait for every outstanding load there,
+    // the next chunks' B included.
     auto chunk = [&](int c, int buf, int slot) __attribute__((always_inline)) {
         GM_LOAD_A(min(c + 1, ce - 1));
         GM_LOAD_B(min(c + GM_BD, ce - 1), (slot + GM_BD) % NB);
+        __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the steps
 #pragma unroll
         for (int s = 0; s < 4; s++) {
+            if (s == GM_STORE_STEP) {  // the last chunk stores its reload, unread
+                __builtin_amdgcn_sched_barrier(0);
+                GM_STORE_A(buf ^ 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
             half8_t a[NMS];
 #pragma unroll
             for (int ms = 0; ms < NMS; ms++)
@@ -267,14 +279,12 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
 #pragma unroll
             for (int f = 0; f < NF; f++) {
                 const uint32_t w = bq[slot][f][s];
-                const half8_t b =
-                    q4_frag(w, __builtin_bit_cast(_Float16, (unsigned short)bd[slot][f]));
+                const half8_t b = q4_frag(w, bd[slot][f]);
 #pragma unroll
                 for (int ms = 0; ms < NMS; ms++)
                     acc[f][ms] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[ms], b, acc[f][ms], 0, 0, 0);
             }
         }
-        if (c + 1 < ce) GM_STORE_A(buf ^ 1);
         __syncthreads();
     };
     for (int c = c0; c < ce; c += UNR) {
