@@ -357,23 +357,29 @@ __global__ __launch_bounds__(256, MOE_P_BLOCKS) void k_moe_gateup_p(
     XSlice<2> xs;
     int t_x = ts_a / k;
     xslice_load<2>(xs, x + (size_t)t_x * f.cols, 0, f.nb);
+    // The next item's loads go out without a branch (past the range the last
+    // item is loaded again and not used), after any reload of x: the waits
+    // before an item's products then never cover the next item's loads (a
+    // load under a branch makes the compiler wait for all of them).
     for (int i = i0;;) {
         // A holds item i
-        if (i + 1 < i1) {
-            ts_b = (int)((i + 1) / per_ts);
-            if (ts_b != ts_e) e = ids[ts_e = ts_b];
-            gu_issue<T>(rb, gate, up, stride, f, (long long)e * eff + 2 * ((i + 1) % per_ts), bl0, bl1);
-        }
         if (ts_a / k != t_x) xslice_load<2>(xs, x + (size_t)(t_x = ts_a / k) * f.cols, 0, f.nb);
+        {
+            const int in = min(i + 1, i1 - 1);
+            ts_b = (int)(in / per_ts);
+            if (ts_b != ts_e) e = ids[ts_e = ts_b];
+            gu_issue<T>(rb, gate, up, stride, f, (long long)e * eff + 2 * (in % per_ts), bl0, bl1);
+        }
         gu_finish<T>(ra, xs, ok0, ok1, hbuf + (size_t)ts_a * eff + 2 * (i % per_ts));
         if (++i >= i1) break;
         // B holds item i
-        if (i + 1 < i1) {
-            ts_a = (int)((i + 1) / per_ts);
-            if (ts_a != ts_e) e = ids[ts_e = ts_a];
-            gu_issue<T>(ra, gate, up, stride, f, (long long)e * eff + 2 * ((i + 1) % per_ts), bl0, bl1);
-        }
         if (ts_b / k != t_x) xslice_load<2>(xs, x + (size_t)(t_x = ts_b / k) * f.cols, 0, f.nb);
+        {
+            const int in = min(i + 1, i1 - 1);
+            ts_a = (int)(in / per_ts);
+            if (ts_a != ts_e) e = ids[ts_e = ts_a];
+            gu_issue<T>(ra, gate, up, stride, f, (long long)e * eff + 2 * (in % per_ts), bl0, bl1);
+        }
         gu_finish<T>(rb, xs, ok0, ok1, hbuf + (size_t)ts_b * eff + 2 * (i % per_ts));
         if (++i >= i1) break;
     }
@@ -429,35 +435,37 @@ __global__ __launch_bounds__(256, MOE_P_BLOCKS) void k_moe_down_p(
     int sc_h = sc_a, ts_h = ts_e;
     XSlice<1> hs;
     xslice_load<1>(hs, hbuf + (size_t)ts_h * f.cols, (sc_h - ts_h * n_chunks) * 64, f.nb);
+    // next item's loads without a branch, after any reload of h (as in
+    // k_moe_gateup_p)
     for (int i = i0;;) {
-        if (i + 1 < i1) {
-            sc_b = (i + 1) / per_chunk;
-            const int tsb = sc_b / n_chunks;
-            if (tsb != ts_e) e = ids[ts_e = tsb];
-            dn_issue<T>(rb, down, stride, f,
-                        (long long)e * hidden + MOE_DN_P * (i + 1 - sc_b * per_chunk),
-                        min((sc_b - tsb * n_chunks) * 64 + lane, f.nb - 1));
-        }
         if (sc_a != sc_h) {
             sc_h = sc_a;
             ts_h = sc_a / n_chunks;
             xslice_load<1>(hs, hbuf + (size_t)ts_h * f.cols, (sc_h - ts_h * n_chunks) * 64, f.nb);
         }
+        {
+            const int in = min(i + 1, i1 - 1);
+            sc_b = in / per_chunk;
+            const int tsb = sc_b / n_chunks;
+            if (tsb != ts_e) e = ids[ts_e = tsb];
+            dn_issue<T>(rb, down, stride, f, (long long)e * hidden + MOE_DN_P * (in - sc_b * per_chunk),
+                        min((sc_b - tsb * n_chunks) * 64 + lane, f.nb - 1));
+        }
         dn_finish<T>(ra, hs, (sc_h - ts_h * n_chunks) * 64 + lane < f.nb,
                      part + (size_t)sc_h * hidden + MOE_DN_P * (i - sc_a * per_chunk));
         if (++i >= i1) break;
-        if (i + 1 < i1) {
-            sc_a = (i + 1) / per_chunk;
-            const int tsa = sc_a / n_chunks;
-            if (tsa != ts_e) e = ids[ts_e = tsa];
-            dn_issue<T>(ra, down, stride, f,
-                        (long long)e * hidden + MOE_DN_P * (i + 1 - sc_a * per_chunk),
-                        min((sc_a - tsa * n_chunks) * 64 + lane, f.nb - 1));
-        }
         if (sc_b != sc_h) {
             sc_h = sc_b;
             ts_h = sc_b / n_chunks;
             xslice_load<1>(hs, hbuf + (size_t)ts_h * f.cols, (sc_h - ts_h * n_chunks) * 64, f.nb);
+        }
+        {
+            const int in = min(i + 1, i1 - 1);
+            sc_a = in / per_chunk;
+            const int tsa = sc_a / n_chunks;
+            if (tsa != ts_e) e = ids[ts_e = tsa];
+            dn_issue<T>(ra, down, stride, f, (long long)e * hidden + MOE_DN_P * (in - sc_a * per_chunk),
+                        min((sc_a - tsa * n_chunks) * 64 + lane, f.nb - 1));
         }
         dn_finish<T>(rb, hs, (sc_h - ts_h * n_chunks) * 64 + lane < f.nb,
                      part + (size_t)sc_h * hidden + MOE_DN_P * (i - sc_b * per_chunk));
