@@ -770,6 +770,28 @@ def test_falcon_forward(dev, rng, n_kv, t):
     m.release()
 
 
+def test_falcon_wide_hidden_layernorm_reduction(dev, rng):
+    """hidden 8224 (257 blocks) is above what the QKV LayerNorm merges from the
+    residual's block statistics, so the prologue forms the mean and variance
+    with workgroup reductions (and the LM head runs in column chunks);
+    against the oracle at every position (forward.go:258-301, ops.go:138-165)."""
+    d = dict(FALCON_GPU, hidden=8224, n_heads=4, n_kv=1, head_dim=64, ff=512, vocab=256,
+             rank=16, n_layers=1, max_seq=16)
+    w = make_falcon(rng, d, gg.Q4_0)
+    toks = rng.integers(0, d["vocab"], 6)
+    _, nact, thr = ref_falcon_f64(w, d, toks)
+    ref = R.Falcon(d, w, thr)
+    m = llg.FalconModel(dev, d, w, thr)
+    for s, tk in enumerate(toks):
+        lg, nxt, na = m.forward(int(tk), s)
+        rl, rn = ref.forward(int(tk), s)
+        assert np.array_equal(na, rn) and np.array_equal(na, nact[s]), (s, na, rn)
+        assert max_rel_err(lg, rl) <= TOL, s
+        if _top2_gap(rl) > 1e-3 * np.max(np.abs(rl)):
+            assert nxt == R.argmax(rl), s
+    m.release()
+
+
 def test_falcon_wide_heads_chunked_wo(dev, rng):
     """48 query heads of 128 over 4 KV heads: Wo's rows are 6144 wide, so its
     matvec runs in column chunks whose partial sums the model adds in order;
