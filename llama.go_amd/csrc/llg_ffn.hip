@@ -129,10 +129,12 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
         // whole workgroup ahead of any weight load.  A CU returns vector loads
         // in request order, so otherwise a wavefront's x (or LayerNorm inputs)
         // would arrive behind the weights of the wavefronts before it.
+        // The fold task's loads go before the weights: the fold is computed
+        // first, and its wait would otherwise cover every weight load.
         __builtin_amdgcn_s_barrier();
-        issue(min(r_first, r_end - 1), 0);
         if constexpr (PF)
             if (ft0 < n_tasks) fold_issue(ft0);
+        issue(min(r_first, r_end - 1), 0);
     };
     if constexpr (LNP > 0)  // x is the LayerNorm of the residual sum (one chunk: cb0 = 0)
         llg_stage_ln<MV_XS, LNP>(xs, ln, red, issue_first);
@@ -142,9 +144,9 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
     else
         llg_stage_x_sum<MV_XS>(xs, x + (size_t)cb0 * 32, cnb, issue_first);
     __syncthreads();
-    if constexpr (PF) {
-        for (int t = ft0; t < n_tasks; t += fstep) {
-            if (t != ft0) fold_issue(t);
+    // the fold task t from pr (x staged)
+    auto fold_dot = [&](int t) {
+        if constexpr (PF) {
             const int j = t / pf.n_split, sp = t % pf.n_split;
             const int nq = fold_nq(sp);
             const float *xb = xs + (size_t)sp * pf.split_blocks * MV_XS;
@@ -164,7 +166,19 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
             acc = llg_wave_sum(acc);
             if (lane == 0) pf.part[sp * pf.rank + j] = acc;
         }
-    }
+    };
+    // the first task's loads went out before the weights: its wait leaves them in flight
+    if constexpr (PF)
+        if (ft0 < n_tasks) fold_dot(ft0);
+    // a wavefront's further fold tasks (more tasks than wavefronts), after its
+    // rows: a load loop ahead of the dots would make them wait for every block
+    auto fold_rest = [&]() {
+        if constexpr (PF)
+            for (int t = ft0 + fstep; t < n_tasks; t += fstep) {
+                fold_issue(t);
+                fold_dot(t);
+            }
+    };
     // the dots of one kb step of the pass at r0 from the blocks in src
     auto dots = [&](const BlockRaw<T>(&src)[NR], int kb, int r0, float(&sv)[MV_ROWS]) {
         if constexpr (FLAT) {
@@ -217,6 +231,19 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
     };
     const int step = (int)(blockDim.x >> 6) * RW;
     constexpr int KSTEP = 64 * (FLAT ? MV_NI : MV_BATCH);
+    if (n_slots <= KSTEP && r_first + step >= r_end) {
+        // One pass of one step (every balanced launch), without the loops: at
+        // a loop head the compiler waits for every outstanding load, so the
+        // first dot would wait for the last block.  Here each dot waits for
+        // its own blocks only.
+        if (r_first < r_end) {
+            float sv[MV_ROWS] = {0.0f, 0.0f};
+            dots(r, 0, r_first, sv);
+            finish(sv, r_first);
+        }
+        fold_rest();
+        return;
+    }
     for (int r0 = r_first; r0 < r_end; r0 += step) {
         float sv[MV_ROWS] = {0.0f, 0.0f};
         for (int kb = 0; kb < n_slots; kb += KSTEP) {
@@ -225,6 +252,7 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
         }
         finish(sv, r0);
     }
+    fold_rest();
 }
 
 // y[r] = act(sum over the chunks c of part[c][r]), chunks in order.
