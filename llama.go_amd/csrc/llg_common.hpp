@@ -361,6 +361,22 @@ struct BlockRaw<LLG_TYPE_F32> {
     float4 q[8];
 };
 
+// r, or (keep false) a block whose dot is 0 for finite x: the scale (or
+// the values) zeroed by a select, so a dot can run unconditionally on every
+// lane and the compiler has no branch to move the block's loads into.
+template <int T>
+__device__ __forceinline__ void llg_block_keep(BlockRaw<T> &r, bool keep) {
+    if constexpr (T == LLG_TYPE_Q4_0 || T == LLG_TYPE_Q8_0) {
+        r.d = keep ? r.d : (unsigned short)0;
+    } else if constexpr (T == LLG_TYPE_F16) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.q[i] = keep ? r.q[i] : make_uint4(0u, 0u, 0u, 0u);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) r.q[i] = keep ? r.q[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
 template <int T>
 __device__ __forceinline__ void llg_block_load(BlockRaw<T> &r, const uint8_t *__restrict__ row,
                                                const RowFmt &f, int b);

@@ -144,11 +144,13 @@ constexpr int bc_first() {
     return T == LLG_TYPE_Q4_0 || T == LLG_TYPE_Q8_0 ? 5 : 1;
 }
 
-// Up-row dot products of NR rows (wavefront-uniform indices, < 0: none) by
-// one wavefront, NBATCH blocks per lane per pass, all loads of a pass issued
-// before any is used; same conventions as row_dot2.  issued(): called once,
-// when the first pass's loads are issued (before any is used).
-template <int T, int NR, int NBATCH, typename Issued = LlgNoIssue>
+// Up-row dot products of NR rows (wavefront-uniform indices, < 0: none, sum
+// unspecified) by one wavefront, NBATCH blocks per lane per pass, all loads
+// of a pass issued before any is used.  WHOLE: the caller guarantees that the
+// first pass reaches past block 64 (NBATCH - 1) (its batches before the last
+// are whole).  issued(): called once, when the first pass's loads are issued
+// (before any is used).
+template <int T, int NR, int NBATCH, bool WHOLE, typename Issued = LlgNoIssue>
 __device__ __forceinline__ void row_dotn(const uint8_t *__restrict__ base, long long bstride,
                                          const int (&row)[NR], const RowFmt &f, const float *xs,
                                          float (&s)[NR], Issued &&issued = Issued()) {
@@ -162,17 +164,43 @@ __device__ __forceinline__ void row_dotn(const uint8_t *__restrict__ base, long 
         p[q] = base + (long long)(v[q] ? r : 0) * bstride;
         s[q] = 0.0f;
     }
-    for (int b0 = 0; b0 < f.nb; b0 += 64 * NBATCH) {
-        BlockRaw<T> r[NBATCH][NR];
+    using Pass = BlockRaw<T>[NBATCH][NR];
+    auto load = [&](Pass &r, int b0) {
 #pragma unroll
         for (int i = 0; i < NBATCH; i++)
 #pragma unroll
             for (int q = 0; q < NR; q++)
                 llg_block_load<T>(r[i][q], p[q], f, min(b0 + lane + 64 * i, f.nb - 1));
-        if (b0 == 0) {
-            __builtin_amdgcn_sched_barrier(0);  // issued() stays behind these loads
-            issued();
+    };
+    {
+        // The first pass straight-line, issued() right behind its loads, and
+        // no dot under a condition: lanes past the row's end (only in the last
+        // batch, if WHOLE) dot the clamped copy with its scale zeroed
+        // (llg_block_keep).  A fixed number of
+        // loads then follows each block, so each dot waits for its own
+        // blocks; a conditional dot would let the compiler sink its loads
+        // behind issued()'s (or a loop head would wait for all).  The sum of
+        // a row < 0 is left unspecified (the caller drops it).
+        Pass r;
+        load(r, 0);
+        __builtin_amdgcn_sched_barrier(0);  // issued() stays behind these loads
+        issued();
+#pragma unroll
+        for (int i = 0; i < NBATCH; i++) {
+            const int b = lane + 64 * i;
+            const float *xb = xs + min(b, f.nb - 1) * XS_STRIDE;
+            const float4 *x4 = reinterpret_cast<const float4 *>(xb);
+#pragma unroll
+            for (int q = 0; q < NR; q++) {
+                BlockRaw<T> rb = r[i][q];
+                if (!WHOLE || i == NBATCH - 1) llg_block_keep<T>(rb, b < f.nb);
+                s[q] += llg_raw_dot<T>(rb, x4, xb[32]);
+            }
         }
+    }
+    for (int b0 = 64 * NBATCH; b0 < f.nb; b0 += 64 * NBATCH) {  // rows past 64 NBATCH blocks
+        Pass r;
+        load(r, b0);
 #pragma unroll
         for (int i = 0; i < NBATCH; i++) {
             const int b = b0 + lane + 64 * i;
@@ -180,10 +208,7 @@ __device__ __forceinline__ void row_dotn(const uint8_t *__restrict__ base, long 
                 const float *xb = xs + b * XS_STRIDE;
                 const float4 *x4 = reinterpret_cast<const float4 *>(xb);
 #pragma unroll
-                for (int q = 0; q < NR; q++) {
-                    const float d = llg_raw_dot<T>(r[i][q], x4, xb[32]);
-                    s[q] += v[q] ? d : 0.0f;
-                }
+                for (int q = 0; q < NR; q++) s[q] += llg_raw_dot<T>(r[i][q], x4, xb[32]);
             }
         }
     }
@@ -314,24 +339,36 @@ __device__ __forceinline__ float dn_wave_transpose_sum(const float (&v)[32]) {
 // first nw wavefronts: active neuron k = k0 + wave + nw*i (i < NR) of the
 // tile on this wavefront, ul[k] = act(up . x).  issued(): called once this
 // wavefront's loads of the round are issued (at once when it has no row).
-template <int T, int NR, typename Issued = LlgNoIssue>
+// FIRST: the first round (its own copy of the dot per row length).
+template <int T, int NR, bool FIRST, typename Issued = LlgNoIssue>
 __device__ __forceinline__ void tile_u_round(const uint8_t *__restrict__ base, long long bstride,
                                              const RowFmt &f, const float *xs, const int *tl,
                                              int cnt, int k0, int tile0, int act, float *ul,
                                              int nw, Issued &&issued = Issued()) {
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int rows[NR];
 #pragma unroll
     for (int i = 0; i < NR; i++) {
         const int k = k0 + wave + nw * i;
-        rows[i] = k < cnt ? tile0 + tl[k] : -1;
+        rows[i] = __builtin_amdgcn_readfirstlane(k < cnt ? tile0 + tl[k] : -1);
     }
     if (rows[0] < 0) {  // wavefront-uniform: nothing in this round
         issued();
         return;
     }
     float s[NR];
-    row_dotn<T, NR, 3>(base, bstride, rows, f, xs, s, issued);
+    if constexpr (FIRST) {
+        // batches per pass: the fewest whose first pass reaches the row's end
+        // (at most 3), so only the last batch has lanes past it
+        if (f.nb > 128)
+            row_dotn<T, NR, 3, true>(base, bstride, rows, f, xs, s, issued);
+        else if (f.nb > 64)
+            row_dotn<T, NR, 2, true>(base, bstride, rows, f, xs, s, issued);
+        else
+            row_dotn<T, NR, 1, true>(base, bstride, rows, f, xs, s, issued);
+    } else {  // further rounds (more active neurons than wavefronts): one copy
+        row_dotn<T, NR, 3, false>(base, bstride, rows, f, xs, s, issued);
+    }
     if ((threadIdx.x & 63) == 0) {
 #pragma unroll
         for (int i = 0; i < NR; i++)
@@ -582,29 +619,35 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
     const uint8_t *dbase = base + f.stride;  // down row of neuron n: dbase + n * bstride
     QuarterRaw<T> dr[DK];
     // lane q of a down wavefront holds active neuron k0 + q's workgroup-local
-    // index (one LDS read per round; each row index is then a readlane)
-    int trow = lane < cnt ? tl[lane] : 0;
+    // index (one LDS read per round; each row index is then a readlane); in
+    // the first round the lanes past the count repeat the last active neuron
+    int trow = cnt > 0 ? tl[min(lane, cnt - 1)] : 0;
     // the first quarter block's down bytes of the first DK active neurons,
     // requested right after this wavefront's up-row loads, so that they
     // arrive in the round of the up rows (address clamped for the lanes past
-    // the last quarter block)
+    // the last quarter block).  All DK slots are requested, a slot past the
+    // active count rereading the last active neuron's lines (the tile's first
+    // row if none is active): with a fixed number of loads behind the up row,
+    // its dot waits for the up row alone, where a count-dependent number made
+    // it wait for every down load.
     auto issue_down = [&]() {
-        if (wave >= n_uw) {
-            const int ic = min(j, n_qb - 1);
+        const int ic = min(j, n_qb - 1);
 #pragma unroll
-            for (int k = 0; k < DK; k++) {
-                if (k < cnt) {
-                    const int n = n0 + __builtin_amdgcn_readlane(trow, k);
-                    quarter_load<T>(dr[k], dbase + (long long)n * bstride, f, ic >> 2, ic & 3);
-                }
-            }
+        for (int k = 0; k < DK; k++) {
+            const int n = n0 + __builtin_amdgcn_readlane(trow, k);
+            quarter_load<T>(dr[k], dbase + (long long)n * bstride, f, ic >> 2, ic & 3);
         }
     };
     // up rows: every wavefront takes active neuron k = wave (+ 16 per further
-    // round, which a workgroup needs for more than 16 active neurons)
-    tile_u_round<T, 1>(base, bstride, f, xs, tl, cnt, 0, n0, act, ul, NW, issue_down);
+    // round, which a workgroup needs for more than 16 active neurons).  The
+    // down and the up-only wavefronts have separate copies of the first
+    // round, each with its own fixed count of loads behind the up row.
+    if (wave >= n_uw)
+        tile_u_round<T, 1, true>(base, bstride, f, xs, tl, cnt, 0, n0, act, ul, NW, issue_down);
+    else
+        tile_u_round<T, 1, true>(base, bstride, f, xs, tl, cnt, 0, n0, act, ul, NW);
     for (int k0 = NW; k0 < cnt; k0 += NW)
-        tile_u_round<T, 1>(base, bstride, f, xs, tl, cnt, k0, n0, act, ul, NW);
+        tile_u_round<T, 1, false>(base, bstride, f, xs, tl, cnt, k0, n0, act, ul, NW);
     __syncthreads();
     if (wave < n_uw) return;  // uniform per wavefront (no barrier follows)
     for (int i = j; i - j < n_qb; i += dstep) {  // uniform bound: every lane runs each pass
