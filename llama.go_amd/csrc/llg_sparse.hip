@@ -696,7 +696,7 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
 // of active neurons (the popcounts of the tile masks).  stats (optional, cols
 // a multiple of 32): the block's (sum, M2) of the values written, for the
 // LayerNorm prologue of the next matvec over out (LlgLnArgs).
-#define TR_GROUPS 32
+#define TR_GROUPS 32  // the tree below is written for 32 groups
 #define TR_BATCH 5
 template <bool ACC>
 __global__ __launch_bounds__(256) void k_tile_reduce(const float *__restrict__ part, int pstride,
@@ -710,54 +710,86 @@ __global__ __launch_bounds__(256) void k_tile_reduce(const float *__restrict__ p
     const int b = blockIdx.x, tid = threadIdx.x;
     const int c = tid & 7, g = tid >> 3;
     const int o = b * 32 + 4 * c;
-    float4 prev = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (ACC && g == 0) {  // early, off the path
-        if (o + 0 < cols) prev.x = out[o + 0];
-        if (o + 1 < cols) prev.y = out[o + 1];
-        if (o + 2 < cols) prev.z = out[o + 2];
-        if (o + 3 < cols) prev.w = out[o + 3];
-    }
-    int na = 0;
-    if (n_active_out && b == 0)
-        for (int i = tid; i < n_tiles; i += 256) na += __popcll(mask[i]);
     const float4 *p = reinterpret_cast<const float4 *>(part + b * 32) + c;
     const int ps4 = pstride / 4;
+    // v with every bit cleared unless keep (an exact 0 or v, by an AND the
+    // compiler cannot turn into a branch, so no load is sunk into one)
+    auto keep4 = [](float4 v, bool keep) {
+        const uint32_t m = keep ? 0xFFFFFFFFu : 0u;
+        uint32_t r[4];
+        const uint32_t x[4] = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
+                               __float_as_uint(v.w)};
+#pragma unroll
+        for (int k = 0; k < 4; k++) asm("v_and_b32 %0, %1, %2" : "=v"(r[k]) : "v"(x[k]), "v"(m));
+        return make_float4(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[2]),
+                           __uint_as_float(r[3]));
+    };
+    // The first batch of partial rows, straight-line and first: a loop head
+    // would wait for every earlier load, and loads requested before these
+    // would return ahead of them.
+    float4 v[TR_BATCH];
+#pragma unroll
+    for (int i = 0; i < TR_BATCH; i++)
+        v[i] = p[(long long)min(g + TR_GROUPS * i, n_parts - 1) * ps4];
+    // the residual (stored by group 0), behind the partial rows; requested by
+    // every wavefront, so that each has the same count of loads to wait on
+    __builtin_amdgcn_sched_barrier(0);
+    float4 prev = make_float4(0.f, 0.f, 0.f, 0.f);
+    if constexpr (ACC)
+        prev = make_float4(out[min(o + 0, cols - 1)], out[min(o + 1, cols - 1)],
+                           out[min(o + 2, cols - 1)], out[min(o + 3, cols - 1)]);
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int t0 = g; t0 < n_parts; t0 += TR_GROUPS * TR_BATCH) {  // uniform over the workgroup
-        float4 v[TR_BATCH];
+#pragma unroll
+    for (int i = 0; i < TR_BATCH; i++) {  // rows in the order g, g + 32, ...
+        const float4 a = keep4(v[i], g + TR_GROUPS * i < n_parts);
+        s.x += a.x;
+        s.y += a.y;
+        s.z += a.z;
+        s.w += a.w;
+    }
+    for (int t0 = g + TR_GROUPS * TR_BATCH; t0 < n_parts; t0 += TR_GROUPS * TR_BATCH) {
 #pragma unroll
         for (int i = 0; i < TR_BATCH; i++)
             v[i] = p[(long long)min(t0 + TR_GROUPS * i, n_parts - 1) * ps4];
 #pragma unroll
         for (int i = 0; i < TR_BATCH; i++) {
-            if (t0 + TR_GROUPS * i < n_parts) {
-                s.x += v[i].x;
-                s.y += v[i].y;
-                s.z += v[i].z;
-                s.w += v[i].w;
-            }
+            const float4 a = keep4(v[i], t0 + TR_GROUPS * i < n_parts);
+            s.x += a.x;
+            s.y += a.y;
+            s.z += a.z;
+            s.w += a.w;
         }
     }
+    int na = 0;
+    if (n_active_out && b == 0)
+        for (int i = tid; i < n_tiles; i += 256) na += __popcll(mask[i]);
     red[g][c] = s;
     if (n_active_out && b == 0) {
         for (int d = 32; d > 0; d >>= 1) na += __shfl_xor(na, d, 64);
         if ((tid & 63) == 0) cnt[tid >> 6] = na;
     }
     __syncthreads();
-    // the group sums pairwise in a fixed tree (the same order on every run)
+    // The group sums pairwise in a fixed tree (the same order on every run):
+    // level h adds group g + h into g for g < h, h = 16, 8, 4, 2, 1.  Wavefront
+    // 0 (groups 0-7) forms levels 16 and 8 from LDS and the rest by shuffles
+    // (group g + h sits 8 h lanes up), so one barrier serves the whole tree.
+    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (tid < 64) {
+        auto add = [](float4 a, float4 v) {
+            return make_float4(a.x + v.x, a.y + v.y, a.z + v.z, a.w + v.w);
+        };
+        float4 t = add(add(red[g][c], red[g + 16][c]), add(red[g + 8][c], red[g + 24][c]));
 #pragma unroll
-    for (int hg = TR_GROUPS / 2; hg > 0; hg >>= 1) {
-        if (g < hg) {
-            const float4 a = red[g][c], v = red[g + hg][c];
-            red[g][c] = make_float4(a.x + v.x, a.y + v.y, a.z + v.z, a.w + v.w);
+        for (int h = 4; h > 0; h >>= 1) {
+            const float4 v = make_float4(__shfl_down(t.x, 8 * h, 64), __shfl_down(t.y, 8 * h, 64),
+                                         __shfl_down(t.z, 8 * h, 64), __shfl_down(t.w, 8 * h, 64));
+            t = add(t, v);
         }
-        __syncthreads();
+        sum = t;  // the tree's result in lanes 0-7 (group 0)
     }
+    const float4 val =
+        ACC ? make_float4(prev.x + sum.x, prev.y + sum.y, prev.z + sum.z, prev.w + sum.w) : sum;
     if (g == 0) {
-        const float4 sum = red[0][c];
-        const float4 val = ACC ? make_float4(prev.x + sum.x, prev.y + sum.y, prev.z + sum.z,
-                                             prev.w + sum.w)
-                               : sum;
         if (o + 0 < cols) out[o + 0] = val.x;
         if (o + 1 < cols) out[o + 1] = val.y;
         if (o + 2 < cols) out[o + 2] = val.z;
