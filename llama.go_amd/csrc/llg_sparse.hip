@@ -630,7 +630,11 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
     // row if none is active): with a fixed number of loads behind the up row,
     // its dot waits for the up row alone, where a count-dependent number made
     // it wait for every down load.
+    // Every wavefront passes one workgroup barrier (no memory wait) right
+    // after requesting its first up row: a CU returns loads in request order,
+    // so this puts every up row ahead of every down load.
     auto issue_down = [&]() {
+        __builtin_amdgcn_s_barrier();
         const int ic = min(j, n_qb - 1);
 #pragma unroll
         for (int k = 0; k < DK; k++) {
@@ -645,7 +649,8 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
     if (wave >= n_uw)
         tile_u_round<T, 1, true>(base, bstride, f, xs, tl, cnt, 0, n0, act, ul, NW, issue_down);
     else
-        tile_u_round<T, 1, true>(base, bstride, f, xs, tl, cnt, 0, n0, act, ul, NW);
+        tile_u_round<T, 1, true>(base, bstride, f, xs, tl, cnt, 0, n0, act, ul, NW,
+                                 [] { __builtin_amdgcn_s_barrier(); });
     for (int k0 = NW; k0 < cnt; k0 += NW)
         tile_u_round<T, 1, false>(base, bstride, f, xs, tl, cnt, k0, n0, act, ul, NW);
     __syncthreads();
