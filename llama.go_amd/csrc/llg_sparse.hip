@@ -44,8 +44,10 @@
 #define DN_THREADS 512    // k_sparse_down workgroup: one tile (or list stride) per thread
 #define WIN_XWG 8         // workgroups that take the folded window update's side work
 
-__device__ __forceinline__ void stage_x(float *xs, const float *__restrict__ x, int nb) {
-    llg_stage_x_sum<XS_STRIDE>(xs, x, nb);
+template <class Issue = LlgNoIssue>
+__device__ __forceinline__ void stage_x(float *xs, const float *__restrict__ x, int nb,
+                                        Issue &&issue = Issue()) {
+    llg_stage_x_sum<XS_STRIDE>(xs, x, nb, issue);
 }
 
 // Up-row dot products of two rows by one wavefront (row < 0: no row, result
@@ -234,6 +236,16 @@ __global__ __launch_bounds__(256) void k_list_up(
     const int32_t *__restrict__ n_active_p, int cap, int n_rows, int act,
     int2 *__restrict__ pairs, LlgWinUpd u) {
     extern __shared__ float xs[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int first = blockIdx.x * 4;
+    const int stride = ((int)gridDim.x - (WIN ? WIN_XWG : 0)) * 4;
+    // This wavefront's first pair of entries, requested with the count (an
+    // index past the count reads a list slot that is then not used), so the
+    // neurons are known one memory round earlier.
+    const int jf = first + wave;
+    const int a0 = cap > 0 ? active[min(jf, cap - 1)] : -1;
+    const int a1 = cap > 0 ? active[min(jf + stride, cap - 1)] : -1;
     const int n_active = min(max(*n_active_p, 0), cap);
     if constexpr (WIN) {
         // the last WIN_XWG workgroups take the expiring set, beside the list
@@ -244,32 +256,40 @@ __global__ __launch_bounds__(256) void k_list_up(
             return;
         }
     }
-    const int first = blockIdx.x * 4;
     if (first >= n_active) return;  // whole workgroup idle: skip the x staging
-    stage_x(xs, x, f.nb);
-    __syncthreads();
-    const int lane = threadIdx.x & 63;
-    const int stride = ((int)gridDim.x - (WIN ? WIN_XWG : 0)) * 4;
-    for (int j = first + (threadIdx.x >> 6); j < n_active; j += 2 * stride) {
+    auto valid = [&](int n) { return n >= 0 && n < n_rows ? n : -1; };
+    // One pair: entries j and j1 = j + stride (j < n_active), neurons m0, m1
+    // (-1 past the count or out of range).  note(): WIN records the entries
+    // and reads whether each must be loaded (lane 0); the list path reads
+    // the rows from slot_of.
+    struct Noted {
+        int row0, row1;
+        bool f0, f1;
+    };
+    auto note = [&](int j, int m0, int m1) {
+        Noted r{m0, m1, false, false};
+        if constexpr (WIN) {
+            int ld0 = 0, ld1 = 0;
+            if (lane == 0) {
+                ld0 = win_note_active(u, j, m0);
+                if (j + stride < n_active) ld1 = win_note_active(u, j + stride, m1);
+            }
+            r.f0 = __builtin_amdgcn_readfirstlane(ld0);
+            r.f1 = __builtin_amdgcn_readfirstlane(ld1);
+        } else {
+            r.row0 = m0 < 0 ? -1 : (slot_of ? slot_of[m0] : m0);
+            r.row1 = m1 < 0 ? -1 : (slot_of ? slot_of[m1] : m1);
+        }
+        return r;
+    };
+    auto pair = [&](int j, int m0, int m1, const Noted &nt) {
         const int j1 = j + stride;
-        auto neuron = [&](int jj) {
-            const int n = active[jj];
-            return n >= 0 && n < n_rows ? n : -1;
-        };
-        const int n0 = neuron(j);
-        const int n1 = j1 < n_active ? neuron(j1) : -1;
         int row0, row1;
         float s0, s1;
         if constexpr (WIN) {
-            row0 = __builtin_amdgcn_readfirstlane(n0);
-            row1 = __builtin_amdgcn_readfirstlane(n1);
-            int ld0 = 0, ld1 = 0;
-            if (lane == 0) {
-                ld0 = win_note_active(u, j, n0);
-                if (j1 < n_active) ld1 = win_note_active(u, j1, n1);
-            }
-            const bool f0 = __builtin_amdgcn_readfirstlane(ld0);
-            const bool f1 = __builtin_amdgcn_readfirstlane(ld1);
+            row0 = __builtin_amdgcn_readfirstlane(m0);
+            row1 = __builtin_amdgcn_readfirstlane(m1);
+            const bool f0 = nt.f0, f1 = nt.f1;
             const uint8_t *p0 = (f0 ? u.src : base) + (long long)(row0 >= 0 ? row0 : 0) * bstride;
             const uint8_t *p1 = (f1 ? u.src : base) + (long long)(row1 >= 0 ? row1 : 0) * bstride;
             const int n16 = (int)(bstride >> 4);
@@ -289,12 +309,12 @@ __global__ __launch_bounds__(256) void k_list_up(
             if (f0) bc_rest<NC>(sp0, dp0, n16);
             if (f1) bc_rest<NC>(sp1, dp1, n16);
             if (lane == 0) {
-                if (f0) win_note_load(u, n0);
-                if (f1) win_note_load(u, n1);
+                if (f0) win_note_load(u, m0);
+                if (f1) win_note_load(u, m1);
             }
         } else {
-            row0 = n0 < 0 ? -1 : (slot_of ? slot_of[n0] : n0);
-            row1 = n1 < 0 ? -1 : (slot_of ? slot_of[n1] : n1);
+            row0 = nt.row0;
+            row1 = nt.row1;
             row_dot2<T>(base, bstride, row0, row1, f, xs, s0, s1);
         }
         if (lane == 0) {  // a non-resident row keeps activation 0 (window.go:150-152)
@@ -302,6 +322,23 @@ __global__ __launch_bounds__(256) void k_list_up(
             if (j1 < n_active)
                 pairs[j1] = make_int2(row1, __float_as_int(row1 >= 0 ? llg_act(act, s1) : 0.0f));
         }
+    };
+    // The first pair is noted while x is in flight: its residency (or row)
+    // reads share x's memory round.
+    const bool has0 = jf < n_active;
+    const int m0 = has0 ? valid(a0) : -1;
+    const int m1 = jf + stride < n_active ? valid(a1) : -1;
+    Noted nt0{-1, -1, false, false};
+    stage_x(xs, x, f.nb, [&]() {
+        if (has0) nt0 = note(jf, m0, m1);
+    });
+    __syncthreads();
+    if (has0) pair(jf, m0, m1, nt0);
+    for (int j = jf + 2 * stride; j < n_active; j += 2 * stride) {
+        const int j1 = j + stride;
+        const int n0 = valid(active[j]);
+        const int n1 = j1 < n_active ? valid(active[j1]) : -1;
+        pair(j, n0, n1, note(j, n0, n1));
     }
 }
 
