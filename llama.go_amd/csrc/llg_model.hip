@@ -424,13 +424,19 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
     }
     __syncthreads();
     if (tid < HD) {  // this workgroup's (acc, m, l), merged with the other splits by the reader
+        static_assert(NW <= 64, "one wavefront partial per lane");
         float M = wm[0];
 #pragma unroll
         for (int w = 1; w < NW; w++) M = fmaxf(M, wm[w]);
+        // lane w takes partial w's weight once; the sums read it back with
+        // readlane in the order w = 0, 1, ... (the same values and order as
+        // every thread forming all NW exponentials itself)
+        const float mw = wm[min(lane, NW - 1)];
+        const float ew = mw == -INFINITY ? 0.0f : expf(mw - M);
         float L = 0.0f, R = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; w++) {
-            const float e = wm[w] == -INFINITY ? 0.0f : expf(wm[w] - M);
+            const float e = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ew), w));
             L += wl[w] * e;
             R += wacc[w][tid] * e;
         }
