@@ -23,7 +23,7 @@
 
 #define MV_ROWS 2
 #define MV_TILE_SMALL 8   // rows per workgroup: one pass of 4 wavefronts x MV_ROWS ...
-#define MV_MAX_WG 4096    // ... doubled (up to 32) while the grid has more workgroups than this
+#define MV_MAX_WG 8192    // ... doubled (up to 32) while the grid has more workgroups than this
 #define MV_SMALL_ROWS 8192
 #define MV_BAL_MIN 2048   // balanced launch from this many rows (at least 4 wavefronts per CU)
 #define MV_CHUNK 160      // max blocks of x staged per workgroup
@@ -393,7 +393,7 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
     // Rows per workgroup: one pass per wavefront (8 rows) gives the most
     // loads in flight; very tall matrices take 16 or 32 rows so that the grid
     // stays within MV_MAX_WG workgroups (an 18176-row Q4_0 matvec: 13.6 us at
-    // 8 rows, 15.2 at 16, 16.8 at 32; 65024 rows: 41.0, 38.7, 39.3).
+    // 8 rows, 15.2 at 16, 16.8 at 32; 65024 rows: 36.0 at 8, 36.2 at 16).
     int tr = MV_TILE_SMALL;
     while (tr < 32 && (long long)(w->rows + tr - 1) / tr * n_chunks > MV_MAX_WG) tr *= 2;
     a.tile_rows = tr / (up ? 2 : 1);
