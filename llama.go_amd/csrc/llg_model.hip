@@ -31,7 +31,8 @@
 // differ from WUp . attn_out by fp32 rounding only (a few ulps).  Models
 // whose Wo rows are too long for one workgroup's staged x keep the separate
 // hidden kernel on attn_out.
-//   k_resid_norm      output LayerNorm of r                    (ffn_flash.go:126-129)
+//   k_out_norm        output LayerNorm of r from its block     (ffn_flash.go:126-129)
+//                     statistics (k_resid_norm without them)
 //   k_matvec_q        logits = LMHead . normed                 (ffn_flash.go:130)
 //   k_argmax          next token = first index of the maximum  (generate.go:197-205)
 // The token comes from device memory, so a greedy decode loop never waits on
@@ -162,6 +163,48 @@ __global__ __launch_bounds__(NORM_THREADS) void k_resid_norm(
         const int i = tid + k * NORM_THREADS;
         if (i < n) out[i] = (v[k] - mean) / std_ * w[i] + b[i];
     }
+}
+
+// The output LayerNorm of r (ffn_flash.go:126-129) from r's block
+// statistics (each 32-element block's (sum, M2), left by the last layer's
+// k_tile_reduce), merged as in the QKV prologue (llg_stage_ln): every
+// wavefront merges the pairs in the same order, so no workgroup reduction is
+// needed and the row is spread over several workgroups, one float4 group per
+// thread.  n: a multiple of 32, at most 32 * 64 * LLG_LN_STATS_PER.
+#define ONORM_THREADS 256
+__global__ __launch_bounds__(ONORM_THREADS) void k_out_norm(const float *__restrict__ x,
+                                                            const float2 *__restrict__ stats,
+                                                            const float *__restrict__ w,
+                                                            const float *__restrict__ b, int n,
+                                                            float eps, float *__restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int nbk = n / 32, n4 = n / 4;
+    const int g = blockIdx.x * ONORM_THREADS + threadIdx.x;
+    const int i = min(g, n4 - 1);
+    const float4 v = reinterpret_cast<const float4 *>(x)[i];
+    const float4 wv = reinterpret_cast<const float4 *>(w)[i];
+    const float4 bv = reinterpret_cast<const float4 *>(b)[i];
+    float2 st[LLG_LN_STATS_PER];
+#pragma unroll
+    for (int k = 0; k < LLG_LN_STATS_PER; k++) st[k] = stats[min(lane + 64 * k, nbk - 1)];
+    float sm = 0.0f;
+#pragma unroll
+    for (int k = 0; k < LLG_LN_STATS_PER; k++)
+        if (lane + 64 * k < nbk) sm += st[k].x;
+    const float mean = llg_wave_sum(sm) / (float)n;
+    float m2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < LLG_LN_STATS_PER; k++)
+        if (lane + 64 * k < nbk) {
+            const float d = st[k].x / 32.0f - mean;
+            m2 += st[k].y + 32.0f * d * d;
+        }
+    const float var = llg_wave_sum(m2) / (float)n;
+    const float std_ = (float)sqrt((double)var + (double)eps);  // ops.go:159
+    if (g < n4)
+        reinterpret_cast<float4 *>(out)[i] =
+            make_float4((v.x - mean) / std_ * wv.x + bv.x, (v.y - mean) / std_ * wv.y + bv.y,
+                        (v.z - mean) / std_ * wv.z + bv.z, (v.w - mean) / std_ * wv.w + bv.w);
 }
 
 // Sum over each 16-lane row (all lanes of the row get the total).
@@ -639,6 +682,16 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
     }
     const float *fw = reinterpret_cast<const float *>(m.out_w->d);
     const float *fb = reinterpret_cast<const float *>(m.out_b->d);
+    if (m.rstats) {  // r's block statistics are there (the last layer's reduce left them)
+        hipLaunchKernelGGL(k_out_norm, dim3((m.hidden / 4 + ONORM_THREADS - 1) / ONORM_THREADS),
+                           dim3(ONORM_THREADS), 0, st, r, (const float2 *)m.rstats, fw, fb,
+                           m.hidden, m.eps, m.normed);
+        int rc = llg_matvec_enqueue(d, m.lm_head, m.normed, -1, m.logits, m.mvpart);
+        if (rc) return rc;
+        hipLaunchKernelGGL(k_argmax, dim3(1), dim3(AM_THREADS), 0, st, m.logits, m.vocab, token_out);
+        LLG_LAUNCH_CHECK(d, "model step");
+        return 0;
+    }
     const int np = (m.hidden + NORM_THREADS - 1) / NORM_THREADS;
 #define RN(NP)                                                                                    \
     hipLaunchKernelGGL((k_resid_norm<NP>), dim3(1), dim3(NORM_THREADS), 0, st, r,                 \
