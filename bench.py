@@ -638,7 +638,7 @@ def bench_falcon(args, torch, llg, dev):
            "roofline": {"bound": "hbm", "kernel": "one decode token: k_embed, 32 x (k_matvec_q "
                         "qkv with the LayerNorm prologue, k_attn, k_matvec_q wo with the "
                         "attention merge and the predictor fold, k_tile_ffn, k_tile_reduce) + "
-                        "k_resid_norm, k_matvec_q lm head, k_argmax",
+                        "k_out_norm, k_matvec_q lm head, k_argmax",
                         "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": gbs / HBM_PEAK_GBS, "traffic": None, "alg_bytes_per_step": alg,
                         "avg_step_us": ms * 1e3}}
