@@ -74,6 +74,11 @@ const char *llg_hip_last_error(LlgHipDevice dev);
 /* The hipStream_t (as void*) that llg_hipd_* calls enqueue on. */
 void *llg_hip_stream(LlgHipDevice dev);
 int llg_hip_sync(LlgHipDevice dev);
+/* Bytes of the handle's growable device workspace (0 until an entry point
+ * first needs one; it only grows, until llg_hip_free).  No counterpart in the
+ * reference: a diagnostic that lets a caller confirm that the
+ * allocation-free entry points left the workspace untouched. */
+int llg_hip_workspace_bytes(LlgHipDevice dev, size_t *bytes);
 
 /* ---- Metal-parity entry points: metal_bridge.h:12-20 -------------------- */
 /* y[rows] = W[rows*cols] @ x[cols], fp32 (llama_metal_matvec, used by

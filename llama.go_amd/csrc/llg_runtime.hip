@@ -304,6 +304,14 @@ void *llg_hip_stream(LlgHipDevice h) {
     return d ? reinterpret_cast<void *>(d->stream) : nullptr;
 }
 
+int llg_hip_workspace_bytes(LlgHipDevice h, size_t *bytes) {
+    LlgDevice *d = llg_dev(h);
+    if (!d) return LLG_E_NODEV;
+    if (!bytes) return llg_set_error(d, LLG_E_ARG, "workspace_bytes: null output");
+    *bytes = d->ws_bytes;
+    return 0;
+}
+
 int llg_hip_sync(LlgHipDevice h) {
     LlgDevice *d = llg_dev(h);
     if (!d) return LLG_E_NODEV;

@@ -90,10 +90,23 @@ static LlgWindow *get_window(LlgDevice *d, int64_t h) {
     return o ? reinterpret_cast<LlgWindow *>(o->ext) : nullptr;
 }
 
+// Number of the update after `e`.  Loads are counted in cntr[epoch & 1] and
+// each update clears the other counter for the next one, so consecutive
+// numbers must alternate in parity, across the wrap too: after 0x7FFFFFFF
+// (odd) comes 2, never 1 (0 stays "never listed").
+constexpr int llg_next_epoch(int e) { return e == 0x7FFFFFFF ? 2 : e + 1; }
+static_assert(llg_next_epoch(0) == 1 && llg_next_epoch(1) == 2, "updates are numbered from 1");
+static_assert(llg_next_epoch(0x7FFFFFFF) == 2 && llg_next_epoch(0x7FFFFFFE) == 0x7FFFFFFF,
+              "the wrap keeps 0 reserved");
+static_assert(((llg_next_epoch(0x7FFFFFFF) ^ 0x7FFFFFFF) & 1) &&
+                  ((llg_next_epoch(0x7FFFFFFE) ^ 0x7FFFFFFE) & 1) &&
+                  ((llg_next_epoch(llg_next_epoch(0x7FFFFFFF)) ^ llg_next_epoch(0x7FFFFFFF)) & 1),
+              "consecutive updates alternate in parity across the wrap");
+
 // The folded update of the next set: numbers it, and names its ring slot and
 // the expiring one.
 static LlgWinUpd next_update(LlgWindow *w) {
-    w->epoch = w->epoch == 0x7FFFFFFF ? 1 : w->epoch + 1;
+    w->epoch = llg_next_epoch(w->epoch);
     const int e = (w->head + 1) % (w->k + 1);  // the set of k updates ago
     const size_t ff = (size_t)w->ff;
     LlgWinUpd u;

@@ -64,6 +64,7 @@ _SIGS = {
     "llg_hip_last_error": (C.c_char_p, [_vp]),
     "llg_hip_stream": (_vp, [_vp]),
     "llg_hip_sync": (C.c_int, [_vp]),
+    "llg_hip_workspace_bytes": (C.c_int, [_vp, C.POINTER(C.c_size_t)]),
     "llg_hip_matvec": (C.c_int, [_vp, _vp, C.c_int, C.c_int, _vp, _vp]),
     "llg_hip_rmsnorm": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_float]),
     "llg_hip_upload_matrix": (C.c_int, [_vp, _vp, C.c_int, C.c_int, C.c_int, _i64p]),
@@ -188,6 +189,12 @@ class Device:
 
     def sync(self):
         self.check(self.lib.llg_hip_sync(self.h), "sync")
+
+    def workspace_bytes(self) -> int:
+        """Bytes of the handle's growable device workspace (0 until first needed)."""
+        n = C.c_size_t(0)
+        self.check(self.lib.llg_hip_workspace_bytes(self.h, C.byref(n)), "workspace_bytes")
+        return int(n.value)
 
     # -- Metal-parity calls -------------------------------------------------
     def mat_mul_vec(self, w, rows: int, cols: int, x) -> np.ndarray:

@@ -98,6 +98,47 @@ def make_falcon(rng, d: dict, t: int = gg.Q4_0, std: float = 0.05) -> dict:
     return w
 
 
+def make_falcon_gpu(seed: int, d: dict, t: int = gg.Q4_0, std: float = 0.02) -> dict:
+    """make_falcon's layout at full-model sizes, drawn and quantized on the GPU
+    (torch CUDA tensors for the matrices and predictors; host f32 for the
+    norms, which are random so that weight and bias count)."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    h, nh, nkv, hd, ff = d["hidden"], d["n_heads"], d["n_kv"], d["head_dim"], d["ff"]
+    V, r, L = d["vocab"], d["rank"], d["n_layers"]
+
+    def rnd(rows, cols, sd):
+        return torch.randn((rows, cols), generator=g, device="cuda", dtype=torch.float32) * sd
+
+    def q(rows, cols):
+        return gg.quantize(rnd(rows, cols, std), t)
+
+    w = {"embed": q(V, h), "lm_head": q(V, h),
+         "out_w": 1.0 + normal(rng, h, 0.1), "out_b": normal(rng, h, 0.1)}
+    for k in ["norm_w", "norm_b", "wq", "wk", "wv", "wo", "pwup", "pwout", "up", "down_t"]:
+        w[k] = []
+    for _ in range(L):
+        w["norm_w"].append(1.0 + normal(rng, h, 0.1))
+        w["norm_b"].append(normal(rng, h, 0.1))
+        w["wq"].append(q(nh * hd, h))
+        w["wk"].append(q(nkv * hd, h))
+        w["wv"].append(q(nkv * hd, h))
+        w["wo"].append(q(h, nh * hd))
+        w["pwup"].append(rnd(r, h, 0.05).contiguous())
+        w["pwout"].append(rnd(ff, r, 0.05).contiguous())
+        w["up"].append(q(ff, h))
+        w["down_t"].append(q(ff, h))
+    return w
+
+
+def to_host(w: dict) -> dict:
+    """The same weights as host numpy arrays (for the oracle)."""
+    def h(a):
+        return a.cpu().numpy() if hasattr(a, "is_cuda") else np.asarray(a)
+    return {k: ([h(x) for x in v] if isinstance(v, list) else h(v)) for k, v in w.items()}
+
+
 def _gap_threshold(lg: np.ndarray, frac: float) -> float:
     """A float32 threshold near the (1-frac) quantile of lg, at the midpoint of
     the widest gap between neighbouring values there (so selection does not

@@ -20,7 +20,9 @@ predictor logits near the 5% point over the whole sequence, chosen so that
 the device's and the oracle's logits fall on the same side of it; where,
 over millions of logits, a neuron still straddles it by fp32 noise, that
 position's selection is decided by rounding and it is exempt from the exact
-comparison (at most 20% of positions, one-layer models only)."""
+comparison (at most 20% of positions, one-layer models only): there the
+per-layer counts may differ by at most the number of straddling neurons and
+the logits must still agree within 1e-2 of the max-abs."""
 import numpy as np
 import pytest
 
@@ -76,7 +78,7 @@ def _calibrate(m: llg.FalconModel, d, w, toks, frac: float = 0.05):
     are exempt from the exact comparison)."""
     L = d["n_layers"]
     thr = np.full(L, 3.0e38, np.float32)
-    exempt = set()
+    exempt = {}
     for l in range(L):
         m.set_thresholds(thr)
         ref = R.Falcon(d, w, thr)
@@ -96,7 +98,8 @@ def _calibrate(m: llg.FalconModel, d, w, toks, frac: float = 0.05):
             pos, neu = flips[:, 0], flips[:, 1]
             dist = np.abs(o[pos, neu].astype(np.float64) - thr[l]) / np.max(np.abs(o[pos]), 1)
             assert np.all(dist <= 1e-4), (l, dist.max())
-            exempt.update(int(p) for p in pos)
+            for p in pos:
+                exempt.setdefault(int(p), np.zeros(L, np.int64))[l] += 1
     m.set_thresholds(thr)
     return thr, exempt
 
@@ -118,6 +121,12 @@ def _decode_vs_oracle(dev, d, w, n_pos, seed):
             rl, rn = ref.forward(int(tk), s)
             counts.append(rn)
             if s in exempt:
+                # the straddling neurons alone may differ: a count is off by at
+                # most the flips of its layer, and their products (a few
+                # activations at the threshold, so near zero) move the logits
+                # by far less than a looser bound
+                assert np.all(np.abs(na.astype(np.int64) - rn) <= exempt[s]), (s, na, rn)
+                assert max_rel_err(lg, rl) <= 10 * TOL, s
                 continue
             assert np.array_equal(na, rn), (s, na, rn)
             assert max_rel_err(lg, rl) <= TOL, s

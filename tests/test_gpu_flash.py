@@ -60,7 +60,7 @@ def set_threshold(pred, host, attn_out):
     return act
 
 
-@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0])
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16, gg.F32])
 def test_paths_without_window(dev, rng, t):
     layers, host, pred = build(dev, rng, t)
     ffn = FlashFFN(dev, layers, FlashFFNConfig(predictors=PredictorSet([None, pred])))

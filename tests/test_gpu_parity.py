@@ -158,43 +158,55 @@ def test_ffn_sparse_edge_cases(dev, rng):
     b.release()
 
 
-def test_ffn_predict_sparse_config0(dev, rng):
-    """Path 2 of ffnFlash: predictor + selection + gathered FFN in one call."""
+@pytest.mark.parametrize("t,bias", [(gg.Q4_0, False), (gg.Q4_0, True), (gg.F16, False),
+                                    (gg.F16, True), (gg.F32, False)])
+def test_ffn_predict_sparse_config0(dev, rng, t, bias):
+    """Path 2 of ffnFlash (ffn_flash.go:225-231): predictor + selection +
+    gathered FFN in one call at the config-0 shape with exactly 909 active
+    neurons.  Q4_0 rows are the config's; F16 and F32 bundles take the
+    fused kernel's wide-row layout (dtype.go:12-38 dequant).  With a bias the
+    logits are B.(A.x) + bias (predictor.go:69-73)."""
     h, ff, rank = 4544, 18176, 128
-    up = gpu_quant((ff, h), 0.02, 21, gg.Q4_0)
-    dn = gpu_quant((ff, h), 0.02, 22, gg.Q4_0)
+    up = gpu_quant((ff, h), 0.02, 21, t)
+    dn = gpu_quant((ff, h), 0.02, 22, t)
     wup, wout = normal(rng, (rank, h), 0.05), normal(rng, (ff, rank), 0.05)
+    bv = normal(rng, ff, 0.05) if bias else None
     x = normal(rng, h, 1.0)
-    _, lg = R.predict(wup, wout, None, x, 0.0)
+    _, lg = R.predict(wup, wout, bv, x, 0.0)
     thr = threshold_for(lg, 909)
-    ref_act, _ = R.predict(wup, wout, None, x, thr)
-    ref = R.ffn_sparse_load(up, dn, gg.Q4_0, h, ff, x, ref_act)
-    b = dev.upload_bundle(up, dn, gg.Q4_0, h, ff)
-    p = llg.Predictor(dev, wup, wout, None, thr)
+    ref_act, _ = R.predict(wup, wout, bv, x, thr)
+    assert ref_act.size == 909
+    ref = R.ffn_sparse_load(up, dn, t, h, ff, x, ref_act)
+    b = dev.upload_bundle(up, dn, t, h, ff)
+    p = llg.Predictor(dev, wup, wout, bv, thr)
     out, act = llg.ffn_predict_sparse(dev, p, b, x, x)
     assert np.array_equal(act, ref_act)
     assert max_rel_err(out, ref) <= TOL
     b.release()
 
 
-@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0])
-@pytest.mark.parametrize("h,ff,rank", [(256, 1024, 32), (160, 1000, 20)])
-def test_ffn_predict_sparse_densities(dev, rng, t, h, ff, rank):
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16, gg.F32])
+@pytest.mark.parametrize("h,ff,rank", [(256, 1024, 32), (160, 1000, 20), (4544, 2048, 128)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_ffn_predict_sparse_densities(dev, rng, t, h, ff, rank, bias):
     """The fused predictor -> selection -> gathered FFN at the extremes of
     density: no neuron (a zero output), about half of them (tiles with more
     active neurons than one round of up rows covers) and every neuron; the
-    second shape has a partial last tile and a hidden size of 5 blocks."""
+    second shape has a partial last tile and a hidden size of 5 blocks, the
+    third the config-0 hidden size (F16/F32: two passes of the down loop).
+    With a bias vector the logits carry it (predictor.go:69-73)."""
     up, dn = make_sparse_layer(rng, h, ff, t)
     wup, wout = normal(rng, (rank, h), 0.05), normal(rng, (ff, rank), 0.05)
+    bv = normal(rng, ff, 0.05) if bias else None
     x, a = normal(rng, h, 1.0), normal(rng, h, 1.0)
-    _, lg = R.predict(wup, wout, None, a, 0.0)
+    _, lg = R.predict(wup, wout, bv, a, 0.0)
     b = dev.upload_bundle(up, dn, t, h, ff)
     for n_target in (0, ff // 2, ff):
         thr = float(np.max(lg)) + 1.0 if n_target == 0 else (
             float(np.min(lg)) - 1.0 if n_target == ff else threshold_for(lg, n_target))
-        ref_act, _ = R.predict(wup, wout, None, a, thr)
+        ref_act, _ = R.predict(wup, wout, bv, a, thr)
         assert ref_act.size == n_target
-        p = llg.Predictor(dev, wup, wout, None, thr)
+        p = llg.Predictor(dev, wup, wout, bv, thr)
         out, act = llg.ffn_predict_sparse(dev, p, b, a, x)
         assert np.array_equal(act, ref_act), n_target
         ref = R.ffn_sparse_load(up, dn, t, h, ff, x, ref_act)

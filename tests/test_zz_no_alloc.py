@@ -82,6 +82,32 @@ def test_noalloc_matches_allocating_entry(dev):
         L["bundle"].release()
 
 
+def test_noalloc_first_on_fresh_handle_allocates_nothing():
+    """On a fresh device handle, whose workspace is still empty (uploads take
+    none), the allocation-free entry point runs first and leaves the workspace
+    at 0 bytes, twice; its results match the oracle.  The allocating entry
+    point, called only afterwards, then grows the workspace, which shows that
+    the first calls would have had to allocate through it."""
+    fresh = llg.Device()
+    try:
+        rng = np.random.default_rng(20262)
+        big = _layer(fresh, rng, 4544, 18176, 128, 909)
+        small = _layer(fresh, rng, 1024, 4096, 32, 205)
+        assert fresh.workspace_bytes() == 0
+        for L in (big, small):
+            rc, out, act = _call(fresh, fresh.lib.llg_hipd_ffn_predict_sparse_noalloc, L)
+            fresh.check(rc, "predict_sparse_noalloc")
+            assert fresh.workspace_bytes() == 0
+            assert np.array_equal(act, L["ref_act"])
+            assert max_rel_err(out, L["ref"]) <= TOL
+        rc, out0, act0 = _call(fresh, fresh.lib.llg_hipd_ffn_predict_sparse, big)
+        fresh.check(rc, "predict_sparse")
+        assert fresh.workspace_bytes() > 0
+        assert np.array_equal(act0, big["ref_act"]) and max_rel_err(out0, big["ref"]) <= TOL
+    finally:
+        fresh.close()
+
+
 def test_noalloc_rejects_workload_above_scratch(dev):
     """d_ff 65536 at h 2048 needs 1024 partial rows of 2048 floats (8 MiB) beside
     the predictor's partials, more than the fixed scratch holds: the
