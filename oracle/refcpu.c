@@ -138,46 +138,68 @@ static int g_threads = 1;
 
 void refcpu_set_threads(int n) { g_threads = n < 1 ? 1 : (n > 64 ? 64 : n); }
 
-static void matmulvec_rows(const float *w, int r0, int r1, int in_dim, const float *x, float *y) {
-    for (int i = r0; i < r1; i++) { /* ops.go:51-58 */
-        float sum = 0.0f;
-        const float *row = w + (size_t)i * in_dim;
-        for (int j = 0; j < in_dim; j++) sum += row[j] * x[j];
-        y[i] = sum;
+/* [0, n) split into g_threads contiguous ranges, one per thread (this thread
+ * takes the first); with fewer than min_each items per thread fewer threads
+ * are used.  Every caller gives each item its own outputs, computed in the
+ * reference's order, so the split changes no result. */
+typedef void (*range_fn)(void *ctx, int i0, int i1);
+typedef struct {
+    range_fn fn;
+    void *ctx;
+    int i0, i1;
+} range_part;
+
+static void *range_worker(void *arg) {
+    range_part *p = (range_part *)arg;
+    p->fn(p->ctx, p->i0, p->i1);
+    return NULL;
+}
+
+static void par_for(int n, int min_each, range_fn fn, void *ctx) {
+    int nt = g_threads;
+    if (min_each < 1) min_each = 1;
+    if (nt > n / min_each) nt = n / min_each;
+    if (nt <= 1) {
+        fn(ctx, 0, n);
+        return;
+    }
+    range_part parts[64];
+    pthread_t th[64];
+    int started[64];
+    for (int k = 0; k < nt; k++) {
+        parts[k] = (range_part){fn, ctx, (int)((int64_t)n * k / nt), (int)((int64_t)n * (k + 1) / nt)};
+        started[k] = k > 0 && pthread_create(&th[k], NULL, range_worker, &parts[k]) == 0;
+    }
+    range_worker(&parts[0]);
+    for (int k = 1; k < nt; k++) {
+        if (started[k]) pthread_join(th[k], NULL);
+        else range_worker(&parts[k]); /* no thread: this one takes that range */
     }
 }
 
 typedef struct {
     const float *w, *x;
     float *y;
-    int r0, r1, in_dim;
-} mv_part;
+    int in_dim;
+} mv_ctx;
 
-static void *mv_worker(void *arg) {
-    mv_part *p = (mv_part *)arg;
-    matmulvec_rows(p->w, p->r0, p->r1, p->in_dim, p->x, p->y);
-    return NULL;
+static void matmulvec_rows(void *arg, int r0, int r1) {
+    const mv_ctx *c = (const mv_ctx *)arg;
+    for (int i = r0; i < r1; i++) { /* ops.go:51-58 */
+        float sum = 0.0f;
+        const float *row = c->w + (size_t)i * c->in_dim;
+        for (int j = 0; j < c->in_dim; j++) sum += row[j] * c->x[j];
+        c->y[i] = sum;
+    }
 }
 
 void refcpu_matmulvec(const float *w, int out_dim, int in_dim, const float *x, float *y) {
-    const int nt = g_threads;
-    if (nt <= 1 || (int64_t)out_dim * in_dim < (1 << 20) || out_dim < nt) {
-        matmulvec_rows(w, 0, out_dim, in_dim, x, y);
+    mv_ctx c = {w, x, y, in_dim};
+    if ((int64_t)out_dim * in_dim < (1 << 20)) { /* small: not worth a thread */
+        matmulvec_rows(&c, 0, out_dim);
         return;
     }
-    mv_part parts[64];
-    pthread_t th[64];
-    int started[64];
-    for (int k = 0; k < nt; k++) {
-        parts[k] = (mv_part){w, x, y, (int)((int64_t)out_dim * k / nt),
-                             (int)((int64_t)out_dim * (k + 1) / nt), in_dim};
-        started[k] = k > 0 && pthread_create(&th[k], NULL, mv_worker, &parts[k]) == 0;
-    }
-    mv_worker(&parts[0]);
-    for (int k = 1; k < nt; k++) {
-        if (started[k]) pthread_join(th[k], NULL);
-        else mv_worker(&parts[k]); /* no thread: this one computes those rows */
-    }
+    par_for(out_dim, 1, matmulvec_rows, &c);
 }
 
 void refcpu_relu(float *x, int n) { /* ops.go:168-174: NaN and -0.0 pass through */
@@ -273,17 +295,40 @@ int refcpu_predict(const float *wup, const float *wout, const float *bias, int h
 }
 
 /* ---- flash/storage.go:246-319 ------------------------------------------- */
+typedef struct {
+    const uint8_t *raw;
+    int64_t rb;
+    int t, in_dim, out_dim;
+    const int32_t *rows;
+    float *out;
+    int *errs;
+} rr_ctx;
+
+static void read_rows_range(void *arg, int i0, int i1) {
+    rr_ctx *c = (rr_ctx *)arg;
+    for (int i = i0; i < i1; i++) {
+        int32_t r = c->rows[i];
+        if (r < 0 || r >= c->out_dim) { /* :292-294 */
+            c->errs[i] = -2;
+            continue;
+        }
+        int64_t off = (int64_t)r * c->rb; /* :296 */
+        if (refcpu_dequantize(c->raw + off, c->rb, c->t, c->out + (size_t)i * c->in_dim) < 0)
+            c->errs[i] = -1;
+    }
+}
+
 int refcpu_read_rows(const uint8_t *raw, int t, int in_dim, int out_dim, const int32_t *rows,
                      int n_rows, float *out) {
     int64_t rb = refcpu_byte_size(t, in_dim); /* :253 */
     if (rb < 0) return -1;
-    for (int i = 0; i < n_rows; i++) {
-        int32_t r = rows[i];
-        if (r < 0 || r >= out_dim) return -2; /* :292-294 */
-        int64_t off = (int64_t)r * rb;        /* :296 */
-        if (refcpu_dequantize(raw + off, rb, t, out + (size_t)i * in_dim) < 0) return -1;
-    }
-    return 0;
+    if (n_rows <= 0) return 0;
+    rr_ctx c = {raw, rb, t, in_dim, out_dim, rows, out, (int *)calloc((size_t)n_rows, sizeof(int))};
+    par_for(n_rows, 64, read_rows_range, &c);
+    int rc = 0;
+    for (int i = 0; i < n_rows && rc == 0; i++) rc = c.errs[i]; /* the first failing row */
+    free(c.errs);
+    return rc;
 }
 
 /* ---- flash/storage.go:246-319 ReadRowsParallel --------------------------- */
@@ -357,23 +402,42 @@ int refcpu_read_rows_file(const char *path, int64_t tensor_offset, int t, int in
 }
 
 /* ---- inference/ffn_flash.go:254-299 ------------------------------------- */
-/* :272-298 on rows already read and dequantized */
+/* :272-298 on rows already read and dequantized.  The up dots split over
+ * neurons and the down sums over output elements; every output element still
+ * adds the neurons in ascending order, so the split changes no result. */
+typedef struct {
+    const float *up_rows, *down_rows, *x;
+    float *inter, *out;
+    int h, n_active;
+} sc_ctx;
+
+static void sparse_up_range(void *arg, int j0, int j1) {
+    sc_ctx *c = (sc_ctx *)arg;
+    for (int j = j0; j < j1; j++) { /* :273-281 */
+        const float *row = c->up_rows + (size_t)j * c->h;
+        float dot = 0.0f;
+        for (int d = 0; d < c->h; d++) dot += row[d] * c->x[d];
+        c->inter[j] = dot;
+    }
+}
+
+static void sparse_down_range(void *arg, int d0, int d1) {
+    sc_ctx *c = (sc_ctx *)arg;
+    for (int j = 0; j < c->n_active; j++) { /* :288-298 */
+        if (c->inter[j] == 0) continue;
+        const float *row = c->down_rows + (size_t)j * c->h;
+        float scale = c->inter[j];
+        for (int d = d0; d < d1; d++) c->out[d] += scale * row[d];
+    }
+}
+
 static void sparse_compute(const float *up_rows, const float *down_rows, int h, const float *x,
                            int n_active, int act, float *out) {
     float *inter = (float *)malloc(sizeof(float) * (size_t)n_active);
-    for (int j = 0; j < n_active; j++) { /* :273-281 */
-        const float *row = up_rows + (size_t)j * h;
-        float dot = 0.0f;
-        for (int d = 0; d < h; d++) dot += row[d] * x[d];
-        inter[j] = dot;
-    }
+    sc_ctx c = {up_rows, down_rows, x, inter, out, h, n_active};
+    par_for(n_active, 64, sparse_up_range, &c);
     refcpu_activation(act, inter, n_active); /* :284-285 */
-    for (int j = 0; j < n_active; j++) {     /* :288-298 */
-        if (inter[j] == 0) continue;
-        const float *row = down_rows + (size_t)j * h;
-        float scale = inter[j];
-        for (int d = 0; d < h; d++) out[d] += scale * row[d];
-    }
+    par_for(h, 256, sparse_down_range, &c);
     free(inter);
 }
 
@@ -736,6 +800,11 @@ struct refcpu_falcon {
     float *embed, *wq, *wk, *wv, *wo, *lm; /* dequantized at load (loader/ReadTensor) */
     float *kcache, *vcache;                 /* [n_layers][max_seq][kv_dim] (kvcache.go:25-37) */
     int seq_len;                            /* KVCache.SeqLen */
+    /* FFN rows read from a GGUF file by ReadRowsParallel (ffn_flash.go:262-270)
+     * instead of from p.up / p.down_t when ffn_path is set */
+    char *ffn_path;
+    int64_t *ffn_up_off, *ffn_down_off; /* [n_layers] tensor offsets in the file */
+    int ffn_threads;
 };
 
 static float *dequant_rows(const uint8_t *raw, int t, int64_t rows, int cols) {
@@ -773,6 +842,9 @@ refcpu_falcon *refcpu_falcon_new(const refcpu_falcon_params *p) {
 
 void refcpu_falcon_free(refcpu_falcon *m) {
     if (!m) return;
+    free(m->ffn_path);
+    free(m->ffn_up_off);
+    free(m->ffn_down_off);
     free(m->embed);
     free(m->wq);
     free(m->wk);
@@ -785,6 +857,58 @@ void refcpu_falcon_free(refcpu_falcon *m) {
 }
 
 void refcpu_falcon_commit(refcpu_falcon *m) { m->seq_len++; }
+
+int refcpu_falcon_ffn_file(refcpu_falcon *m, const char *path, const int64_t *up_off,
+                           const int64_t *down_off, int nthreads) {
+    free(m->ffn_path);
+    free(m->ffn_up_off);
+    free(m->ffn_down_off);
+    m->ffn_path = NULL;
+    m->ffn_up_off = m->ffn_down_off = NULL;
+    if (!path) return 0;
+    const size_t L = (size_t)m->p.n_layers;
+    m->ffn_path = strdup(path);
+    m->ffn_up_off = (int64_t *)malloc(sizeof(int64_t) * L);
+    m->ffn_down_off = (int64_t *)malloc(sizeof(int64_t) * L);
+    if (!m->ffn_path || !m->ffn_up_off || !m->ffn_down_off) {
+        refcpu_falcon_ffn_file(m, NULL, NULL, NULL, 0);
+        return -1;
+    }
+    memcpy(m->ffn_up_off, up_off, sizeof(int64_t) * L);
+    memcpy(m->ffn_down_off, down_off, sizeof(int64_t) * L);
+    m->ffn_threads = nthreads;
+    return 0;
+}
+
+/* forward.go:263-301 for query heads [h0, h1) of one layer; each head has its
+ * own score row, so heads split over threads change no result */
+typedef struct {
+    const float *q, *kc, *vc;
+    float *att, *scores;
+    int n_heads, n_kv, hd, kvd, seq;
+    float scale;
+} attn_ctx;
+
+static void attn_heads(void *arg, int h0, int h1) {
+    const attn_ctx *c = (const attn_ctx *)arg;
+    for (int hh = h0; hh < h1; hh++) {
+        const float *qh = c->q + (size_t)hh * c->hd;
+        const int kvh = hh * c->n_kv / c->n_heads;
+        float *scores = c->scores + (size_t)hh * c->seq;
+        for (int t = 0; t < c->seq; t++) {
+            const float *kh = c->kc + (size_t)t * c->kvd + (size_t)kvh * c->hd;
+            float dot = 0.0f;
+            for (int d = 0; d < c->hd; d++) dot += qh[d] * kh[d];
+            scores[t] = dot * c->scale;
+        }
+        refcpu_softmax_inplace(scores, c->seq);
+        float *oh = c->att + (size_t)hh * c->hd;
+        for (int t = 0; t < c->seq; t++) {
+            const float *vh = c->vc + (size_t)t * c->kvd + (size_t)kvh * c->hd;
+            for (int d = 0; d < c->hd; d++) oh[d] += scores[t] * vh[d];
+        }
+    }
+}
 
 /* inference/forward.go:483-497 */
 static void rope_inplace(float *vec, int n_heads, int head_dim, int pos, float base) {
@@ -820,7 +944,7 @@ int refcpu_falcon_forward_ex(refcpu_falcon *m, int32_t token, int pos, float *lo
     float *att = (float *)malloc(sizeof(float) * (size_t)qd);
     float *attn_out = (float *)malloc(sizeof(float) * (size_t)h);
     float *ffn_out = (float *)malloc(sizeof(float) * (size_t)h);
-    float *scores = (float *)malloc(sizeof(float) * (size_t)(m->seq_len + 1));
+    float *scores = (float *)malloc(sizeof(float) * (size_t)p->n_heads * (m->seq_len + 1));
     int32_t *active = (int32_t *)malloc(sizeof(int32_t) * (size_t)p->ff);
     memcpy(x, m->embed + (size_t)token * h, sizeof(float) * (size_t)h); /* forward.go:449-454 */
     const int seq = m->seq_len + 1;                                     /* forward.go:249 */
@@ -842,22 +966,8 @@ int refcpu_falcon_forward_ex(refcpu_falcon *m, int32_t token, int pos, float *lo
         memcpy(kc + (size_t)m->seq_len * kvd, k, sizeof(float) * (size_t)kvd); /* :245-246 */
         memcpy(vc + (size_t)m->seq_len * kvd, v, sizeof(float) * (size_t)kvd);
         memset(att, 0, sizeof(float) * (size_t)qd);
-        for (int hh = 0; hh < p->n_heads; hh++) { /* forward.go:263-301 */
-            const float *qh = q + (size_t)hh * hd;
-            const int kvh = hh * p->n_kv / p->n_heads;
-            for (int t = 0; t < seq; t++) {
-                const float *kh = kc + (size_t)t * kvd + (size_t)kvh * hd;
-                float dot = 0.0f;
-                for (int d = 0; d < hd; d++) dot += qh[d] * kh[d];
-                scores[t] = dot * scale;
-            }
-            refcpu_softmax_inplace(scores, seq);
-            float *oh = att + (size_t)hh * hd;
-            for (int t = 0; t < seq; t++) {
-                const float *vh = vc + (size_t)t * kvd + (size_t)kvh * hd;
-                for (int d = 0; d < hd; d++) oh[d] += scores[t] * vh[d];
-            }
-        }
+        attn_ctx ac = {q, kc, vc, att, scores, p->n_heads, p->n_kv, hd, kvd, seq, scale};
+        par_for(p->n_heads, 1, attn_heads, &ac); /* forward.go:263-301 */
         refcpu_matmulvec(m->wo + (size_t)l * h * qd, h, qd, att, attn_out); /* :305 */
         /* ffnFlash path 2: predictor on the attention output (ffn_flash.go:157,
          * 225-231), sparse FFN on the normed input */
@@ -867,9 +977,28 @@ int refcpu_falcon_forward_ex(refcpu_falcon *m, int32_t token, int pos, float *lo
                                          pred_logits_out ? pred_logits_out + (size_t)l * p->ff
                                                          : NULL);
         if (n_active_out) n_active_out[l] = n_act;
-        refcpu_ffn_sparse_load(p->up + (size_t)l * p->ff * rb_h,
-                               p->down_t + (size_t)l * p->ff * rb_h, p->t, h, p->ff, normed,
-                               active, n_act, p->act, ffn_out);
+        int frc;
+        if (m->ffn_path) /* the rows from the file by the row-read pool */
+            frc = refcpu_ffn_sparse_load_file(m->ffn_path, m->ffn_up_off[l], m->ffn_down_off[l],
+                                              p->t, h, p->ff, normed, active, n_act, p->act,
+                                              m->ffn_threads, ffn_out);
+        else
+            frc = refcpu_ffn_sparse_load(p->up + (size_t)l * p->ff * rb_h,
+                                         p->down_t + (size_t)l * p->ff * rb_h, p->t, h, p->ff,
+                                         normed, active, n_act, p->act, ffn_out);
+        if (frc) { /* a row the file could not give (ffn_flash.go:263-270 returns the error) */
+            free(x);
+            free(normed);
+            free(q);
+            free(k);
+            free(v);
+            free(att);
+            free(attn_out);
+            free(ffn_out);
+            free(scores);
+            free(active);
+            return -2;
+        }
         for (int i = 0; i < h; i++) x[i] += attn_out[i]; /* ffn_flash.go:161-166 */
         for (int i = 0; i < h; i++) x[i] += ffn_out[i];
     }

@@ -153,7 +153,9 @@ int refcpu_moe_route(const float *logits, int n_exp, int k, int32_t *ids_out, fl
  * Matrices are GGUF rows of type t; per-layer arrays are concatenated layer
  * after layer.  As the reference does at load, the embedding, attention and
  * LM-head matrices are dequantized to fp32 once in refcpu_falcon_new; the FFN
- * rows are dequantized per token (ffnSparseLoad). */
+ * rows are dequantized per token (ffnSparseLoad).  refcpu_set_threads splits
+ * the matvecs, the attention heads and the FFN rows over threads without
+ * changing any result. */
 typedef struct {
     int n_layers, hidden, n_heads, n_kv, head_dim, ff, vocab, max_seq, rank, act, t;
     float rope_base, eps;
@@ -181,6 +183,15 @@ int refcpu_falcon_forward_ex(refcpu_falcon *m, int32_t token, int pos, float *lo
                              int32_t *n_active_out, float *pred_logits_out);
 /* kvcache.go:55-57 (generate.go:94,119 call it after every token). */
 void refcpu_falcon_commit(refcpu_falcon *m);
+/* From the next forward on, the FFN rows of layer l are read from the GGUF
+ * file at `path` (tensors at byte offsets up_off[l] and down_off[l], ff rows
+ * of ByteSize(hidden) each) by a ReadRowsParallel pool of nthreads
+ * (flash/storage.go:246-319, as ffn_flash.go:262-270 does) instead of from
+ * p.up / p.down_t; the results are the same.  path NULL goes back to the
+ * rows in memory.  Returns 0, or -1 when out of memory.  A forward whose rows
+ * cannot be read returns -2. */
+int refcpu_falcon_ffn_file(refcpu_falcon *m, const char *path, const int64_t *up_off,
+                           const int64_t *down_off, int nthreads);
 /* cmd/generate.go:197-205 */
 int refcpu_argmax(const float *v, int n);
 

@@ -362,6 +362,7 @@ _SIGS.update({
     "refcpu_falcon_forward": (C.c_int, [_vp, C.c_int32, C.c_int, _vp, _vp]),
     "refcpu_falcon_forward_ex": (C.c_int, [_vp, C.c_int32, C.c_int, _vp, _vp, _vp]),
     "refcpu_falcon_commit": (None, [_vp]),
+    "refcpu_falcon_ffn_file": (C.c_int, [_vp, C.c_char_p, _vp, _vp, C.c_int]),
     "refcpu_argmax": (C.c_int, [_vp, C.c_int]),
 })
 
@@ -403,10 +404,28 @@ class Falcon:
         lg = np.empty(self.vocab, np.float32)
         na = np.empty(self.n_layers, np.int32)
         pl = np.empty((self.n_layers, self.ff), np.float32) if pred_logits else None
-        if lib().refcpu_falcon_forward_ex(self.m, token, pos, _p(lg), _p(na), _p(pl)):
+        rc = lib().refcpu_falcon_forward_ex(self.m, token, pos, _p(lg), _p(na), _p(pl))
+        if rc == -2:
+            raise OSError("falcon forward: FFN rows could not be read from the file")
+        if rc:
             raise ValueError("falcon forward: token or position out of range")
         lib().refcpu_falcon_commit(self.m)
         return (lg, na, pl) if pred_logits else (lg, na)
+
+    def ffn_file(self, path, up_offsets, down_offsets, nthreads: int = 32) -> None:
+        """From the next token on, read each layer's FFN rows from the GGUF file
+        at `path` (tensor byte offsets per layer) with the ReadRowsParallel
+        pool of nthreads (ffn_flash.go:262-270, storage.go:246-319) instead of
+        from memory; the results are the same.  path None: rows from memory."""
+        if path is None:
+            lib().refcpu_falcon_ffn_file(self.m, None, None, None, 0)
+            return
+        self._offs = (np.ascontiguousarray(up_offsets, np.int64),
+                      np.ascontiguousarray(down_offsets, np.int64))
+        assert all(o.size == self.n_layers for o in self._offs)
+        if lib().refcpu_falcon_ffn_file(self.m, str(path).encode(), _p(self._offs[0]),
+                                        _p(self._offs[1]), int(nthreads)):
+            raise MemoryError("refcpu_falcon_ffn_file failed")
 
     def __del__(self):
         if getattr(self, "m", None) and _lib is not None:  # the module may be gone at exit

@@ -34,6 +34,12 @@ check that a plausible restatement mistake would fail:
                                            to the lower index; weights sum to 1
   moeFFN experts (moe_forward.go:83-150)   float64 brute force at d=64, eff=96, E=4, k=2
   RMSNorm / LayerNorm (ops.go:114-165)     float64 formulas
+  ForwardFlash (ffn_flash.go:115-185)      float64 brute force over 7 tokens (MQA/GQA/MHA),
+                                           no-RoPE variant, closed form at position 0
+  row threads of the oracle                1, 5 and 16 threads bit-equal (MatMulVec, the
+                                           sparse FFN, the attention heads)
+  ForwardFlash with rows from a file       bit-equal to the in-memory rows from any
+  (ffn_flash.go:262-270)                   position on; unreadable rows are an error
 
 Functions whose last-ulp behaviour only running Go could pin (sequential dot
 rounding under Go's FMA rules, math.Exp ulps, sort.Slice tie order for n > 12)
@@ -527,3 +533,66 @@ def test_matmulvec_threads_bit_identical():
         R.set_threads(1)
     ref = (w.astype(np.float64) @ x.astype(np.float64))
     assert np.max(np.abs(one - ref)) <= 1e-4 * np.max(np.abs(ref))
+
+
+def test_sparse_ffn_and_falcon_threads_bit_identical(rng, tmp_path):
+    """set_threads also splits the sparse FFN's up dots over neurons, its down
+    sums over output elements and the attention over heads; every output still
+    adds its terms in the reference's order, so the bits do not change."""
+    h, ff = 512, 1024
+    up, dn = make_sparse_layer(rng, h, ff, gg.Q4_0)
+    x = normal(rng, h, 1.0)
+    act = np.sort(rng.choice(ff, 300, replace=False)).astype(np.int32)
+    d = dict(FALCON_TINY, n_heads=8, hidden=256, ff=512, max_seq=8)
+    w = make_falcon(rng, d)
+    toks = rng.integers(0, d["vocab"], 6)
+    thr = np.zeros(d["n_layers"], np.float32)
+    one = R.ffn_sparse_load(up, dn, gg.Q4_0, h, ff, x, act)
+    m1 = R.Falcon(d, w, thr)
+    ref = [m1.forward(int(t), s) for s, t in enumerate(toks)]
+    try:
+        R.set_threads(5)
+        assert np.array_equal(R.ffn_sparse_load(up, dn, gg.Q4_0, h, ff, x, act), one)
+        m5 = R.Falcon(d, w, thr)
+        for s, t in enumerate(toks):
+            lg, na = m5.forward(int(t), s)
+            assert np.array_equal(lg, ref[s][0]) and np.array_equal(na, ref[s][1]), s
+    finally:
+        R.set_threads(1)
+    assert np.max(np.abs(one - ref_sparse_f64(up, dn, gg.Q4_0, h, x, act))) <= 1e-4 * np.max(
+        np.abs(one))
+
+
+def test_falcon_ffn_rows_from_file_bit_identical(rng, tmp_path):
+    """ForwardFlash with every layer's FFN rows read from a GGUF file by the
+    ReadRowsParallel pool (ffn_flash.go:262-270, storage.go:246-319) gives the
+    bits of the in-memory rows, from any position on; a file that cannot give
+    the rows is an error of the forward."""
+    from llg import gguf_file as GF
+
+    d = dict(FALCON_TINY)
+    w = make_falcon(rng, d)
+    L, h, ff = d["n_layers"], d["hidden"], d["ff"]
+    path = tmp_path / "ffn.gguf"
+    tensors = []
+    for l in range(L):
+        tensors += [(f"blk.{l}.ffn_up.weight", [h, ff], gg.Q4_0, w["up"][l]),
+                    (f"blk.{l}.ffn_down_t.weight", [h, ff], gg.Q4_0, w["down_t"][l])]
+    GF.write_gguf(str(path), [("general.architecture", GF.T_STRING, "falcon")], tensors)
+    gf = GF.open_gguf(str(path))
+    up_off = [gf.by_name[f"blk.{l}.ffn_up.weight"].offset for l in range(L)]
+    dn_off = [gf.by_name[f"blk.{l}.ffn_down_t.weight"].offset for l in range(L)]
+    toks = rng.integers(0, d["vocab"], 8)
+    _, _, thr = ref_falcon_f64(w, d, toks)
+    mem, fil = R.Falcon(d, w, thr), R.Falcon(d, w, thr)
+    for s, t in enumerate(toks):
+        if s == 3:
+            fil.ffn_file(path, up_off, dn_off, nthreads=4)
+        a, b = mem.forward(int(t), s), fil.forward(int(t), s)
+        assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1]), s
+    assert np.sum([mem.forward(int(toks[0]), 8)[1]]) > 0  # rows were read at all
+    fil.forward(int(toks[0]), 8)
+    bad = R.Falcon(d, w, thr)
+    bad.ffn_file(path, [path.stat().st_size] * L, dn_off, nthreads=2)
+    with pytest.raises(OSError):
+        bad.forward(int(toks[0]), 0)
