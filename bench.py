@@ -14,12 +14,14 @@ their average event-timed duration on the library's stream) and a
 `cpu_baseline` object (the oracle's restatement of the reference CPU path,
 timed on a bounded sample on this host).
 
-Other workloads (--workload dense-q4_0 | dense-q8_0 | dense-f16 | window |
-moe-decode | moe-prefill | falcon-decode | swiglu-q4_0 | swiglu-q8_0 |
-swiglu-f16) measure the remaining hot-path configurations; falcon-decode is
-the full 32-layer model around the sparse FFN (--steps = generated tokens
-after the 512-token prompt); swiglu-* is the SiLU architecture's dense FFN
-(ffnSwiGLU) at a LLaMA-7B layer's shape.
+The default run (--workload all) prints that line with every other workload
+measured in the same process under its `workloads` key, each with its own
+metric, roofline and, for the window and the full model, CPU baseline.  One
+workload alone: --workload sparse | dense-q4_0 | dense-q8_0 | dense-f16 |
+window | moe-decode | moe-prefill | falcon-decode | swiglu-q4_0 | swiglu-q8_0 |
+swiglu-f16.  falcon-decode is the full 32-layer model around the sparse FFN
+(--steps = generated tokens after the 512-token prompt); swiglu-* is the SiLU
+architecture's dense FFN (ffnSwiGLU) at a LLaMA-7B layer's shape.
 """
 from __future__ import annotations
 
@@ -811,15 +813,93 @@ def bench_moe(args, torch, llg, dev, prefill: bool):
             "roofline": roof}
 
 
+def default_layers(workload: str) -> int:
+    """Distinct HBM copies a workload rotates over (enough to defeat the MALL)."""
+    return {"sparse": 128, "all": 128, "window": 16, "moe-decode": 8,
+            "moe-prefill": 1}.get(workload, 6)
+
+
+def set_vs_baseline(res: dict) -> None:
+    """The reference publishes no figure for these metrics; its baseline is its
+    own CPU path timed in this run on this host (cpu_baseline), so vs_baseline
+    is the ratio to that, and null when the CPU leg was skipped."""
+    cb = res.get("cpu_baseline")
+    res["vs_baseline"] = res["value"] / cb["value"] if cb and cb.get("value") else None
+    res["vs_baseline_basis"] = ("value / cpu_baseline.value (the reference CPU path timed in "
+                                "this run; no published figure exists)" if cb else None)
+
+
+def run_workload(args, torch, llg, dev) -> dict:
+    gg = llg.gguf
+    if args.workload == "sparse":
+        return bench_sparse(args, torch, llg, dev)
+    if args.workload == "window":
+        return bench_window(args, torch, llg, dev)
+    if args.workload == "falcon-decode":
+        return bench_falcon(args, torch, llg, dev)
+    if args.workload.startswith("moe-"):
+        return bench_moe(args, torch, llg, dev, args.workload == "moe-prefill")
+    if args.workload.startswith("swiglu-"):
+        t = {"swiglu-q4_0": gg.Q4_0, "swiglu-q8_0": gg.Q8_0, "swiglu-f16": gg.F16}[args.workload]
+        return bench_swiglu(args, torch, llg, dev, t)
+    t = {"dense-q4_0": gg.Q4_0, "dense-q8_0": gg.Q8_0, "dense-f16": gg.F16}[args.workload]
+    return bench_dense(args, torch, llg, dev, t)
+
+
+# The other workloads of the default run: (name, steps, warmup, CPU baseline).
+# Config 1 (dense, three types), config 2 (window), config 3 (MoE decode and
+# 512-token prefill), config 4 (the 32-layer model, 256 greedy tokens after the
+# 512-token prompt, its CPU baseline at positions from 512) and the SwiGLU
+# dense FFN at a LLaMA-7B layer.
+SECONDARY = [("dense-q4_0", 500, 50, False), ("dense-q8_0", 500, 50, False),
+             ("dense-f16", 500, 50, False), ("window", 640, 64, True),
+             ("moe-decode", 500, 50, False), ("moe-prefill", 40, 5, False),
+             ("falcon-decode", 256, 0, True), ("swiglu-q4_0", 500, 50, False),
+             ("swiglu-q8_0", 500, 50, False), ("swiglu-f16", 500, 50, False)]
+
+
+def run_secondary(args, torch, llg, dev) -> dict:
+    """Each other workload in turn, in this process, each with its own result
+    (or the error it raised, so that one failing workload does not lose the
+    others)."""
+    import gc
+
+    out = {}
+    for name, steps, warmup, cpu in SECONDARY:
+        a = argparse.Namespace(**vars(args))
+        a.workload, a.steps, a.warmup = name, steps, warmup
+        a.layers = default_layers(name)
+        a.no_cpu = args.no_cpu or not cpu
+        a.cpu_seconds = min(args.cpu_seconds, 15.0)
+        log(f"workload {name}: {steps} steps")
+        t0 = time.perf_counter()
+        try:
+            r = run_workload(a, torch, llg, dev)
+            r.update({"steps": steps, "warmup": warmup})
+            r.setdefault("cpu_baseline", None)
+            set_vs_baseline(r)
+        except Exception as e:  # a host-side error of one workload
+            r = {"error": f"{type(e).__name__}: {e}"}
+            log(f"workload {name} failed: {r['error']}")
+        r["wall_s"] = time.perf_counter() - t0
+        out[name] = r
+        gc.collect()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", default="sparse",
-                    choices=["sparse", "dense-q4_0", "dense-q8_0", "dense-f16", "window",
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "sparse", "dense-q4_0", "dense-q8_0", "dense-f16", "window",
                              "moe-decode", "moe-prefill", "falcon-decode", "swiglu-q4_0",
-                             "swiglu-q8_0", "swiglu-f16"])
+                             "swiglu-q8_0", "swiglu-f16"],
+                    help="all (default): the sparse step as the headline line, then every "
+                         "other workload in the same process under its `workloads` key")
     ap.add_argument("--layers", type=int, default=0,
                     help="distinct HBM copies rotated per step (0 = enough to defeat the MALL)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -837,8 +917,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     if args.layers <= 0:
-        args.layers = {"sparse": 128, "window": 16, "moe-decode": 8,
-                       "moe-prefill": 1}.get(args.workload, 6)
+        args.layers = default_layers(args.workload)
 
     import torch
     import llg
@@ -857,31 +936,16 @@ def main():
         torch.cuda.synchronize()
         log(f"calibration: 4 copies of {args.calib_mib} MiB (read and write each)")
         del src, dst
-    if args.workload == "sparse":
+    if args.workload == "all":
         res = bench_sparse(args, torch, llg, dev)
-    elif args.workload == "window":
-        res = bench_window(args, torch, llg, dev)
-    elif args.workload == "falcon-decode":
-        res = bench_falcon(args, torch, llg, dev)
-    elif args.workload.startswith("moe-"):
-        res = bench_moe(args, torch, llg, dev, args.workload == "moe-prefill")
-    elif args.workload.startswith("swiglu-"):
-        t = {"swiglu-q4_0": gg.Q4_0, "swiglu-q8_0": gg.Q8_0, "swiglu-f16": gg.F16}[args.workload]
-        res = bench_swiglu(args, torch, llg, dev, t)
+        res["workloads"] = run_secondary(args, torch, llg, dev)
     else:
-        t = {"dense-q4_0": gg.Q4_0, "dense-q8_0": gg.Q8_0, "dense-f16": gg.F16}[args.workload]
-        res = bench_dense(args, torch, llg, dev, t)
+        res = run_workload(args, torch, llg, dev)
     res.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
                 "higher_is_better": True, "scaling": "weak",
                 "data": "synthetic (seeded N(0,0.02) weights, N(0,1) inputs)"})
     res.setdefault("cpu_baseline", None)
-    # The reference publishes no figure for this metric; its baseline is its own
-    # CPU path timed in this run on this host (cpu_baseline), so vs_baseline is
-    # the ratio to that, and null when the CPU leg was skipped.
-    cb = res["cpu_baseline"]
-    res["vs_baseline"] = res["value"] / cb["value"] if cb and cb.get("value") else None
-    res["vs_baseline_basis"] = ("value / cpu_baseline.value (the reference CPU path timed in "
-                                "this run; no published figure exists)" if cb else None)
+    set_vs_baseline(res)
     order = ["metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
              "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config", "roofline",
              "cpu_baseline"]
