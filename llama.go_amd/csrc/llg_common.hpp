@@ -596,24 +596,30 @@ __device__ __forceinline__ void llg_x_sum_store(float *xs, const float4 &v, int 
     }
 }
 
-template <int XS, class Issue = LlgNoIssue>
+// KN: float4 rounds of the one-pass form (the row must fit KN * blockDim.x
+// float4, else the looped form runs).  Callers pass the fewest that cover
+// their rows: a clamped round past the row's end rereads its last float4 and
+// costs the CU's address unit as much as a real one, ahead of every later
+// wavefront's x.
+template <int XS, int KN = 8, class Issue = LlgNoIssue>
 __device__ __forceinline__ void llg_stage_x_sum(float *xs, const float *__restrict__ x, int nb,
                                                 Issue &&issue = Issue()) {
     static_assert(XS >= 33, "room for the block sum");
+    static_assert(KN >= 1 && KN <= 8, "rounds of the one-pass form");
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
     const int n4 = nb * 8;
     const int lane = threadIdx.x & 63;
     const int base0 = threadIdx.x - lane;
-    if (n4 <= 8 * (int)blockDim.x) {
+    if (n4 <= KN * (int)blockDim.x) {
         // one pass, straight-line: the wait before the stores covers the x
         // loads only (clamped addresses, so no load sits under a branch)
-        float4 v[8];
+        float4 v[KN];
 #pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = x4[min(base0 + k * (int)blockDim.x + lane, n4 - 1)];
+        for (int k = 0; k < KN; k++) v[k] = x4[min(base0 + k * (int)blockDim.x + lane, n4 - 1)];
         __builtin_amdgcn_sched_barrier(0);  // keep the caller's loads behind these
         issue();
 #pragma unroll
-        for (int k = 0; k < 8; k++)
+        for (int k = 0; k < KN; k++)
             llg_x_sum_store<XS>(xs, v[k], base0 + k * blockDim.x + lane, n4);
         return;
     }

@@ -142,7 +142,8 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
         // Q8_0's 1024-thread instance has registers for one group per round
         llg_stage_attn<MV_XS, T == LLG_TYPE_Q8_0 ? 1 : 2>(xs, ap, cb0, cnb, issue_first);
     else
-        llg_stage_x_sum<MV_XS>(xs, x + (size_t)cb0 * 32, cnb, issue_first);
+        llg_stage_x_sum<MV_XS, (MV_CHUNK * 8 + NT - 1) / NT>(xs, x + (size_t)cb0 * 32, cnb,
+                                                             issue_first);
     __syncthreads();
     // the fold task t from pr (x staged)
     auto fold_dot = [&](int t) {

@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256) void k_moe_gateup(const uint8_t *__restrict__ 
     }
     MoeRows<T, 2 * MOE_GU_J, NB> m;
     m.issue(rp, f, 0, f.nb);
-    llg_stage_x_sum<MOE_XS>(xs, x + (size_t)t * f.cols, f.nb);
+    llg_stage_x_sum<MOE_XS, 5>(xs, x + (size_t)t * f.cols, f.nb);  // 256 threads: 160 blocks
     __syncthreads();
     if (j0 >= eff) return;
     float s[2 * MOE_GU_J];
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(256) void k_moe_down(const uint8_t *__restrict__ do
         rp[q] = down + ((long long)e * hidden + min(d0 + q, hidden - 1)) * stride;
     MoeRows<T, MOE_DN_R, NB> m;
     m.issue(rp, f, cb0, cnb);
-    llg_stage_x_sum<MOE_XS>(xs, hbuf + (size_t)ts * f.cols + (size_t)cb0 * 32, cnb);
+    llg_stage_x_sum<MOE_XS, 5>(xs, hbuf + (size_t)ts * f.cols + (size_t)cb0 * 32, cnb);
     __syncthreads();
     if (d0 >= hidden) return;
     float s[MOE_DN_R];

@@ -44,11 +44,15 @@
 #define DN_THREADS 512    // k_sparse_down workgroup: one tile (or list stride) per thread
 #define WIN_XWG 8         // workgroups that take the folded window update's side work
 
-template <class Issue = LlgNoIssue>
+// KN: one-pass rounds of float4 per thread (rows past KN * blockDim float4
+// take the looped form); callers pass the fewest that cover 160 blocks.
+template <int KN = 8, class Issue = LlgNoIssue>
 __device__ __forceinline__ void stage_x(float *xs, const float *__restrict__ x, int nb,
                                         Issue &&issue = Issue()) {
-    llg_stage_x_sum<XS_STRIDE>(xs, x, nb, issue);
+    llg_stage_x_sum<XS_STRIDE, KN>(xs, x, nb, issue);
 }
+// rounds that cover 160 blocks (1280 float4) with nt threads
+constexpr int stage_rounds(int nt) { return (1280 + nt - 1) / nt; }
 
 // Up-row dot products of two rows by one wavefront (row < 0: no row, result
 // 0): lane l owns blocks l, l+64, ...; the bytes of up to BATCH blocks of both
@@ -329,7 +333,7 @@ __global__ __launch_bounds__(256) void k_list_up(
     const int m0 = has0 ? valid(a0) : -1;
     const int m1 = jf + stride < n_active ? valid(a1) : -1;
     Noted nt0{-1, -1, false, false};
-    stage_x(xs, x, f.nb, [&]() {
+    stage_x<stage_rounds(256)>(xs, x, f.nb, [&]() {
         if (has0) nt0 = note(jf, m0, m1);
     });
     __syncthreads();
@@ -608,7 +612,7 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
     WoutTile t;  // logits: wavefronts with neurons in the tile
     const bool lw = wave * 16 < n1 - n0;
     if (lw) load_wout_tile(t, wout, wstride, n1, rank, n0);  // used after the barrier
-    stage_x(xs, x, f.nb);
+    stage_x<stage_rounds(NTH)>(xs, x, f.nb);
     load_hidden<PRED_SPLIT_N>(hid, partial, rank);
     __syncthreads();
     if (wave < NT / 16) {
