@@ -932,6 +932,17 @@ void *llg_ws(LlgDevice *d, size_t bytes, int *rc);
 // (LLG_E_SCRATCH) or the address lookup at init failed.
 #define LLG_SCRATCH_BYTES (8 * 1024 * 1024)
 uint8_t *llg_dev_scratch(LlgDevice *d, size_t bytes, int *rc);
+// Sync area of a fused predictor launch (llg_pred_tile.hpp): a 256-byte head
+// (the epoch word) and LLG_SYNC_COPIES copies of one 64-bit slot per hidden
+// unit, for ranks up to LLG_SYNC_SLOTS.  It starts zeroed and keeps its
+// contents between calls.
+#define LLG_SYNC_HEAD 256
+#define LLG_SYNC_SLOTS 1024
+#define LLG_SYNC_COPIES 8
+#define LLG_SYNC_BYTES (LLG_SYNC_HEAD + 8 * LLG_SYNC_SLOTS * LLG_SYNC_COPIES)
+// The handle's own sync area (allocated and zeroed on the stream at first
+// use), or null with *rc set.
+uint8_t *llg_dev_sync(LlgDevice *d, int *rc);
 // Copy host -> device workspace slot / device -> host, on the stream.
 int llg_h2d(LlgDevice *d, void *dst, const void *src, size_t bytes);
 int llg_d2h(LlgDevice *d, void *dst, const void *src, size_t bytes);

@@ -587,13 +587,17 @@ int llg_hipd_ffn_predict_sparse(LlgHipDevice h, int64_t hwup, int64_t hwout, int
     if (!d_a || !d_x || !d_out) return llg_set_error(d, LLG_E_ARG, "predict_sparse: null pointer");
     uint8_t *ws = (uint8_t *)llg_ws(d, llg_fused_ws_bytes(wup->rows, wout->rows, b->fmt.nb), &rc);
     if (rc) return rc;
+    uint8_t *sync = llg_dev_sync(d, &rc);
+    if (rc) return rc;
     return llg_fused_enqueue(d, wup, wout, bias, b, d_a, d_x, thr, act, d_out, d_active,
-                             d_n_active, ws);
+                             d_n_active, ws, sync);
 }
 
 // The same path with its workspace in the GPU's fixed scratch array: no
-// allocation, and nothing in the scratch needs clearing (every slot the
-// kernels read is written earlier in the same call).
+// allocation.  The scratch starts with the sync area (zero when the library
+// loads; its slots carry an epoch, so it is never cleared), then the
+// workspace, whose every slot the kernels read is written earlier in the
+// same call.
 int llg_hipd_ffn_predict_sparse_noalloc(LlgHipDevice h, int64_t hwup, int64_t hwout,
                                         int64_t hbias, int64_t hb, const float *d_a,
                                         const float *d_x, float thr, int act, float *d_out,
@@ -604,10 +608,11 @@ int llg_hipd_ffn_predict_sparse_noalloc(LlgHipDevice h, int64_t hwup, int64_t hw
     int rc = check_fused(d, hwup, hwout, hbias, hb, &wup, &wout, &bias, &b);
     if (rc) return rc;
     if (!d_a || !d_x || !d_out) return llg_set_error(d, LLG_E_ARG, "predict_sparse: null pointer");
-    uint8_t *ws = llg_dev_scratch(d, llg_fused_ws_bytes(wup->rows, wout->rows, b->fmt.nb), &rc);
-    if (!ws) return rc;
+    uint8_t *sync = llg_dev_scratch(
+        d, LLG_SYNC_BYTES + llg_fused_ws_bytes(wup->rows, wout->rows, b->fmt.nb), &rc);
+    if (!sync) return rc;
     return llg_fused_enqueue(d, wup, wout, bias, b, d_a, d_x, thr, act, d_out, d_active,
-                             d_n_active, ws);
+                             d_n_active, sync + LLG_SYNC_BYTES, sync);
 }
 
 int llg_hip_ffn_predict_sparse(LlgHipDevice h, int64_t hwup, int64_t hwout, int64_t hbias,
@@ -628,12 +633,14 @@ int llg_hip_ffn_predict_sparse(LlgHipDevice h, int64_t hwup, int64_t hwout, int6
     const long long o_ws = o_n + 256;
     uint8_t *ws = (uint8_t *)llg_ws(d, o_ws + llg_fused_ws_bytes(wup->rows, ff, b->fmt.nb), &rc);
     if (rc) return rc;
+    uint8_t *sync = llg_dev_sync(d, &rc);
+    if (rc) return rc;
     if ((rc = llg_h2d(d, ws + o_a, a, (size_t)hd * 4))) return rc;
     if ((rc = llg_h2d(d, ws + o_x, x, (size_t)hd * 4))) return rc;
     rc = llg_fused_enqueue(d, wup, wout, bias, b, (const float *)(ws + o_a),
                            (const float *)(ws + o_x), thr, act, (float *)(ws + o_out),
                            active ? (int32_t *)(ws + o_act) : nullptr, (int32_t *)(ws + o_n),
-                           ws + o_ws);
+                           ws + o_ws, sync);
     if (rc) return rc;
     int32_t n = 0;
     if ((rc = llg_d2h(d, out, ws + o_out, (size_t)hd * 4))) return rc;

@@ -91,10 +91,13 @@ int llg_matvec_ln_enqueue(LlgDevice *d, const LlgObject *w, const LlgLnArgs &ln,
 // Predictor-fused sparse FFN (ffnFlash path 2) (llg_sparse.hip).
 // nb: 32-element blocks of the bundle rows (the tiles' partial outputs).
 size_t llg_fused_ws_bytes(int rank, int ff, int nb);
+// sync: a sync area of LLG_SYNC_BYTES (the predictor then runs inside the tile
+// launch), or null (a separate predictor kernel first).
 int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
                       LlgObject *b, const float *d_a, const float *d_x, float thr, int act,
                       float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws,
-                      const float *d_out_add = nullptr, float2 *d_stats = nullptr);
+                      uint8_t *sync, const float *d_out_add = nullptr,
+                      float2 *d_stats = nullptr);
 // The same after the hidden partials are in ws (llg_pred_ws_layout): the
 // tile kernel and the partial-sum kernel; accumulate: d_out += the FFN output.
 // d_stats (optional): per 32 outputs, (sum, M2) of d_out as written (LlgLnArgs).

@@ -677,7 +677,7 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
         // r += attn_out by its first kernel, then r += the FFN output
         rc = llg_fused_enqueue(d, L.pwup, L.pwout, nullptr, L.bundle, m.attn_out, m.normed, L.thr,
                                m.act, r, nullptr, n_active_out ? n_active_out + l : nullptr, m.ws,
-                               m.attn_out, m.rstats);
+                               nullptr, m.attn_out, m.rstats);
         if (rc) return rc;
     }
     const float *fw = reinterpret_cast<const float *>(m.out_w->d);

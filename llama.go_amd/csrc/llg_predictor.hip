@@ -12,8 +12,7 @@
 #include "llg_internal.hpp"
 #include "llg_pred_tile.hpp"
 
-#define PRED_SPLIT 8
-#define HID_LOADS 4  // float4 loads a lane issues together
+#define PRED_SPLIT LLG_PRED_SPLIT
 
 // partial[s * rank + r] = WUp[r, chunk s] . a[chunk s].  The grid also zeroes
 // `zero_out`, `zero_ctr[0..n_ctr)` and `*zero_extra` (each optional), which
@@ -37,38 +36,9 @@ __global__ __launch_bounds__(256) void k_pred_hidden(const uint8_t *__restrict__
     if (wid >= rank * PRED_SPLIT) return;
     const int r = wid / PRED_SPLIT;
     const int s = wid % PRED_SPLIT;
-    const int lane = threadIdx.x & 63;
     const float *row = reinterpret_cast<const float *>(wup + (long long)r * stride);
-    float acc = 0.0f;
-    if ((h & 3) == 0) {
-        const int h4 = h >> 2;
-        const int chunk = (h4 + PRED_SPLIT - 1) / PRED_SPLIT;
-        const int c0 = s * chunk, c1 = min(h4, c0 + chunk);
-        const float4 *r4 = reinterpret_cast<const float4 *>(row);
-        const float4 *a4 = reinterpret_cast<const float4 *>(a);
-        for (int j0 = c0 + lane; j0 < c1; j0 += 64 * HID_LOADS) {
-            float4 w[HID_LOADS], v[HID_LOADS];
-#pragma unroll
-            for (int i = 0; i < HID_LOADS; i++) {
-                const int j = j0 + 64 * i;
-                w[i] = j < c1 ? r4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-                v[i] = j < c1 ? a4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-#pragma unroll
-            for (int i = 0; i < HID_LOADS; i++) {
-                acc += w[i].x * v[i].x;
-                acc += w[i].y * v[i].y;
-                acc += w[i].z * v[i].z;
-                acc += w[i].w * v[i].w;
-            }
-        }
-    } else {
-        const int chunk = (h + PRED_SPLIT - 1) / PRED_SPLIT;
-        const int c0 = s * chunk, c1 = min(h, c0 + chunk);
-        for (int j = c0 + lane; j < c1; j += 64) acc += row[j] * a[j];
-    }
-    acc = llg_wave_sum(acc);
-    if (lane == 0) partial[s * rank + r] = acc;
+    const float acc = llg_pred_split_dot(row, a, h, s);
+    if ((threadIdx.x & 63) == 0) partial[s * rank + r] = acc;
 }
 
 // One workgroup of 256 threads per 64-neuron tile: logits, optional output,

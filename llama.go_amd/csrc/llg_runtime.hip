@@ -22,6 +22,7 @@ struct LlgDevice {
     int64_t next_id = 1;
     void *ws = nullptr;
     size_t ws_bytes = 0;
+    uint8_t *sync = nullptr;  // LLG_SYNC_BYTES, zeroed at allocation
     std::string last_error;
     bool tearing_down = false;  // llg_hip_free: every object is freed in one sweep
 };
@@ -50,6 +51,22 @@ uint8_t *llg_dev_scratch(LlgDevice *d, size_t bytes, int *rc) {
         return nullptr;
     }
     return d->scratch;
+}
+uint8_t *llg_dev_sync(LlgDevice *d, int *rc) {
+    *rc = 0;
+    if (d->sync) return d->sync;
+    if (hipMalloc(&d->sync, LLG_SYNC_BYTES) != hipSuccess) {
+        d->sync = nullptr;
+        *rc = llg_set_error(d, LLG_E_NOMEM, "sync area allocation failed");
+        return nullptr;
+    }
+    if (hipError_t e = hipMemsetAsync(d->sync, 0, LLG_SYNC_BYTES, d->stream); e != hipSuccess) {
+        hipFree(d->sync);
+        d->sync = nullptr;
+        *rc = llg_hip_error(d, e, "sync area clear");
+        return nullptr;
+    }
+    return d->sync;
 }
 hipStream_t llg_dev_stream(LlgDevice *d) { return d->stream; }
 int llg_device_id(LlgDevice *d) { return d->device; }
@@ -289,6 +306,7 @@ void llg_hip_free(LlgHipDevice h) {
     for (auto &kv : d->objects) destroy_object(d, kv.second);
     d->objects.clear();
     if (d->ws) hipFree(d->ws);
+    if (d->sync) hipFree(d->sync);
     hipStreamDestroy(d->stream);
     delete d;
 }

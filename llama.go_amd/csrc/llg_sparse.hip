@@ -537,21 +537,7 @@ __device__ __forceinline__ float tile_logit(const WoutTile &t, const uint8_t *__
                                             long long stride, int ff, int rank, int tile0,
                                             const float *hid) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (t.v) {
-        const float4 *h4 = reinterpret_cast<const float4 *>(hid);
-        float acc = 0.0f;
-#pragma unroll
-        for (int k = 0; k < PRED_MAXV; k++) {
-            if (k < t.v) {
-                const float4 hv = h4[4 * k + t.q];
-                acc += t.w[k].x * hv.x;
-                acc += t.w[k].y * hv.y;
-                acc += t.w[k].z * hv.z;
-                acc += t.w[k].w * hv.w;
-            }
-        }
-        return llg_quad_sum(acc);
-    }
+    if (t.v) return wout_tile_dot(t, hid);
     float mine = 0.0f;
     for (int r = 0; r < 16; r++) {
         const int i = tile0 + wave * 16 + r;
@@ -576,6 +562,111 @@ __device__ __forceinline__ uint32_t quad_bits(unsigned long long m) {
     return (uint32_t)m;
 }
 
+// The predictor inside the tile launch (ffnFlash path 2 with the predictor
+// input given): the first n_hid workgroups compute the hidden units and hand
+// them to the tile workgroups through the sync slots (llg_pred_tile.hpp).
+// They come first in the grid, so they are dispatched before any tile
+// workgroup that waits for them.  n_hid = 0: the hidden partials are in
+// `partial`, written by an earlier kernel.
+struct HidArgs {
+    const uint8_t *wup;  // WUp (rank rows of h floats)
+    long long wstride;
+    int h;
+    const float *a;          // predictor input
+    uint64_t *slots;         // sync slots, after the epoch word at ctr
+    const uint32_t *ctr;
+    int n_hid;               // predictor workgroups at the head of the grid
+    float *acc_out;          // optional: acc_out[i] += acc_add[i], i < acc_n
+    const float *acc_add;
+    int acc_n;
+};
+
+#ifndef LLG_WOUT_DELAY
+#define LLG_WOUT_DELAY 0
+#endif
+#ifndef LLG_TILE_ORDER
+#define LLG_TILE_ORDER 0
+#endif
+// Spin bound of a tile workgroup's wait for its hidden units (about 30 ms);
+// past it the workgroup computes the missing units itself.
+#define HID_POLLS (1 << 16)
+
+// A predictor workgroup: RPW hidden units; wavefront s < LLG_PRED_SPLIT takes
+// chunk s of each unit's WUp row (the sums of k_pred_hidden, the rows sharing
+// the loads of a), then every copy of the units' slots is written.
+template <int NW>
+__device__ __forceinline__ void tile_hid_role(const HidArgs &ha, int rank, float *sh) {
+    constexpr int RPW = NW / LLG_PRED_SPLIT;  // hidden units per workgroup
+    static_assert(RPW >= 1 && NW % LLG_PRED_SPLIT == 0, "whole units per workgroup");
+    // the epoch word as a vector load ahead of the row loads, waited on only
+    // at the slot stores
+    const uint32_t ctr = llg_epoch_get(ha.ctr);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r0 = blockIdx.x * RPW;
+    if (wave < LLG_PRED_SPLIT) {
+        const float *rows[RPW];
+#pragma unroll
+        for (int k = 0; k < RPW; k++)  // a unit past rank rereads the last row
+            rows[k] = reinterpret_cast<const float *>(ha.wup + (long long)min(r0 + k, rank - 1) * ha.wstride);
+        float p[RPW];
+        llg_pred_split_dots<RPW>(rows, ha.a, ha.h, wave, p);
+        if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+            for (int k = 0; k < RPW; k++) sh[k * LLG_PRED_SPLIT + wave] = p[k];
+        }
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < RPW * LLG_SYNC_COPIES) {
+        const int k = threadIdx.x % RPW, c = threadIdx.x / RPW;
+        if (r0 + k < rank)
+            llg_slot_put(ha.slots + c * LLG_SYNC_SLOTS + r0 + k, ctr + 1u,
+                         llg_hidden_from_parts(sh + k * LLG_PRED_SPLIT));
+    }
+    if (ha.acc_out)
+        for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < ha.acc_n; i += ha.n_hid * blockDim.x)
+            ha.acc_out[i] += ha.acc_add[i];
+}
+
+// The copy of the slots a tile workgroup reads: one per group of workgroups
+// that the round-robin dispatch puts on one XCD.
+__device__ __forceinline__ const uint64_t *tile_slot_copy(const HidArgs &ha) {
+    return ha.slots + (blockIdx.x % LLG_SYNC_COPIES) * LLG_SYNC_SLOTS;
+}
+
+// A tile workgroup's hidden units from the slots: wavefront w takes units w
+// * 64 + lane (+ the thread count per further pass); v0 is the first pass's
+// slot value, requested with the x staging.  A unit whose slot does not show
+// the epoch within HID_POLLS polls is computed here with the predictor
+// workgroups' sums (the same value), so the wait always ends.
+__device__ __forceinline__ void tile_take_hidden(float *hid, const HidArgs &ha, int rank,
+                                                 uint32_t epoch, uint64_t v0) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint64_t *slots = tile_slot_copy(ha);
+    for (int r0 = wave * 64; r0 < rank; r0 += blockDim.x) {
+        const int r = min(r0 + lane, rank - 1);
+        uint64_t v = r0 == wave * 64 ? v0 : llg_slot_get(slots + r);
+        for (int polls = 0; !__all((uint32_t)(v >> 32) == epoch) && polls < HID_POLLS; polls++) {
+            __builtin_amdgcn_s_sleep(1);
+            v = llg_slot_get(slots + r);
+        }
+        float hv = __uint_as_float((uint32_t)v);
+        unsigned long long miss = __ballot((uint32_t)(v >> 32) != epoch);
+        while (miss) {  // wavefront-uniform
+            const int l = __ffsll((long long)miss) - 1;
+            miss &= miss - 1;
+            const int u = r0 + l;
+            if (u >= rank) continue;
+            const float *row = reinterpret_cast<const float *>(ha.wup + (long long)u * ha.wstride);
+            float val = 0.0f;  // the chunk sums in order, as llg_hidden_from_parts
+#pragma unroll 1
+            for (int s = 0; s < LLG_PRED_SPLIT; s++) val += llg_pred_split_dot(row, ha.a, ha.h, s);
+            if (lane == l) hv = val < 0.0f ? 0.0f : val;
+        }
+        if (r0 + lane < rank) hid[r0 + lane] = hv;
+    }
+}
+
 // A'. The predictor-fused tiles with their down products (the form the step
 // uses): a workgroup owns tf_tiles 64-neuron tiles (WOut rows: 16 per
 // wavefront; the ballot writes one mask word per tile and the workgroup's
@@ -598,9 +689,15 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
     const uint8_t *__restrict__ wout, long long wstride, int ff, int rank,
     const float *__restrict__ partial, const float *__restrict__ bias, float thr,
     const uint8_t *__restrict__ base, long long bstride, RowFmt f, const float *__restrict__ x,
-    int act, unsigned long long *__restrict__ mask, float *__restrict__ part, int pstride) {
+    int act, unsigned long long *__restrict__ mask, float *__restrict__ part, int pstride,
+    HidArgs ha) {
     extern __shared__ float sh[];
     constexpr int TW = tf_tiles<T>(), NT = TW * TU, NTH = tf_threads<T>(), NW = NTH / 64;
+    if ((int)blockIdx.x < ha.n_hid) {
+        tile_hid_role<NW>(ha, rank, sh);
+        return;
+    }
+    const int ti = blockIdx.x - ha.n_hid;  // this workgroup's tiles
     float *xs = sh;                                     // nb * XS_STRIDE
     float *hid = xs + f.nb * XS_STRIDE;                 // rank (16-byte aligned)
     float *ul = hid + ((rank + 3) & ~3);                // NT activations
@@ -608,12 +705,35 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int *tl = reinterpret_cast<int *>(wm + NW) + wave * NT;  // this wavefront's active list
-    const int n0 = blockIdx.x * NT, n1 = min(ff, n0 + NT);
+    const int n0 = ti * NT, n1 = min(ff, n0 + NT);
     WoutTile t;  // logits: wavefronts with neurons in the tile
     const bool lw = wave * 16 < n1 - n0;
-    if (lw) load_wout_tile(t, wout, wstride, n1, rank, n0);  // used after the barrier
-    stage_x<stage_rounds(NTH)>(xs, x, f.nb);
-    load_hidden<PRED_SPLIT_N>(hid, partial, rank);
+    uint64_t hv0 = 0;
+    uint32_t ctr = 0;
+    if (ha.n_hid && LLG_TILE_ORDER == 1) {
+        // x staged first, then WOut, the epoch word and the first poll
+        stage_x<stage_rounds(NTH)>(xs, x, f.nb);
+        if (lw) load_wout_tile(t, wout, wstride, n1, rank, n0);
+        __builtin_amdgcn_sched_barrier(0);
+        ctr = llg_epoch_get(ha.ctr);
+        if (wave * 64 < rank) hv0 = llg_slot_get(tile_slot_copy(ha) + min(wave * 64 + lane, rank - 1));
+    } else if (ha.n_hid) {
+        // WOut (after an optional delay that leaves the predictor rows ahead
+        // in the memory queues), x, then the epoch word and the first poll
+        if (LLG_WOUT_DELAY) __builtin_amdgcn_s_sleep(LLG_WOUT_DELAY);
+        if (lw) load_wout_tile(t, wout, wstride, n1, rank, n0);
+        stage_x<stage_rounds(NTH)>(xs, x, f.nb, [&]() {
+            ctr = llg_epoch_get(ha.ctr);
+            if (wave * 64 < rank) hv0 = llg_slot_get(tile_slot_copy(ha) + min(wave * 64 + lane, rank - 1));
+        });
+    } else {
+        if (lw) load_wout_tile(t, wout, wstride, n1, rank, n0);  // used after the barrier
+        stage_x<stage_rounds(NTH)>(xs, x, f.nb);
+    }
+    if (ha.n_hid)
+        tile_take_hidden(hid, ha, rank, ctr + 1u, hv0);
+    else
+        load_hidden<PRED_SPLIT_N>(hid, partial, rank);
     __syncthreads();
     if (wave < NT / 16) {
         // the strict '>' of the logits of this wavefront's 16 rows (the four
@@ -643,7 +763,7 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
         const unsigned long long lt = (1ull << lane) - 1ull;
         if ((mw[w] >> lane) & 1ull) tl[cnt + __popcll(mw[w] & lt)] = TU * w + lane;
         cnt += __popcll(mw[w]);
-        if (wave == 0 && lane == 0 && n0 + TU * w < n1) mask[blockIdx.x * TW + w] = mw[w];
+        if (wave == 0 && lane == 0 && n0 + TU * w < n1) mask[ti * TW + w] = mw[w];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -724,7 +844,7 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
             }
         }
         if (i < n_qb) {
-            float4 *o4 = reinterpret_cast<float4 *>(part + (long long)blockIdx.x * pstride + i * 8);
+            float4 *o4 = reinterpret_cast<float4 *>(part + (long long)ti * pstride + i * 8);
 #pragma unroll
             for (int e = 0; e < 2; e++)
                 o4[e] = make_float4(acc[4 * e] - corr, acc[4 * e + 1] - corr,
@@ -741,7 +861,8 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
 // added to out (a residual), else stored.  Workgroup 0 also writes the number
 // of active neurons (the popcounts of the tile masks).  stats (optional, cols
 // a multiple of 32): the block's (sum, M2) of the values written, for the
-// LayerNorm prologue of the next matvec over out (LlgLnArgs).
+// LayerNorm prologue of the next matvec over out (LlgLnArgs).  ctr
+// (optional): the epoch word of the tile launch's sync area, advanced here.
 #define TR_GROUPS 32  // the tree below is written for 32 groups
 #define TR_BATCH 5
 template <bool ACC>
@@ -750,7 +871,8 @@ __global__ __launch_bounds__(256) void k_tile_reduce(const float *__restrict__ p
                                                      const unsigned long long *__restrict__ mask,
                                                      int32_t *__restrict__ n_active_out,
                                                      float *__restrict__ out,
-                                                     float2 *__restrict__ stats) {
+                                                     float2 *__restrict__ stats,
+                                                     uint32_t *__restrict__ ctr) {
     __shared__ float4 red[TR_GROUPS][8];
     __shared__ int cnt[4];
     const int b = blockIdx.x, tid = threadIdx.x;
@@ -777,6 +899,9 @@ __global__ __launch_bounds__(256) void k_tile_reduce(const float *__restrict__ p
 #pragma unroll
     for (int i = 0; i < TR_BATCH; i++)
         v[i] = p[(long long)min(g + TR_GROUPS * i, n_parts - 1) * ps4];
+    // the epoch word, read unconditionally (a word of the first partial row
+    // without one) so that no branch waits for it, and advanced at the end
+    const uint32_t c0 = llg_epoch_get(ctr ? ctr : reinterpret_cast<const uint32_t *>(part));
     // the residual (stored by group 0), behind the partial rows; requested by
     // every wavefront, so that each has the same count of loads to wait on
     __builtin_amdgcn_sched_barrier(0);
@@ -846,6 +971,7 @@ __global__ __launch_bounds__(256) void k_tile_reduce(const float *__restrict__ p
         }
     }
     if (n_active_out && b == 0 && tid == 0) *n_active_out = cnt[0] + cnt[1] + cnt[2] + cnt[3];
+    if (ctr && b == 0 && tid == 0) *ctr = c0 + 1u;  // the next launch's epoch
 }
 
 // Most pairs a k_sparse_down thread loads at once, by type (the row bytes of
@@ -1061,54 +1187,33 @@ template <int T>
 static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial,
                          const float *bias, float thr, LlgObject *b, const float *x, int act,
                          unsigned long long *mask, float *part, int32_t *n_active, float *out,
-                         bool accumulate, float2 *stats) {
+                         bool accumulate, float2 *stats, HidArgs ha) {
     const int ff = wout->rows, rank = wout->fmt.cols;
     const int n_tiles = (ff + 63) / 64;
     const RowFmt &f = b->fmt;
     const int pstride = f.nb * 32;
-    constexpr int NT = tf_tiles<T>() * TU;
-    const int n_parts = (ff + NT - 1) / NT;  // workgroups, one partial row each
+    constexpr int NT = tf_tiles<T>() * TU, NW = tf_threads<T>() / 64;
+    const int n_parts = (ff + NT - 1) / NT;  // tile workgroups, one partial row each
+    if (ha.slots) ha.n_hid = (rank + NW / LLG_PRED_SPLIT - 1) / (NW / LLG_PRED_SPLIT);
     const size_t lds = tile_lds_bytes<T>(f, rank);
-    hipLaunchKernelGGL((k_tile_ffn<T>), dim3(n_parts), dim3(tf_threads<T>()), lds, st, wout->d,
-                       wout->stride, ff, rank, partial, bias, thr, b->d, b->stride, f, x, act,
-                       mask, part, pstride);
+    hipLaunchKernelGGL((k_tile_ffn<T>), dim3(ha.n_hid + n_parts), dim3(tf_threads<T>()), lds, st,
+                       wout->d, wout->stride, ff, rank, partial, bias, thr, b->d, b->stride, f, x,
+                       act, mask, part, pstride, ha);
+    uint32_t *ctr = ha.slots ? const_cast<uint32_t *>(ha.ctr) : nullptr;
     if (accumulate)
         hipLaunchKernelGGL((k_tile_reduce<true>), dim3(f.nb), dim3(256), 0, st,
                            (const float *)part, pstride, n_parts, n_tiles, f.cols,
-                           (const unsigned long long *)mask, n_active, out, stats);
+                           (const unsigned long long *)mask, n_active, out, stats, ctr);
     else
         hipLaunchKernelGGL((k_tile_reduce<false>), dim3(f.nb), dim3(256), 0, st,
                            (const float *)part, pstride, n_parts, n_tiles, f.cols,
-                           (const unsigned long long *)mask, n_active, out, stats);
+                           (const unsigned long long *)mask, n_active, out, stats, ctr);
 }
 
-// ffnFlash path 2 on the device: k_pred_hidden, k_tile_ffn, k_tile_reduce,
-// plus the ascending active list through k_compact when d_active is given.
-// d_n_active (optional) receives the number of active neurons.
-int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
-                      LlgObject *b, const float *d_a, const float *d_x, float thr, int act,
-                      float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws,
-                      const float *d_out_add, float2 *d_stats) {
-    if (int rc = llg_check_act(d, act)) return rc;
-    float *partial;
-    unsigned long long *mask;
-    int psplit;
-    // k_sparse_down stores out; with d_out_add, k_pred_hidden first adds
-    // d_out_add to out and k_sparse_down adds the FFN output to that (out ends
-    // as (out + d_out_add) + the FFN output, the residual order of
-    // ffn_flash.go:161-166)
-    int rc = llg_pred_hidden_enqueue(d, wup, d_a, ws, &partial, &mask, &psplit,
-                                     d_out_add ? d_out : nullptr, b->fmt.cols, nullptr, 0,
-                                     nullptr, d_out_add);
-    if (rc) return rc;
-    return llg_fused_tail_enqueue(d, wout, bias, b, d_x, thr, act, d_out, d_active, d_n_active,
-                                  ws, d_out_add != nullptr, d_stats);
-}
-
-int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgObject *b,
-                           const float *d_x, float thr, int act, float *d_out,
-                           int32_t *d_active, int32_t *d_n_active, uint8_t *ws, bool accum,
-                           float2 *d_stats) {
+static int fused_tail(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgObject *b,
+                      const float *d_x, float thr, int act, float *d_out, int32_t *d_active,
+                      int32_t *d_n_active, uint8_t *ws, bool accum, float2 *d_stats,
+                      const HidArgs &ha) {
     if (int rc = llg_check_act(d, act)) return rc;
     const RowFmt &f = b->fmt;
     if (d_stats && f.cols % 32)
@@ -1131,19 +1236,19 @@ int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgOb
     switch (f.type) {
     case LLG_TYPE_Q4_0:
         launch_fused<LLG_TYPE_Q4_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
-                                    d_n_active, d_out, accum, d_stats);
+                                    d_n_active, d_out, accum, d_stats, ha);
         break;
     case LLG_TYPE_Q8_0:
         launch_fused<LLG_TYPE_Q8_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
-                                    d_n_active, d_out, accum, d_stats);
+                                    d_n_active, d_out, accum, d_stats, ha);
         break;
     case LLG_TYPE_F16:
         launch_fused<LLG_TYPE_F16>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
-                                   d_n_active, d_out, accum, d_stats);
+                                   d_n_active, d_out, accum, d_stats, ha);
         break;
     case LLG_TYPE_F32:
         launch_fused<LLG_TYPE_F32>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
-                                   d_n_active, d_out, accum, d_stats);
+                                   d_n_active, d_out, accum, d_stats, ha);
         break;
     default:
         return llg_set_error(d, LLG_E_TYPE, "predict_sparse: unsupported type %d", f.type);
@@ -1151,4 +1256,54 @@ int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgOb
     LLG_LAUNCH_CHECK(d, "predict_sparse");
     if (d_active) return llg_compact_enqueue(d, mask, n_tiles, d_active, nullptr);
     return 0;
+}
+
+// ffnFlash path 2 on the device.  With a sync area (sync, LLG_SYNC_BYTES)
+// and rank <= LLG_SYNC_SLOTS: the tile launch computes the predictor's hidden
+// units in its first workgroups, then k_tile_reduce; otherwise k_pred_hidden
+// first.  Plus the ascending active list through k_compact when d_active is
+// given; d_n_active (optional) receives the number of active neurons.
+int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *bias,
+                      LlgObject *b, const float *d_a, const float *d_x, float thr, int act,
+                      float *d_out, int32_t *d_active, int32_t *d_n_active, uint8_t *ws,
+                      uint8_t *sync, const float *d_out_add, float2 *d_stats) {
+    if (int rc = llg_check_act(d, act)) return rc;
+    if (sync && wup->rows <= LLG_SYNC_SLOTS && wup->fmt.type == LLG_TYPE_F32) {
+        HidArgs ha{};
+        ha.wup = wup->d;
+        ha.wstride = wup->stride;
+        ha.h = wup->fmt.cols;
+        ha.a = d_a;
+        ha.ctr = reinterpret_cast<const uint32_t *>(sync);
+        ha.slots = reinterpret_cast<uint64_t *>(sync + LLG_SYNC_HEAD);
+        // with d_out_add, the predictor workgroups first add d_out_add to out
+        // and k_tile_reduce adds the FFN output to that (out ends as (out +
+        // d_out_add) + the FFN output, the residual order of ffn_flash.go:161-166)
+        if (d_out_add) {
+            ha.acc_out = d_out;
+            ha.acc_add = d_out_add;
+            ha.acc_n = b->fmt.cols;
+        }
+        return fused_tail(d, wout, bias, b, d_x, thr, act, d_out, d_active, d_n_active, ws,
+                          d_out_add != nullptr, d_stats, ha);
+    }
+    float *partial;
+    unsigned long long *mask;
+    int psplit;
+    // k_tile_reduce stores out; with d_out_add, k_pred_hidden first adds
+    // d_out_add to out and k_tile_reduce adds the FFN output to that
+    int rc = llg_pred_hidden_enqueue(d, wup, d_a, ws, &partial, &mask, &psplit,
+                                     d_out_add ? d_out : nullptr, b->fmt.cols, nullptr, 0,
+                                     nullptr, d_out_add);
+    if (rc) return rc;
+    return llg_fused_tail_enqueue(d, wout, bias, b, d_x, thr, act, d_out, d_active, d_n_active,
+                                  ws, d_out_add != nullptr, d_stats);
+}
+
+int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgObject *b,
+                           const float *d_x, float thr, int act, float *d_out,
+                           int32_t *d_active, int32_t *d_n_active, uint8_t *ws, bool accum,
+                           float2 *d_stats) {
+    return fused_tail(d, wout, bias, b, d_x, thr, act, d_out, d_active, d_n_active, ws, accum,
+                      d_stats, HidArgs{});
 }
