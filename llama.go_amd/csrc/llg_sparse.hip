@@ -581,12 +581,6 @@ struct HidArgs {
     int acc_n;
 };
 
-#ifndef LLG_WOUT_DELAY
-#define LLG_WOUT_DELAY 0
-#endif
-#ifndef LLG_TILE_ORDER
-#define LLG_TILE_ORDER 0
-#endif
 // Spin bound of a tile workgroup's wait for its hidden units (about 30 ms);
 // past it the workgroup computes the missing units itself.
 #define HID_POLLS (1 << 16)
@@ -710,17 +704,8 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
     const bool lw = wave * 16 < n1 - n0;
     uint64_t hv0 = 0;
     uint32_t ctr = 0;
-    if (ha.n_hid && LLG_TILE_ORDER == 1) {
-        // x staged first, then WOut, the epoch word and the first poll
-        stage_x<stage_rounds(NTH)>(xs, x, f.nb);
-        if (lw) load_wout_tile(t, wout, wstride, n1, rank, n0);
-        __builtin_amdgcn_sched_barrier(0);
-        ctr = llg_epoch_get(ha.ctr);
-        if (wave * 64 < rank) hv0 = llg_slot_get(tile_slot_copy(ha) + min(wave * 64 + lane, rank - 1));
-    } else if (ha.n_hid) {
-        // WOut (after an optional delay that leaves the predictor rows ahead
-        // in the memory queues), x, then the epoch word and the first poll
-        if (LLG_WOUT_DELAY) __builtin_amdgcn_s_sleep(LLG_WOUT_DELAY);
+    if (ha.n_hid) {
+        // WOut, x, then the epoch word and the hidden units' first poll
         if (lw) load_wout_tile(t, wout, wstride, n1, rank, n0);
         stage_x<stage_rounds(NTH)>(xs, x, f.nb, [&]() {
             ctr = llg_epoch_get(ha.ctr);
@@ -902,6 +887,11 @@ __global__ __launch_bounds__(256) void k_tile_reduce(const float *__restrict__ p
     // the epoch word, read unconditionally (a word of the first partial row
     // without one) so that no branch waits for it, and advanced at the end
     const uint32_t c0 = llg_epoch_get(ctr ? ctr : reinterpret_cast<const uint32_t *>(part));
+    // the tile masks (block 0 counts the active neurons from them), also
+    // requested now rather than after the sums
+    unsigned long long mk[2];
+#pragma unroll
+    for (int k = 0; k < 2; k++) mk[k] = mask[min(tid + 256 * k, n_tiles - 1)];
     // the residual (stored by group 0), behind the partial rows; requested by
     // every wavefront, so that each has the same count of loads to wait on
     __builtin_amdgcn_sched_barrier(0);
@@ -932,8 +922,12 @@ __global__ __launch_bounds__(256) void k_tile_reduce(const float *__restrict__ p
         }
     }
     int na = 0;
-    if (n_active_out && b == 0)
-        for (int i = tid; i < n_tiles; i += 256) na += __popcll(mask[i]);
+    if (n_active_out && b == 0) {
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+            if (tid + 256 * k < n_tiles) na += __popcll(mk[k]);
+        for (int i = tid + 512; i < n_tiles; i += 256) na += __popcll(mask[i]);
+    }
     red[g][c] = s;
     if (n_active_out && b == 0) {
         for (int d = 32; d > 0; d >>= 1) na += __shfl_xor(na, d, 64);
