@@ -45,12 +45,13 @@ Q4_ROW = H // 32 * 18                # 2556 B per GGUF Q4_0 row
 BUNDLE_ALG = 2 * Q4_ROW              # 5112 B per neuron (unpadded)
 PRED_BYTES = (RANK * H + FF * RANK) * 4
 # HBM bytes per sparse step from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE over
-# k_pred_hidden + k_tile_ffn + k_tile_reduce, each counter scaled by its reading
-# for a 1 GiB streaming copy (FETCH x2.0, WRITE x1.0), measured on this bench
+# k_tile_ffn (its predictor workgroups and tiles) + k_tile_reduce, each counter
+# scaled by its reading for a 1 GiB streaming copy (FETCH x2.0, WRITE x1.0),
+# measured on this bench
 # line (exactly 909 active neurons per step): the weights once plus the
 # workgroups' partial outputs written and read back; the summary with the
 # commands is profiles/sparse_step_falcon7b_q4_0_hbm_traffic.md.
-SPARSE_STEP_TRAFFIC = 22.15e6
+SPARSE_STEP_TRAFFIC = 22.28e6
 SPARSE_STEP_TRAFFIC_ACTIVE = 909
 
 
@@ -100,7 +101,7 @@ def bench_sparse(args, torch, llg, dev):
     lib = dev.lib
 
     def step(i):
-        """ffnFlash path 2: predictor -> selection -> gathered FFN, 3 launches."""
+        """ffnFlash path 2: predictor -> selection -> gathered FFN, 2 launches."""
         l = i % L
         x = X[i % n_x]
         rc = lib.llg_hipd_ffn_predict_sparse(dev.h, wups[l].id, wouts[l].id, 0, bundles[l].id,
@@ -174,7 +175,8 @@ def bench_sparse(args, torch, llg, dev):
                                 "predictor logit", "batch": 1,
                    "layer_copies_rotated": L, "step": "predict+select+gathered up/down FFN"},
         "roofline": {"bound": "hbm",
-                     "kernel": "k_pred_hidden + k_tile_ffn + k_tile_reduce (one decode step)",
+                     "kernel": "k_tile_ffn (predictor workgroups + tiles) + k_tile_reduce "
+                               "(one decode step)",
                      "achieved": step_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": step_gbs / HBM_PEAK_GBS, "traffic": SPARSE_STEP_TRAFFIC,
                      "traffic_active_neurons": SPARSE_STEP_TRAFFIC_ACTIVE,

@@ -232,12 +232,13 @@ int llg_hipd_ffn_predict_sparse(LlgHipDevice dev, int64_t wup, int64_t wout, int
 /* Allocation-free form of llg_hipd_ffn_predict_sparse: no counterpart in the
  * reference.  It is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * Same arguments, results and errors; its kernels take their hidden partials,
+ * Same arguments, results and errors; its kernels take their sync area (the
+ * hand-off of the predictor's hidden units, zero at load and never cleared),
  * tile masks and partial output rows from a fixed array in each GPU's memory
  * (8 MiB per GPU, held until the process ends) instead of the handle's
  * growable workspace, and it calls no hipMalloc, hipFree or hipMemset.  A
  * predictor and bundle whose workspace exceeds the array give LLG_E_SCRATCH
- * (the Falcon-7B layer, rank 128 x d_ff 18176, needs 4.9 MiB).  Every call on one GPU shares
+ * (the Falcon-7B layer, rank 128 x d_ff 18176, needs 5.0 MiB).  Every call on one GPU shares
  * the array: calls that overlap on one GPU (from several handles or streams)
  * race; calls ordered on one stream do not. */
 int llg_hipd_ffn_predict_sparse_noalloc(LlgHipDevice dev, int64_t wup, int64_t wout,
