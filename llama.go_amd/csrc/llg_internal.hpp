@@ -34,7 +34,7 @@ int llg_compact_enqueue(LlgDevice *d, const unsigned long long *mask, int n_tile
                         int32_t *d_active, int32_t *d_n_active);
 
 // Sparse FFN over bundles (llg_sparse.hip).  Neuron n's bundle is at
-// base + (slot_of ? slot_of[n] : n) * bstride.  max_active bounds *d_n_active.
+// base + n * bstride.  max_active bounds *d_n_active.
 size_t llg_sparse_ws_bytes(int max_active);
 // The activations of model.ActivationType (model.go:97-103) an entry point
 // accepts; anything else is an argument error.
@@ -45,31 +45,43 @@ inline int llg_check_act(LlgDevice *d, int act) {
     return llg_act_ok(act) ? 0 : llg_set_error(d, LLG_E_ARG, "activation %d is not ReLU, GELU or SiLU", act);
 }
 
-// The window update folded into the two launches of the window's update + FFN
-// step (llg_window.hip, window.go:71-117).  Neuron n is resident in row n of
-// dst (slot_of[n] == n) or not (slot_of[n] == -1).  The list launch records
-// the set in ring_new, marks each listed neuron (cur_ep = epoch) and counts it
-// in cnt, subtracts the expiring set ring_exp from cnt, and reads a listed
-// neuron that is not resident from row n of src, copying its bundle to row n
-// of dst (fresh = epoch; the loads are counted in cntr[epoch & 1]).  The down
-// launch then evicts the expiring neurons whose count reached 0 and that the
-// set does not hold, marks the loaded ones resident, and leaves the counts in
-// state ([2] resident neurons, [3] loads of this update).
+// One update (number `epoch`) of a window (llg_window.hip, window.go:71-117).
+// Neuron n lives in row n of the resident buffer dst.  res[n] is the number of
+// the update that loaded n, 0 when n is not resident; during update e, n is
+// resident at the start of the update exactly when res[n] is neither 0 nor e
+// (llg_window_upd.hpp), so the update can mark its loads while readers of the
+// same launch still see the state at its start.  cnt[n]: entries of the last
+// k sets that hold n; state[2]: resident neurons.  ring_new receives this
+// update's set, ring_exp holds the expiring one (set k updates ago; its
+// *ring_set_exp is 0 until the ring has wrapped).  uslot: the update + FFN
+// step's activations, one 64-bit slot per list entry, tagged with the update's
+// number (llg_pred_tile.hpp).  cntr[2]: the loads of an update are counted in
+// cntr[epoch & 1] (consecutive update numbers alternate in parity).
 struct LlgWinUpd {
     const uint8_t *src;
     uint8_t *dst;
-    int32_t *slot_of, *cnt, *cur_ep, *fresh, *state, *cntr;
+    int32_t *res, *cnt, *state, *cntr;
     int32_t *ring_new, *ring_len_new, *ring_set_new;
     const int32_t *ring_exp, *ring_len_exp, *ring_set_exp;
+    uint64_t *uslot;
     int epoch;
 };
 // max_active: capacity of the list and of the pair workspace (the count read
 // on the device is clamped to it); n_rows: the neurons of the bundle or window
-// (an index outside [0, n_rows) counts as absent).
+// (an index outside [0, n_rows) counts as absent).  res (optional): a window's
+// residency (a neuron with res[n] == 0 is not resident and keeps activation 0,
+// window.go:150-152); the rows are then base + n * bstride, as without res.
 int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, const RowFmt &f,
-                       const int32_t *slot_of, const float *d_x, const int32_t *d_active,
+                       const int32_t *res, const float *d_x, const int32_t *d_active,
                        const int32_t *d_n_active, int max_active, int n_rows, int act,
-                       float *d_out, uint8_t *ws, const LlgWinUpd *win = nullptr);
+                       float *d_out, uint8_t *ws);
+// The window's update + FFN step in one launch (k_win_step): the FFN over the
+// listed neurons (loaded ones read from u.src and copied to their rows) and
+// update u.epoch of the counts and the residency.  cap: the list capacity
+// (the device count is clamped to it); n_rows: the window's neurons.
+int llg_win_step_enqueue(LlgDevice *d, const LlgWinUpd &u, const RowFmt &f, long long bstride,
+                         const float *d_x, const int32_t *d_active, const int32_t *d_n_active,
+                         int cap, int n_rows, int act, float *d_out);
 
 // Dense quantized matvec y[rows] = act(W . x) (llg_ffn.hip); act < 0 = none.
 // part: room for llg_matvec_part_bytes(w, act) (column-chunked rows keep

@@ -1,23 +1,31 @@
 // llg_sparse.hip -- gathered sparse FFN over row-column bundles
 // (inference/ffn_flash.go:195-299, window.go:143-180).
 //
-// Two ways in:
+// Three ways in:
 //
-//  A. predictor-fused step (ffnFlash path 2, ffn_flash.go:225-231), 3 launches:
-//     K1 k_pred_hidden (llg_predictor.hip): hidden partials (and x += attn_out
-//        for a caller that accumulates into a residual)
-//     K2 k_tile_ffn: one workgroup per two 64-neuron tiles (Q4_0/Q8_0; one
+//  A. predictor-fused step (ffnFlash path 2, ffn_flash.go:225-231), 2 launches:
+//     K1 k_tile_ffn: its first workgroups compute the predictor's hidden units
+//        (the sums of k_pred_hidden, llg_predictor.hip) and hand them to the
+//        tile workgroups as epoch-tagged slots (a caller without a sync area,
+//        or with hidden partials of its own, runs k_pred_hidden first); then
+//        one workgroup per two 64-neuron tiles (Q4_0/Q8_0; one
 //        tile for F16/F32): logits from WOut rows, strict '>' against the
 //        threshold via a wavefront ballot (one mask word per tile), then each
 //        active neuron's up row (u = act(up . x)) and, in the same round of
 //        loads, its down row (the two rows are one contiguous bundle); the
 //        workgroup's partial output, sum of u * down over its active neurons
 //        in ascending order, goes to its own row of `part`
-//     K3 k_tile_reduce: out = sum of the partial rows in row order
+//     K2 k_tile_reduce: out = sum of the partial rows in row order
 //  B. explicit active list (ffnSparseLoad, NeuronCache.FFNForward), 2 launches:
 //     k_list_up: one wavefront per listed neuron, pair j = (row, u_j)
 //     k_sparse_down: one workgroup per output block of 32 outputs reads every
 //        pair (each thread a stride of the list)
+//  C. the window's update + FFN step (NeuronCache.Update then FFNForward,
+//     window.go:71-180), 1 launch: k_win_step's up workgroups (B's up rows,
+//     a loaded neuron read from the layer's bundle and copied into its row),
+//     down workgroups (B's down sums, their rows requested before the
+//     activations exist, which arrive as epoch-tagged slots) and one
+//     workgroup for the update of the counts and the residency
 //
 // No output is summed with atomics, and every sum has a fixed order, so the
 // results are bit-identical from run to run.  u == 0 rows are skipped as at
@@ -38,11 +46,12 @@
 #include "llg_pred_tile.hpp"
 #include "llg_window_upd.hpp"
 
+#include <algorithm>
+
 #define XS_STRIDE 36      // floats per staged 32-float x block (bank-conflict-free)
 #define BATCH 4           // blocks whose loads a lane issues together
 #define PRED_SPLIT_N 8    // partials per hidden unit written by k_pred_hidden
 #define DN_THREADS 512    // k_sparse_down workgroup: one tile (or list stride) per thread
-#define WIN_XWG 8         // workgroups that take the folded window update's side work
 
 // KN: one-pass rounds of float4 per thread (rows past KN * blockDim float4
 // take the looped form); callers pass the fewest that cover 160 blocks.
@@ -225,124 +234,66 @@ __device__ __forceinline__ void row_dotn(const uint8_t *__restrict__ base, long 
 // B. explicit list: pair j = (row of active[j], act(up . x)).
 // The count read on the device is clamped to the pair capacity `cap`, and a
 // neuron outside [0, n_rows) counts as absent (activation 0), so no list
-// makes the kernel read or write out of bounds.
-// WIN (the window's update + FFN step): the first half of the folded update
-// (llg_window_upd.hpp): lane 0 of each entry's wavefront records, marks and
-// counts it, and a listed neuron that is not resident is read from row n of
-// u.src and its whole bundle copied to row n of the resident buffer (base) on
-// the way (the gather of loadRows, window.go:207-245); the last WIN_XWG
-// workgroups take the expiring set.  The pair's row is then n (the down
-// launch reads every listed neuron from its resident row).
-template <int T, bool WIN>
+// makes the kernel read or write out of bounds.  res (a window's residency,
+// optional): a neuron with res[n] == 0 is not resident and keeps activation 0
+// (window.go:150-152).
+template <int T>
 __global__ __launch_bounds__(256) void k_list_up(
-    const uint8_t *base, long long bstride, RowFmt f, const int32_t *__restrict__ slot_of,
+    const uint8_t *base, long long bstride, RowFmt f, const int32_t *__restrict__ res,
     const float *__restrict__ x, const int32_t *__restrict__ active,
     const int32_t *__restrict__ n_active_p, int cap, int n_rows, int act,
-    int2 *__restrict__ pairs, LlgWinUpd u) {
+    int2 *__restrict__ pairs) {
     extern __shared__ float xs[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int first = blockIdx.x * 4;
-    const int stride = ((int)gridDim.x - (WIN ? WIN_XWG : 0)) * 4;
-    // This wavefront's first pair of entries, requested with the count (an
-    // index past the count reads a list slot that is then not used), so the
-    // neurons are known one memory round earlier.
+    const int stride = (int)gridDim.x * 4;
     const int jf = first + wave;
-    const int a0 = cap > 0 ? active[min(jf, cap - 1)] : -1;
-    const int a1 = cap > 0 ? active[min(jf + stride, cap - 1)] : -1;
     const int n_active = min(max(*n_active_p, 0), cap);
-    if constexpr (WIN) {
-        // the last WIN_XWG workgroups take the expiring set, beside the list
-        const int gl = (int)gridDim.x - WIN_XWG;
-        if ((int)blockIdx.x >= gl) {
-            win_expire_all(u, n_active, n_rows, (blockIdx.x - gl) * blockDim.x + threadIdx.x,
-                           WIN_XWG * blockDim.x);
-            return;
-        }
-    }
     if (first >= n_active) return;  // whole workgroup idle: skip the x staging
     auto valid = [&](int n) { return n >= 0 && n < n_rows ? n : -1; };
     // One pair: entries j and j1 = j + stride (j < n_active), neurons m0, m1
-    // (-1 past the count or out of range).  note(): WIN records the entries
-    // and reads whether each must be loaded (lane 0); the list path reads
-    // the rows from slot_of.
-    struct Noted {
+    // (-1 past the count or out of range); with res, a neuron not resident
+    // has no row.
+    struct Rows {
         int row0, row1;
-        bool f0, f1;
     };
-    auto note = [&](int j, int m0, int m1) {
-        Noted r{m0, m1, false, false};
-        if constexpr (WIN) {
-            int ld0 = 0, ld1 = 0;
-            if (lane == 0) {
-                ld0 = win_note_active(u, j, m0);
-                if (j + stride < n_active) ld1 = win_note_active(u, j + stride, m1);
-            }
-            r.f0 = __builtin_amdgcn_readfirstlane(ld0);
-            r.f1 = __builtin_amdgcn_readfirstlane(ld1);
-        } else {
-            r.row0 = m0 < 0 ? -1 : (slot_of ? slot_of[m0] : m0);
-            r.row1 = m1 < 0 ? -1 : (slot_of ? slot_of[m1] : m1);
+    auto rows = [&](int m0, int m1) {
+        Rows r{m0, m1};
+        if (res) {
+            r.row0 = m0 < 0 || res[m0] == 0 ? -1 : m0;
+            r.row1 = m1 < 0 || res[m1] == 0 ? -1 : m1;
         }
         return r;
     };
-    auto pair = [&](int j, int m0, int m1, const Noted &nt) {
+    auto pair = [&](int j, const Rows &r) {
         const int j1 = j + stride;
-        int row0, row1;
         float s0, s1;
-        if constexpr (WIN) {
-            row0 = __builtin_amdgcn_readfirstlane(m0);
-            row1 = __builtin_amdgcn_readfirstlane(m1);
-            const bool f0 = nt.f0, f1 = nt.f1;
-            const uint8_t *p0 = (f0 ? u.src : base) + (long long)(row0 >= 0 ? row0 : 0) * bstride;
-            const uint8_t *p1 = (f1 ? u.src : base) + (long long)(row1 >= 0 ? row1 : 0) * bstride;
-            const int n16 = (int)(bstride >> 4);
-            constexpr int NC = bc_first<T>();
-            const bc_u4 *sp0 = reinterpret_cast<const bc_u4 *>(p0);
-            const bc_u4 *sp1 = reinterpret_cast<const bc_u4 *>(p1);
-            bc_u4 *dp0 = reinterpret_cast<bc_u4 *>(u.dst + (long long)(f0 ? row0 : 0) * bstride);
-            bc_u4 *dp1 = reinterpret_cast<bc_u4 *>(u.dst + (long long)(f1 ? row1 : 0) * bstride);
-            BundleCopy<NC> c0, c1;
-            if (f0) bc_issue(c0, sp0, n16);
-            if (f1) bc_issue(c1, sp1, n16);
-            // the copies are stored once the dot's loads are in flight
-            row_dot2p<T>(p0, p1, row0 >= 0, row1 >= 0, f, xs, s0, s1, [&]() {
-                if (f0) bc_store(c0, dp0, n16);
-                if (f1) bc_store(c1, dp1, n16);
-            });
-            if (f0) bc_rest<NC>(sp0, dp0, n16);
-            if (f1) bc_rest<NC>(sp1, dp1, n16);
-            if (lane == 0) {
-                if (f0) win_note_load(u, m0);
-                if (f1) win_note_load(u, m1);
-            }
-        } else {
-            row0 = nt.row0;
-            row1 = nt.row1;
-            row_dot2<T>(base, bstride, row0, row1, f, xs, s0, s1);
-        }
-        if (lane == 0) {  // a non-resident row keeps activation 0 (window.go:150-152)
-            pairs[j] = make_int2(row0, __float_as_int(row0 >= 0 ? llg_act(act, s0) : 0.0f));
+        row_dot2<T>(base, bstride, r.row0, r.row1, f, xs, s0, s1);
+        if (lane == 0) {  // a row without a neuron keeps activation 0 (window.go:150-152)
+            pairs[j] = make_int2(r.row0, __float_as_int(r.row0 >= 0 ? llg_act(act, s0) : 0.0f));
             if (j1 < n_active)
-                pairs[j1] = make_int2(row1, __float_as_int(row1 >= 0 ? llg_act(act, s1) : 0.0f));
+                pairs[j1] = make_int2(r.row1, __float_as_int(r.row1 >= 0 ? llg_act(act, s1) : 0.0f));
         }
     };
-    // The first pair is noted while x is in flight: its residency (or row)
-    // reads share x's memory round.
+    // The first pair's entries (never past the count: the list holds
+    // n_active entries) are requested while x is in flight.
     const bool has0 = jf < n_active;
+    int a0 = -1, a1 = -1;
+    stage_x<stage_rounds(256)>(xs, x, f.nb, [&]() {
+        a0 = active[min(jf, n_active - 1)];
+        a1 = active[min(jf + stride, n_active - 1)];
+    });
     const int m0 = has0 ? valid(a0) : -1;
     const int m1 = jf + stride < n_active ? valid(a1) : -1;
-    Noted nt0{-1, -1, false, false};
-    stage_x<stage_rounds(256)>(xs, x, f.nb, [&]() {
-        if (has0) nt0 = note(jf, m0, m1);
-    });
+    const Rows r0 = rows(m0, m1);
     __syncthreads();
-    if (has0) pair(jf, m0, m1, nt0);
+    if (has0) pair(jf, r0);
     for (int j = jf + 2 * stride; j < n_active; j += 2 * stride) {
         const int j1 = j + stride;
         const int n0 = valid(active[j]);
         const int n1 = j1 < n_active ? valid(active[j1]) : -1;
-        pair(j, n0, n1, note(j, n0, n1));
+        pair(j, rows(n0, n1));
     }
 }
 
@@ -1036,24 +987,12 @@ __device__ __forceinline__ void dn_list(const uint8_t *__restrict__ base, long l
 // Down products over a plain pair list pairs[0..*count) (the count is
 // clamped to `cap`), split evenly over the threads.  Workgroup = output block
 // b (32 outputs): out[32 b + e] = sum over the pairs of u * down_row[32 b +
-// e], the wavefronts' sums added in order.  WIN: the last WIN_XWG workgroups
-// take the second half of the folded window update (llg_window_upd.hpp).
-template <int T, bool WIN>
+// e], the wavefronts' sums added in order.
+template <int T>
 __global__ __launch_bounds__(DN_THREADS) void k_sparse_down(
     const uint8_t *__restrict__ base, long long bstride, RowFmt f, const int2 *__restrict__ pairs,
-    const int32_t *__restrict__ count_p, int cap, int n_rows, int per_xcd, float *__restrict__ out,
-    LlgWinUpd u) {
+    const int32_t *__restrict__ count_p, int cap, int per_xcd, float *__restrict__ out) {
     __shared__ float red[DN_THREADS / 64][32];
-    if constexpr (WIN) {
-        // the last WIN_XWG workgroups finish the window update, beside the
-        // down products
-        const int gd = (int)gridDim.x - WIN_XWG;
-        if ((int)blockIdx.x >= gd) {
-            win_finish_all(u, min(max(*count_p, 0), cap), n_rows,
-                           (blockIdx.x - gd) * blockDim.x + threadIdx.x, WIN_XWG * blockDim.x);
-            return;
-        }
-    }
     const int b = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
     if (b >= f.nb) return;  // uniform over the workgroup
     const int tid = threadIdx.x, bd = blockDim.x, lane = tid & 63, wave = tid >> 6;
@@ -1078,6 +1017,239 @@ __global__ __launch_bounds__(DN_THREADS) void k_sparse_down(
 }
 
 // ---------------------------------------------------------------------------
+// C. The window's update + FFN step in one launch (window.go:71-180).
+// Workgroups of ws_threads<T>() threads:
+//   [0, n_up)            up rows: wavefront-pair entries (j, j + S), S = the
+//                        up wavefronts.  A neuron not resident at the start of
+//                        the update (win_resident) is read from the layer's
+//                        bundle (u.src) while its whole bundle is copied into
+//                        its row of the resident buffer (loadRows,
+//                        window.go:207-245), a resident one from its row; the
+//                        activation of entry j goes to u.uslot[j], tagged with
+//                        the update's number;
+//   [n_up, n_up + n_dn)  one output block each: every thread requests block b
+//                        of the down rows of its entries (from the source of
+//                        the entry's up row) and then waits for their slots;
+//                        the sums of k_sparse_down;
+//   the last WS_UPD ones the update of the counts and the residency, split
+//                        over them (win_update_part), from the state at the
+//                        start.
+// The up workgroups wait for nothing and come first in the grid, so every
+// wait of a down workgroup ends.  A slot still stale after WS_POLLS polls is
+// computed by the down workgroup itself with the up workgroups' sums (x staged
+// the same way), so the result does not depend on which one computed it.
+#define WS_POLLS (1 << 16)
+#define WS_UP_MAX 64   // up workgroups (two entries per wavefront and round)
+#define WS_UPD 16      // update workgroups
+
+// Threads of a k_win_step workgroup: 512, or 256 for F32 rows (whose up-row
+// dots need the registers of two wavefronts per SIMD).
+template <int T>
+constexpr int ws_threads() {
+    return T == LLG_TYPE_F32 ? 256 : 512;
+}
+
+// The up row's source of neuron n (< 0: none) in update e: the layer's bundle
+// when n was not resident at the start, else its resident row.
+__device__ __forceinline__ bool ws_from_src(const LlgWinUpd &u, int n) {
+    return n >= 0 && !win_resident(u.res, n, u.epoch);
+}
+
+// One batch of K entries j = tid + bd * (i0 + k) of the down role (nvalid of
+// them are below the count): block b of each down row requested from the
+// entry's source, then the activation slots polled.  missing: entries whose
+// slot stayed stale (their activation is then computed by ws_fill_missing).
+template <int T, int K>
+__device__ __forceinline__ void ws_down_batch(const LlgWinUpd &u, long long bstride,
+                                              const RowFmt &f, int b, const int32_t *active,
+                                              int n_rows, int n, int i0, int tid, int bd,
+                                              float (&acc)[32], float &corr, float *xs, int act,
+                                              const float *x) {
+    BlockRaw<T> r[K];
+    int nn[K];
+    bool fs[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int j = min(tid + bd * (i0 + k), n - 1);
+        const int a = active[j];
+        nn[k] = a >= 0 && a < n_rows ? a : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < K; k++) fs[k] = ws_from_src(u, nn[k]);
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const uint8_t *row = (fs[k] ? u.src : u.dst) + (long long)(nn[k] >= 0 ? nn[k] : 0) * bstride;
+        llg_block_load<T>(r[k], row + f.stride, f, b);
+    }
+    const int mine = (n - tid + bd - 1) / bd;  // entries of this thread in the list
+    const int nvalid = min(max(mine - i0, 0), K);
+    uint64_t v[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) v[k] = llg_slot_get(u.uslot + min(tid + bd * (i0 + k), n - 1));
+    auto ready = [&]() {
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < K; k++)
+            ok = ok && (k >= nvalid || nn[k] < 0 || (uint32_t)(v[k] >> 32) == (uint32_t)u.epoch);
+        return ok;
+    };
+    for (int polls = 0; !__all(ready()) && polls < WS_POLLS; polls++) {
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int k = 0; k < K; k++)
+            if (k < nvalid && nn[k] >= 0 && (uint32_t)(v[k] >> 32) != (uint32_t)u.epoch)
+                v[k] = llg_slot_get(u.uslot + tid + bd * (i0 + k));
+    }
+    // A slot still stale (never seen in a working launch): in rounds, every
+    // thread with a stale entry lists one of them, the wavefronts compute the
+    // listed up rows with the up workgroups' sums (x staged the same way) and
+    // write their slots, and the threads read their slots again.
+    if (__syncthreads_or(!ready())) {
+        __shared__ int ws_n;
+        __shared__ int3 ws_list[ws_threads<T>()];
+        const int lane = threadIdx.x & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        auto stale = [&](int k) {
+            return k < nvalid && nn[k] >= 0 && (uint32_t)(v[k] >> 32) != (uint32_t)u.epoch;
+        };
+        stage_x<stage_rounds(ws_threads<T>())>(xs, x, f.nb);
+        for (;;) {  // uniform: ends when no thread has a stale entry
+            if (threadIdx.x == 0) ws_n = 0;
+            __syncthreads();
+            int3 mine = make_int3(-1, 0, 0);
+#pragma unroll
+            for (int k = K - 1; k >= 0; k--)
+                if (stale(k)) mine = make_int3(tid + bd * (i0 + k), nn[k], fs[k] ? 1 : 0);
+            if (mine.x >= 0) ws_list[atomicAdd(&ws_n, 1)] = mine;
+            __syncthreads();
+            const int cnt = ws_n;
+            if (cnt == 0) break;
+            for (int i = wave; i < cnt; i += ws_threads<T>() / 64) {
+                const int3 e = ws_list[i];
+                const uint8_t *p = (e.z ? u.src : u.dst) + (long long)e.y * bstride;
+                float s0, s1;
+                row_dot2p<T>(p, p, true, false, f, xs, s0, s1);
+                if (lane == 0) llg_slot_put(u.uslot + e.x, u.epoch, llg_act(act, s0));
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < K; k++)
+                if (stale(k)) v[k] = llg_slot_get(u.uslot + tid + bd * (i0 + k));
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const float uk = __uint_as_float((uint32_t)v[k]);
+        if (k < nvalid && nn[k] >= 0 && uk != 0.0f) llg_raw_axpy<T>(r[k], uk, acc, corr);
+    }
+}
+
+template <int T>
+__global__ __launch_bounds__(ws_threads<T>()) void k_win_step(
+    RowFmt f, long long bstride, const float *__restrict__ x, const int32_t *__restrict__ active,
+    const int32_t *__restrict__ n_active_p, int cap, int n_rows, int act, int n_up, int per_xcd,
+    float *__restrict__ out, LlgWinUpd u) {
+    constexpr int NTH = ws_threads<T>(), NW = NTH / 64;
+    extern __shared__ float xs[];
+    __shared__ float red[NW][32];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n_dn = 8 * per_xcd;
+    if ((int)blockIdx.x >= n_up + n_dn) {  // the update (the bitmap in the x staging's LDS)
+        win_update_part(u, active, min(max(*n_active_p, 0), cap), n_rows,
+                        (int)blockIdx.x - n_up - n_dn, WS_UPD, reinterpret_cast<uint32_t *>(xs));
+        return;
+    }
+    auto valid = [&](int n) { return n >= 0 && n < n_rows ? n : -1; };
+    if ((int)blockIdx.x < n_up) {
+        const int S = n_up * NW;  // up wavefronts
+        const int jf = blockIdx.x * NW + wave;
+        const int n_act = min(max(*n_active_p, 0), cap);
+        if ((int)blockIdx.x * NW >= n_act) return;  // whole workgroup idle
+        const int n16 = (int)(bstride >> 4);
+        constexpr int NC = bc_first<T>();
+        auto pair = [&](int j, int m0, int m1, bool f0, bool f1) {
+            const int j1 = j + S;
+            const int row0 = __builtin_amdgcn_readfirstlane(m0);
+            const int row1 = __builtin_amdgcn_readfirstlane(m1);
+            const uint8_t *p0 = (f0 ? u.src : u.dst) + (long long)(row0 >= 0 ? row0 : 0) * bstride;
+            const uint8_t *p1 = (f1 ? u.src : u.dst) + (long long)(row1 >= 0 ? row1 : 0) * bstride;
+            const bc_u4 *sp0 = reinterpret_cast<const bc_u4 *>(p0);
+            const bc_u4 *sp1 = reinterpret_cast<const bc_u4 *>(p1);
+            bc_u4 *dp0 = reinterpret_cast<bc_u4 *>(u.dst + (long long)(f0 ? row0 : 0) * bstride);
+            bc_u4 *dp1 = reinterpret_cast<bc_u4 *>(u.dst + (long long)(f1 ? row1 : 0) * bstride);
+            BundleCopy<NC> c0, c1;
+            if (f0) bc_issue(c0, sp0, n16);
+            if (f1) bc_issue(c1, sp1, n16);
+            float s0, s1;
+            // the copies are stored once the dot's loads are in flight
+            row_dot2p<T>(p0, p1, row0 >= 0, row1 >= 0, f, xs, s0, s1, [&]() {
+                if (f0) bc_store(c0, dp0, n16);
+                if (f1) bc_store(c1, dp1, n16);
+            });
+            if (f0) bc_rest<NC>(sp0, dp0, n16);
+            if (f1) bc_rest<NC>(sp1, dp1, n16);
+            if (lane == 0) {  // an entry without a neuron has activation 0
+                llg_slot_put(u.uslot + j, u.epoch, row0 >= 0 ? llg_act(act, s0) : 0.0f);
+                if (j1 < n_act)
+                    llg_slot_put(u.uslot + j1, u.epoch, row1 >= 0 ? llg_act(act, s1) : 0.0f);
+            }
+        };
+        // the first pair's entries (never past the count: the list holds
+        // n_act entries) are requested while x is in flight
+        const bool has0 = jf < n_act;
+        int a0 = -1, a1 = -1;
+        stage_x<stage_rounds(NTH)>(xs, x, f.nb, [&]() {
+            a0 = active[min(jf, n_act - 1)];
+            a1 = active[min(jf + S, n_act - 1)];
+        });
+        const int m0 = has0 ? valid(a0) : -1;
+        const int m1 = jf + S < n_act ? valid(a1) : -1;
+        const bool f0 = __builtin_amdgcn_readfirstlane((int)ws_from_src(u, m0));
+        const bool f1 = __builtin_amdgcn_readfirstlane((int)ws_from_src(u, m1));
+        __syncthreads();
+        if (has0) pair(jf, m0, m1, f0, f1);
+        for (int j = jf + 2 * S; j < n_act; j += 2 * S) {
+            const int j1 = j + S;
+            const int n0 = valid(active[j]);
+            const int n1 = j1 < n_act ? valid(active[j1]) : -1;
+            pair(j, n0, n1, __builtin_amdgcn_readfirstlane((int)ws_from_src(u, n0)),
+                 __builtin_amdgcn_readfirstlane((int)ws_from_src(u, n1)));
+        }
+        return;
+    }
+    // the down role: output block b
+    const int bi = (int)blockIdx.x - n_up;
+    const int b = (bi & 7) * per_xcd + (bi >> 3);
+    if (b >= f.nb) return;  // uniform over the workgroup
+    const int tid = threadIdx.x, bd = blockDim.x;
+    const int o = b * 32 + (lane >> 1);
+    float acc[32];
+    float corr = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 32; e++) acc[e] = 0.0f;
+    const int n = min(max(*n_active_p, 0), cap);
+    // entries per batch: the config's 909 entries are 2 per thread; a longer
+    // list takes more batches
+    constexpr int KM = T == LLG_TYPE_F32 ? 1 : (T == LLG_TYPE_F16 ? 2 : 4);
+    const int per = (n + bd - 1) / bd;
+    for (int i0 = 0; i0 < per; i0 += KM)  // uniform over the workgroup
+        ws_down_batch<T, KM>(u, bstride, f, b, active, n_rows, n, i0, tid, bd, acc, corr, xs, act,
+                             x);
+#pragma unroll
+    for (int e = 0; e < 32; e++) acc[e] -= corr;
+    const float ws = dn_wave_transpose_sum(acc);
+    if ((lane & 1) == 0) red[wave][lane >> 1] = ws;
+    __syncthreads();
+    if (wave == 0 && (lane & 1) == 0) {
+        float sum = 0.0f;
+        for (int w = 0; w < NW; w++) sum += red[w][lane >> 1];
+        if (o < f.cols) out[o] = sum;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Host-side enqueue helpers
 // ---------------------------------------------------------------------------
 size_t llg_sparse_ws_bytes(int max_active) {
@@ -1095,70 +1267,100 @@ static int down_threads(int items) {
     return t < 64 ? 64 : (t > DN_THREADS ? DN_THREADS : t);
 }
 
-template <int T, bool WIN>
-static void launch_down(hipStream_t st, const uint8_t *base, long long bstride, const RowFmt &f,
-                        const int2 *pairs, const int32_t *count, int max_pairs, int n_rows,
-                        float *out, const LlgWinUpd &u) {
-    const int px = down_per_xcd(f);
-    hipLaunchKernelGGL((k_sparse_down<T, WIN>), dim3(8 * px + (WIN ? WIN_XWG : 0)),
-                       dim3(down_threads(max_pairs)), 0, st, base, bstride, f, pairs, count,
-                       max_pairs, n_rows, px, out, u);
-}
-
 template <int T>
 static void launch_list(hipStream_t st, const uint8_t *base, long long bstride, const RowFmt &f,
-                        const int32_t *slot_of, const float *x, const int32_t *active,
+                        const int32_t *res, const float *x, const int32_t *active,
                         const int32_t *n_active, int max_active, int n_rows, int act,
-                        float *out, int2 *pairs, const LlgWinUpd *win) {
+                        float *out, int2 *pairs) {
     int grid = (max_active + 3) / 4;
     if (grid < 1) grid = 1;
     if (grid > 512) grid = 512;
-    const LlgWinUpd u = win ? *win : LlgWinUpd{};
-    if (win) {
-        hipLaunchKernelGGL((k_list_up<T, true>), dim3(grid + WIN_XWG), dim3(256), xs_bytes(f), st, base,
-                           bstride, f, slot_of, x, active, n_active, max_active, n_rows, act,
-                           pairs, u);
-        launch_down<T, true>(st, base, bstride, f, pairs, n_active, max_active, n_rows, out, u);
-    } else {
-        hipLaunchKernelGGL((k_list_up<T, false>), dim3(grid), dim3(256), xs_bytes(f), st, base,
-                           bstride, f, slot_of, x, active, n_active, max_active, n_rows, act,
-                           pairs, u);
-        launch_down<T, false>(st, base, bstride, f, pairs, n_active, max_active, n_rows, out, u);
-    }
+    hipLaunchKernelGGL((k_list_up<T>), dim3(grid), dim3(256), xs_bytes(f), st, base, bstride, f,
+                       res, x, active, n_active, max_active, n_rows, act, pairs);
+    const int px = down_per_xcd(f);
+    hipLaunchKernelGGL((k_sparse_down<T>), dim3(8 * px), dim3(down_threads(max_active)), 0, st,
+                       base, bstride, f, (const int2 *)pairs, n_active, max_active, px, out);
 }
 
 int llg_sparse_enqueue(LlgDevice *d, const uint8_t *base, long long bstride, const RowFmt &f,
-                       const int32_t *slot_of, const float *d_x, const int32_t *d_active,
+                       const int32_t *res, const float *d_x, const int32_t *d_active,
                        const int32_t *d_n_active, int max_active, int n_rows, int act,
-                       float *d_out, uint8_t *ws, const LlgWinUpd *win) {
+                       float *d_out, uint8_t *ws) {
     if (int rc = llg_check_act(d, act)) return rc;
-    if (win && (!win->src || win->dst != base || (bstride & 15)))
-        return llg_set_error(d, LLG_E_ARG, "sparse ffn: the window step reads its resident rows");
     if (xs_bytes(f) > 64 * 1024)
         return llg_set_error(d, LLG_E_ARG, "sparse ffn: hidden size %d too large", f.cols);
     hipStream_t st = llg_dev_stream(d);
     int2 *pairs = reinterpret_cast<int2 *>(ws);
     switch (f.type) {
     case LLG_TYPE_Q4_0:
-        launch_list<LLG_TYPE_Q4_0>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                   max_active, n_rows, act, d_out, pairs, win);
+        launch_list<LLG_TYPE_Q4_0>(st, base, bstride, f, res, d_x, d_active, d_n_active,
+                                   max_active, n_rows, act, d_out, pairs);
         break;
     case LLG_TYPE_Q8_0:
-        launch_list<LLG_TYPE_Q8_0>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                   max_active, n_rows, act, d_out, pairs, win);
+        launch_list<LLG_TYPE_Q8_0>(st, base, bstride, f, res, d_x, d_active, d_n_active,
+                                   max_active, n_rows, act, d_out, pairs);
         break;
     case LLG_TYPE_F16:
-        launch_list<LLG_TYPE_F16>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                  max_active, n_rows, act, d_out, pairs, win);
+        launch_list<LLG_TYPE_F16>(st, base, bstride, f, res, d_x, d_active, d_n_active,
+                                  max_active, n_rows, act, d_out, pairs);
         break;
     case LLG_TYPE_F32:
-        launch_list<LLG_TYPE_F32>(st, base, bstride, f, slot_of, d_x, d_active, d_n_active,
-                                  max_active, n_rows, act, d_out, pairs, win);
+        launch_list<LLG_TYPE_F32>(st, base, bstride, f, res, d_x, d_active, d_n_active,
+                                  max_active, n_rows, act, d_out, pairs);
         break;
     default:
         return llg_set_error(d, LLG_E_TYPE, "sparse ffn: unsupported type %d", f.type);
     }
     LLG_LAUNCH_CHECK(d, "sparse ffn");
+    return 0;
+}
+
+template <int T>
+static void launch_win_step(hipStream_t st, const LlgWinUpd &u, const RowFmt &f,
+                            long long bstride, const float *x, const int32_t *active,
+                            const int32_t *n_active, int cap, int n_rows, int act, float *out) {
+    constexpr int PER_WG = 2 * (ws_threads<T>() / 64);  // entries of an up workgroup per round
+    int n_up = (cap + PER_WG - 1) / PER_WG;
+    n_up = n_up < 1 ? 1 : (n_up > WS_UP_MAX ? WS_UP_MAX : n_up);
+    const int px = down_per_xcd(f);
+    // LDS: the staged x, or an update workgroup's bitmap of the listed set
+    const size_t lds = std::max(xs_bytes(f), (size_t)win_bitmap_words(n_rows) * 4);
+    hipLaunchKernelGGL((k_win_step<T>), dim3(n_up + 8 * px + WS_UPD), dim3(ws_threads<T>()), lds,
+                       st, f, bstride, x, active, n_active, cap, n_rows, act, n_up, px, out, u);
+}
+
+int llg_win_step_enqueue(LlgDevice *d, const LlgWinUpd &u, const RowFmt &f, long long bstride,
+                         const float *d_x, const int32_t *d_active, const int32_t *d_n_active,
+                         int cap, int n_rows, int act, float *d_out) {
+    if (int rc = llg_check_act(d, act)) return rc;
+    if (!u.src || !u.dst || !u.uslot || (bstride & 15) || cap < 1)
+        return llg_set_error(d, LLG_E_ARG, "window step: bad window state");
+    if (xs_bytes(f) > 64 * 1024)
+        return llg_set_error(d, LLG_E_ARG, "window step: hidden size %d too large", f.cols);
+    if ((size_t)win_bitmap_words(n_rows) * 4 > 48 * 1024)
+        return llg_set_error(d, LLG_E_ARG, "window step: %d neurons too many", n_rows);
+    hipStream_t st = llg_dev_stream(d);
+    switch (f.type) {
+    case LLG_TYPE_Q4_0:
+        launch_win_step<LLG_TYPE_Q4_0>(st, u, f, bstride, d_x, d_active, d_n_active, cap, n_rows,
+                                       act, d_out);
+        break;
+    case LLG_TYPE_Q8_0:
+        launch_win_step<LLG_TYPE_Q8_0>(st, u, f, bstride, d_x, d_active, d_n_active, cap, n_rows,
+                                       act, d_out);
+        break;
+    case LLG_TYPE_F16:
+        launch_win_step<LLG_TYPE_F16>(st, u, f, bstride, d_x, d_active, d_n_active, cap, n_rows,
+                                      act, d_out);
+        break;
+    case LLG_TYPE_F32:
+        launch_win_step<LLG_TYPE_F32>(st, u, f, bstride, d_x, d_active, d_n_active, cap, n_rows,
+                                      act, d_out);
+        break;
+    default:
+        return llg_set_error(d, LLG_E_TYPE, "window step: unsupported type %d", f.type);
+    }
+    LLG_LAUNCH_CHECK(d, "window step");
     return 0;
 }
 

@@ -1,27 +1,27 @@
 // llg_window.hip -- sliding-window resident neuron set (inference/window.go).
 //
 // Device state per window (one FFN layer):
-//   slot_of[ff]   n when neuron n is resident (its bundle in row n of the
-//                 resident buffer), else -1            (the inCache map, window.go:27)
+//   res[ff]       the number of the update that loaded n while n is resident
+//                 (its bundle in row n of the resident buffer), else 0
+//                                                      (the inCache map, window.go:27)
 //   cnt[ff]       entries of the last k sets that hold n
-//   cur_ep[ff]    the number of the last update whose set held n
-//   fresh[ff]     the number of the update that last loaded n
 //   ring[k+1][ff] the last k sets (k+1 slots, so the set of this update and
 //                 the expiring one never share a slot)   (lastKActive, window.go:30)
-//   state         [2] resident neurons (NumCached), [3] loads of the last update
+//   state         [2] resident neurons (NumCached)
+//   cntr[2]       loads of an update, in cntr[epoch & 1]
+//   uslot[ff]     the update + FFN step's activations (64-bit, epoch-tagged)
 //   resident      ff bundles of bstride bytes            (matrix, window.go:23)
 //
-// Neuron n always takes row n, so an update needs no slot allocation and
-// splits into per-entry steps (llg_window_upd.hpp) over two launches:
-//   1. each entry of the set is recorded, marked and counted; each entry of
-//      the expiring set is uncounted (window.go:73-80); a listed neuron that
-//      is not resident is copied from the layer's bundle into its row
-//      (loadRows, window.go:207-245);
-//   2. an expiring neuron whose count is 0 and that the set does not hold is
-//      evicted (window.go:84-95); the loaded ones become resident.
-// A plain update runs them as k_win_update1 / k_win_update2; the update + FFN
-// step folds them into the list FFN's two launches (llg_sparse.hip), whose
-// first launch reads every loaded neuron's up row as it copies the bundle.
+// Neuron n always takes row n, so an update needs no slot allocation.  The
+// update of the counts and the residency is split over workgroups, each
+// working from the state at the start of the update and a bitmap of the
+// listed set (win_update_part, llg_window_upd.hpp); during update e a neuron
+// is resident at the start of the update exactly when res[n] is neither 0 nor
+// e, so the update marks its loads (res = e) while the bundle copies and the
+// FFN of the same launch still read the state at its start.  A plain update
+// runs the copies (k_win_copy) and then the update (k_win_update); the
+// update + FFN step runs the update beside the FFN in one launch (k_win_step,
+// llg_sparse.hip), whose up rows copy each loaded bundle as they read it.
 //
 // Physical row order differs from the reference's swap-with-last order
 // (window.go:188-204); it is unobservable, because FFNForward walks the
@@ -37,7 +37,8 @@ struct LlgWindow {
     LlgObject *bundle;  // source bundle (the layer in HBM)
     int k, ff, head;    // head: ring slot of the next set
     int epoch;          // number of the last update (tags); starts at 1
-    int32_t *slot_of, *cnt, *cur_ep, *fresh, *ring, *ring_len, *ring_set, *state, *cntr;
+    int32_t *res, *cnt, *ring, *ring_len, *ring_set, *state, *cntr;
+    uint64_t *uslot;
     uint8_t *resident;
     long long bstride;
 };
@@ -45,45 +46,46 @@ struct LlgWindow {
 void llg_window_destroy(LlgDevice *d, LlgObject *o) {
     LlgWindow *w = reinterpret_cast<LlgWindow *>(o->ext);
     if (!w) return;
-    hipFree(w->slot_of);
+    hipFree(w->res);
+    hipFree(w->uslot);
     hipFree(w->resident);
     llg_unref(d, w->bundle);
     delete w;
     o->ext = nullptr;
 }
 
-// Step 1 of a plain update: one wavefront per listed entry (grid-stride);
-// every thread also takes a share of the expiring set.  A device list is not
-// checked on the host, so the count is clamped to [0, ff] and an index outside
-// [0, ff) is recorded as -1 and skipped: every access stays in bounds.
-__global__ __launch_bounds__(256) void k_win_update1(LlgWinUpd u, const int32_t *__restrict__ active,
-                                                     const int32_t *__restrict__ n_active_p,
-                                                     int ff, long long bstride) {
+// The copies of a plain update: one wavefront per listed entry (grid-stride)
+// copies the bundle of a neuron that is not resident into its row
+// (loadRows, window.go:207-245).  A device list is not checked on the host,
+// so the count is clamped to [0, ff] and an index outside [0, ff) is skipped:
+// every access stays in bounds.
+__global__ __launch_bounds__(256) void k_win_copy(LlgWinUpd u, const int32_t *__restrict__ active,
+                                                  const int32_t *__restrict__ n_active_p, int ff,
+                                                  long long bstride) {
     const int n_act = min(max(*n_active_p, 0), ff);
-    win_expire_all(u, n_act, ff, blockIdx.x * blockDim.x + threadIdx.x, gridDim.x * blockDim.x);
     const int lane = threadIdx.x & 63;
     const int n16 = (int)(bstride >> 4);
     for (int j = blockIdx.x * 4 + (threadIdx.x >> 6); j < n_act; j += gridDim.x * 4) {
-        int n = active[j];
-        n = n >= 0 && n < ff ? n : -1;
-        int ld = 0;
-        if (lane == 0) ld = win_note_active(u, j, n);
-        if (__builtin_amdgcn_readfirstlane(ld)) {
-            const uint4 *sp = reinterpret_cast<const uint4 *>(u.src + (long long)n * bstride);
-            uint4 *dp = reinterpret_cast<uint4 *>(u.dst + (long long)n * bstride);
-            for (int c = lane; c < n16; c += 64) dp[c] = sp[c];
-            if (lane == 0) win_note_load(u, n);
-        }
+        const int n = active[j];
+        if (n < 0 || n >= ff || __builtin_amdgcn_readfirstlane((int)win_resident(u.res, n, u.epoch)))
+            continue;
+        const uint4 *sp = reinterpret_cast<const uint4 *>(u.src + (long long)n * bstride);
+        uint4 *dp = reinterpret_cast<uint4 *>(u.dst + (long long)n * bstride);
+        for (int c = lane; c < n16; c += 64) dp[c] = sp[c];
     }
 }
 
-// Step 2 of a plain update.
-__global__ __launch_bounds__(256) void k_win_update2(LlgWinUpd u,
-                                                     const int32_t *__restrict__ n_active_p,
-                                                     int ff) {
-    win_finish_all(u, min(max(*n_active_p, 0), ff), ff, blockIdx.x * blockDim.x + threadIdx.x,
-                   gridDim.x * blockDim.x);
+// The counts and the residency of a plain update, part blockIdx.x of
+// gridDim.x (LDS: the bitmap of the listed set).
+__global__ __launch_bounds__(256) void k_win_update(LlgWinUpd u, const int32_t *__restrict__ active,
+                                                    const int32_t *__restrict__ n_active_p,
+                                                    int ff) {
+    extern __shared__ uint32_t bm[];
+    win_update_part(u, active, min(max(*n_active_p, 0), ff), ff, blockIdx.x, gridDim.x, bm);
 }
+
+// Workgroups of an update (each takes every WIN_UPD_PARTS-th entry).
+#define WIN_UPD_PARTS 16
 
 static LlgWindow *get_window(LlgDevice *d, int64_t h) {
     LlgObject *o = llg_get(d, h, LLG_KIND_WINDOW);
@@ -93,7 +95,7 @@ static LlgWindow *get_window(LlgDevice *d, int64_t h) {
 // Number of the update after `e`.  Loads are counted in cntr[epoch & 1] and
 // each update clears the other counter for the next one, so consecutive
 // numbers must alternate in parity, across the wrap too: after 0x7FFFFFFF
-// (odd) comes 2, never 1 (0 stays "never listed").
+// (odd) comes 2, never 1 (0 marks a neuron that is not resident).
 constexpr int llg_next_epoch(int e) { return e == 0x7FFFFFFF ? 2 : e + 1; }
 static_assert(llg_next_epoch(0) == 1 && llg_next_epoch(1) == 2, "updates are numbered from 1");
 static_assert(llg_next_epoch(0x7FFFFFFF) == 2 && llg_next_epoch(0x7FFFFFFE) == 0x7FFFFFFF,
@@ -103,19 +105,21 @@ static_assert(((llg_next_epoch(0x7FFFFFFF) ^ 0x7FFFFFFF) & 1) &&
                   ((llg_next_epoch(llg_next_epoch(0x7FFFFFFF)) ^ llg_next_epoch(0x7FFFFFFF)) & 1),
               "consecutive updates alternate in parity across the wrap");
 
-// The folded update of the next set: numbers it, and names its ring slot and
-// the expiring one.
-static LlgWinUpd next_update(LlgWindow *w) {
+// The next update: numbers it, and names its ring slot and the expiring one.
+// When the numbers wrap, the activation slots are cleared, so that no slot
+// keeps a tag from 2^31 updates ago (a neuron that has stayed resident since
+// then counts one load more).
+static LlgWinUpd next_update(LlgWindow *w, hipStream_t st) {
+    const bool wraps = w->epoch == 0x7FFFFFFF;
     w->epoch = llg_next_epoch(w->epoch);
+    if (wraps) (void)hipMemsetAsync(w->uslot, 0, (size_t)w->ff * 8, st);
     const int e = (w->head + 1) % (w->k + 1);  // the set of k updates ago
     const size_t ff = (size_t)w->ff;
     LlgWinUpd u;
     u.src = w->bundle->d;
     u.dst = w->resident;
-    u.slot_of = w->slot_of;
+    u.res = w->res;
     u.cnt = w->cnt;
-    u.cur_ep = w->cur_ep;
-    u.fresh = w->fresh;
     u.state = w->state;
     u.cntr = w->cntr;
     u.ring_new = w->ring + (size_t)w->head * ff;
@@ -124,6 +128,7 @@ static LlgWinUpd next_update(LlgWindow *w) {
     u.ring_exp = w->ring + (size_t)e * ff;
     u.ring_len_exp = w->ring_len + e;
     u.ring_set_exp = w->ring_set + e;
+    u.uslot = w->uslot;
     u.epoch = w->epoch;
     w->head = (w->head + 1) % (w->k + 1);
     return u;
@@ -132,11 +137,12 @@ static LlgWinUpd next_update(LlgWindow *w) {
 static int window_update_enqueue(LlgDevice *d, LlgWindow *w, const int32_t *d_active,
                                  const int32_t *d_n_active, int max_active) {
     hipStream_t st = llg_dev_stream(d);
-    const LlgWinUpd u = next_update(w);
+    const LlgWinUpd u = next_update(w, st);
     const int grid = std::max(1, std::min((std::max(max_active, 1) + 3) / 4, 2048));
-    hipLaunchKernelGGL(k_win_update1, dim3(grid), dim3(256), 0, st, u, d_active, d_n_active, w->ff,
+    hipLaunchKernelGGL(k_win_copy, dim3(grid), dim3(256), 0, st, u, d_active, d_n_active, w->ff,
                        w->bstride);
-    hipLaunchKernelGGL(k_win_update2, dim3(grid), dim3(256), 0, st, u, d_n_active, w->ff);
+    hipLaunchKernelGGL(k_win_update, dim3(WIN_UPD_PARTS), dim3(256),
+                       (size_t)win_bitmap_words(w->ff) * 4, st, u, d_active, d_n_active, w->ff);
     LLG_LAUNCH_CHECK(d, "window_update");
     return 0;
 }
@@ -157,33 +163,36 @@ int llg_hip_window_create(LlgHipDevice h, int64_t hb, int k, int64_t *win) {
     w->bstride = b->stride;
     const size_t ff = (size_t)w->ff, slots = (size_t)k + 1;
     // one allocation for the int32 state arrays
-    const size_t n_ints = ff * 4 + slots * ff + 2 * slots + 4 + 2;
+    const size_t n_ints = ff * 2 + slots * ff + 2 * slots + 4 + 2;
     int32_t *m = nullptr;
     if (hipMalloc(&m, n_ints * 4) != hipSuccess) {
         delete w;
         return llg_set_error(d, LLG_E_NOMEM, "window_create: state allocation failed");
     }
-    w->slot_of = m;
+    w->res = m;  // 0: nothing resident
     w->cnt = m + ff;
-    w->cur_ep = w->cnt + ff;  // 0: never listed (updates are numbered from 1)
-    w->fresh = w->cur_ep + ff;
-    w->ring = w->fresh + ff;
+    w->ring = w->cnt + ff;
     w->ring_len = w->ring + slots * ff;
     w->ring_set = w->ring_len + slots;
     w->state = w->ring_set + slots;
     w->cntr = w->state + 4;
     w->epoch = 0;
-    if (hipMalloc(&w->resident, ff * w->bstride) != hipSuccess) {
+    w->uslot = nullptr;
+    w->resident = nullptr;
+    if (hipMalloc(&w->uslot, ff * 8) != hipSuccess ||
+        hipMalloc(&w->resident, ff * w->bstride) != hipSuccess) {
         hipFree(m);
+        if (w->uslot) hipFree(w->uslot);
         delete w;
         return llg_set_error(d, LLG_E_NOMEM, "window_create: resident buffer allocation failed");
     }
     hipStream_t st = llg_dev_stream(d);
     hipError_t e = hipMemsetAsync(m, 0, n_ints * 4, st);
-    if (e == hipSuccess) e = hipMemsetAsync(w->slot_of, 0xFF, ff * 4, st);  // -1: nothing resident
+    if (e == hipSuccess) e = hipMemsetAsync(w->uslot, 0, ff * 8, st);  // tag 0: no update
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (e != hipSuccess) {
         hipFree(m);
+        hipFree(w->uslot);
         hipFree(w->resident);
         delete w;
         return llg_hip_error(d, e, "window_create");
@@ -227,10 +236,10 @@ int llg_hip_window_update(LlgHipDevice h, int64_t hw, const int32_t *active, int
     if ((rc = window_update_enqueue(d, w, (const int32_t *)ws, (const int32_t *)(ws + o_n),
                                     n_active)))
         return rc;
-    int32_t st[4];
+    int32_t st[6];  // state[0..3] and cntr[0..1]
     if ((rc = llg_d2h(d, st, w->state, sizeof st))) return rc;
     if ((rc = llg_sync_dev(d))) return rc;
-    if (n_loaded) *n_loaded = st[3];
+    if (n_loaded) *n_loaded = st[4 + (w->epoch & 1)];
     if (n_resident) *n_resident = st[2];
     return 0;
 }
@@ -263,7 +272,7 @@ int llg_hip_window_ffn(LlgHipDevice h, int64_t hw, const float *x, const int32_t
     if ((rc = llg_h2d(d, ws, x, (size_t)hd * 4))) return rc;
     if ((rc = llg_h2d(d, ws + o_act, active, (size_t)n_active * 4))) return rc;
     if ((rc = llg_h2d(d, ws + o_n, &n32, 4))) return rc;
-    rc = llg_sparse_enqueue(d, w->resident, w->bstride, w->bundle->fmt, w->slot_of,
+    rc = llg_sparse_enqueue(d, w->resident, w->bstride, w->bundle->fmt, w->res,
                             (const float *)ws, (const int32_t *)(ws + o_act),
                             (const int32_t *)(ws + o_n), n_active, w->ff, act,
                             (float *)(ws + o_out), ws + o_ws);
@@ -280,12 +289,10 @@ int llg_hipd_window_step(LlgHipDevice h, int64_t hw, const float *d_x, const int
     if (!w) return llg_set_error(d, LLG_E_HANDLE, "window_step: unknown window");
     if (!d_x || !d_active || !d_n_active || !d_out)
         return llg_set_error(d, LLG_E_ARG, "window_step: null pointer");
-    int rc;
-    uint8_t *ws = (uint8_t *)llg_ws(d, llg_sparse_ws_bytes(w->ff), &rc);
-    if (rc) return rc;
-    const LlgWinUpd u = next_update(w);
-    return llg_sparse_enqueue(d, w->resident, w->bstride, w->bundle->fmt, w->slot_of, d_x,
-                              d_active, d_n_active, w->ff, w->ff, act, d_out, ws, &u);
+    if (int rc = llg_check_act(d, act)) return rc;
+    const LlgWinUpd u = next_update(w, llg_dev_stream(d));
+    return llg_win_step_enqueue(d, u, w->bundle->fmt, w->bstride, d_x, d_active, d_n_active,
+                                w->ff, w->ff, act, d_out);
 }
 
 int llg_hip_window_resident(LlgHipDevice h, int64_t hw, uint8_t *resident, int *n_resident) {
@@ -293,14 +300,14 @@ int llg_hip_window_resident(LlgHipDevice h, int64_t hw, uint8_t *resident, int *
     if (!d) return LLG_E_NODEV;
     LlgWindow *w = get_window(d, hw);
     if (!w) return llg_set_error(d, LLG_E_HANDLE, "window_resident: unknown window");
-    std::vector<int32_t> slots((size_t)w->ff);
+    std::vector<int32_t> res((size_t)w->ff);
     int32_t st[4];
     int rc;
-    if ((rc = llg_d2h(d, slots.data(), w->slot_of, (size_t)w->ff * 4))) return rc;
+    if ((rc = llg_d2h(d, res.data(), w->res, (size_t)w->ff * 4))) return rc;
     if ((rc = llg_d2h(d, st, w->state, sizeof st))) return rc;
     if ((rc = llg_sync_dev(d))) return rc;
     if (resident)
-        for (int i = 0; i < w->ff; i++) resident[i] = slots[i] >= 0 ? 1 : 0;
+        for (int i = 0; i < w->ff; i++) resident[i] = res[i] != 0 ? 1 : 0;
     if (n_resident) *n_resident = st[2];
     return 0;
 }
