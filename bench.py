@@ -485,9 +485,9 @@ def bench_window(args, torch, llg, dev):
                       "d_ff": FF, "window_k": WIN_K, "active": N_ACTIVE, "keep_from_prev": WIN_KEEP,
                       "tokens_per_sequence": WIN_SEQ, "mean_loaded_per_token": n_load,
                       "bundle_copies": n_copies},
-           "roofline": {"bound": "hbm", "kernel": "k_list_up (with the window update's first half "
-                        "and the gather of loaded bundles) + k_sparse_down (with its second "
-                        "half), one token", "achieved": gbs, "peak": HBM_PEAK_GBS,
+           "roofline": {"bound": "hbm", "kernel": "k_win_step (up rows with the gather of "
+                        "loaded bundles, down products, and the window update), one token",
+                        "achieved": gbs, "peak": HBM_PEAK_GBS,
                         "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None,
                         "alg_bytes_per_step": alg, "avg_step_us": ms * 1e3}}
     if not args.no_cpu:

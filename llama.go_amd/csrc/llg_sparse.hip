@@ -1093,12 +1093,12 @@ __device__ __forceinline__ void ws_down_batch(const LlgWinUpd &u, long long bstr
             ok = ok && (k >= nvalid || nn[k] < 0 || (uint32_t)(v[k] >> 32) == (uint32_t)u.epoch);
         return ok;
     };
+    // every slot polled again together (a slot already seen holds the same
+    // word), so that each poll is one memory round
     for (int polls = 0; !__all(ready()) && polls < WS_POLLS; polls++) {
         __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-        for (int k = 0; k < K; k++)
-            if (k < nvalid && nn[k] >= 0 && (uint32_t)(v[k] >> 32) != (uint32_t)u.epoch)
-                v[k] = llg_slot_get(u.uslot + tid + bd * (i0 + k));
+        for (int k = 0; k < K; k++) v[k] = llg_slot_get(u.uslot + min(tid + bd * (i0 + k), n - 1));
     }
     // A slot still stale (never seen in a working launch): in rounds, every
     // thread with a stale entry lists one of them, the wavefronts compute the
