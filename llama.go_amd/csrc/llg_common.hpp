@@ -909,6 +909,9 @@ struct LlgObject {
     int rows;            // matrix rows, or bundle neurons (ff)
     long long stride;    // matrix: bytes per row; bundle: bytes per neuron (2 * fmt.stride)
     void *ext;           // kind-specific state (window, model)
+    // Q4_0 matrix: the grouped GEMM's fragment-major copy (llg_moe_gemm.hip),
+    // made at its first use and freed with the object; null until then
+    mutable uint8_t *tiled;
     int refs;            // windows / models holding this object
     bool released;       // handle retired; freed when refs reaches 0
 };

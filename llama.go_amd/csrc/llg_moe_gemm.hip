@@ -19,7 +19,11 @@
 // group g word j of block g, so a lane's 16-byte load of one block holds its
 // B fragments for all 4 steps of the chunk.  The B fragment is built from the
 // word with two and-or's per nibble pair (q4_frag), an exact subtraction of
-// the offset and a multiply by the block scale.  Tiles: 64 rows per
+// the offset and a multiply by the block scale.  The weights are read from
+// a fragment-major copy of each matrix (k_gm_pack, made once per matrix at its
+// first use), where the B fragments of one 16-column group and K chunk are
+// 1152 contiguous bytes, so each B load instruction reads whole cache lines.
+// Tiles: 64 rows per
 // workgroup, 4 wavefronts of 64 rows each; a gate/up wavefront owns 32 columns
 // of gate and the same 32 of up, a down wavefront 64 columns, so each A
 // fragment feeds 4 MFMAs.  A in K chunks of 128 staged in LDS (double
@@ -105,6 +109,52 @@ __global__ void k_moe_x16(const float *__restrict__ x, long long n8, _Float16 *_
     reinterpret_cast<half8_t *>(x16)[dst] = h;
 }
 
+// The fragment-major copy of a Q4_0 matrix (rows a multiple of 16, columns of
+// GM_KC): 16-row group g and K chunk c (GM_KB blocks) take the 1152 bytes at
+// (g * nck + c) * 1152: lane l's 16 quant bytes (row 16 g + l % 16, block
+// GM_KB c + l / 16) at l * 16, then the lanes' block scales at 1024 + 2 l.
+// That is a wavefront's B fragments for the chunk's 4 MFMA steps (and their
+// scales) in the lane order of k_moe_gemm's loads.  One thread per (g, c, l).
+#define GM_FRAG_BYTES 1152
+__global__ void k_gm_pack(const uint8_t *__restrict__ src, long long stride, int d_off, int nck,
+                          long long n_units, uint8_t *__restrict__ dst) {
+    const long long u = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (u >= n_units) return;
+    const int l = (int)(u & 63);
+    const long long gc = u >> 6;  // g * nck + c
+    const long long g = gc / nck;
+    const int c = (int)(gc % nck);
+    const uint8_t *row = src + (g * 16 + (l & 15)) * stride;
+    const int blk = GM_KB * c + (l >> 4);
+    uint8_t *o = dst + gc * GM_FRAG_BYTES;
+    *reinterpret_cast<uint4 *>(o + l * 16) = *reinterpret_cast<const uint4 *>(row + blk * 16);
+    *reinterpret_cast<unsigned short *>(o + 1024 + l * 2) =
+        *reinterpret_cast<const unsigned short *>(row + d_off + blk * 2);
+}
+
+// The fragment-major copy of w, made (on the stream) at the first call.
+static const uint8_t *gm_tiled(LlgDevice *d, const LlgObject *w, int *rc) {
+    *rc = 0;
+    if (w->tiled) return w->tiled;
+    const int nck = w->fmt.cols / GM_KC;
+    const size_t bytes = (size_t)w->rows / 16 * nck * GM_FRAG_BYTES;
+    uint8_t *t = nullptr;
+    if (hipMalloc(&t, bytes) != hipSuccess) {
+        *rc = llg_set_error(d, LLG_E_NOMEM, "moe gemm: fragment-major copy (%zu bytes)", bytes);
+        return nullptr;
+    }
+    const long long n_units = (long long)w->rows / 16 * nck * 64;
+    hipLaunchKernelGGL(k_gm_pack, dim3((unsigned)((n_units + 255) / 256)), dim3(256), 0,
+                       llg_dev_stream(d), w->d, w->stride, w->fmt.d_off, nck, n_units, t);
+    if (hipError_t e = hipGetLastError(); e != hipSuccess) {
+        hipFree(t);
+        *rc = llg_hip_error(d, e, "moe gemm: fragment-major copy");
+        return nullptr;
+    }
+    w->tiled = t;
+    return t;
+}
+
 // (a & m) | o in one instruction
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
     uint32_t r;
@@ -173,8 +223,8 @@ template <int MODE>
 __global__ __launch_bounds__(256, 2) void k_moe_gemm(
     const int4 *__restrict__ tiles, const int32_t *__restrict__ n_tiles_p,
     const int32_t *__restrict__ row_pair, int k_slots, const _Float16 *__restrict__ A,
-    const uint8_t *__restrict__ W0, const uint8_t *__restrict__ W1, long long wstride,
-    int d_off, int rows_per_expert, int K, int N, _Float16 *__restrict__ H,
+    const uint8_t *__restrict__ W0, const uint8_t *__restrict__ W1, int rows_per_expert, int K,
+    int N, _Float16 *__restrict__ H,
     float *__restrict__ Y, int ksplit, long long ystride) {
     constexpr int NF = 4;                     // B fragments per wavefront per K step
     constexpr int WC = gm_wave_cols<MODE>();  // columns per wavefront per matrix
@@ -208,15 +258,19 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
         const long long arow = MODE == 0 ? row_pair[row0 + rr] / k_slots : row0 + rr;
         a_off[q] = arow * K + part * 8;
     }
-    // B: fragment f = (matrix m, 16-column group ns) -> column
-    // n0 + wave*WC + ns*16 + li of matrix m (gate/up: m = f / 2, ns = f % 2;
-    // down: m = 0, ns = f); the lane's block of chunk c is 4c + lg.
+    // B: fragment f = (matrix m, 16-column group ns) -> columns
+    // n0 + wave*WC + ns*16 .. + 15 of matrix m (gate/up: m = f / 2, ns = f % 2;
+    // down: m = 0, ns = f), the 16-row group of the fragment-major copy whose
+    // chunk c holds the lane's block 4c + lg of column n0 + wave*WC + ns*16 + li
+    // at lane * 16 (its scale at 1024 + lane * 2).
+    const int nck = K / GM_KC;
     const uint8_t *brow[NF];
 #pragma unroll
     for (int f = 0; f < NF; f++) {
         const int m = MODE == 0 ? f / 2 : 0, ns = MODE == 0 ? f % 2 : f;
         const uint8_t *W = m == 1 ? W1 : W0;
-        brow[f] = W + ((long long)e * rows_per_expert + n0 + wave * WC + ns * 16 + li) * wstride;
+        const long long g = ((long long)e * rows_per_expert + n0 + wave * WC + ns * 16) / 16;
+        brow[f] = W + g * nck * GM_FRAG_BYTES;
     }
 
     constexpr int NB = GM_BD + 1;                  // B register slots
@@ -229,9 +283,9 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
         *reinterpret_cast<const u32x4_t *>(A + a_off[q] + (long long)(c) * GM_KC)
 #define GM_LOAD_B(c, slot)                                                                       \
     _Pragma("unroll") for (int f = 0; f < NF; f++) {                                             \
-        const int blk = 4 * (c) + lg;                                                            \
-        bq[slot][f] = *reinterpret_cast<const u32x4_t *>(brow[f] + blk * 16);                    \
-        bd[slot][f] = *reinterpret_cast<const _Float16 *>(brow[f] + d_off + blk * 2);            \
+        const uint8_t *fr = brow[f] + (long long)(c) * GM_FRAG_BYTES;                            \
+        bq[slot][f] = *reinterpret_cast<const u32x4_t *>(fr + lane * 16);                        \
+        bd[slot][f] = *reinterpret_cast<const _Float16 *>(fr + 1024 + lane * 2);                 \
     }
 #define GM_STORE_A(buf)                                                                          \
     _Pragma("unroll") for (int q = 0; q < NMS; q++) {                                           \
@@ -382,6 +436,11 @@ int llg_moe_gemm_enqueue(LlgDevice *d, const LlgObject *gate, const LlgObject *u
                          const LlgObject *down, int n_exp, int k, int hidden, int eff,
                          const float *d_x, int n_tok, const int32_t *ids, const float *w,
                          float *d_out, uint8_t *ws) {
+    int rc = 0;
+    const uint8_t *tg = gm_tiled(d, gate, &rc);
+    const uint8_t *tu = rc ? nullptr : gm_tiled(d, up, &rc);
+    const uint8_t *td = rc ? nullptr : gm_tiled(d, down, &rc);
+    if (rc) return rc;
     hipStream_t st = llg_dev_stream(d);
     const long long np = (long long)n_tok * k;
     const long long nt_max = np / GM_BM + n_exp + 1;
@@ -407,15 +466,15 @@ int llg_moe_gemm_enqueue(LlgDevice *d, const LlgObject *gate, const LlgObject *u
                        x16);
     hipLaunchKernelGGL((k_moe_gemm<0>), dim3((unsigned)(nt_max * (eff / (4 * gm_wave_cols<0>())))),
                        dim3(256), 0, st,
-                       tiles, n_tiles, row_pair, k, x16, gate->d, up->d, gate->stride,
-                       gate->fmt.d_off, eff, hidden, eff, H, (float *)nullptr, 1, 0ll);
+                       tiles, n_tiles, row_pair, k, x16, tg, tu, eff, hidden, eff, H,
+                       (float *)nullptr, 1, 0ll);
     const int ksplit = down_split(eff);
     const long long ystride = llg_align(np * hidden * 4, 256) / 4;
     hipLaunchKernelGGL((k_moe_gemm<1>),
                        dim3((unsigned)(nt_max * (hidden / (4 * gm_wave_cols<1>())) * ksplit)),
-                       dim3(256), 0, st, tiles, n_tiles, row_pair, k, H, down->d,
-                       (const uint8_t *)nullptr, down->stride, down->fmt.d_off, hidden, eff,
-                       hidden, (_Float16 *)nullptr, Y, ksplit, ystride);
+                       dim3(256), 0, st, tiles, n_tiles, row_pair, k, H, td,
+                       (const uint8_t *)nullptr, hidden, eff, hidden, (_Float16 *)nullptr, Y,
+                       ksplit, ystride);
     const long long n4 = (long long)n_tok * hidden / 4;
     hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, Y,
                        pair_row, w, k, n_tok, hidden, ksplit, ystride, d_out);

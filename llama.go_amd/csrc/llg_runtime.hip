@@ -111,6 +111,7 @@ static void destroy_object(LlgDevice *d, LlgObject *o) {
     if (o->kind == LLG_KIND_WINDOW) llg_window_destroy(d, o);
     if (o->kind == LLG_KIND_MODEL) llg_model_destroy(d, o);
     if (o->d) hipFree(o->d);
+    if (o->tiled) hipFree(o->tiled);
     delete o;
 }
 
