@@ -4,7 +4,8 @@
 //
 //   1. k_moe_router (llg_moe.hip): ids / weights per token
 //   2. k_moe_group: counting sort of the (token, slot) pairs by expert, the
-//      pair <-> row maps, and a list of 64-row M-tiles (expert, first row, rows)
+//      pair <-> row maps, and a list of M-tiles (expert, first row, rows):
+//      each expert's rows in the fewest tiles of at most 80 rows, balanced
 //   3. k_moe_x16: X -> f16 in the MFMA K order (k_order)
 //   4. k_moe_gemm<0>: G = X_e . gate_e^T, U = X_e . up_e^T on v_mfma_f32_16x16x32_f16,
 //      epilogue H = silu(G) * U (moe_forward.go:128-132) stored f16, same K order
@@ -23,8 +24,8 @@
 // a fragment-major copy of each matrix (k_gm_pack, made once per matrix at its
 // first use), where the B fragments of one 16-column group and K chunk are
 // 1152 contiguous bytes, so each B load instruction reads whole cache lines.
-// Tiles: 64 rows per
-// workgroup, 4 wavefronts of 64 rows each; a gate/up wavefront owns 32 columns
+// Tiles: up to 80 rows per
+// workgroup, 4 wavefronts of all the tile's rows each; a gate/up wavefront owns 32 columns
 // of gate and the same 32 of up, a down wavefront 64 columns, so each A
 // fragment feeds 4 MFMAs.  A in K chunks of 128 staged in LDS (double
 // buffered; the next chunk is loaded into registers while the current one is
@@ -39,7 +40,8 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
-#define GM_BM 64
+#define GM_BM 80
+#define GM_MS (GM_BM / 16)  // 16-row MFMA groups of a tile
 #define GM_KC 128                 // K per chunk
 #define GM_KB (GM_KC / 32)        // Q4_0 blocks per chunk
 #define GM_AST (GM_KC + 8)        // LDS A row stride (halves)
@@ -71,8 +73,14 @@ __global__ __launch_bounds__(1024) void k_moe_group(const int32_t *__restrict__ 
         int o = 0, nt = 0;
         for (int e = 0; e < n_exp; e++) {
             off[e] = o;
-            for (int r = 0; r < cnt[e]; r += GM_BM)
-                tiles[nt++] = make_int4(e, o + r, min(GM_BM, cnt[e] - r), 0);
+            // the fewest tiles of at most GM_BM rows (each streams the
+            // expert's weights once), their sizes within one of each other
+            const int n = (cnt[e] + GM_BM - 1) / GM_BM;
+            for (int i = 0, r = 0; i < n; i++) {
+                const int rows = cnt[e] / n + (i < cnt[e] % n ? 1 : 0);
+                tiles[nt++] = make_int4(e, o + r, rows, 0);
+                r += rows;
+            }
             o += cnt[e];
         }
         off[n_exp] = o;
@@ -206,7 +214,7 @@ __device__ __forceinline__ int k_order(int k) {
 // q writes its partial product to Y + q * ystride (the combine adds them).
 // blockIdx = (M tile * N tiles + N tile) * ksplit + slice.
 // A rows: MODE 0 gathers X16 row row_pair[r] / k (the pair's token); MODE 1
-// reads H row r.  A goes through LDS (every wavefront reads all 64 rows); B
+// reads H row r.  A goes through LDS (every wavefront reads all the rows); B
 // is private to a wavefront (its columns), so each lane loads its own
 // block of each column straight into registers: lane (column n, group g)
 // takes the 16 quant bytes and the scale of block 4c + g of chunk c, whose
@@ -240,16 +248,16 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lg = lane >> 4;
 
-    // The tile's rows take NMS = ceil(nrows / 16) of the four 16-row MFMA
+    // The tile's rows take NMS = ceil(nrows / 16) of the GM_MS 16-row MFMA
     // groups; the body is instantiated per NMS and chosen once per workgroup,
     // so a ragged tile issues no MFMAs, A loads or stores for its empty groups
     // and each instance stays straight-line code.
     auto body = [&](auto nms_c) __attribute__((always_inline)) {
     constexpr int NMS = decltype(nms_c)::value;
-    // A: 64 rows x 16 uint4 per chunk -> thread load q covers rows 16 q ..
+    // A: GM_BM rows x 16 uint4 per chunk -> thread load q covers rows 16 q ..
     // 16 q + 15, so only q < NMS are needed (rows past the tile reload the
     // tile's last row; their results are dropped).
-    long long a_off[4];
+    long long a_off[GM_MS];
 #pragma unroll
     for (int q = 0; q < NMS; q++) {
         const int idx = tid + 256 * q;
@@ -275,7 +283,7 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
 
     constexpr int NB = GM_BD + 1;                  // B register slots
     constexpr int UNR = NB % 2 == 0 ? NB : 2 * NB;  // loop unroll: static A buffer and B slot
-    u32x4_t ra[4];
+    u32x4_t ra[GM_MS];
     u32x4_t bq[NB][NF];
     _Float16 bd[NB][NF];  // block scales as loaded (no conversion that would wait for them)
 #define GM_LOAD_A(c)                                                                             \
@@ -376,7 +384,8 @@ __global__ __launch_bounds__(256, 2) void k_moe_gemm(
     case 1: body(std::integral_constant<int, 1>{}); break;
     case 2: body(std::integral_constant<int, 2>{}); break;
     case 3: body(std::integral_constant<int, 3>{}); break;
-    default: body(std::integral_constant<int, 4>{}); break;
+    case 4: body(std::integral_constant<int, 4>{}); break;
+    default: body(std::integral_constant<int, 5>{}); break;
     }
 }
 
