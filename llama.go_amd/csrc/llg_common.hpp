@@ -643,6 +643,66 @@ struct LlgAttnParts {
 };
 #define LLG_ATTN_SPLIT_MAX 4
 
+// One float4 of the merged attention output from its splits' acc and (m, l)
+// (the slots past n_split are ignored).
+__device__ __forceinline__ float4 llg_attn_merge4(const float4 (&a)[LLG_ATTN_SPLIT_MAX],
+                                                  const float2 (&ml)[LLG_ATTN_SPLIT_MAX],
+                                                  int n_split) {
+    float M = ml[0].x;
+#pragma unroll
+    for (int s = 1; s < LLG_ATTN_SPLIT_MAX; s++)
+        if (s < n_split) M = fmaxf(M, ml[s].x);
+    float L = 0.0f;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int s = 0; s < LLG_ATTN_SPLIT_MAX; s++)
+        if (s < n_split) {
+            const float e = ml[s].x == -INFINITY ? 0.0f : expf(ml[s].x - M);
+            L += ml[s].y * e;
+            v.x += a[s].x * e;
+            v.y += a[s].y * e;
+            v.z += a[s].z * e;
+            v.w += a[s].w * e;
+        }
+    const float rl = 1.0f / L;
+    v.x *= rl;
+    v.y *= rl;
+    v.z *= rl;
+    v.w *= rl;
+    return v;
+}
+
+// Float4 j of the merged attention output, read from the splits directly,
+// one split at a time (few registers): the operations of llg_attn_merge4 in
+// the same order, so the same value.
+__device__ __forceinline__ float4 llg_attn_merged4(const LlgAttnParts &ap, int j) {
+    const int cols = ap.n_heads * ap.head_dim, h = 4 * j / ap.head_dim;
+    const float2 *ml = reinterpret_cast<const float2 *>(ap.ml) + h;
+    const float4 *a = reinterpret_cast<const float4 *>(ap.acc) + j;
+    float M = ml[0].x;
+#pragma unroll 1
+    for (int s = 1; s < ap.n_split; s++) M = fmaxf(M, ml[s * ap.n_heads].x);
+    float L = 0.0f;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 1
+    for (int s = 0; s < ap.n_split; s++) {
+        const float2 m = ml[s * ap.n_heads];
+        const float4 x = a[(size_t)s * cols >> 2];
+        const float e = m.x == -INFINITY ? 0.0f : expf(m.x - M);
+        L += m.y * e;
+        v.x += x.x * e;
+        v.y += x.y * e;
+        v.z += x.z * e;
+        v.w += x.w * e;
+    }
+    const float rl = 1.0f / L;
+    v.x *= rl;
+    v.y *= rl;
+    v.z *= rl;
+    v.w *= rl;
+    return v;
+}
+
 // Stage the merged attention output, x[c] = sum_s acc_s[c] e_s / sum_s l_s e_s
 // with e_s = exp(m_s - max_s m_s) for the head of column c (0 for an empty
 // split), like llg_stage_x_sum (the nb blocks from block cb0).  Each thread
@@ -678,30 +738,9 @@ __device__ __forceinline__ void llg_stage_attn(float *xs, const LlgAttnParts &ap
     };
     auto merge = [&](int k0) {
 #pragma unroll
-        for (int k = 0; k < KB; k++) {
-            float M = ml[k][0].x;
-#pragma unroll
-            for (int s = 1; s < LLG_ATTN_SPLIT_MAX; s++)
-                if (s < ap.n_split) M = fmaxf(M, ml[k][s].x);
-            float L = 0.0f;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-            for (int s = 0; s < LLG_ATTN_SPLIT_MAX; s++)
-                if (s < ap.n_split) {
-                    const float e = ml[k][s].x == -INFINITY ? 0.0f : expf(ml[k][s].x - M);
-                    L += ml[k][s].y * e;
-                    v.x += a[k][s].x * e;
-                    v.y += a[k][s].y * e;
-                    v.z += a[k][s].z * e;
-                    v.w += a[k][s].w * e;
-                }
-            const float rl = 1.0f / L;
-            v.x *= rl;
-            v.y *= rl;
-            v.z *= rl;
-            v.w *= rl;
-            llg_x_sum_store<XS>(xs, v, base0 + (k0 + k) * bd + lane, n4);
-        }
+        for (int k = 0; k < KB; k++)
+            llg_x_sum_store<XS>(xs, llg_attn_merge4(a[k], ml[k], ap.n_split),
+                                base0 + (k0 + k) * bd + lane, n4);
     };
     load(0);
     __builtin_amdgcn_sched_barrier(0);  // keep the caller's loads behind these

@@ -118,6 +118,20 @@ int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgOb
                            int32_t *d_active, int32_t *d_n_active, uint8_t *ws, bool accumulate,
                            float2 *d_stats = nullptr);
 
+// The sparse step of a Falcon layer with Wo in the tile launch: its first
+// workgroups stage the attention output from its splits (ap), add Wo . attn
+// into d_resid (x += attnOut, ffn_flash.go:161) and compute the predictor's
+// hidden partials P . attn (P = WUp . Wo, rank rows of Wo's width), which
+// they hand to the tile workgroups through the sync area (sync,
+// LLG_SYNC_BYTES); then k_tile_reduce adds the FFN output into d_resid (x +=
+// ffnOut) with its block statistics.  llg_fused_wo_ok: whether Wo's type and
+// sizes allow it.
+bool llg_fused_wo_ok(const LlgObject *wo, int rank, int hidden);
+int llg_fused_wo_enqueue(LlgDevice *d, const LlgObject *wo, const LlgAttnParts &ap,
+                         const float *p, LlgObject *wout, LlgObject *bias, LlgObject *b,
+                         const float *d_x, float thr, int act, float *d_resid,
+                         int32_t *d_n_active, uint8_t *ws, uint8_t *sync, float2 *d_stats);
+
 // MoE prefill as grouped MFMA GEMMs (llg_moe_gemm.hip).
 bool llg_moe_gemm_supported(int type, int hidden, int eff, int n_tok);
 size_t llg_moe_gemm_ws_bytes(int n_tok, int k, int n_exp, int hidden, int eff);

@@ -70,6 +70,9 @@ struct LlgModel {
     float2 *rstats;
     int32_t *token, *n_active, *act_scratch;
     uint8_t *ws;
+    // the device's sync area when every layer runs Wo and the predictor fold
+    // inside its tile launch (llg_fused_wo_enqueue), else null
+    uint8_t *sync;
 };
 
 // The objects a model reads, each once per use (llg_ref / llg_unref pairs).
@@ -643,6 +646,17 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
         else
             launch_attn<128>(st, m, pos, kvl);
         LLG_LAUNCH_CHECK(d, "model attention");
+        if (L.pfold && m.sync && !pred_logits) {
+            // one tile launch: r += Wo . attn and the hidden partials P . attn
+            // in its first workgroups, then the tiles; the reduce adds the FFN
+            // output into r
+            if ((rc = llg_fused_wo_enqueue(d, L.wo, attn_parts(m, pos), L.pfold, L.pwout, nullptr,
+                                           L.bundle, m.normed, L.thr, m.act, r,
+                                           n_active_out ? n_active_out + l : nullptr, m.ws,
+                                           m.sync, m.rstats)))
+                return rc;
+            continue;
+        }
         if (L.pfold) {  // Wo with the predictor fold: r += attn_out, hidden partials in ws
             LlgPredFold pf;
             unsigned long long *mask;
@@ -843,6 +857,18 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
         p += fold ? v_pf1 : 0;
     }
     m->ws = p;
+    bool in_tile = fold && use_stats;
+    for (const LlgModelLayer &L : m->layers)
+        in_tile = in_tile && llg_fused_wo_ok(L.wo, m->rank, m->hidden);
+    if (in_tile) {  // the sync area is taken (and cleared) here, outside any capture
+        int rc = 0;
+        m->sync = llg_dev_sync(d, &rc);
+        if (rc) {
+            (void)hipFree(buf);
+            delete m;
+            return rc;
+        }
+    }
     hipStream_t st = llg_dev_stream(d);
     hipError_t e = hipMemsetAsync(buf, 0, total, st);
     const int n_rope = m->max_seq * (m->head_dim / 2);

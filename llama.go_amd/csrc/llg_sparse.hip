@@ -532,6 +532,31 @@ struct HidArgs {
     int acc_n;
 };
 
+// Wo . attn and the predictor fold in the first workgroups of the tile
+// launch (a Falcon layer, llg_model.hip).  The predictor's input is attn_out =
+// Wo . attn (ffnFlash path 2 after attention, ffn_flash.go:157-161), and its
+// first product WUp . attn_out (predictor.go:57) is linear in attn, so it
+// equals P . attn with P = WUp . Wo formed once at load.  Workgroup b stages
+// the merged attention output (llg_stage_attn), adds its rows of Wo . attn
+// into resid (x += attnOut, ffn_flash.go:161) and computes fold tasks t (of
+// rank x LLG_PRED_SPLIT): the dot of P row t / LLG_PRED_SPLIT with chunk
+// t % LLG_PRED_SPLIT (split_blocks 32-float blocks) of the staged output,
+// written to sync slot (t % LLG_PRED_SPLIT) * rank + t / LLG_PRED_SPLIT of
+// every copy.  The tile workgroups add a unit's partials in chunk order.
+struct WoArgs {
+    const uint8_t *w;  // Wo rows (Q4_0 or Q8_0), f.cols = the attention width
+    long long stride;
+    RowFmt f;
+    int rows;          // Wo's rows: the residual's length
+    float *resid;
+    LlgAttnParts ap;
+    const float *p;    // P: rank rows of f.cols floats
+    int split_blocks;
+    int n_wo;          // workgroups at the head of the grid (0: none)
+};
+#define WO_NB 3   // Wo blocks per lane per row (rows of at most 192 blocks)
+#define WO_PFL 3  // float4 loads per lane of a fold task (split_blocks <= 24)
+
 // Spin bound of a tile workgroup's wait for its hidden units (about 30 ms);
 // past it the workgroup computes the missing units itself.
 #define HID_POLLS (1 << 16)
@@ -570,6 +595,116 @@ __device__ __forceinline__ void tile_hid_role(const HidArgs &ha, int rank, float
     if (ha.acc_out)
         for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < ha.acc_n; i += ha.n_hid * blockDim.x)
             ha.acc_out[i] += ha.acc_add[i];
+}
+
+// Fold task t's dot over the staged chunk (xs) or, with xs null, over the
+// merged attention output read from the splits (the same values and sums):
+// lane l takes float4 groups l, l + 64, l + 128 of the chunk.
+__device__ __forceinline__ float wo_fold_dot(const WoArgs &wa, int rank, int t, const float *xs,
+                                             const float4 (&pr)[WO_PFL]) {
+    const int lane = threadIdx.x & 63;
+    const int sp = t % LLG_PRED_SPLIT;
+    const int nq = max(0, min(wa.split_blocks, wa.f.nb - sp * wa.split_blocks)) * 8;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < WO_PFL; k++) {
+        const int q = lane + 64 * k;
+        if (q < nq) {
+            const float4 xv =
+                xs ? *reinterpret_cast<const float4 *>(xs + (size_t)(sp * wa.split_blocks + (q >> 3)) * XS_STRIDE + (q & 7) * 4)
+                   : llg_attn_merged4(wa.ap, sp * wa.split_blocks * 8 + q);
+            acc += pr[k].x * xv.x;
+            acc += pr[k].y * xv.y;
+            acc += pr[k].z * xv.z;
+            acc += pr[k].w * xv.w;
+        }
+    }
+    return llg_wave_sum(acc);
+}
+
+// P's float4 groups of fold task t for this lane (a lane past the chunk
+// rereads its last group).
+__device__ __forceinline__ void wo_fold_load(const WoArgs &wa, int t, float4 (&pr)[WO_PFL]) {
+    const int lane = threadIdx.x & 63;
+    const int j = t / LLG_PRED_SPLIT, sp = t % LLG_PRED_SPLIT;
+    const int nq = max(0, min(wa.split_blocks, wa.f.nb - sp * wa.split_blocks)) * 8;
+    const float4 *row = reinterpret_cast<const float4 *>(wa.p + (size_t)j * wa.f.cols) +
+                        (nq > 0 ? (size_t)sp * wa.split_blocks * 8 : 0);
+#pragma unroll
+    for (int k = 0; k < WO_PFL; k++) pr[k] = row[min(lane + 64 * k, max(nq, 1) - 1)];
+}
+
+// A Wo workgroup: in pass p < WO_PASSES, wavefront w takes row (WO_PASSES b
+// + p) NW + w (lane l: blocks l, l + 64, l + 128), and fold task w * n_wo + b
+// (and further ones every n_wo * NW).  The fold's P loads and the first
+// pass's row loads go behind the staging loads; the fold is computed right
+// after the staging barrier, so the tiles' hidden units do not wait for the
+// rows.  Each pass's row loads are requested before the previous pass's dots
+// (two buffers).  The Wo workgroups are few enough that every tile workgroup
+// has a CU from the start, and the rows are not on the tiles' path (only the
+// partial-sum kernel reads resid).
+#define WO_PASSES 4
+template <int WT, int NW>
+__device__ __forceinline__ void tile_wo_role(const WoArgs &wa, const HidArgs &ha, int rank,
+                                             float *xs) {
+    const uint32_t ctr = llg_epoch_get(ha.ctr);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const RowFmt &f = wa.f;
+    const int b = blockIdx.x;
+    const int n_tasks = rank * LLG_PRED_SPLIT;
+    const int t0 = wave * wa.n_wo + b, tstep = wa.n_wo * NW;
+    BlockRaw<WT> q[2][WO_NB];
+    float4 pr[WO_PFL];
+    auto row_of = [&](int p) { return (WO_PASSES * b + p) * NW + wave; };
+    auto issue = [&](int p, int buf) {
+#pragma unroll
+        for (int i = 0; i < WO_NB; i++)
+            llg_block_load<WT>(q[buf][i], wa.w + (long long)min(row_of(p), wa.rows - 1) * wa.stride,
+                               f, min(lane + 64 * i, f.nb - 1));
+    };
+    llg_stage_attn<XS_STRIDE, WT == LLG_TYPE_Q8_0 ? 1 : 2>(xs, wa.ap, 0, f.nb, [&]() {
+        // every wavefront's staging loads ahead of any other load (a CU
+        // returns vector loads in request order)
+        __builtin_amdgcn_s_barrier();
+        if (t0 < n_tasks) wo_fold_load(wa, t0, pr);
+        issue(0, 0);
+    });
+    __syncthreads();
+    if (WO_PASSES > 1) issue(1, 1);
+    auto put = [&](int t, float v) {  // lanes 0..7 write one copy each
+        if (lane < LLG_SYNC_COPIES)
+            llg_slot_put(ha.slots + lane * LLG_SYNC_SLOTS + (t % LLG_PRED_SPLIT) * rank +
+                             t / LLG_PRED_SPLIT,
+                         ctr + 1u, v);
+    };
+    if (t0 < n_tasks) put(t0, wo_fold_dot(wa, rank, t0, xs, pr));
+#pragma unroll
+    for (int p = 0; p < WO_PASSES; p++) {
+        float sv = 0.0f;
+#pragma unroll
+        for (int i = 0; i < WO_NB; i++) {
+            const int bl = lane + 64 * i;
+            if (bl < f.nb) {
+                const float *xb = xs + bl * XS_STRIDE;
+                sv += llg_raw_dot<WT>(q[p & 1][i], reinterpret_cast<const float4 *>(xb), xb[32]);
+            }
+        }
+        if (p + 2 < WO_PASSES) issue(p + 2, p & 1);
+        const float v = llg_wave_sum(sv);
+        const int r = row_of(p);
+        if (lane == 0 && r < wa.rows) wa.resid[r] = wa.resid[r] + v;
+    }
+    for (int t = t0 + tstep; t < n_tasks; t += tstep) {  // more tasks than wavefronts
+        wo_fold_load(wa, t, pr);
+        put(t, wo_fold_dot(wa, rank, t, xs, pr));
+    }
+}
+
+// Rows of Wo per workgroup of the tile launch.
+template <int NW>
+constexpr int wo_rows_per_wg() {
+    return WO_PASSES * NW;
 }
 
 // The copy of the slots a tile workgroup reads: one per group of workgroups
@@ -612,6 +747,54 @@ __device__ __forceinline__ void tile_take_hidden(float *hid, const HidArgs &ha, 
     }
 }
 
+// A tile workgroup's hidden units from the Wo workgroups' fold partials:
+// thread r < rank polls the LLG_PRED_SPLIT slots of unit r, all of them in
+// each poll (one memory round), and adds them in chunk order (load_hidden's
+// sums).  A partial whose slot does not show the epoch within HID_POLLS polls
+// is computed by the wavefront (the same sums, from the attention splits), so
+// the wait always ends.
+__device__ __forceinline__ void tile_take_fold(float *hid, const WoArgs &wa, const HidArgs &ha,
+                                               int rank, uint32_t epoch) {
+    const int lane = threadIdx.x & 63;
+    const uint64_t *slots = tile_slot_copy(ha);
+    for (int r0 = threadIdx.x - lane; r0 < rank; r0 += blockDim.x) {  // uniform per wavefront
+        const int r = min(r0 + lane, rank - 1);
+        uint64_t v[LLG_PRED_SPLIT];
+#pragma unroll
+        for (int sp = 0; sp < LLG_PRED_SPLIT; sp++) v[sp] = llg_slot_get(slots + sp * rank + r);
+        auto ready = [&]() {
+            bool ok = true;
+#pragma unroll
+            for (int sp = 0; sp < LLG_PRED_SPLIT; sp++) ok = ok && (uint32_t)(v[sp] >> 32) == epoch;
+            return ok;
+        };
+        for (int polls = 0; !__all(ready()) && polls < HID_POLLS; polls++) {
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int sp = 0; sp < LLG_PRED_SPLIT; sp++) v[sp] = llg_slot_get(slots + sp * rank + r);
+        }
+        float sum = 0.0f;  // the partials in chunk order, as llg_hidden_from_parts
+#pragma unroll
+        for (int sp = 0; sp < LLG_PRED_SPLIT; sp++) {
+            float pv = __uint_as_float((uint32_t)v[sp]);
+            unsigned long long miss = __ballot((uint32_t)(v[sp] >> 32) != epoch);
+            while (miss) {  // wavefront-uniform
+                const int l = __ffsll((long long)miss) - 1;
+                miss &= miss - 1;
+                const int u = r0 + l;
+                if (u >= rank) continue;
+                const int t = u * LLG_PRED_SPLIT + sp;
+                float4 pr[WO_PFL];
+                wo_fold_load(wa, t, pr);
+                const float val = wo_fold_dot(wa, rank, t, nullptr, pr);
+                if (lane == l) pv = val;
+            }
+            sum += pv;
+        }
+        if (r0 + lane < rank) hid[r0 + lane] = sum < 0.0f ? 0.0f : sum;
+    }
+}
+
 // A'. The predictor-fused tiles with their down products (the form the step
 // uses): a workgroup owns tf_tiles 64-neuron tiles (WOut rows: 16 per
 // wavefront; the ballot writes one mask word per tile and the workgroup's
@@ -629,20 +812,30 @@ __device__ __forceinline__ void tile_take_hidden(float *hid, const HidArgs &ha, 
 // Every workgroup writes its partial (zeros when nothing is active), and
 // k_tile_reduce adds the partials in a fixed order, so the result is the
 // same on every run.
-template <int T>
-__global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile_ffn(
+// WO: the instance with Wo's workgroups at the head of the grid (k_tile_wo_ffn).
+template <int T, bool WO>
+__device__ __forceinline__ void tile_ffn_body(
     const uint8_t *__restrict__ wout, long long wstride, int ff, int rank,
     const float *__restrict__ partial, const float *__restrict__ bias, float thr,
     const uint8_t *__restrict__ base, long long bstride, RowFmt f, const float *__restrict__ x,
     int act, unsigned long long *__restrict__ mask, float *__restrict__ part, int pstride,
-    HidArgs ha) {
+    const HidArgs &ha, const WoArgs &wa) {
     extern __shared__ float sh[];
     constexpr int TW = tf_tiles<T>(), NT = TW * TU, NTH = tf_threads<T>(), NW = NTH / 64;
     if ((int)blockIdx.x < ha.n_hid) {
         tile_hid_role<NW>(ha, rank, sh);
         return;
     }
-    const int ti = blockIdx.x - ha.n_hid;  // this workgroup's tiles
+    if constexpr (WO) {
+        if ((int)blockIdx.x < wa.n_wo) {
+            if (wa.f.type == LLG_TYPE_Q4_0)
+                tile_wo_role<LLG_TYPE_Q4_0, NW>(wa, ha, rank, sh);
+            else
+                tile_wo_role<LLG_TYPE_Q8_0, NW>(wa, ha, rank, sh);
+            return;
+        }
+    }
+    const int ti = blockIdx.x - ha.n_hid - (WO ? wa.n_wo : 0);  // this workgroup's tiles
     float *xs = sh;                                     // nb * XS_STRIDE
     float *hid = xs + f.nb * XS_STRIDE;                 // rank (16-byte aligned)
     float *ul = hid + ((rank + 3) & ~3);                // NT activations
@@ -662,12 +855,17 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
             ctr = llg_epoch_get(ha.ctr);
             if (wave * 64 < rank) hv0 = llg_slot_get(tile_slot_copy(ha) + min(wave * 64 + lane, rank - 1));
         });
+    } else if (WO) {
+        if (lw) load_wout_tile(t, wout, wstride, n1, rank, n0);  // used after the barrier
+        stage_x<stage_rounds(NTH)>(xs, x, f.nb, [&]() { ctr = llg_epoch_get(ha.ctr); });
     } else {
         if (lw) load_wout_tile(t, wout, wstride, n1, rank, n0);  // used after the barrier
         stage_x<stage_rounds(NTH)>(xs, x, f.nb);
     }
     if (ha.n_hid)
         tile_take_hidden(hid, ha, rank, ctr + 1u, hv0);
+    else if constexpr (WO)
+        tile_take_fold(hid, wa, ha, rank, ctr + 1u);
     else
         load_hidden<PRED_SPLIT_N>(hid, partial, rank);
     __syncthreads();
@@ -787,6 +985,29 @@ __global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile
                                     acc[4 * e + 2] - corr, acc[4 * e + 3] - corr);
         }
     }
+}
+
+template <int T>
+__global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile_ffn(
+    const uint8_t *__restrict__ wout, long long wstride, int ff, int rank,
+    const float *__restrict__ partial, const float *__restrict__ bias, float thr,
+    const uint8_t *__restrict__ base, long long bstride, RowFmt f, const float *__restrict__ x,
+    int act, unsigned long long *__restrict__ mask, float *__restrict__ part, int pstride,
+    HidArgs ha) {
+    tile_ffn_body<T, false>(wout, wstride, ff, rank, partial, bias, thr, base, bstride, f, x, act,
+                            mask, part, pstride, ha, WoArgs{});
+}
+
+// The same with Wo's workgroups (WoArgs) at the head of the grid.
+template <int T>
+__global__ __launch_bounds__(tf_threads<T>(), tf_threads<T>() / 256) void k_tile_wo_ffn(
+    const uint8_t *__restrict__ wout, long long wstride, int ff, int rank,
+    const float *__restrict__ bias, float thr, const uint8_t *__restrict__ base,
+    long long bstride, RowFmt f, const float *__restrict__ x, int act,
+    unsigned long long *__restrict__ mask, float *__restrict__ part, int pstride, HidArgs ha,
+    WoArgs wa) {
+    tile_ffn_body<T, true>(wout, wstride, ff, rank, nullptr, bias, thr, base, bstride, f, x, act,
+                           mask, part, pstride, ha, wa);
 }
 
 // out[32 b + e] (+)= sum over the partial rows t < n_parts of part[t][32 b +
@@ -1383,18 +1604,27 @@ template <int T>
 static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial,
                          const float *bias, float thr, LlgObject *b, const float *x, int act,
                          unsigned long long *mask, float *part, int32_t *n_active, float *out,
-                         bool accumulate, float2 *stats, HidArgs ha) {
+                         bool accumulate, float2 *stats, HidArgs ha, WoArgs wa) {
     const int ff = wout->rows, rank = wout->fmt.cols;
     const int n_tiles = (ff + 63) / 64;
     const RowFmt &f = b->fmt;
     const int pstride = f.nb * 32;
     constexpr int NT = tf_tiles<T>() * TU, NW = tf_threads<T>() / 64;
     const int n_parts = (ff + NT - 1) / NT;  // tile workgroups, one partial row each
-    if (ha.slots) ha.n_hid = (rank + NW / LLG_PRED_SPLIT - 1) / (NW / LLG_PRED_SPLIT);
-    const size_t lds = tile_lds_bytes<T>(f, rank);
-    hipLaunchKernelGGL((k_tile_ffn<T>), dim3(ha.n_hid + n_parts), dim3(tf_threads<T>()), lds, st,
-                       wout->d, wout->stride, ff, rank, partial, bias, thr, b->d, b->stride, f, x,
-                       act, mask, part, pstride, ha);
+    if (ha.slots && ha.wup) ha.n_hid = (rank + NW / LLG_PRED_SPLIT - 1) / (NW / LLG_PRED_SPLIT);
+    size_t lds = tile_lds_bytes<T>(f, rank);
+    if (wa.w) {
+        wa.n_wo = (wa.rows + wo_rows_per_wg<NW>() - 1) / wo_rows_per_wg<NW>();
+        lds = std::max(lds, (size_t)wa.f.nb * XS_STRIDE * 4);
+    }
+    if (wa.w)
+        hipLaunchKernelGGL((k_tile_wo_ffn<T>), dim3(wa.n_wo + n_parts), dim3(tf_threads<T>()), lds,
+                           st, wout->d, wout->stride, ff, rank, bias, thr, b->d, b->stride, f, x,
+                           act, mask, part, pstride, ha, wa);
+    else
+        hipLaunchKernelGGL((k_tile_ffn<T>), dim3(ha.n_hid + n_parts), dim3(tf_threads<T>()), lds,
+                           st, wout->d, wout->stride, ff, rank, partial, bias, thr, b->d,
+                           b->stride, f, x, act, mask, part, pstride, ha);
     uint32_t *ctr = ha.slots ? const_cast<uint32_t *>(ha.ctr) : nullptr;
     if (accumulate)
         hipLaunchKernelGGL((k_tile_reduce<true>), dim3(f.nb), dim3(256), 0, st,
@@ -1409,7 +1639,7 @@ static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial,
 static int fused_tail(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgObject *b,
                       const float *d_x, float thr, int act, float *d_out, int32_t *d_active,
                       int32_t *d_n_active, uint8_t *ws, bool accum, float2 *d_stats,
-                      const HidArgs &ha) {
+                      const HidArgs &ha, const WoArgs &wa = WoArgs{}) {
     if (int rc = llg_check_act(d, act)) return rc;
     const RowFmt &f = b->fmt;
     if (d_stats && f.cols % 32)
@@ -1432,19 +1662,19 @@ static int fused_tail(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgObject 
     switch (f.type) {
     case LLG_TYPE_Q4_0:
         launch_fused<LLG_TYPE_Q4_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
-                                    d_n_active, d_out, accum, d_stats, ha);
+                                    d_n_active, d_out, accum, d_stats, ha, wa);
         break;
     case LLG_TYPE_Q8_0:
         launch_fused<LLG_TYPE_Q8_0>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
-                                    d_n_active, d_out, accum, d_stats, ha);
+                                    d_n_active, d_out, accum, d_stats, ha, wa);
         break;
     case LLG_TYPE_F16:
         launch_fused<LLG_TYPE_F16>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
-                                   d_n_active, d_out, accum, d_stats, ha);
+                                   d_n_active, d_out, accum, d_stats, ha, wa);
         break;
     case LLG_TYPE_F32:
         launch_fused<LLG_TYPE_F32>(st, wout, partial, d_bias, thr, b, d_x, act, mask, part,
-                                   d_n_active, d_out, accum, d_stats, ha);
+                                   d_n_active, d_out, accum, d_stats, ha, wa);
         break;
     default:
         return llg_set_error(d, LLG_E_TYPE, "predict_sparse: unsupported type %d", f.type);
@@ -1502,4 +1732,37 @@ int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgOb
                            float2 *d_stats) {
     return fused_tail(d, wout, bias, b, d_x, thr, act, d_out, d_active, d_n_active, ws, accum,
                       d_stats, HidArgs{});
+}
+
+bool llg_fused_wo_ok(const LlgObject *wo, int rank, int hidden) {
+    const RowFmt &f = wo->fmt;
+    const int split_blocks = (f.nb + LLG_PRED_SPLIT - 1) / LLG_PRED_SPLIT;
+    return rank * LLG_PRED_SPLIT <= LLG_SYNC_SLOTS && split_blocks * 8 <= 64 * WO_PFL &&
+           (f.type == LLG_TYPE_Q4_0 || f.type == LLG_TYPE_Q8_0) && f.nb <= WO_NB * 64 &&
+           (size_t)f.nb * XS_STRIDE * 4 <= 64 * 1024 && wo->rows == hidden && f.cols % 32 == 0;
+}
+
+int llg_fused_wo_enqueue(LlgDevice *d, const LlgObject *wo, const LlgAttnParts &ap,
+                         const float *p, LlgObject *wout, LlgObject *bias, LlgObject *b,
+                         const float *d_x, float thr, int act, float *d_resid,
+                         int32_t *d_n_active, uint8_t *ws, uint8_t *sync, float2 *d_stats) {
+    const int rank = wout->fmt.cols;
+    if (!sync || !llg_fused_wo_ok(wo, rank, b->fmt.cols) || ap.n_split < 1 ||
+        ap.n_split > LLG_ATTN_SPLIT_MAX || ap.n_heads * ap.head_dim != wo->fmt.cols)
+        return llg_set_error(d, LLG_E_ARG, "Wo in the tile launch: rank %d, width %d", rank,
+                             wo->fmt.cols);
+    HidArgs ha{};
+    ha.ctr = reinterpret_cast<const uint32_t *>(sync);
+    ha.slots = reinterpret_cast<uint64_t *>(sync + LLG_SYNC_HEAD);
+    WoArgs wa{};
+    wa.w = wo->d;
+    wa.stride = wo->stride;
+    wa.f = wo->fmt;
+    wa.rows = wo->rows;
+    wa.resid = d_resid;
+    wa.ap = ap;
+    wa.p = p;
+    wa.split_blocks = (wo->fmt.nb + LLG_PRED_SPLIT - 1) / LLG_PRED_SPLIT;
+    return fused_tail(d, wout, bias, b, d_x, thr, act, d_resid, nullptr, d_n_active, ws, true,
+                      d_stats, ha, wa);
 }
