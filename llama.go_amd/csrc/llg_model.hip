@@ -13,24 +13,26 @@
 //                     row pos of the layer's cache (kvcache.go:42-52), softmax
 //                     attention of every query head over rows 0..pos of its KV
 //                     head (forward.go:258-301)
-//     k_matvec_q      attn_out = Wo . attn (forward.go:305), added into r
-//                     (x += attnOut, ffn_flash.go:161); the same launch
-//                     computes the predictor's hidden partials P . attn, where
-//                     P = WUp . Wo was formed once at load (below)
-//     sparse step     ffnFlash path 2 (ffn_flash.go:157-163, 225-231): logits
-//                     from the hidden partials, the active up rows on normed,
-//                     and the down sums added into r (x += ffnOut, :164-166),
-//                     so r ends as the next layer's residual
+//     k_tile_wo_ffn   its first workgroups: attn_out = Wo . attn (forward.go:
+//                     305), added into r (x += attnOut, ffn_flash.go:161), and
+//                     the predictor's hidden partials P . attn, where P = WUp .
+//                     Wo was formed once at load (below), handed to the tile
+//                     workgroups inside the launch; the tiles: ffnFlash path 2
+//                     (ffn_flash.go:157-163, 225-231), logits from the hidden
+//                     units, the active up rows on normed, partial down sums
+//     k_tile_reduce   the down sums added into r (x += ffnOut, :164-166), so r
+//                     ends as the next layer's residual
 //
 // The predictor fold.  The reference's predictor input is attn_out = Wo .
 // attn, and its first product WUp . attn_out (predictor.go:57) is linear in
 // attn, so it equals P . attn with P = WUp . Wo ([rank x n_heads head_dim]).
 // k_fold_pred forms P once per layer at load, in fp64 sums rounded once to
-// f32, and the Wo launch computes P . attn beside Wo . attn, which removes
+// f32, and the Wo workgroups compute P . attn beside Wo . attn, which removes
 // a launch and a dependent read of attn_out per layer.  The hidden values
-// differ from WUp . attn_out by fp32 rounding only (a few ulps).  Models
-// whose Wo rows are too long for one workgroup's staged x keep the separate
-// hidden kernel on attn_out.
+// differ from WUp . attn_out by fp32 rounding only (a few ulps).  A model
+// whose Wo is not Q4_0/Q8_0 keeps Wo (with the fold) as its own launch before
+// the tile launch, and one whose Wo rows are too long for one workgroup's
+// staged x also keeps the separate hidden kernel on attn_out.
 //   k_out_norm        output LayerNorm of r from its block     (ffn_flash.go:126-129)
 //                     statistics (k_resid_norm without them)
 //   k_matvec_q        logits = LMHead . normed                 (ffn_flash.go:130)
