@@ -644,8 +644,9 @@ def bench_falcon(args, torch, llg, dev):
                       "prefill_ms": prefill_ms, "prefill_tokens_per_s": F4_PROMPT / prefill_ms * 1e3,
                       "mean_active_per_layer": mean_act},
            "roofline": {"bound": "hbm", "kernel": "one decode token: k_embed, 32 x (k_matvec_q "
-                        "qkv with the LayerNorm prologue, k_attn, k_tile_wo_ffn (wo with the "
-                        "attention merge and the predictor fold, then the tiles), k_tile_reduce) + "
+                        "qkv with the LayerNorm prologue, k_attn with the predictor products, "
+                        "k_tile_wo_ffn (the predictor's hidden units, the tiles, then wo with the "
+                        "attention merge), k_tile_reduce) + "
                         "k_out_norm, k_matvec_q lm head, k_argmax",
                         "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": gbs / HBM_PEAK_GBS, "traffic": None, "alg_bytes_per_step": alg,

@@ -118,17 +118,19 @@ int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgOb
                            int32_t *d_active, int32_t *d_n_active, uint8_t *ws, bool accumulate,
                            float2 *d_stats = nullptr);
 
-// The sparse step of a Falcon layer with Wo in the tile launch: its first
-// workgroups stage the attention output from its splits (ap), add Wo . attn
-// into d_resid (x += attnOut, ffn_flash.go:161) and compute the predictor's
-// hidden partials P . attn (P = WUp . Wo, rank rows of Wo's width), which
-// they hand to the tile workgroups through the sync area (sync,
-// LLG_SYNC_BYTES); then k_tile_reduce adds the FFN output into d_resid (x +=
-// ffnOut) with its block statistics.  llg_fused_wo_ok: whether Wo's type and
-// sizes allow it.
+// The sparse step of a Falcon layer with Wo and the predictor in the tile
+// launch.  The attention kernel left pd[s][h][j] = P[j][head h] . acc_s per
+// split s and head h (P = WUp . Wo, rank rows of Wo's width) beside the
+// splits' (m, l) in ap.  The launch's first workgroups merge them into the
+// predictor's hidden units (as the attention splits merge) and hand them to
+// the tile workgroups through the sync area (sync, LLG_SYNC_BYTES); its last
+// workgroups stage the attention output and add Wo . attn into d_resid (x +=
+// attnOut, ffn_flash.go:161); then k_tile_reduce adds the FFN output into
+// d_resid (x += ffnOut) with its block statistics.  llg_fused_wo_ok: whether
+// Wo's type and sizes allow it.
 bool llg_fused_wo_ok(const LlgObject *wo, int rank, int hidden);
 int llg_fused_wo_enqueue(LlgDevice *d, const LlgObject *wo, const LlgAttnParts &ap,
-                         const float *p, LlgObject *wout, LlgObject *bias, LlgObject *b,
+                         const float *pd, LlgObject *wout, LlgObject *bias, LlgObject *b,
                          const float *d_x, float thr, int act, float *d_resid,
                          int32_t *d_n_active, uint8_t *ws, uint8_t *sync, float2 *d_stats);
 

@@ -12,14 +12,16 @@
 //     k_attn          NeoX RoPE of q and k (forward.go:483-497), K/V appended at
 //                     row pos of the layer's cache (kvcache.go:42-52), softmax
 //                     attention of every query head over rows 0..pos of its KV
-//                     head (forward.go:258-301)
-//     k_tile_wo_ffn   its first workgroups: attn_out = Wo . attn (forward.go:
-//                     305), added into r (x += attnOut, ffn_flash.go:161), and
-//                     the predictor's hidden partials P . attn, where P = WUp .
-//                     Wo was formed once at load (below), handed to the tile
-//                     workgroups inside the launch; the tiles: ffnFlash path 2
-//                     (ffn_flash.go:157-163, 225-231), logits from the hidden
-//                     units, the active up rows on normed, partial down sums
+//                     head (forward.go:258-301), split over workgroups by rows;
+//                     each split also forms P . acc for its head, P = WUp . Wo
+//                     formed once at load (below)
+//     k_tile_wo_ffn   its first workgroups merge those products over the splits
+//                     and heads into the predictor's hidden units, handed to
+//                     the tile workgroups inside the launch; the tiles: ffnFlash
+//                     path 2 (ffn_flash.go:157-163, 225-231), logits from the
+//                     hidden units, the active up rows on normed, partial down
+//                     sums; its last workgroups: attn_out = Wo . attn (forward.
+//                     go:305), added into r (x += attnOut, ffn_flash.go:161)
 //     k_tile_reduce   the down sums added into r (x += ffnOut, :164-166), so r
 //                     ends as the next layer's residual
 //
@@ -27,12 +29,14 @@
 // attn, and its first product WUp . attn_out (predictor.go:57) is linear in
 // attn, so it equals P . attn with P = WUp . Wo ([rank x n_heads head_dim]).
 // k_fold_pred forms P once per layer at load, in fp64 sums rounded once to
-// f32, and the Wo workgroups compute P . attn beside Wo . attn, which removes
-// a launch and a dependent read of attn_out per layer.  The hidden values
-// differ from WUp . attn_out by fp32 rounding only (a few ulps).  A model
-// whose Wo is not Q4_0/Q8_0 keeps Wo (with the fold) as its own launch before
-// the tile launch, and one whose Wo rows are too long for one workgroup's
-// staged x also keeps the separate hidden kernel on attn_out.
+// f32.  The attention splits apply P to their unnormalised outputs and the
+// tile launch merges the products as the splits merge, so the hidden units
+// need neither attn_out nor the merged attn, which removes a launch and two
+// dependent reads per layer.  The hidden values differ from WUp . attn_out by
+// fp32 rounding only (a few ulps).  A model whose Wo is not Q4_0/Q8_0 or
+// whose head size is not a multiple of 8 keeps Wo (with the fold) as its own
+// launch before the tile launch, and one whose Wo rows are too long for one
+// workgroup's staged x also keeps the separate hidden kernel on attn_out.
 //   k_out_norm        output LayerNorm of r from its block     (ffn_flash.go:126-129)
 //                     statistics (k_resid_norm without them)
 //   k_matvec_q        logits = LMHead . normed                 (ffn_flash.go:130)
@@ -75,6 +79,8 @@ struct LlgModel {
     // the device's sync area when every layer runs Wo and the predictor fold
     // inside its tile launch (llg_fused_wo_enqueue), else null
     uint8_t *sync;
+    // with sync: the attention splits' predictor products [split][head][rank]
+    float *pd;
 };
 
 // The objects a model reads, each once per use (llg_ref / llg_unref pairs).
@@ -353,7 +359,9 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
                                                        const float2 *__restrict__ rope,
                                                        int max_seq, float *__restrict__ kv,
                                                        int n_split, float *__restrict__ acc_out,
-                                                       float *__restrict__ ml_out) {
+                                                       float *__restrict__ ml_out,
+                                                       const float *__restrict__ pfold, int rank,
+                                                       float *__restrict__ pd_out) {
     using S = AttnShape<HD>;
     constexpr int LP = S::LP, PW = S::PW, NW = S::NW, PR = NW * PW * U;
     static_assert(U <= LP, "lane u of a group computes the exponential of load u");
@@ -381,6 +389,17 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
         }
     };
     issue(0);
+    // the predictor fold's columns of this head (P = WUp . Wo): thread (j,
+    // seg) of the first pass takes P[j][h HD + 8 seg .. + 8], requested now
+    constexpr int TPU = HD / 8, UPP = ATTN_THREADS / TPU;  // threads per unit, units per pass
+    const int fj = tid / TPU, fseg = tid % TPU;
+    float4 pf[2];
+    if (pfold) {
+        const float4 *pr4 = reinterpret_cast<const float4 *>(
+            pfold + (size_t)min(fj, rank - 1) * (n_heads * HD) + (size_t)h * HD + 8 * fseg);
+        pf[0] = pr4[0];
+        pf[1] = pr4[1];
+    }
     const float *q = qkv + (size_t)h * HD;
     const float *kcur = qkv + (size_t)n_heads * HD + (size_t)kvh * HD;
     const float *vcur = kcur + kv_dim;
@@ -493,6 +512,36 @@ __global__ __launch_bounds__(ATTN_THREADS) void k_attn(const float *__restrict__
             ml_out[((size_t)sp * n_heads + h) * 2] = M;
             ml_out[((size_t)sp * n_heads + h) * 2 + 1] = L;
         }
+        if (pfold) qh[tid] = R;  // q is no longer read
+    }
+    if (pfold) {
+        // pd[j] = P[j][h HD ..] . R (this split's unnormalised output): 8
+        // products per thread in order, then the TPU threads of a unit by a
+        // butterfly, so every run adds in the same order
+        __syncthreads();
+        float4 w0 = pf[0], w1 = pf[1];
+        for (int j0 = 0; j0 < rank; j0 += UPP) {
+            if (j0 > 0) {
+                const float4 *pr4 = reinterpret_cast<const float4 *>(
+                    pfold + (size_t)min(j0 + fj, rank - 1) * (n_heads * HD) + (size_t)h * HD + 8 * fseg);
+                w0 = pr4[0];
+                w1 = pr4[1];
+            }
+            const float4 r0 = *reinterpret_cast<const float4 *>(&qh[8 * fseg]);
+            const float4 r1 = *reinterpret_cast<const float4 *>(&qh[8 * fseg + 4]);
+            float d = w0.x * r0.x;
+            d += w0.y * r0.y;
+            d += w0.z * r0.z;
+            d += w0.w * r0.w;
+            d += w1.x * r1.x;
+            d += w1.y * r1.y;
+            d += w1.z * r1.z;
+            d += w1.w * r1.w;
+#pragma unroll
+            for (int o = 1; o < TPU; o <<= 1) d += __shfl_xor(d, o, 64);
+            if (fseg == 0 && j0 + fj < rank)
+                pd_out[((size_t)sp * n_heads + h) * rank + j0 + fj] = d;
+        }
     }
 }
 
@@ -586,14 +635,17 @@ static int attn_splits(const LlgModel &m, int pos) {
 // the fewest loads per lane U whose round covers a workgroup's rows, else
 // rounds of the largest.
 template <int HD>
-static void launch_attn(hipStream_t st, const LlgModel &m, int pos, float *kvl) {
+// pfold (optional): the layer's P, whose per-split products go to m.pd.
+static void launch_attn(hipStream_t st, const LlgModel &m, int pos, float *kvl,
+                        const float *pfold) {
     using S = AttnShape<HD>;
     const int ns = attn_splits(m, pos);
     const int n = (pos + ns) / ns;
     const dim3 grid(m.n_heads * ns);
 #define ATT(U)                                                                                     \
     hipLaunchKernelGGL((k_attn<HD, U>), grid, dim3(ATTN_THREADS), 0, st, m.qkv, m.n_heads,        \
-                       m.n_kv, pos, m.rope, m.max_seq, kvl, ns, m.attn, m.attn_ml)
+                       m.n_kv, pos, m.rope, m.max_seq, kvl, ns, m.attn, m.attn_ml, pfold,       \
+                       m.rank, m.pd)
     if (n <= S::per_round(1)) ATT(1);
     else if (n <= S::per_round(2)) ATT(2);
     else if (n <= S::per_round(4)) ATT(4);
@@ -643,16 +695,19 @@ static int model_step(LlgDevice *d, LlgModel &m, const int32_t *token_in, int po
         int rc = llg_matvec_ln_enqueue(d, L.wqkv, ln, m.qkv);
         if (rc) return rc;
         float *kvl = m.kv + (size_t)l * 2 * m.max_seq * m.n_kv * m.head_dim;
+        // with Wo in the tile launch, the attention kernel also forms the
+        // predictor's per-split products P . acc
+        const float *pf = L.pfold && m.sync && !pred_logits ? L.pfold : nullptr;
         if (m.head_dim == 64)
-            launch_attn<64>(st, m, pos, kvl);
+            launch_attn<64>(st, m, pos, kvl, pf);
         else
-            launch_attn<128>(st, m, pos, kvl);
+            launch_attn<128>(st, m, pos, kvl, pf);
         LLG_LAUNCH_CHECK(d, "model attention");
         if (L.pfold && m.sync && !pred_logits) {
             // one tile launch: r += Wo . attn and the hidden partials P . attn
             // in its first workgroups, then the tiles; the reduce adds the FFN
             // output into r
-            if ((rc = llg_fused_wo_enqueue(d, L.wo, attn_parts(m, pos), L.pfold, L.pwout, nullptr,
+            if ((rc = llg_fused_wo_enqueue(d, L.wo, attn_parts(m, pos), m.pd, L.pwout, nullptr,
                                            L.bundle, m.normed, L.thr, m.act, r,
                                            n_active_out ? n_active_out + l : nullptr, m.ws,
                                            m.sync, m.rstats)))
@@ -827,9 +882,14 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
     size_t v_mp = llg_matvec_part_bytes(m->lm_head, -1);
     for (const LlgModelLayer &L : m->layers) v_mp = std::max(v_mp, llg_matvec_part_bytes(L.wo, -1));
     v_mp = llg_align((long long)v_mp, 256);
+    bool in_tile = fold && use_stats && m->head_dim % 8 == 0;
+    for (const LlgModelLayer &L : m->layers)
+        in_tile = in_tile && llg_fused_wo_ok(L.wo, m->rank, m->hidden);
+    const size_t v_pd =
+        in_tile ? llg_align((long long)LLG_ATTN_SPLIT_MAX * m->n_heads * m->rank * 4, 256) : 0;
     const size_t total =
         3 * v_h + v_qkv + v_att + v_aml + v_log + v_kv + v_i + v_ff + v_pl + v_rope + v_st + v_mp +
-        v_pf + wsb;
+        v_pf + v_pd + wsb;
     uint8_t *buf = nullptr;
     if (hipMalloc(&buf, total) != hipSuccess) return fail(LLG_E_NOMEM, "buffer allocation failed");
     uint8_t *p = buf;
@@ -858,10 +918,9 @@ int llg_hip_falcon_create(LlgHipDevice h, const int32_t *dims, float rope_base, 
         L.pfold = fold ? reinterpret_cast<float *>(p) : nullptr;
         p += fold ? v_pf1 : 0;
     }
+    m->pd = in_tile ? reinterpret_cast<float *>(p) : nullptr;
+    p += v_pd;
     m->ws = p;
-    bool in_tile = fold && use_stats;
-    for (const LlgModelLayer &L : m->layers)
-        in_tile = in_tile && llg_fused_wo_ok(L.wo, m->rank, m->hidden);
     if (in_tile) {  // the sync area is taken (and cleared) here, outside any capture
         int rc = 0;
         m->sync = llg_dev_sync(d, &rc);

@@ -532,17 +532,18 @@ struct HidArgs {
     int acc_n;
 };
 
-// Wo . attn and the predictor fold in the first workgroups of the tile
-// launch (a Falcon layer, llg_model.hip).  The predictor's input is attn_out =
-// Wo . attn (ffnFlash path 2 after attention, ffn_flash.go:157-161), and its
-// first product WUp . attn_out (predictor.go:57) is linear in attn, so it
-// equals P . attn with P = WUp . Wo formed once at load.  Workgroup b stages
-// the merged attention output (llg_stage_attn), adds its rows of Wo . attn
-// into resid (x += attnOut, ffn_flash.go:161) and computes fold tasks t (of
-// rank x LLG_PRED_SPLIT): the dot of P row t / LLG_PRED_SPLIT with chunk
-// t % LLG_PRED_SPLIT (split_blocks 32-float blocks) of the staged output,
-// written to sync slot (t % LLG_PRED_SPLIT) * rank + t / LLG_PRED_SPLIT of
-// every copy.  The tile workgroups add a unit's partials in chunk order.
+// Wo . attn and the predictor in the tile launch (a Falcon layer,
+// llg_model.hip).  The predictor's input is attn_out = Wo . attn (ffnFlash
+// path 2 after attention, ffn_flash.go:157-161), and its first product WUp .
+// attn_out (predictor.go:57) is linear in attn, so it equals P . attn with P
+// = WUp . Wo formed once at load.  The attention kernel leaves, per (split s,
+// head h), pd[s][h][j] = P[j][head h's columns] . acc_s (the split's
+// unnormalised output) beside its (m, l).  The first n_comb workgroups merge
+// them per unit as the attention splits merge (e = exp(m - max m), the sum
+// of pd e times 1 / sum of l e, llg_attn_merge4's steps), add the heads and
+// hand ReLU of the sum to the tile workgroups through the sync slots.  The
+// last n_wo workgroups stage the merged attention output (llg_stage_attn) and
+// add their rows of Wo . attn into resid (x += attnOut, ffn_flash.go:161).
 struct WoArgs {
     const uint8_t *w;  // Wo rows (Q4_0 or Q8_0), f.cols = the attention width
     long long stride;
@@ -550,12 +551,10 @@ struct WoArgs {
     int rows;          // Wo's rows: the residual's length
     float *resid;
     LlgAttnParts ap;
-    const float *p;    // P: rank rows of f.cols floats
-    int split_blocks;
-    int n_wo;          // workgroups at the head of the grid (0: none)
+    const float *pd;   // [n_split][n_heads][rank]
+    int n_comb, n_wo;  // workgroups at the head and at the tail of the grid
 };
 #define WO_NB 3   // Wo blocks per lane per row (rows of at most 192 blocks)
-#define WO_PFL 3  // float4 loads per lane of a fold task (split_blocks <= 24)
 
 // Spin bound of a tile workgroup's wait for its hidden units (about 30 ms);
 // past it the workgroup computes the missing units itself.
@@ -597,111 +596,117 @@ __device__ __forceinline__ void tile_hid_role(const HidArgs &ha, int rank, float
             ha.acc_out[i] += ha.acc_add[i];
 }
 
-// Fold task t's dot over the staged chunk (xs) or, with xs null, over the
-// merged attention output read from the splits (the same values and sums):
-// lane l takes float4 groups l, l + 64, l + 128 of the chunk.
-__device__ __forceinline__ float wo_fold_dot(const WoArgs &wa, int rank, int t, const float *xs,
-                                             const float4 (&pr)[WO_PFL]) {
+// Hidden unit j of the predictor (ReLU'd, predictor.go:61) from the attention
+// kernel's per-split fold partials, by the whole wavefront: lane l takes
+// heads l, l + 64, ..., each merged over the splits with llg_attn_merge4's
+// steps, and the lanes' sums are added by llg_wave_sum.  Every lane gets the
+// value.
+__device__ __forceinline__ float comb_unit(const WoArgs &wa, int rank, int j) {
     const int lane = threadIdx.x & 63;
-    const int sp = t % LLG_PRED_SPLIT;
-    const int nq = max(0, min(wa.split_blocks, wa.f.nb - sp * wa.split_blocks)) * 8;
+    const LlgAttnParts &ap = wa.ap;
+    const float2 *ml = reinterpret_cast<const float2 *>(ap.ml);
     float acc = 0.0f;
+    for (int h0 = 0; h0 < ap.n_heads; h0 += 128) {  // two heads per lane per round
+        // every split slot of both heads requested before any is used (a slot
+        // past n_split rereads split 0 and is skipped)
+        float2 m[2][LLG_ATTN_SPLIT_MAX];
+        float a[2][LLG_ATTN_SPLIT_MAX];
 #pragma unroll
-    for (int k = 0; k < WO_PFL; k++) {
-        const int q = lane + 64 * k;
-        if (q < nq) {
-            const float4 xv =
-                xs ? *reinterpret_cast<const float4 *>(xs + (size_t)(sp * wa.split_blocks + (q >> 3)) * XS_STRIDE + (q & 7) * 4)
-                   : llg_attn_merged4(wa.ap, sp * wa.split_blocks * 8 + q);
-            acc += pr[k].x * xv.x;
-            acc += pr[k].y * xv.y;
-            acc += pr[k].z * xv.z;
-            acc += pr[k].w * xv.w;
+        for (int k = 0; k < 2; k++) {
+            const int h = min(h0 + lane + 64 * k, ap.n_heads - 1);
+#pragma unroll
+            for (int s = 0; s < LLG_ATTN_SPLIT_MAX; s++) {
+                const int sc = s < ap.n_split ? s : 0;
+                m[k][s] = ml[sc * ap.n_heads + h];
+                a[k][s] = wa.pd[((size_t)sc * ap.n_heads + h) * rank + j];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            if (h0 + lane + 64 * k >= ap.n_heads) continue;
+            float M = m[k][0].x;
+#pragma unroll
+            for (int s = 1; s < LLG_ATTN_SPLIT_MAX; s++)
+                if (s < ap.n_split) M = fmaxf(M, m[k][s].x);
+            float L = 0.0f, v = 0.0f;
+#pragma unroll
+            for (int s = 0; s < LLG_ATTN_SPLIT_MAX; s++)
+                if (s < ap.n_split) {
+                    const float e = m[k][s].x == -INFINITY ? 0.0f : expf(m[k][s].x - M);
+                    L += m[k][s].y * e;
+                    v += a[k][s] * e;
+                }
+            const float rl = 1.0f / L;
+            acc += v * rl;
         }
     }
-    return llg_wave_sum(acc);
+    const float hv = llg_wave_sum(acc);
+    return hv < 0.0f ? 0.0f : hv;
 }
 
-// P's float4 groups of fold task t for this lane (a lane past the chunk
-// rereads its last group).
-__device__ __forceinline__ void wo_fold_load(const WoArgs &wa, int t, float4 (&pr)[WO_PFL]) {
-    const int lane = threadIdx.x & 63;
-    const int j = t / LLG_PRED_SPLIT, sp = t % LLG_PRED_SPLIT;
-    const int nq = max(0, min(wa.split_blocks, wa.f.nb - sp * wa.split_blocks)) * 8;
-    const float4 *row = reinterpret_cast<const float4 *>(wa.p + (size_t)j * wa.f.cols) +
-                        (nq > 0 ? (size_t)sp * wa.split_blocks * 8 : 0);
-#pragma unroll
-    for (int k = 0; k < WO_PFL; k++) pr[k] = row[min(lane + 64 * k, max(nq, 1) - 1)];
-}
-
-// A Wo workgroup: in pass p < WO_PASSES, wavefront w takes row (WO_PASSES b
-// + p) NW + w (lane l: blocks l, l + 64, l + 128), and fold task w * n_wo + b
-// (and further ones every n_wo * NW).  The fold's P loads and the first
-// pass's row loads go behind the staging loads; the fold is computed right
-// after the staging barrier, so the tiles' hidden units do not wait for the
-// rows.  Each pass's row loads are requested before the previous pass's dots
-// (two buffers).  The Wo workgroups are few enough that every tile workgroup
-// has a CU from the start, and the rows are not on the tiles' path (only the
-// partial-sum kernel reads resid).
-#define WO_PASSES 4
-template <int WT, int NW>
-__device__ __forceinline__ void tile_wo_role(const WoArgs &wa, const HidArgs &ha, int rank,
-                                             float *xs) {
+// A combiner workgroup: wavefront w takes hidden unit NW b + w and writes it
+// to every copy of its slot.
+template <int NW>
+__device__ __forceinline__ void tile_comb_role(const WoArgs &wa, const HidArgs &ha, int rank) {
     const uint32_t ctr = llg_epoch_get(ha.ctr);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j = blockIdx.x * NW + wave;
+    if (j >= rank) return;  // uniform per wavefront
+    const float hv = comb_unit(wa, rank, j);
+    if (lane < LLG_SYNC_COPIES) llg_slot_put(ha.slots + lane * LLG_SYNC_SLOTS + j, ctr + 1u, hv);
+}
+
+// A Wo workgroup b: in pass p, wavefront w takes row (p n_wo + b) NW + w
+// (lane l: blocks l, l + 64, l + 128) of the staged merged attention output;
+// each pass's row loads are requested before the previous pass's dots (two
+// buffers).  The rows are not on the tiles' path (only the partial-sum kernel
+// reads resid).
+template <int WT, int NW>
+__device__ __forceinline__ void tile_wo_role(const WoArgs &wa, int b, float *xs) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const RowFmt &f = wa.f;
-    const int b = blockIdx.x;
-    const int n_tasks = rank * LLG_PRED_SPLIT;
-    const int t0 = wave * wa.n_wo + b, tstep = wa.n_wo * NW;
     BlockRaw<WT> q[2][WO_NB];
-    float4 pr[WO_PFL];
-    auto row_of = [&](int p) { return (WO_PASSES * b + p) * NW + wave; };
+    const int n_pass = (wa.rows + wa.n_wo * NW - 1) / (wa.n_wo * NW);
+    auto row_of = [&](int p) { return (p * wa.n_wo + b) * NW + wave; };
     auto issue = [&](int p, int buf) {
 #pragma unroll
         for (int i = 0; i < WO_NB; i++)
             llg_block_load<WT>(q[buf][i], wa.w + (long long)min(row_of(p), wa.rows - 1) * wa.stride,
                                f, min(lane + 64 * i, f.nb - 1));
     };
-    llg_stage_attn<XS_STRIDE, WT == LLG_TYPE_Q8_0 ? 1 : 2>(xs, wa.ap, 0, f.nb, [&]() {
-        // every wavefront's staging loads ahead of any other load (a CU
-        // returns vector loads in request order)
-        __builtin_amdgcn_s_barrier();
-        if (t0 < n_tasks) wo_fold_load(wa, t0, pr);
-        issue(0, 0);
-    });
-    __syncthreads();
-    if (WO_PASSES > 1) issue(1, 1);
-    auto put = [&](int t, float v) {  // lanes 0..7 write one copy each
-        if (lane < LLG_SYNC_COPIES)
-            llg_slot_put(ha.slots + lane * LLG_SYNC_SLOTS + (t % LLG_PRED_SPLIT) * rank +
-                             t / LLG_PRED_SPLIT,
-                         ctr + 1u, v);
-    };
-    if (t0 < n_tasks) put(t0, wo_fold_dot(wa, rank, t0, xs, pr));
-#pragma unroll
-    for (int p = 0; p < WO_PASSES; p++) {
+    auto pass = [&](int p, int buf) {
         float sv = 0.0f;
 #pragma unroll
         for (int i = 0; i < WO_NB; i++) {
             const int bl = lane + 64 * i;
             if (bl < f.nb) {
                 const float *xb = xs + bl * XS_STRIDE;
-                sv += llg_raw_dot<WT>(q[p & 1][i], reinterpret_cast<const float4 *>(xb), xb[32]);
+                sv += llg_raw_dot<WT>(q[buf][i], reinterpret_cast<const float4 *>(xb), xb[32]);
             }
         }
-        if (p + 2 < WO_PASSES) issue(p + 2, p & 1);
+        if (p + 2 < n_pass) issue(p + 2, buf);
         const float v = llg_wave_sum(sv);
         const int r = row_of(p);
         if (lane == 0 && r < wa.rows) wa.resid[r] = wa.resid[r] + v;
-    }
-    for (int t = t0 + tstep; t < n_tasks; t += tstep) {  // more tasks than wavefronts
-        wo_fold_load(wa, t, pr);
-        put(t, wo_fold_dot(wa, rank, t, xs, pr));
+    };
+    llg_stage_attn<XS_STRIDE, WT == LLG_TYPE_Q8_0 ? 1 : 2>(xs, wa.ap, 0, f.nb, [&]() {
+        // every wavefront's staging loads ahead of any row load (a CU returns
+        // vector loads in request order)
+        __builtin_amdgcn_s_barrier();
+        issue(0, 0);
+    });
+    __syncthreads();
+    if (n_pass > 1) issue(1, 1);
+    for (int p = 0; p < n_pass; p += 2) {  // uniform
+        pass(p, 0);
+        if (p + 1 < n_pass) pass(p + 1, 1);
     }
 }
 
-// Rows of Wo per workgroup of the tile launch.
+// Rows of Wo per workgroup of the tile launch: WO_PASSES passes.
+#define WO_PASSES 4
 template <int NW>
 constexpr int wo_rows_per_wg() {
     return WO_PASSES * NW;
@@ -747,51 +752,33 @@ __device__ __forceinline__ void tile_take_hidden(float *hid, const HidArgs &ha, 
     }
 }
 
-// A tile workgroup's hidden units from the Wo workgroups' fold partials:
-// thread r < rank polls the LLG_PRED_SPLIT slots of unit r, all of them in
-// each poll (one memory round), and adds them in chunk order (load_hidden's
-// sums).  A partial whose slot does not show the epoch within HID_POLLS polls
-// is computed by the wavefront (the same sums, from the attention splits), so
-// the wait always ends.
-__device__ __forceinline__ void tile_take_fold(float *hid, const WoArgs &wa, const HidArgs &ha,
+// A tile workgroup's hidden units from the combiner workgroups' slots, as
+// tile_take_hidden: a unit whose slot does not show the epoch within
+// HID_POLLS polls is combined by the wavefront itself (comb_unit, the same
+// value), so the wait always ends.
+__device__ __forceinline__ void tile_take_comb(float *hid, const WoArgs &wa, const HidArgs &ha,
                                                int rank, uint32_t epoch) {
     const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint64_t *slots = tile_slot_copy(ha);
-    for (int r0 = threadIdx.x - lane; r0 < rank; r0 += blockDim.x) {  // uniform per wavefront
+    for (int r0 = wave * 64; r0 < rank; r0 += blockDim.x) {
         const int r = min(r0 + lane, rank - 1);
-        uint64_t v[LLG_PRED_SPLIT];
-#pragma unroll
-        for (int sp = 0; sp < LLG_PRED_SPLIT; sp++) v[sp] = llg_slot_get(slots + sp * rank + r);
-        auto ready = [&]() {
-            bool ok = true;
-#pragma unroll
-            for (int sp = 0; sp < LLG_PRED_SPLIT; sp++) ok = ok && (uint32_t)(v[sp] >> 32) == epoch;
-            return ok;
-        };
-        for (int polls = 0; !__all(ready()) && polls < HID_POLLS; polls++) {
+        uint64_t v = llg_slot_get(slots + r);
+        for (int polls = 0; !__all((uint32_t)(v >> 32) == epoch) && polls < HID_POLLS; polls++) {
             __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-            for (int sp = 0; sp < LLG_PRED_SPLIT; sp++) v[sp] = llg_slot_get(slots + sp * rank + r);
+            v = llg_slot_get(slots + r);
         }
-        float sum = 0.0f;  // the partials in chunk order, as llg_hidden_from_parts
-#pragma unroll
-        for (int sp = 0; sp < LLG_PRED_SPLIT; sp++) {
-            float pv = __uint_as_float((uint32_t)v[sp]);
-            unsigned long long miss = __ballot((uint32_t)(v[sp] >> 32) != epoch);
-            while (miss) {  // wavefront-uniform
-                const int l = __ffsll((long long)miss) - 1;
-                miss &= miss - 1;
-                const int u = r0 + l;
-                if (u >= rank) continue;
-                const int t = u * LLG_PRED_SPLIT + sp;
-                float4 pr[WO_PFL];
-                wo_fold_load(wa, t, pr);
-                const float val = wo_fold_dot(wa, rank, t, nullptr, pr);
-                if (lane == l) pv = val;
-            }
-            sum += pv;
+        float hv = __uint_as_float((uint32_t)v);
+        unsigned long long miss = __ballot((uint32_t)(v >> 32) != epoch);
+        while (miss) {  // wavefront-uniform
+            const int l = __ffsll((long long)miss) - 1;
+            miss &= miss - 1;
+            const int u = r0 + l;
+            if (u >= rank) continue;
+            const float val = comb_unit(wa, rank, u);
+            if (lane == l) hv = val;
         }
-        if (r0 + lane < rank) hid[r0 + lane] = sum < 0.0f ? 0.0f : sum;
+        if (r0 + lane < rank) hid[r0 + lane] = hv;
     }
 }
 
@@ -827,15 +814,20 @@ __device__ __forceinline__ void tile_ffn_body(
         return;
     }
     if constexpr (WO) {
-        if ((int)blockIdx.x < wa.n_wo) {
+        if ((int)blockIdx.x < wa.n_comb) {
+            tile_comb_role<NW>(wa, ha, rank);
+            return;
+        }
+        const int wb = (int)blockIdx.x - ((int)gridDim.x - wa.n_wo);  // Wo workgroups last
+        if (wb >= 0) {
             if (wa.f.type == LLG_TYPE_Q4_0)
-                tile_wo_role<LLG_TYPE_Q4_0, NW>(wa, ha, rank, sh);
+                tile_wo_role<LLG_TYPE_Q4_0, NW>(wa, wb, sh);
             else
-                tile_wo_role<LLG_TYPE_Q8_0, NW>(wa, ha, rank, sh);
+                tile_wo_role<LLG_TYPE_Q8_0, NW>(wa, wb, sh);
             return;
         }
     }
-    const int ti = blockIdx.x - ha.n_hid - (WO ? wa.n_wo : 0);  // this workgroup's tiles
+    const int ti = blockIdx.x - ha.n_hid - (WO ? wa.n_comb : 0);  // this workgroup's tiles
     float *xs = sh;                                     // nb * XS_STRIDE
     float *hid = xs + f.nb * XS_STRIDE;                 // rank (16-byte aligned)
     float *ul = hid + ((rank + 3) & ~3);                // NT activations
@@ -865,7 +857,7 @@ __device__ __forceinline__ void tile_ffn_body(
     if (ha.n_hid)
         tile_take_hidden(hid, ha, rank, ctr + 1u, hv0);
     else if constexpr (WO)
-        tile_take_fold(hid, wa, ha, rank, ctr + 1u);
+        tile_take_comb(hid, wa, ha, rank, ctr + 1u);
     else
         load_hidden<PRED_SPLIT_N>(hid, partial, rank);
     __syncthreads();
@@ -1614,11 +1606,12 @@ static void launch_fused(hipStream_t st, LlgObject *wout, const float *partial,
     if (ha.slots && ha.wup) ha.n_hid = (rank + NW / LLG_PRED_SPLIT - 1) / (NW / LLG_PRED_SPLIT);
     size_t lds = tile_lds_bytes<T>(f, rank);
     if (wa.w) {
+        wa.n_comb = (rank + NW - 1) / NW;
         wa.n_wo = (wa.rows + wo_rows_per_wg<NW>() - 1) / wo_rows_per_wg<NW>();
         lds = std::max(lds, (size_t)wa.f.nb * XS_STRIDE * 4);
     }
     if (wa.w)
-        hipLaunchKernelGGL((k_tile_wo_ffn<T>), dim3(wa.n_wo + n_parts), dim3(tf_threads<T>()), lds,
+        hipLaunchKernelGGL((k_tile_wo_ffn<T>), dim3(wa.n_comb + n_parts + wa.n_wo), dim3(tf_threads<T>()), lds,
                            st, wout->d, wout->stride, ff, rank, bias, thr, b->d, b->stride, f, x,
                            act, mask, part, pstride, ha, wa);
     else
@@ -1736,14 +1729,13 @@ int llg_fused_tail_enqueue(LlgDevice *d, LlgObject *wout, LlgObject *bias, LlgOb
 
 bool llg_fused_wo_ok(const LlgObject *wo, int rank, int hidden) {
     const RowFmt &f = wo->fmt;
-    const int split_blocks = (f.nb + LLG_PRED_SPLIT - 1) / LLG_PRED_SPLIT;
-    return rank * LLG_PRED_SPLIT <= LLG_SYNC_SLOTS && split_blocks * 8 <= 64 * WO_PFL &&
-           (f.type == LLG_TYPE_Q4_0 || f.type == LLG_TYPE_Q8_0) && f.nb <= WO_NB * 64 &&
-           (size_t)f.nb * XS_STRIDE * 4 <= 64 * 1024 && wo->rows == hidden && f.cols % 32 == 0;
+    return rank <= LLG_SYNC_SLOTS && (f.type == LLG_TYPE_Q4_0 || f.type == LLG_TYPE_Q8_0) &&
+           f.nb <= WO_NB * 64 && (size_t)f.nb * XS_STRIDE * 4 <= 64 * 1024 && wo->rows == hidden &&
+           f.cols % 32 == 0;
 }
 
 int llg_fused_wo_enqueue(LlgDevice *d, const LlgObject *wo, const LlgAttnParts &ap,
-                         const float *p, LlgObject *wout, LlgObject *bias, LlgObject *b,
+                         const float *pd, LlgObject *wout, LlgObject *bias, LlgObject *b,
                          const float *d_x, float thr, int act, float *d_resid,
                          int32_t *d_n_active, uint8_t *ws, uint8_t *sync, float2 *d_stats) {
     const int rank = wout->fmt.cols;
@@ -1761,8 +1753,7 @@ int llg_fused_wo_enqueue(LlgDevice *d, const LlgObject *wo, const LlgAttnParts &
     wa.rows = wo->rows;
     wa.resid = d_resid;
     wa.ap = ap;
-    wa.p = p;
-    wa.split_blocks = (wo->fmt.nb + LLG_PRED_SPLIT - 1) / LLG_PRED_SPLIT;
+    wa.pd = pd;
     return fused_tail(d, wout, bias, b, d_x, thr, act, d_resid, nullptr, d_n_active, ws, true,
                       d_stats, ha, wa);
 }
