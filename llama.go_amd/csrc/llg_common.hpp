@@ -596,6 +596,19 @@ __device__ __forceinline__ void llg_x_sum_store(float *xs, const float4 &v, int 
     }
 }
 
+// The block sum llg_x_sum_store leaves, formed by one lane from the block's
+// 8 float4 groups (s_k = (x + y) + (z + w) of group k): the quad sums of
+// lanes 0-3 and 4-7 in their DPP order, then the half-row mirror's add.
+__device__ __forceinline__ float llg_block_xsum(const float4 *__restrict__ x4) {
+    float s[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float4 v = x4[k];
+        s[k] = (v.x + v.y) + (v.z + v.w);
+    }
+    return ((s[0] + s[1]) + (s[2] + s[3])) + ((s[6] + s[7]) + (s[4] + s[5]));
+}
+
 // KN: float4 rounds of the one-pass form (the row must fit KN * blockDim.x
 // float4, else the looped form runs).  Callers pass the fewest that cover
 // their rows: a clamped round past the row's end rereads its last float4 and
@@ -985,6 +998,11 @@ uint8_t *llg_dev_scratch(LlgDevice *d, size_t bytes, int *rc);
 // The handle's own sync area (allocated and zeroed on the stream at first
 // use), or null with *rc set.
 uint8_t *llg_dev_sync(LlgDevice *d, int *rc);
+// Hand-off slots of the chunked matvecs (k_matvec_q): at least `bytes`,
+// zeroed at allocation, and every slot is zero again at the end of each
+// launch that uses it.  Growth synchronises the stream first; null with *rc
+// set on failure.
+uint64_t *llg_dev_mvslots(LlgDevice *d, size_t bytes, int *rc);
 // Copy host -> device workspace slot / device -> host, on the stream.
 int llg_h2d(LlgDevice *d, void *dst, const void *src, size_t bytes);
 int llg_d2h(LlgDevice *d, void *dst, const void *src, size_t bytes);

@@ -11,15 +11,24 @@
 // rows (one pass of 4 wavefronts), 16 or 32 for very tall matrices; a matrix
 // of 2048-8191 whole rows instead gets one workgroup per CU (the balanced
 // launch, below).  With one chunk the row sum is final and the activation is
-// applied; with several chunks each workgroup stores its partial sums,
-// part[chunk][row], and k_chunk_sum adds the chunks in order (a fixed order:
-// results are the same on every run).
+// applied.  With several chunks, each workgroup hands its partial sums over
+// as tagged 64-bit slots, (1 << 32) | bits, one per (chunk, row)
+// (llg_dev_mvslots: zero between launches), and the last workgroups of the
+// same grid reduce them (mv_reduce): they come after every chunk workgroup,
+// add the chunks in order, apply the activation, store y and clear the
+// slots.  A slot not filled within MV_POLLS polls is computed by the reducer
+// itself from x in memory (the chunk workgroup's blocks, block sums and
+// order), so the wait always ends.  Without slots (more than MV_HAND_MAX
+// chunks) the partial sums go to part[chunk][row] and k_chunk_sum adds them.
+// Either way the chunks are added in a fixed order, so results are the same
+// on every run.
 //
 // Gated (G): y[r] = silu(gate_r . x) * (up_r . x) (ffnSwiGLU, forward.go:
 // 368-389) with gate = w and up = w2; a wavefront's two row slots hold gate
 // row r and up row r, so it takes one output row per pass.
 #include "llg_common.hpp"
 #include "llg_internal.hpp"
+#include "llg_pred_tile.hpp"
 
 #define MV_ROWS 2
 #define MV_TILE_SMALL 8   // rows per workgroup: one pass of 4 wavefronts x MV_ROWS ...
@@ -30,6 +39,97 @@
 #define MV_XS 36          // staged floats per 32-float block
 #define MV_BATCH 3        // pair layout: blocks per lane per row and step
 #define MV_NI 5           // flat layout: slots per lane per step (MV_ROWS x MV_CHUNK / 64, rounded up)
+#define MV_HAND_MAX 4       // chunks reduced inside the launch (more: k_chunk_sum); 4 keeps
+                            // the Q4_0 instance at 96 registers (5 wavefronts per SIMD)
+#define MV_POLLS (1 << 16)  // a reducer's polls of its slots before it computes a sum itself
+
+// Row rq's partial sum over chunk c from x in memory, by the whole
+// wavefront: the blocks each lane of a chunk workgroup's wavefront takes in
+// that chunk (pair layout, or the flat layout of Q8_0 with q the row's slot
+// in its row pair), in the same order, each with the staged block sum
+// (llg_block_xsum), then llg_wave_sum: the value that workgroup hands over.
+template <int T>
+__device__ __forceinline__ float mv_chunk_direct(const uint8_t *__restrict__ w, long long stride,
+                                                 const RowFmt &f, int chunk_blocks,
+                                                 const float *__restrict__ x, int c, int rq,
+                                                 int q) {
+    const int lane = threadIdx.x & 63;
+    const int c0 = c * chunk_blocks, cn = min(chunk_blocks, f.nb - c0);
+    const uint8_t *row = w + (long long)rq * stride;
+    float s = 0.0f;
+    auto one = [&](int b) {
+        BlockRaw<T> blk;
+        llg_block_load<T>(blk, row, f, c0 + b);
+        const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)(c0 + b) * 32);
+        s += llg_raw_dot<T>(blk, x4, llg_block_xsum(x4));
+    };
+    if constexpr (T == LLG_TYPE_Q8_0) {
+        for (int i = 0; i < MV_NI; i++) {
+            const int k = lane + 64 * i;
+            if (k < MV_ROWS * cn && (k >= cn) == (q == 1)) one(k - (q ? cn : 0));
+        }
+    } else {
+        for (int i = 0; i < MV_BATCH; i++)
+            if (lane + 64 * i < cn) one(lane + 64 * i);
+    }
+    return llg_wave_sum(s);
+}
+
+// A reducer workgroup rb: thread t takes row rb * blockDim.x + t, polls its
+// n_chunks slots (all in each poll), adds chunk 0, 1, ... in order (as
+// k_chunk_sum), applies the activation, stores y and zeroes the slots.
+template <int T>
+__device__ __forceinline__ void mv_reduce(const uint8_t *__restrict__ w, long long stride,
+                                          const RowFmt &f, int rows, int chunk_blocks,
+                                          int n_chunks, const float *__restrict__ x, int act,
+                                          float *__restrict__ y, uint64_t *__restrict__ slots,
+                                          int rb) {
+    const int lane = threadIdx.x & 63;
+    const int r = rb * (int)blockDim.x + (int)threadIdx.x;
+    const int rc = min(r, rows - 1);
+    uint64_t v[MV_HAND_MAX];
+    auto load = [&]() {  // every slot (a chunk past the last rereads it)
+#pragma unroll
+        for (int c = 0; c < MV_HAND_MAX; c++)
+            v[c] = llg_slot_get(slots + (size_t)min(c, n_chunks - 1) * rows + rc);
+    };
+    auto ready = [&]() {
+        bool ok = true;
+#pragma unroll
+        for (int c = 0; c < MV_HAND_MAX; c++) ok = ok && (uint32_t)(v[c] >> 32) == 1u;
+        return ok;
+    };
+    load();
+    for (int polls = 0; !__all(ready()) && polls < MV_POLLS; polls++) {
+        __builtin_amdgcn_s_sleep(1);
+        load();
+    }
+    float p[MV_HAND_MAX];
+#pragma unroll
+    for (int c = 0; c < MV_HAND_MAX; c++) {
+        p[c] = __uint_as_float((uint32_t)v[c]);
+        if (c >= n_chunks) continue;  // uniform
+        unsigned long long miss = __ballot(r < rows && (uint32_t)(v[c] >> 32) != 1u);
+        while (miss) {  // wavefront-uniform
+            const int l = __ffsll((long long)miss) - 1;
+            miss &= miss - 1;
+            const int rr = __builtin_amdgcn_readlane(r, l);
+            // tiles start at even rows, so the row's slot in its pair is its parity
+            const float sv = mv_chunk_direct<T>(w, stride, f, chunk_blocks, x, c, rr, rr & 1);
+            if (lane == l) p[c] = sv;
+        }
+    }
+    float sum = p[0];
+#pragma unroll
+    for (int c = 1; c < MV_HAND_MAX; c++)
+        if (c < n_chunks) sum += p[c];
+    if (r < rows) {
+        y[r] = act >= 0 ? llg_act(act, sum) : sum;
+#pragma unroll
+        for (int c = 0; c < MV_HAND_MAX; c++)
+            if (c < n_chunks) llg_slot_put(slots + (size_t)c * rows + r, 0u, 0.0f);
+    }
+}
 
 // LNP > 0: x is the LayerNorm of a residual sum, staged with LNP float4 groups
 // per thread (llg_stage_ln); LNP = 0: x is read from memory.  NT: the largest
@@ -49,7 +149,8 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
                                                   LlgLnArgs ln,
                                                   const uint8_t *__restrict__ w2 = nullptr,
                                                   LlgPredFold pf = LlgPredFold{},
-                                                  LlgAttnParts ap = LlgAttnParts{}) {
+                                                  LlgAttnParts ap = LlgAttnParts{},
+                                                  uint64_t *__restrict__ slots = nullptr) {
     static_assert(!G || (LNP == 0 && MV_ROWS == 2), "gated rows pair gate and up");
     static_assert(!PF || (LNP == 0 && !G), "the fold rides on a plain matvec");
     static_assert(!AC || (LNP == 0 && !G), "the attention merge replaces the plain x");
@@ -57,6 +158,17 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
     extern __shared__ float xs[];
     __shared__ float red[2 * (NT / 64)];
     const int n_chunks = (f.nb + chunk_blocks - 1) / chunk_blocks;
+    // chunked plain rows with slots: the workgroups past the tiles reduce
+    constexpr bool CAN_HAND = LNP == 0 && !G && !PF && !AC;
+    const bool hand = CAN_HAND && n_chunks > 1 && slots != nullptr;
+    if constexpr (CAN_HAND) {
+        const int n_work = (rows + tile_rows - 1) / tile_rows * n_chunks;
+        if (hand && (int)blockIdx.x >= n_work) {
+            mv_reduce<T>(w, stride, f, rows, chunk_blocks, n_chunks, x, act, y, slots,
+                         (int)blockIdx.x - n_work);
+            return;
+        }
+    }
     const int tile = blockIdx.x / n_chunks;
     const int ch = blockIdx.x % n_chunks;
     const int cb0 = ch * chunk_blocks;
@@ -224,6 +336,8 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
                     const float o = act >= 0 ? llg_act(act, v) : v;
                     if constexpr (PF) pf.resid[r0 + q] = pf.resid[r0 + q] + o;  // x += attnOut
                     if (!PF || y) y[r0 + q] = o;
+                } else if (hand) {
+                    llg_slot_put(slots + (size_t)ch * rows + r0 + q, 1u, v);
                 } else {
                     part[(size_t)ch * rows + r0 + q] = v;
                 }
@@ -300,13 +414,14 @@ struct MvArgs {
     const uint8_t *w2;
     LlgPredFold pf;
     LlgAttnParts ap;
+    uint64_t *slots;  // chunked rows reduced in the launch (llg_dev_mvslots)
 };
 
 template <int T, int LNP, bool G, int NT, bool PF, bool AC>
 static void mv_go(const MvArgs &a) {
     hipLaunchKernelGGL((k_matvec_q<T, LNP, G, NT, PF, AC>), a.grid, dim3(a.threads), a.lds, a.st,
                        a.w->d, a.w->stride, a.w->fmt, a.w->rows, a.tile_rows, a.cb, a.x, a.act,
-                       a.y, a.part, a.ln, a.w2, a.pf, a.ap);
+                       a.y, a.part, a.ln, a.w2, a.pf, a.ap, a.slots);
 }
 
 // Instances with NT = 1024 workgroups (the balanced launch) exist for the
@@ -369,7 +484,11 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
     const size_t lds = (size_t)cb * MV_XS * 4;
     if (lds > 160 * 1024)
         return llg_set_error(d, LLG_E_ARG, "matvec: row of %d elements too long", f.cols);
-    if (n_chunks > 1 && !part)
+    // chunked plain rows (k_matvec_q's CAN_HAND instances): reduced in the
+    // launch through slots; the attention-merge instance, or more than
+    // MV_HAND_MAX chunks: k_chunk_sum from part
+    const bool hand = n_chunks > 1 && n_chunks <= MV_HAND_MAX && !ln && !up && !pf && !ap;
+    if (n_chunks > 1 && !hand && !part)
         return llg_set_error(d, LLG_E_ARG, "matvec: chunked rows need a partial buffer");
     if (pf && (n_chunks > 1 || ln || up || act >= 0 || pf->n_split < 1 ||
                pf->split_blocks * 8 > 64 * MV_PFL ||
@@ -391,6 +510,12 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
     a.w2 = up ? up->d : nullptr;
     a.pf = pf ? *pf : LlgPredFold{};
     a.ap = ap ? *ap : LlgAttnParts{};
+    a.slots = nullptr;
+    if (hand) {
+        int rc = 0;
+        a.slots = llg_dev_mvslots(d, (size_t)n_chunks * w->rows * 8, &rc);
+        if (rc) return rc;
+    }
     // Rows per workgroup: one pass per wavefront (8 rows) gives the most
     // loads in flight; very tall matrices take 16 or 32 rows so that the grid
     // stays within MV_MAX_WG workgroups (an 18176-row Q4_0 matvec: 13.6 us at
@@ -417,7 +542,8 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
             lnp = lnp_b;
         }
     }
-    a.grid = dim3((w->rows + a.tile_rows - 1) / a.tile_rows * n_chunks);
+    a.grid = dim3((w->rows + a.tile_rows - 1) / a.tile_rows * n_chunks +
+                  (hand ? (w->rows + a.threads - 1) / a.threads : 0));
     switch (f.type) {
     case LLG_TYPE_Q4_0:
         mv_dispatch<LLG_TYPE_Q4_0>(a, bal, up != nullptr, pf != nullptr, ap != nullptr, lnp);
@@ -435,7 +561,7 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
         return llg_set_error(d, LLG_E_TYPE, "matvec: unsupported type %d", f.type);
     }
     LLG_LAUNCH_CHECK(d, "matvec_q");
-    if (n_chunks > 1) {
+    if (n_chunks > 1 && !hand) {
         hipLaunchKernelGGL(k_chunk_sum, dim3((w->rows + 255) / 256), dim3(256), 0, a.st,
                            (const float *)part, n_chunks, w->rows, act, d_y);
         LLG_LAUNCH_CHECK(d, "matvec chunk sum");

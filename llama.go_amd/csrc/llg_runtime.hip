@@ -23,6 +23,8 @@ struct LlgDevice {
     void *ws = nullptr;
     size_t ws_bytes = 0;
     uint8_t *sync = nullptr;  // LLG_SYNC_BYTES, zeroed at allocation
+    uint64_t *mvslots = nullptr;  // chunked matvecs' hand-off slots, zero between calls
+    size_t mvslots_bytes = 0;
     std::string last_error;
     bool tearing_down = false;  // llg_hip_free: every object is freed in one sweep
 };
@@ -67,6 +69,31 @@ uint8_t *llg_dev_sync(LlgDevice *d, int *rc) {
         return nullptr;
     }
     return d->sync;
+}
+uint64_t *llg_dev_mvslots(LlgDevice *d, size_t bytes, int *rc) {
+    *rc = 0;
+    if (bytes <= d->mvslots_bytes) return d->mvslots;
+    size_t want = bytes < ((size_t)256 << 10) ? ((size_t)256 << 10) : bytes;
+    want = (want + 4095) & ~(size_t)4095;
+    if (d->mvslots) {  // every slot of the old area is zero again once the stream is idle
+        hipStreamSynchronize(d->stream);
+        hipFree(d->mvslots);
+        d->mvslots = nullptr;
+        d->mvslots_bytes = 0;
+    }
+    if (hipMalloc(&d->mvslots, want) != hipSuccess) {
+        d->mvslots = nullptr;
+        *rc = llg_set_error(d, LLG_E_NOMEM, "matvec slot area of %zu bytes failed", want);
+        return nullptr;
+    }
+    if (hipError_t e = hipMemsetAsync(d->mvslots, 0, want, d->stream); e != hipSuccess) {
+        hipFree(d->mvslots);
+        d->mvslots = nullptr;
+        *rc = llg_hip_error(d, e, "matvec slot area clear");
+        return nullptr;
+    }
+    d->mvslots_bytes = want;
+    return d->mvslots;
 }
 hipStream_t llg_dev_stream(LlgDevice *d) { return d->stream; }
 int llg_device_id(LlgDevice *d) { return d->device; }
@@ -308,6 +335,7 @@ void llg_hip_free(LlgHipDevice h) {
     d->objects.clear();
     if (d->ws) hipFree(d->ws);
     if (d->sync) hipFree(d->sync);
+    if (d->mvslots) hipFree(d->mvslots);
     hipStreamDestroy(d->stream);
     delete d;
 }
