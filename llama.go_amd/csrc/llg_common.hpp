@@ -413,10 +413,13 @@ __device__ __forceinline__ void llg_block_load<LLG_TYPE_F32>(BlockRaw<LLG_TYPE_F
 }
 
 // dot(dequant(block), x[32]) from loaded bytes; xsum = sum of the 32 x values.
-// Q4_0 sums q * x over the raw nibbles q in [0, 15] (v_cvt_f32_ubyte on
-// nibble-masked words) and subtracts 8 * xsum once; Q8_0 flips the sign bit
-// of every byte (q + 128 in [0, 255]) and subtracts 128 * xsum.  F16/F32
-// ignore xsum.
+// Q4_0 sums (64 + q) * x over f16 values built from the nibbles and subtracts
+// 72 * xsum once; Q8_0 flips the sign bit of every byte (q + 128 in [0, 255])
+// and subtracts 128 * xsum.  F16/F32 ignore xsum.  The offset term is an
+// explicit fused multiply-add (as are the F16/F32 products), so a dot rounds
+// the same in every kernel that inlines it: left to the compiler, 72 * xsum
+// shared by two rows' dots stayed a separate multiply, fused elsewhere.  The
+// Q8_0 products are the row's own and contract the same everywhere.
 template <int T>
 __device__ __forceinline__ float llg_raw_dot(const BlockRaw<T> &r, const float4 *x4, float xsum);
 // (a & m) | o in one instruction
@@ -453,7 +456,7 @@ __device__ __forceinline__ float llg_raw_dot<LLG_TYPE_Q4_0>(const BlockRaw<LLG_T
         s = __builtin_fmaf((float)p2[1], xb.z, s);
         s = __builtin_fmaf((float)p3[1], xb.w, s);
     }
-    return (s - 72.0f * xsum) * llg_f16(r.d);
+    return __builtin_fmaf(-72.0f, xsum, s) * llg_f16(r.d);
 }
 template <>
 __device__ __forceinline__ float llg_raw_dot<LLG_TYPE_Q8_0>(const BlockRaw<LLG_TYPE_Q8_0> &r,
@@ -469,7 +472,7 @@ __device__ __forceinline__ float llg_raw_dot<LLG_TYPE_Q8_0>(const BlockRaw<LLG_T
         s += (float)((v >> 16) & 0xFF) * xv.z;
         s += (float)(v >> 24) * xv.w;
     }
-    return (s - 128.0f * xsum) * llg_f16(r.d);
+    return __builtin_fmaf(-128.0f, xsum, s) * llg_f16(r.d);
 }
 template <>
 __device__ __forceinline__ float llg_raw_dot<LLG_TYPE_F16>(const BlockRaw<LLG_TYPE_F16> &r,
@@ -480,14 +483,14 @@ __device__ __forceinline__ float llg_raw_dot<LLG_TYPE_F16>(const BlockRaw<LLG_TY
     for (int i = 0; i < 4; i++) {
         const uint4 q = r.q[i];
         const float4 xa = x4[2 * i], xb = x4[2 * i + 1];
-        s += llg_f16(q.x & 0xFFFF) * xa.x;
-        s += llg_f16(q.x >> 16) * xa.y;
-        s += llg_f16(q.y & 0xFFFF) * xa.z;
-        s += llg_f16(q.y >> 16) * xa.w;
-        s += llg_f16(q.z & 0xFFFF) * xb.x;
-        s += llg_f16(q.z >> 16) * xb.y;
-        s += llg_f16(q.w & 0xFFFF) * xb.z;
-        s += llg_f16(q.w >> 16) * xb.w;
+        s = __builtin_fmaf(llg_f16(q.x & 0xFFFF), xa.x, s);
+        s = __builtin_fmaf(llg_f16(q.x >> 16), xa.y, s);
+        s = __builtin_fmaf(llg_f16(q.y & 0xFFFF), xa.z, s);
+        s = __builtin_fmaf(llg_f16(q.y >> 16), xa.w, s);
+        s = __builtin_fmaf(llg_f16(q.z & 0xFFFF), xb.x, s);
+        s = __builtin_fmaf(llg_f16(q.z >> 16), xb.y, s);
+        s = __builtin_fmaf(llg_f16(q.w & 0xFFFF), xb.z, s);
+        s = __builtin_fmaf(llg_f16(q.w >> 16), xb.w, s);
     }
     return s;
 }
@@ -499,10 +502,10 @@ __device__ __forceinline__ float llg_raw_dot<LLG_TYPE_F32>(const BlockRaw<LLG_TY
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const float4 xv = x4[i];
-        s += r.q[i].x * xv.x;
-        s += r.q[i].y * xv.y;
-        s += r.q[i].z * xv.z;
-        s += r.q[i].w * xv.w;
+        s = __builtin_fmaf(r.q[i].x, xv.x, s);
+        s = __builtin_fmaf(r.q[i].y, xv.y, s);
+        s = __builtin_fmaf(r.q[i].z, xv.z, s);
+        s = __builtin_fmaf(r.q[i].w, xv.w, s);
     }
     return s;
 }
@@ -1003,6 +1006,11 @@ uint8_t *llg_dev_sync(LlgDevice *d, int *rc);
 // launch that uses it.  Growth synchronises the stream first; null with *rc
 // set on failure.
 uint64_t *llg_dev_mvslots(LlgDevice *d, size_t bytes, int *rc);
+// Nonzero when the handle was created with LLG_CHECK_HANDOFF set (a test
+// setting): every consumer of an in-launch hand-off still waits for and
+// clears its slots, then computes each handed-over value itself and uses its
+// own, so that a test can compare the fallback path with the slots bit for bit.
+int llg_dev_check(LlgDevice *d);
 // Copy host -> device workspace slot / device -> host, on the stream.
 int llg_h2d(LlgDevice *d, void *dst, const void *src, size_t bytes);
 int llg_d2h(LlgDevice *d, void *dst, const void *src, size_t bytes);

@@ -78,12 +78,13 @@ __device__ __forceinline__ float mv_chunk_direct(const uint8_t *__restrict__ w, 
 // A reducer workgroup rb: thread t takes row rb * blockDim.x + t, polls its
 // n_chunks slots (all in each poll), adds chunk 0, 1, ... in order (as
 // k_chunk_sum), applies the activation, stores y and zeroes the slots.
+// check (llg_dev_check): every chunk sum computed here after the wait.
 template <int T>
 __device__ __forceinline__ void mv_reduce(const uint8_t *__restrict__ w, long long stride,
                                           const RowFmt &f, int rows, int chunk_blocks,
                                           int n_chunks, const float *__restrict__ x, int act,
                                           float *__restrict__ y, uint64_t *__restrict__ slots,
-                                          int rb) {
+                                          int rb, int check) {
     const int lane = threadIdx.x & 63;
     const int r = rb * (int)blockDim.x + (int)threadIdx.x;
     const int rc = min(r, rows - 1);
@@ -109,7 +110,7 @@ __device__ __forceinline__ void mv_reduce(const uint8_t *__restrict__ w, long lo
     for (int c = 0; c < MV_HAND_MAX; c++) {
         p[c] = __uint_as_float((uint32_t)v[c]);
         if (c >= n_chunks) continue;  // uniform
-        unsigned long long miss = __ballot(r < rows && (uint32_t)(v[c] >> 32) != 1u);
+        unsigned long long miss = __ballot(r < rows && (check || (uint32_t)(v[c] >> 32) != 1u));
         while (miss) {  // wavefront-uniform
             const int l = __ffsll((long long)miss) - 1;
             miss &= miss - 1;
@@ -150,7 +151,8 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
                                                   const uint8_t *__restrict__ w2 = nullptr,
                                                   LlgPredFold pf = LlgPredFold{},
                                                   LlgAttnParts ap = LlgAttnParts{},
-                                                  uint64_t *__restrict__ slots = nullptr) {
+                                                  uint64_t *__restrict__ slots = nullptr,
+                                                  int check = 0) {
     static_assert(!G || (LNP == 0 && MV_ROWS == 2), "gated rows pair gate and up");
     static_assert(!PF || (LNP == 0 && !G), "the fold rides on a plain matvec");
     static_assert(!AC || (LNP == 0 && !G), "the attention merge replaces the plain x");
@@ -165,7 +167,7 @@ __global__ __launch_bounds__(NT) void k_matvec_q(const uint8_t *__restrict__ w, 
         const int n_work = (rows + tile_rows - 1) / tile_rows * n_chunks;
         if (hand && (int)blockIdx.x >= n_work) {
             mv_reduce<T>(w, stride, f, rows, chunk_blocks, n_chunks, x, act, y, slots,
-                         (int)blockIdx.x - n_work);
+                         (int)blockIdx.x - n_work, check);
             return;
         }
     }
@@ -415,13 +417,14 @@ struct MvArgs {
     LlgPredFold pf;
     LlgAttnParts ap;
     uint64_t *slots;  // chunked rows reduced in the launch (llg_dev_mvslots)
+    int check;        // llg_dev_check
 };
 
 template <int T, int LNP, bool G, int NT, bool PF, bool AC>
 static void mv_go(const MvArgs &a) {
     hipLaunchKernelGGL((k_matvec_q<T, LNP, G, NT, PF, AC>), a.grid, dim3(a.threads), a.lds, a.st,
                        a.w->d, a.w->stride, a.w->fmt, a.w->rows, a.tile_rows, a.cb, a.x, a.act,
-                       a.y, a.part, a.ln, a.w2, a.pf, a.ap, a.slots);
+                       a.y, a.part, a.ln, a.w2, a.pf, a.ap, a.slots, a.check);
 }
 
 // Instances with NT = 1024 workgroups (the balanced launch) exist for the
@@ -511,6 +514,7 @@ static int matvec_launch(LlgDevice *d, const LlgObject *w, const float *d_x, int
     a.pf = pf ? *pf : LlgPredFold{};
     a.ap = ap ? *ap : LlgAttnParts{};
     a.slots = nullptr;
+    a.check = llg_dev_check(d);
     if (hand) {
         int rc = 0;
         a.slots = llg_dev_mvslots(d, (size_t)n_chunks * w->rows * 8, &rc);

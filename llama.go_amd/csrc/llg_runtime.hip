@@ -25,6 +25,7 @@ struct LlgDevice {
     uint8_t *sync = nullptr;  // LLG_SYNC_BYTES, zeroed at allocation
     uint64_t *mvslots = nullptr;  // chunked matvecs' hand-off slots, zero between calls
     size_t mvslots_bytes = 0;
+    int check_handoff = 0;  // LLG_CHECK_HANDOFF at creation (llg_dev_check)
     std::string last_error;
     bool tearing_down = false;  // llg_hip_free: every object is freed in one sweep
 };
@@ -96,6 +97,7 @@ uint64_t *llg_dev_mvslots(LlgDevice *d, size_t bytes, int *rc) {
     return d->mvslots;
 }
 hipStream_t llg_dev_stream(LlgDevice *d) { return d->stream; }
+int llg_dev_check(LlgDevice *d) { return d->check_handoff; }
 int llg_device_id(LlgDevice *d) { return d->device; }
 int llg_cu_count(LlgDevice *d) { return d->cus; }
 
@@ -311,6 +313,7 @@ int llg_hip_available(void) {
 LlgHipDevice llg_hip_init(void) {
     if (!llg_hip_available()) return nullptr;
     LlgDevice *d = new LlgDevice();
+    if (const char *e = getenv("LLG_CHECK_HANDOFF")) d->check_handoff = e[0] && e[0] != '0';
     if (hipGetDevice(&d->device) != hipSuccess) d->device = 0;
     if (hipSetDevice(d->device) != hipSuccess || hipStreamCreate(&d->stream) != hipSuccess) {
         delete d;

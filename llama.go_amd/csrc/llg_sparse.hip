@@ -530,6 +530,7 @@ struct HidArgs {
     float *acc_out;          // optional: acc_out[i] += acc_add[i], i < acc_n
     const float *acc_add;
     int acc_n;
+    int check;               // llg_dev_check: every unit computed by the tiles after the wait
 };
 
 // Wo . attn and the predictor in the tile launch (a Falcon layer,
@@ -736,7 +737,7 @@ __device__ __forceinline__ void tile_take_hidden(float *hid, const HidArgs &ha, 
             v = llg_slot_get(slots + r);
         }
         float hv = __uint_as_float((uint32_t)v);
-        unsigned long long miss = __ballot((uint32_t)(v >> 32) != epoch);
+        unsigned long long miss = __ballot(ha.check || (uint32_t)(v >> 32) != epoch);
         while (miss) {  // wavefront-uniform
             const int l = __ffsll((long long)miss) - 1;
             miss &= miss - 1;
@@ -769,7 +770,7 @@ __device__ __forceinline__ void tile_take_comb(float *hid, const WoArgs &wa, con
             v = llg_slot_get(slots + r);
         }
         float hv = __uint_as_float((uint32_t)v);
-        unsigned long long miss = __ballot((uint32_t)(v >> 32) != epoch);
+        unsigned long long miss = __ballot(ha.check || (uint32_t)(v >> 32) != epoch);
         while (miss) {  // wavefront-uniform
             const int l = __ffsll((long long)miss) - 1;
             miss &= miss - 1;
@@ -1695,6 +1696,7 @@ int llg_fused_enqueue(LlgDevice *d, LlgObject *wup, LlgObject *wout, LlgObject *
         ha.a = d_a;
         ha.ctr = reinterpret_cast<const uint32_t *>(sync);
         ha.slots = reinterpret_cast<uint64_t *>(sync + LLG_SYNC_HEAD);
+        ha.check = llg_dev_check(d);
         // with d_out_add, the predictor workgroups first add d_out_add to out
         // and k_tile_reduce adds the FFN output to that (out ends as (out +
         // d_out_add) + the FFN output, the residual order of ffn_flash.go:161-166)
@@ -1746,6 +1748,7 @@ int llg_fused_wo_enqueue(LlgDevice *d, const LlgObject *wo, const LlgAttnParts &
     HidArgs ha{};
     ha.ctr = reinterpret_cast<const uint32_t *>(sync);
     ha.slots = reinterpret_cast<uint64_t *>(sync + LLG_SYNC_HEAD);
+    ha.check = llg_dev_check(d);
     WoArgs wa{};
     wa.w = wo->d;
     wa.stride = wo->stride;
