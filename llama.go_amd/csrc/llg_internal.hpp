@@ -65,6 +65,7 @@ struct LlgWinUpd {
     const int32_t *ring_exp, *ring_len_exp, *ring_set_exp;
     uint64_t *uslot;
     int epoch;
+    int check;  // llg_dev_check: every entry's activation computed by the down role after its wait
 };
 // max_active: capacity of the list and of the pair workspace (the count read
 // on the device is clamped to it); n_rows: the neurons of the bundle or window

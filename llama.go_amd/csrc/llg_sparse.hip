@@ -1317,23 +1317,34 @@ __device__ __forceinline__ void ws_down_batch(const LlgWinUpd &u, long long bstr
     // A slot still stale (never seen in a working launch): in rounds, every
     // thread with a stale entry lists one of them, the wavefronts compute the
     // listed up rows with the up workgroups' sums (x staged the same way) and
-    // write their slots, and the threads read their slots again.
-    if (__syncthreads_or(!ready())) {
+    // write their slots, and the threads read their slots again.  With
+    // u.check every valid entry counts as stale until it has been computed
+    // here once (after the wait, so that value is the last one written to
+    // its slot).
+    if (__syncthreads_or(!ready() || u.check)) {
         __shared__ int ws_n;
         __shared__ int3 ws_list[ws_threads<T>()];
         const int lane = threadIdx.x & 63;
         const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        bool redo[K];
+#pragma unroll
+        for (int k = 0; k < K; k++) redo[k] = u.check;
         auto stale = [&](int k) {
-            return k < nvalid && nn[k] >= 0 && (uint32_t)(v[k] >> 32) != (uint32_t)u.epoch;
+            return k < nvalid && nn[k] >= 0 &&
+                   (redo[k] || (uint32_t)(v[k] >> 32) != (uint32_t)u.epoch);
         };
         stage_x<stage_rounds(ws_threads<T>())>(xs, x, f.nb);
         for (;;) {  // uniform: ends when no thread has a stale entry
             if (threadIdx.x == 0) ws_n = 0;
             __syncthreads();
             int3 mine = make_int3(-1, 0, 0);
+            int mk = -1;
 #pragma unroll
             for (int k = K - 1; k >= 0; k--)
-                if (stale(k)) mine = make_int3(tid + bd * (i0 + k), nn[k], fs[k] ? 1 : 0);
+                if (stale(k)) {
+                    mine = make_int3(tid + bd * (i0 + k), nn[k], fs[k] ? 1 : 0);
+                    mk = k;
+                }
             if (mine.x >= 0) ws_list[atomicAdd(&ws_n, 1)] = mine;
             __syncthreads();
             const int cnt = ws_n;
@@ -1348,8 +1359,10 @@ __device__ __forceinline__ void ws_down_batch(const LlgWinUpd &u, long long bstr
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
 #pragma unroll
-            for (int k = 0; k < K; k++)
+            for (int k = 0; k < K; k++) {
                 if (stale(k)) v[k] = llg_slot_get(u.uslot + tid + bd * (i0 + k));
+                if (k == mk) redo[k] = false;
+            }
         }
     }
 #pragma unroll

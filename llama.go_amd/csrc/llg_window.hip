@@ -130,6 +130,7 @@ static LlgWinUpd next_update(LlgWindow *w, hipStream_t st) {
     u.ring_set_exp = w->ring_set + e;
     u.uslot = w->uslot;
     u.epoch = w->epoch;
+    u.check = 0;
     w->head = (w->head + 1) % (w->k + 1);
     return u;
 }
@@ -290,7 +291,8 @@ int llg_hipd_window_step(LlgHipDevice h, int64_t hw, const float *d_x, const int
     if (!d_x || !d_active || !d_n_active || !d_out)
         return llg_set_error(d, LLG_E_ARG, "window_step: null pointer");
     if (int rc = llg_check_act(d, act)) return rc;
-    const LlgWinUpd u = next_update(w, llg_dev_stream(d));
+    LlgWinUpd u = next_update(w, llg_dev_stream(d));
+    u.check = llg_dev_check(d);
     return llg_win_step_enqueue(d, u, w->bundle->fmt, w->bstride, d_x, d_active, d_n_active,
                                 w->ff, w->ff, act, d_out);
 }

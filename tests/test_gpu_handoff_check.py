@@ -2,7 +2,7 @@
 
 A consumer of a tagged-slot hand-off (the chunked matvec's reducer
 workgroups, the fused sparse step's tile workgroups, the Falcon tile launch's
-tile workgroups) computes a value itself when its slot stays empty for the
+tile workgroups, the window step's down workgroups) computes a value itself when its slot stays empty for the
 poll bound, so that every wait ends.  In a working launch that never
 happens.  A device created with LLG_CHECK_HANDOFF set makes every consumer,
 after the usual wait, compute every handed-over value itself and use its own;
@@ -20,7 +20,7 @@ import llg
 import llg.gguf as gg
 from oracle import refcpu as R
 from tests.helpers import make_falcon, make_sparse_layer, max_rel_err, normal, ref_falcon_f64, \
-    threshold_for
+    threshold_for, window_sets
 
 pytestmark = pytest.mark.gpu
 
@@ -118,3 +118,35 @@ def test_falcon_tile_launch_fallback_bit_identical(dev, dev_check, rng):
     for (l0, _, n0), (l1, _, n1) in zip(*runs):
         assert np.array_equal(_bits(l0), _bits(l1))
         assert np.array_equal(n0, n1)
+
+
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16, gg.F32])
+def test_window_step_fallback_bit_identical(dev, dev_check, rng, t):
+    """Window steps (update + FFN in one launch, k = 3, 20 tokens of 120 active
+    neurons, 60% carried over): each entry's activation from the up
+    workgroups' slot, or computed by the down workgroup itself."""
+    h, ff = 512, 1024
+    up, dn = make_sparse_layer(rng, h, ff, t)
+    sets = window_sets(rng, ff, 120, 20, 0.6)
+    xs = [normal(rng, h, 1.0) for _ in sets]
+    runs = []
+    for dv in (dev, dev_check):
+        b = dv.upload_bundle(up, dn, t, h, ff)
+        nc = llg.NeuronCache(dv, b, 3)
+        d_out = torch.empty(h, device="cuda")
+        d_n = torch.empty(1, dtype=torch.int32, device="cuda")
+        outs = []
+        for a, x in zip(sets, xs):
+            d_x = torch.from_numpy(x).cuda()
+            d_a = torch.from_numpy(np.ascontiguousarray(a, np.int32)).cuda()
+            d_n.fill_(a.size)
+            torch.cuda.synchronize()
+            nc.step_device(d_x.data_ptr(), d_a.data_ptr(), d_n.data_ptr(), d_out.data_ptr())
+            dv.sync()
+            outs.append(d_out.cpu().numpy())
+        runs.append((outs, nc.resident()))
+        nc.win.release()
+        b.release()
+    for o0, o1 in zip(runs[0][0], runs[1][0]):
+        assert np.array_equal(_bits(o0), _bits(o1))
+    assert np.array_equal(runs[0][1], runs[1][1])
