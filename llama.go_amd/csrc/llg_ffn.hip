@@ -19,7 +19,8 @@
 // slots.  A slot not filled within MV_POLLS polls is computed by the reducer
 // itself from x in memory (the chunk workgroup's blocks, block sums and
 // order), so the wait always ends.  Without slots (more than MV_HAND_MAX
-// chunks) the partial sums go to part[chunk][row] and k_chunk_sum adds them.
+// chunks, or the attention-merge instance) the partial sums go to
+// part[chunk][row] and k_chunk_sum adds them.
 // Either way the chunks are added in a fixed order, so results are the same
 // on every run.
 //
