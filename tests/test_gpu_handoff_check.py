@@ -150,3 +150,23 @@ def test_window_step_fallback_bit_identical(dev, dev_check, rng, t):
     for o0, o1 in zip(runs[0][0], runs[1][0]):
         assert np.array_equal(_bits(o0), _bits(o1))
     assert np.array_equal(runs[0][1], runs[1][1])
+
+
+def test_matvec_slot_area_grows(rng):
+    """On a fresh handle, a chunked matvec of 512 rows (4 column chunks) and
+    then one of 20000 rows: the second needs 4 x 20000 slots (640 KB), more
+    than the first call's area (256 KB), so the area is replaced by a larger
+    zeroed one between the calls.  Both against the oracle."""
+    t = gg.Q4_0
+    dv = llg.Device()
+    try:
+        for rows, cols in [(512, 18176), (20000, 18176)]:
+            w = _gpu_quant((rows, cols), 0.02, 81 + rows, t)
+            x = normal(rng, cols, 1.0)
+            m = dv.upload_matrix(w, t, rows, cols)
+            got = dv.matvec_q(m, x)
+            ref = R.matmulvec(np.stack([R.dequantize(w[r], t) for r in range(rows)]), x)
+            assert max_rel_err(got, ref) <= 1e-5, rows
+            m.release()
+    finally:
+        dv.close()
