@@ -229,6 +229,23 @@ def test_matvec_q_small(dev, rng, t):
     m.release()
 
 
+@pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16, gg.F32])
+@pytest.mark.parametrize("cols", [6400, 25600])
+def test_matvec_q_chunked_ragged(dev, rng, t, cols):
+    """Rows wider than one workgroup's staged x: 6400 columns (2 column chunks,
+    reduced inside the launch by one reducer workgroup whose threads past row
+    77 idle) and 25600 columns (5 chunks: partial sums added by k_chunk_sum);
+    77 rows, so the last 8-row tile is partial."""
+    rows = 77
+    w = quant(normal(rng, (rows, cols), 0.02), t)
+    x = normal(rng, cols, 1.0)
+    m = dev.upload_matrix(w, t, rows, cols)
+    ref = R.matmulvec(np.stack([R.dequantize(w[r], t) for r in range(rows)]), x)
+    for _ in range(2):  # the second call finds the slots zeroed by the first
+        assert max_rel_err(dev.matvec_q(m, x), ref) <= 1e-5
+    m.release()
+
+
 @pytest.mark.parametrize("t", [gg.Q4_0, gg.Q8_0, gg.F16])
 @pytest.mark.parametrize("act", [gg.ACT_RELU, gg.ACT_GELU])
 def test_ffn_dense_config1(dev, rng, t, act):
