@@ -1,13 +1,15 @@
-"""HIP graph replay of the chunked matvecs' in-launch reduce.
+"""HIP graph replay of the in-launch hand-offs.
 
 The down matvec of a dense or SwiGLU FFN at these shapes (18176 and 11008
 columns) splits its rows into column chunks that hand their partial sums to
-reducer workgroups of the same launch through tagged slots; the reducers
-zero the slots again, so a replayed graph needs no reset (and records no
-memset).  A call is captured on the handle's stream after eager calls have
-allocated the workspace and the slot area; the graph is then replayed with
-new inputs in the captured buffer, with eager calls and synchronisations in
-between, and every replay must equal the eager result to the bit."""
+reducer workgroups of the same launch through tagged slots, which the
+reducers zero again; the fused sparse step hands the predictor's hidden
+units to its tiles in slots tagged with an epoch that its reduce advances on
+the device.  So a replayed graph needs no reset (and records no memset).  A
+call is captured on the handle's stream after eager calls have allocated
+what it uses; the graph is then replayed with new inputs in the captured
+buffer, with eager calls and synchronisations in between, and every replay
+must equal the eager result to the bit."""
 import ctypes
 
 import numpy as np
@@ -16,7 +18,8 @@ import torch
 
 import llg
 import llg.gguf as gg
-from tests.helpers import normal
+from oracle import refcpu as R
+from tests.helpers import make_sparse_layer, normal, threshold_for
 
 pytestmark = pytest.mark.gpu
 
@@ -79,3 +82,61 @@ def test_chunked_down_graph_replay(dev, rng, kind, h, ff):
     del graph
     for m in (u, d, g):
         m.release()
+
+
+def test_fused_sparse_step_graph_replay(dev, rng):
+    """ffnFlash path 2 at the Falcon-7B layer's shape: the predictor workgroups
+    hand the hidden units to the tiles in slots tagged with the sync area's
+    epoch, and k_tile_reduce advances the epoch word on the device, so a
+    replay never accepts a slot from an earlier one.  Captured once, replayed
+    12 times with new inputs and eager calls between: outputs and active
+    lists equal the eager ones to the bit."""
+    h, ff, rank = 4544, 18176, 128
+    up, dn = make_sparse_layer(rng, h, ff, gg.Q4_0)
+    wup, wout = normal(rng, (rank, h), 0.05), normal(rng, (ff, rank), 0.05)
+    xs = [normal(rng, h, 1.0) for _ in range(4)]
+    _, lg = R.predict(wup, wout, None, xs[0], 0.0)
+    thr = threshold_for(lg, 909)
+    p = llg.Predictor(dev, wup, wout, None, thr)
+    b = dev.upload_bundle(up, dn, gg.Q4_0, h, ff)
+    xd = torch.empty(h, device="cuda")
+    outd = torch.empty(h, device="cuda")
+    actd = torch.empty(ff, dtype=torch.int32, device="cuda")
+    nd = torch.empty(1, dtype=torch.int32, device="cuda")
+
+    def call():
+        dev.check(dev.lib.llg_hipd_ffn_predict_sparse(
+            dev.h, p.w_up.id, p.w_out.id, p.bias_id, b.id, _vp(xd), _vp(xd), ctypes.c_float(thr),
+            gg.ACT_RELU, _vp(outd), _vp(actd), _vp(nd)), "ffn_predict_sparse")
+
+    def result():
+        k = int(nd.cpu()[0])
+        return outd.cpu().numpy().copy(), actd[:k].cpu().numpy().copy()
+
+    refs = []
+    for x in xs:  # eager results (the first call allocates the workspace and sync area)
+        xd.copy_(torch.from_numpy(x))
+        torch.cuda.synchronize()
+        call()
+        dev.sync()
+        refs.append(result())
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.ExternalStream(dev.stream)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        call()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for x, (ro, ra) in zip(xs, refs):
+            xd.copy_(torch.from_numpy(x))
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            o, a = result()
+            assert np.array_equal(_bits(o), _bits(ro)) and np.array_equal(a, ra)
+            call()  # eager work between the replays
+            dev.sync()
+            o, a = result()
+            assert np.array_equal(_bits(o), _bits(ro)) and np.array_equal(a, ra)
+    del graph
+    b.release()
