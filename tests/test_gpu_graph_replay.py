@@ -5,7 +5,8 @@ columns) splits its rows into column chunks that hand their partial sums to
 reducer workgroups of the same launch through tagged slots, which the
 reducers zero again; the fused sparse step hands the predictor's hidden
 units to its tiles in slots tagged with an epoch that its reduce advances on
-the device.  So a replayed graph needs no reset (and records no memset).  A
+the device, as do the layers of the Falcon step.  So a replayed graph needs
+no reset (and records no memset).  A
 call is captured on the handle's stream after eager calls have allocated
 what it uses; the graph is then replayed with new inputs in the captured
 buffer, with eager calls and synchronisations in between, and every replay
@@ -19,7 +20,7 @@ import torch
 import llg
 import llg.gguf as gg
 from oracle import refcpu as R
-from tests.helpers import make_sparse_layer, normal, threshold_for
+from tests.helpers import make_falcon, make_sparse_layer, normal, ref_falcon_f64, threshold_for
 
 pytestmark = pytest.mark.gpu
 
@@ -140,3 +141,61 @@ def test_fused_sparse_step_graph_replay(dev, rng):
             assert np.array_equal(_bits(o), _bits(ro)) and np.array_equal(a, ra)
     del graph
     b.release()
+
+
+FALCON = dict(n_layers=2, hidden=256, n_heads=4, n_kv=1, head_dim=64, ff=512, vocab=300,
+              max_seq=64, rank=16, rope_base=10000.0, eps=1e-5)
+
+
+def test_falcon_step_graph_replay(dev, rng):
+    """One decode step of a Falcon model whose layers run Wo and the predictor
+    in the tile launch (combiner slots, the sync area's epoch), captured at
+    position 23 after an eager prefill of positions 0-22 and replayed with
+    four different tokens, eager steps at the same position in between: the
+    logits (copied out by the step) equal the eager ones to the bit and the
+    next token is the same."""
+    d = dict(FALCON)
+    w = make_falcon(rng, d)
+    prompt = rng.integers(0, d["vocab"], 24)
+    _, _, thr = ref_falcon_f64(w, d, prompt)
+    m = llg.FalconModel(dev, d, w, thr)
+    toks = torch.tensor(prompt.astype(np.int32), device="cuda")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    pos = 23
+    for s_ in range(pos):
+        m.step_device(toks.data_ptr() + 4 * s_, s_, sink.data_ptr())
+    dev.sync()
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+    lg = torch.empty(d["vocab"], device="cuda")
+    cands = [int(c) for c in rng.integers(0, d["vocab"], 4)]
+
+    def step():
+        m.step_device(tok.data_ptr(), pos, nxt.data_ptr(), lg.data_ptr())
+
+    refs = []
+    for c in cands:
+        tok.fill_(c)
+        torch.cuda.synchronize()
+        step()
+        dev.sync()
+        refs.append((lg.cpu().numpy().copy(), int(nxt.cpu()[0])))
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.ExternalStream(dev.stream)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        step()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        for c, (rl, rn) in zip(cands, refs):
+            tok.fill_(c)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(_bits(lg.cpu().numpy()), _bits(rl)) and int(nxt.cpu()[0]) == rn
+            step()  # eager work between the replays
+            dev.sync()
+            assert np.array_equal(_bits(lg.cpu().numpy()), _bits(rl)) and int(nxt.cpu()[0]) == rn
+    del graph
+    m.release()
